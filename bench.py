@@ -1,0 +1,286 @@
+#!/usr/bin/env python3
+"""gdn2 token-mixer benchmark on one MI355X.
+
+Headline workload: chunkwise prefill of B=8 sequences of
+T=4096 tokens, H=16 heads, d_k = d_v = 128, bf16 inputs, fp32 log-decay and
+state, chunk 64, in-kernel q/k L2 norm, final state written.  A "step" is one
+full forward of that batch with the inputs already resident in HBM.
+
+Also measured: the single-token decode step, N=64
+sequences x 16 heads, fp32 state [64,16,128,128] updated in place, 1024
+consecutive steps captured in one HIP graph.
+
+Prints one JSON line: value = prefill tokens/s, with the roofline of the
+prefill kernels (HBM-bound), the decode figures, and the CPU baseline (the C
+restatement of the reference recurrence, oracle/gdn2_cpu.c, timed on this
+host's cores on the same prefill inputs).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+METRIC = "gdn2 prefill tokens/s + decode µs/step; % of MFMA / HBM roofline"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+PREFILL = dict(B=8, T=4096, H=16, K=128, V=128, C=64)
+DECODE = dict(N=64, H=16, K=128, V=128, steps=1024)
+
+
+def prefill_flops(B, T, H, K, V, C):
+    """Dense chunkwise WY work per token-head: 6KV + 2C(3K+2V) + C^2/3."""
+    return B * T * H * (6 * K * V + 2 * C * (3 * K + 2 * V) + C * C / 3.0)
+
+
+def prefill_bytes(B, T, H, K, V):
+    """Algorithmic HBM bytes: q,k,b,v,w bf16 + g fp32 in, o bf16 out, fp32 final state."""
+    per_th = 2 * (3 * K + 2 * V) + 4 * K + 2 * V
+    return B * T * H * per_th + B * H * K * V * 4
+
+
+def decode_bytes(N, H, K, V):
+    """Per step: fp32 state read + write, q,k,b,v,w bf16 + g fp32 in, o bf16 out."""
+    return 2 * N * H * K * V * 4 + N * H * (2 * (3 * K + 2 * V) + 4 * K + 2 * V)
+
+
+def make_prefill_inputs(torch, dev, B, T, H, K, V, seed=1):
+    """Config-1 recipe: q,k ~ N(0,1) L2-normalised; v ~ N(0,1); beta = sigmoid(N);
+    g = -softplus(N + 2); beta and g per (b,t,h), broadcast to the channel-wise API."""
+    F = torch.nn.functional
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    bf = torch.bfloat16
+    q = F.normalize(torch.randn(B, T, H, K, generator=gen, device=dev), dim=-1).to(bf)
+    k = F.normalize(torch.randn(B, T, H, K, generator=gen, device=dev), dim=-1).to(bf)
+    v = torch.randn(B, T, H, V, generator=gen, device=dev).to(bf)
+    beta = torch.sigmoid(torch.randn(B, T, H, 1, generator=gen, device=dev))
+    g = -F.softplus(torch.randn(B, T, H, 1, generator=gen, device=dev) + 2.0)
+    g = g.expand(B, T, H, K).contiguous()
+    b = beta.expand(B, T, H, K).to(bf).contiguous()
+    w = beta.expand(B, T, H, V).to(bf).contiguous()
+    return q, k, v, g, b, w
+
+
+def bench_prefill(torch, nat, dev, steps, warmup):
+    B, T, H, K, V, C = (PREFILL[x] for x in ("B", "T", "H", "K", "V", "C"))
+    q, k, v, g, b, w = make_prefill_inputs(torch, dev, B, T, H, K, V)
+    lib = nat.load()
+    io, gd = nat.DTYPE_BF16, nat.DTYPE_F32
+    ws_bytes = lib.gdn2_chunk_fwd_workspace_size(B, T, H, K, V, io, None, B)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    o = torch.empty_like(v)
+    ht = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
+    scale = K**-0.5
+    flags = nat.FLAG_L2NORM_QK
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def prep():
+        st = lib.gdn2_chunk_fwd_prep(q.data_ptr(), k.data_ptr(), g.data_ptr(), b.data_ptr(), io, gd,
+                                     None, None, 0.0, None, None, B, B, T, H, K, V, scale, flags,
+                                     ws.data_ptr(), ws_bytes, sh)
+        nat.check(st, "gdn2_chunk_fwd_prep")
+
+    def scan():
+        st = lib.gdn2_chunk_fwd_scan(v.data_ptr(), w.data_ptr(), io, o.data_ptr(), None,
+                                     ht.data_ptr(), None, None, B, B, T, H, K, V, ws.data_ptr(),
+                                     ws_bytes, sh)
+        nat.check(st, "gdn2_chunk_fwd_scan")
+
+    for _ in range(warmup):
+        prep()
+        scan()
+    torch.cuda.synchronize(dev)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for e in evs:
+        e[0].record(stream)
+        prep()
+        e[1].record(stream)
+        scan()
+        e[2].record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    t_prep = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    t_scan = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    if not torch.isfinite(o.float()).all() or not torch.isfinite(ht).all():
+        raise RuntimeError("non-finite prefill output")
+    ms_step = wall * 1e3 / steps
+    return dict(ms_step=ms_step, t_prep_ms=t_prep, t_scan_ms=t_scan,
+                inputs=(q, k, v, g, b, w))
+
+
+def bench_decode(torch, nat, dev, reps=3):
+    N, H, K, V, S = (DECODE[x] for x in ("N", "H", "K", "V", "steps"))
+    F = torch.nn.functional
+    gen = torch.Generator(device=dev).manual_seed(2)
+    bf = torch.bfloat16
+    state = torch.randn(N, H, K, V, generator=gen, device=dev) * 0.02
+    q = F.normalize(torch.randn(S, N, 1, H, K, generator=gen, device=dev), dim=-1).to(bf)
+    k = F.normalize(torch.randn(S, N, 1, H, K, generator=gen, device=dev), dim=-1).to(bf)
+    v = torch.randn(S, N, 1, H, V, generator=gen, device=dev).to(bf)
+    beta = torch.sigmoid(torch.randn(S, N, 1, H, 1, generator=gen, device=dev))
+    g = (-F.softplus(torch.randn(S, N, 1, H, 1, generator=gen, device=dev) + 2.0)).expand(
+        S, N, 1, H, K).contiguous()
+    b = beta.expand(S, N, 1, H, K).to(bf).contiguous()
+    w = beta.expand(S, N, 1, H, V).to(bf).contiguous()
+    o = torch.empty(S, N, 1, H, V, dtype=bf, device=dev)
+    lib = nat.load()
+    scale = K**-0.5
+    sz_k, sz_v, sz_g = N * H * K * 2, N * H * V * 2, N * H * K * 4
+
+    def step(i, sh):
+        st = lib.gdn2_recurrent_fwd(
+            q.data_ptr() + i * sz_k, k.data_ptr() + i * sz_k, v.data_ptr() + i * sz_v,
+            g.data_ptr() + i * sz_g, b.data_ptr() + i * sz_k, w.data_ptr() + i * sz_v,
+            nat.DTYPE_BF16, nat.DTYPE_F32, o.data_ptr() + i * sz_v,
+            state.data_ptr(), state.data_ptr(), None, None, 0.0, None, N,
+            N, 1, H, H, K, V, scale, nat.FLAG_L2NORM_QK, sh)
+        nat.check(st, "gdn2_recurrent_fwd")
+
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for i in range(4):
+            step(i, side.cuda_stream)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sh = torch.cuda.current_stream(dev).cuda_stream
+        for i in range(S):
+            step(i, sh)
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    times = []
+    cur = torch.cuda.current_stream(dev)
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        graph.replay()
+        e1.record(cur)
+        torch.cuda.synchronize(dev)
+        times.append(e0.elapsed_time(e1))
+    if not torch.isfinite(state).all() or not torch.isfinite(o.float()).all():
+        raise RuntimeError("non-finite decode output")
+    us_step = statistics.median(times) * 1e3 / S
+    nbytes = decode_bytes(N, H, K, V)
+    gbs = nbytes / (us_step * 1e-6) / 1e9
+    return dict(us_per_step=round(us_step, 3), steps=S, reps=reps,
+                bytes_per_step=nbytes, achieved_GBps=round(gbs, 1),
+                frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4),
+                config={"workload": "C2 decode N64 H16 K128 V128, fp32 state in place, 1024 steps "
+                                    "in one HIP graph", "dtype": "bf16 in / fp32 state"})
+
+
+def cpu_baseline(torch, inputs, max_threads=16, reps=3):
+    """Time the C port of the reference recurrence on this host's cores, same prefill inputs."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import cpu_lib
+
+    q, k, v, g, b, w = (x.float().cpu().numpy() for x in inputs)
+    B, T, H, K = q.shape
+    threads = max(1, min(max_threads, len(os.sched_getaffinity(0))))
+    cpu_lib.recurrent_fwd_f32(q[:, :64], k[:, :64], v[:, :64], g[:, :64], b[:, :64], w[:, :64],
+                              nthreads=threads)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        cpu_lib.recurrent_fwd_f32(q, k, v, g, b, w, nthreads=threads)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(B * T / t, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"full config-1 prefill batch (B{B} T{T} H{H} K{K}), fp32 token recurrence "
+                      f"(oracle/gdn2_cpu.c, OpenMP over sequence-heads), median of {reps} runs "
+                      f"of {t:.2f} s; cpu: {model}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (--gpus 1); multi-GPU sharding of the "
+              "gdn2 path is a design note, not a measured configuration.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from qwendopamine_amd import _native as nat
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    P = PREFILL
+    res = bench_prefill(torch, nat, dev, args.steps, args.warmup)
+    B, T, H, K, V, C = P["B"], P["T"], P["H"], P["K"], P["V"], P["C"]
+    tokens = B * T
+    ms = res["ms_step"]
+    nbytes = prefill_bytes(B, T, H, K, V)
+    flops = prefill_flops(B, T, H, K, V, C)
+    t_op_ms = res["t_prep_ms"] + res["t_scan_ms"]
+    achieved = nbytes / (t_op_ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(tokens / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (BASELINE config-1 recipe, seeded)",
+        "config": {"workload": "C1 gdn2 chunkwise prefill", "B": B, "T": T, "H": H, "d_k": K,
+                   "d_v": V, "chunk": C, "inputs": "bf16 q,k,v,b,w; fp32 g; fp32 state",
+                   "l2norm_in_kernel": True, "final_state": True, "parallelism": "single GPU"},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gdn2 chunk forward = chunk_prep_kernel + chunk_scan_kernel (one op)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes": nbytes,
+            "op_ms": round(t_op_ms, 4),
+            "kernels_ms": {"chunk_prep_kernel": round(res["t_prep_ms"], 4),
+                           "chunk_scan_kernel": round(res["t_scan_ms"], 4)},
+            "mfma": {"algorithmic_flop": flops,
+                     "achieved_TFLOPs": round(flops / (t_op_ms * 1e-3) / 1e12, 2),
+                     "peak_TFLOPs": BF16_PEAK_TFLOPS,
+                     "frac": round(flops / (t_op_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+        },
+    }
+    if not args.no_decode:
+        out["decode"] = bench_decode(torch, nat, dev)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(torch, res["inputs"])
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,134 @@
+/*
+ * gdn2_hip.h -- C ABI of libgdn2_hip.so, the MI355X (gfx950) execution backend
+ * of the gdn2 (GatedDeltaNet2) token mixer.
+ *
+ * Every entry point takes raw device pointers, plain integer sizes and a HIP
+ * stream passed as `void *` (a hipStream_t; NULL = the default stream), and
+ * returns a gdn2_status code.  No torch or HIP types appear in the signatures,
+ * so ctypes / cgo / JNI can bind them directly.
+ *
+ * Tensor layouts (all contiguous, innermost dimension last):
+ *   q, k        [B, T, H,  K]     io_dtype
+ *   v, w, o     [B, T, HV, V]     io_dtype
+ *   g, b        [B, T, HV, K]     g in g_dtype, b in io_dtype
+ *   states      [N, HV, K, V]     float32 (V fastest), N = B, or the number of
+ *                                 packed sequences when cu_seqlens is given
+ * HV must be a multiple of H (grouped value heads); the chunk entry points
+ * require HV == H, as the reference chunk op does.
+ *
+ * Calls are asynchronous on `stream`.  Argument errors are reported before
+ * anything is launched; GDN2_ERR_LAUNCH reports a failed kernel launch.
+ */
+#ifndef GDN2_HIP_H
+#define GDN2_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN2_ABI_VERSION 1
+
+enum gdn2_dtype {
+    GDN2_DTYPE_F32 = 0,
+    GDN2_DTYPE_BF16 = 1,
+    GDN2_DTYPE_F16 = 2,
+};
+
+enum gdn2_status {
+    GDN2_OK = 0,
+    GDN2_ERR_INVALID = -1,     /* bad pointer, shape or flag combination   */
+    GDN2_ERR_UNSUPPORTED = -2, /* valid request this build does not handle */
+    GDN2_ERR_LAUNCH = -3,      /* the HIP runtime rejected a launch        */
+    GDN2_ERR_WORKSPACE = -4,   /* workspace missing or too small           */
+};
+
+/* Flags (bitwise or). */
+#define GDN2_FLAG_L2NORM_QK 1u      /* q, k <- x / max(||x||, 1e-6) in-kernel  */
+#define GDN2_FLAG_GATE_IN_KERNEL 2u /* g is the raw gate pre-activation        */
+#define GDN2_FLAG_LOWER_BOUND 4u    /* with GATE_IN_KERNEL: bounded sigmoid    */
+
+int gdn2_abi_version(void);
+const char *gdn2_status_string(int status);
+
+/*
+ * Token-serial forward: decode steps and short prefills.
+ * Replaces fused_recurrent_gdn2 / fused_recurrent_gdn2_fwd
+ * (reference src/qwendopamine/models/gdn2/gdn2_ops/fused_recurrent_gdn2.py:461-555
+ * and :344-458), whose arithmetic is torch_recurrent_gdn2 (gdn2.py:100-184).
+ *
+ *   initial_state  NULL = zero state.
+ *   final_state    NULL = not stored; may equal initial_state (in-place update,
+ *                  the reference's inplace_final_state).
+ *   A_log [HV], dt_bias [HV*K]  used only with GDN2_FLAG_GATE_IN_KERNEL
+ *                  (dt_bias may be NULL); lower_bound only with LOWER_BOUND.
+ *   cu_seqlens     NULL, or num_seqs+1 int64 offsets into T (then B == 1).
+ */
+int gdn2_recurrent_fwd(const void *q, const void *k, const void *v, const void *g,
+                       const void *b, const void *w, int io_dtype, int g_dtype, void *o,
+                       const float *initial_state, float *final_state, const float *A_log,
+                       const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
+                       int num_seqs, int B, int T, int H, int HV, int K, int V, float scale,
+                       unsigned flags, void *stream);
+
+/*
+ * Bytes of device workspace gdn2_chunk_fwd needs for this shape.
+ */
+size_t gdn2_chunk_fwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,
+                                     const int64_t *cu_seqlens_host, int num_seqs);
+
+/*
+ * Chunkwise-parallel (C = 64) forward: prefill and training forward.
+ * Replaces chunk_gdn2 / chunk_gdn2_fwd
+ * (reference src/qwendopamine/models/gdn2/gdn2_ops/chunk_gdn2.py:1268-1434 and
+ * :1165-1264).  Same arguments as gdn2_recurrent_fwd with HV == H, plus a
+ * device workspace of at least gdn2_chunk_fwd_workspace_size() bytes.
+ * cu_seqlens_host mirrors cu_seqlens on the host (the reference's
+ * cu_seqlens_cpu); both NULL or both given.
+ */
+int gdn2_chunk_fwd(const void *q, const void *k, const void *v, const void *g, const void *b,
+                   const void *w, int io_dtype, int g_dtype, void *o,
+                   const float *initial_state, float *final_state, const float *A_log,
+                   const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
+                   const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H, int K,
+                   int V, float scale, unsigned flags, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
+/*
+ * The two stages of gdn2_chunk_fwd, for callers that schedule or time them
+ * separately.  Calling prep then scan on the same workspace equals
+ * gdn2_chunk_fwd.
+ *
+ * Stage 1 -- per-chunk K-side work, all chunks in parallel (in-kernel L2 norm,
+ * scale and gate; in-chunk cumulative decay; decayed q.k^T and (b*k).k^T
+ * products; the triangular inverse of the WY/UT transform).  Replaces
+ * chunk_gdn2_fwd_intra + recompute_w_u_fwd_gdn2 (reference
+ * gdn2_ops/chunk_gdn2.py:1010-1162).  Reads q, k, g, b; writes the workspace.
+ */
+int gdn2_chunk_fwd_prep(const void *q, const void *k, const void *g, const void *b,
+                        int io_dtype, int g_dtype, const float *A_log, const float *dt_bias,
+                        float lower_bound, const int64_t *cu_seqlens,
+                        const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H,
+                        int K, int V, float scale, unsigned flags, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/*
+ * Stage 2 -- the sequential inter-chunk state scan and the outputs.  Replaces
+ * chunk_gated_delta_rule_fwd_h (reference gdn2_ops/chunk_kda.py:2217-2294) and
+ * the output stage chunk_gla_fwd_o_gk (called at chunk_gdn2.py:1243-1255).
+ * Reads v, w, the initial state and the workspace; writes o and the final
+ * state.
+ */
+int gdn2_chunk_fwd_scan(const void *v, const void *w, int io_dtype, void *o,
+                        const float *initial_state, float *final_state,
+                        const int64_t *cu_seqlens, const int64_t *cu_seqlens_host, int num_seqs,
+                        int B, int T, int H, int K, int V, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN2_HIP_H */

@@ -1,0 +1,338 @@
+r"""CPU oracle for the gdn2 (GatedDeltaNet2) token mixer.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker.  The product package ``qwendopamine_amd`` never imports it and has no
+CPU fallback.
+
+Everything here is plain numpy in float64 (pure-Python loops only over tokens
+and chunks).  Functions and the reference code they restate:
+
+* ``l2normalize``       -- ``F.normalize(x, p=2, dim=-1, eps=1e-6)`` as used at
+                           reference ``models/gdn2/gdn2.py:139-141``.
+* ``recurrent_fwd``     -- ``torch_recurrent_gdn2`` (``gdn2.py:100-184``): the
+                           token-by-token recurrence, the parity oracle.
+                           GVA (value heads = groups x key heads) follows
+                           ``fused_recurrent_gdn2.py:461-480`` (q, k indexed by
+                           ``hv // groups``); varlen follows the ``cu_seqlens``
+                           contract of ``fused_recurrent_gdn2.py:512-525``.
+* ``chunk_fwd``         -- chunkwise WY/UT form of the same recurrence using
+                           only *relative* decays ``exp(G_r - G_i) <= 1``.  It
+                           is the algebra the HIP chunk kernels implement; the
+                           reference's own chunk form (``gdn2.py:243-369``) uses
+                           absolute decays and underflows, so it is not
+                           restated.
+* ``recurrent_vjp``     -- reverse-mode derivative of ``recurrent_fwd``
+                           (the gradients ``ChunkGDN2Function.backward`` returns,
+                           ``chunk_gdn2.py:2461-2547``: dq, dk, dv, dg, db, dw,
+                           dh0), including the L2-norm and scale chain rule.
+* ``make_inputs``       -- the seeded input recipe of BASELINE configs 0-4.
+
+How each function is pinned (tests/test_oracle.py):
+  recurrent_fwd  linear-attention closed form (b=0, w=1, g=0); single-token
+                 closed form; explicit (K x K) matrix form of the update
+                 ``S_t = (I - k (b*k)^T) Diag(e^g) S + k (w*v)^T`` (gdn2.py:10-11);
+                 the third-party scalar gated delta rule of ``transformers``
+                 (qwen3_next) for broadcast scalar gates; split/resume and
+                 zero-padding invariance.
+  chunk_fwd      equals recurrent_fwd for chunk sizes 1..T incl. ragged tails.
+  recurrent_vjp  central finite differences of recurrent_fwd in float64.
+  make_inputs    distribution moments and l2-norms (cheap sanity only; it is a
+                 recipe, not arithmetic of the reference).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "l2normalize",
+    "recurrent_fwd",
+    "chunk_fwd",
+    "recurrent_vjp",
+    "make_inputs",
+    "rel_l2",
+]
+
+L2_EPS = 1e-6
+
+
+def rel_l2(x, ref) -> float:
+    """Relative L2 error ``||x - ref|| / ||ref||`` (the north-star parity metric)."""
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.linalg.norm(ref.ravel())
+    num = np.linalg.norm((x - ref).ravel())
+    if den == 0.0:
+        return float(num)
+    return float(num / den)
+
+
+def l2normalize(x: np.ndarray, eps: float = L2_EPS) -> np.ndarray:
+    """``x / max(||x||_2, eps)`` over the last axis (gdn2.py:139-141, F.normalize)."""
+    n = np.sqrt((x * x).sum(-1, keepdims=True))
+    return x / np.maximum(n, eps)
+
+
+def _prep(q, k, v, g, b, w, scale, use_qk_l2norm):
+    q, k, v, g, b, w = (np.asarray(t, dtype=np.float64) for t in (q, k, v, g, b, w))
+    if use_qk_l2norm:
+        q = l2normalize(q)
+        k = l2normalize(k)
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    return q * scale, k, v, g, b, w
+
+
+def _expand_heads(x, hv):
+    """Repeat key-side heads to ``hv`` value heads (head hv uses key head hv // groups)."""
+    h = x.shape[2]
+    if h == hv:
+        return x
+    assert hv % h == 0
+    return np.repeat(x, hv // h, axis=2)
+
+
+def _seq_slices(B, T, cu_seqlens):
+    if cu_seqlens is None:
+        return [(bi, 0, T) for bi in range(B)]
+    assert B == 1, "cu_seqlens requires batch size 1"
+    cu = [int(c) for c in cu_seqlens]
+    return [(0, cu[i], cu[i + 1]) for i in range(len(cu) - 1)]
+
+
+def recurrent_fwd(
+    q,
+    k,
+    v,
+    g,
+    b,
+    w,
+    initial_state=None,
+    scale=None,
+    use_qk_l2norm_in_kernel=True,
+    cu_seqlens=None,
+    return_states=False,
+):
+    r"""Token-by-token gdn2 recurrence in float64 (gdn2.py:100-184).
+
+    Shapes: ``q, k [B,T,H,K]``; ``v, w [B,T,HV,V]``; ``g, b [B,T,HV,K]``;
+    ``initial_state [N,HV,K,V]`` with ``N = B`` or ``len(cu_seqlens)-1``.
+    Per token and head, with ``q`` normalised and scaled by ``K**-0.5``:
+
+        S <- Diag(exp(g_t)) S                 (gdn2.py:165)
+        r  = S^T (b_t * k_t)                  (gdn2.py:168-169)
+        u  = w_t * v_t - r                    (gdn2.py:172)
+        S <- S + k_t u^T                      (gdn2.py:175)
+        o_t = S^T q_t                         (gdn2.py:178)
+
+    Returns ``(o [B,T,HV,V], final_state [N,HV,K,V])`` in float64; with
+    ``return_states`` also the list of per-token states per sequence.
+    """
+    B, T, H, K = np.shape(q)
+    HV, V = np.shape(v)[2], np.shape(v)[3]
+    q, k, v, g, b, w = _prep(q, k, v, g, b, w, scale, use_qk_l2norm_in_kernel)
+    q = _expand_heads(q, HV)
+    k = _expand_heads(k, HV)
+    seqs = _seq_slices(B, T, cu_seqlens)
+    N = len(seqs)
+    o = np.zeros((B, T, HV, V))
+    final = np.zeros((N, HV, K, V))
+    states = []
+    for n, (bi, t0, t1) in enumerate(seqs):
+        S = np.zeros((HV, K, V)) if initial_state is None else np.array(initial_state[n], dtype=np.float64)
+        seq_states = []
+        for t in range(t0, t1):
+            S = S * np.exp(g[bi, t])[:, :, None]
+            r = np.einsum("hkv,hk->hv", S, b[bi, t] * k[bi, t])
+            u = w[bi, t] * v[bi, t] - r
+            S = S + k[bi, t][:, :, None] * u[:, None, :]
+            o[bi, t] = np.einsum("hkv,hk->hv", S, q[bi, t])
+            if return_states:
+                seq_states.append(S.copy())
+        final[n] = S
+        states.append(seq_states)
+    if return_states:
+        return o, final, states
+    return o, final
+
+
+def chunk_fwd(
+    q,
+    k,
+    v,
+    g,
+    b,
+    w,
+    initial_state=None,
+    scale=None,
+    use_qk_l2norm_in_kernel=True,
+    chunk_size=64,
+):
+    r"""Chunkwise (WY/UT) gdn2 forward in float64 with relative decays only.
+
+    For one chunk with start state ``S0`` and in-chunk cumulative log decay
+    ``G_r = sum_{i<=r} g_i`` (per key channel), with ``e_r = b_r * k_r`` and
+    ``z_r = w_r * v_r``:
+
+        Aqk[r,i] = sum_d q_rd k_id exp(G_rd - G_id)      i <= r
+        L[r,i]   = sum_d e_rd k_id exp(G_rd - G_id)      i <  r
+        X  = (I + L)^{-1}
+        W  = X (e * exp(G)),   U0 = X z,   U = U0 - W S0
+        O  = (q * exp(G)) S0 + Aqk U
+        S1 = Diag(exp(G_last)) S0 + (k * exp(G_last - G))^T U
+
+    This is the algebra of the HIP chunk kernels; it is checked against
+    ``recurrent_fwd`` (the reference recurrence) for every chunk size.
+    """
+    B, T, H, K = np.shape(q)
+    V = np.shape(v)[-1]
+    q, k, v, g, b, w = _prep(q, k, v, g, b, w, scale, use_qk_l2norm_in_kernel)
+    o = np.zeros((B, T, H, V))
+    final = np.zeros((B, H, K, V))
+    for bi in range(B):
+        for h in range(H):
+            S = np.zeros((K, V)) if initial_state is None else np.array(initial_state[bi, h], dtype=np.float64)
+            for t0 in range(0, T, chunk_size):
+                t1 = min(T, t0 + chunk_size)
+                qc, kc, vc = q[bi, t0:t1, h], k[bi, t0:t1, h], v[bi, t0:t1, h]
+                gc, bc, wc = g[bi, t0:t1, h], b[bi, t0:t1, h], w[bi, t0:t1, h]
+                C = t1 - t0
+                G = np.cumsum(gc, axis=0)  # [C,K]
+                causal = np.tril(np.ones((C, C)))
+                expo = np.where(causal[:, :, None] > 0, G[:, None, :] - G[None, :, :], -np.inf)
+                rel = np.exp(expo)  # [C,C,K] indexed (r, i, d); zero above the diagonal
+                strict = np.tril(np.ones((C, C)), -1)
+                e = bc * kc
+                Aqk = np.einsum("rd,id,rid->ri", qc, kc, rel) * causal
+                L = np.einsum("rd,id,rid->ri", e, kc, rel) * strict
+                X = np.linalg.inv(np.eye(C) + L)
+                Wm = X @ (e * np.exp(G))
+                U = X @ (wc * vc) - Wm @ S
+                o[bi, t0:t1, h] = (qc * np.exp(G)) @ S + Aqk @ U
+                S = np.exp(G[-1])[:, None] * S + (kc * np.exp(G[-1][None, :] - G)).T @ U
+            final[bi, h] = S
+    return o, final
+
+
+def _l2norm_vjp(x_raw, dy, eps=L2_EPS):
+    """VJP of ``y = x / max(||x||, eps)`` over the last axis."""
+    n = np.sqrt((x_raw * x_raw).sum(-1, keepdims=True))
+    big = n > eps
+    nn = np.maximum(n, eps)
+    y = x_raw / nn
+    proj = (y * dy).sum(-1, keepdims=True)
+    return np.where(big, (dy - y * proj) / nn, dy / eps)
+
+
+def recurrent_vjp(
+    q,
+    k,
+    v,
+    g,
+    b,
+    w,
+    do,
+    dht=None,
+    initial_state=None,
+    scale=None,
+    use_qk_l2norm_in_kernel=True,
+):
+    r"""Reverse-mode derivative of ``recurrent_fwd`` (no varlen, H == HV).
+
+    Given the upstream gradients ``do [B,T,H,V]`` and optionally ``dht``
+    ``[B,H,K,V]`` (gradient of the final state), returns
+    ``(dq, dk, dv, dg, db, dw, dh0)`` with respect to the raw (un-normalised)
+    inputs -- the set of gradients ``ChunkGDN2Function.backward`` returns
+    (reference ``chunk_gdn2.py:2526-2547``).
+
+    Per step, walking t = T-1 .. 0 with ``dS`` the gradient of ``S_t``:
+
+        dS += q_t do_t^T ;  dq_t = S_t do_t
+        dk_t = dS u_t ;  du = dS^T k_t
+        dw_t = du * v_t ;  dv_t = du * w_t ;  dr = -du
+        dS~ = dS + e_t dr^T ;  de = S~ dr
+        db_t = de * k_t ;  dk_t += de * b_t
+        dg_t = rowsum(dS~ * S~) ;  dS <- Diag(exp(g_t)) dS~
+    """
+    B, T, H, K = np.shape(q)
+    V = np.shape(v)[-1]
+    q_raw = np.asarray(q, dtype=np.float64)
+    k_raw = np.asarray(k, dtype=np.float64)
+    if scale is None:
+        scale = K ** -0.5
+    qs, kn, v, g, b, w = _prep(q, k, v, g, b, w, scale, use_qk_l2norm_in_kernel)
+    do = np.asarray(do, dtype=np.float64)
+    dq = np.zeros_like(qs)
+    dk = np.zeros_like(kn)
+    dv = np.zeros_like(v)
+    dg = np.zeros_like(g)
+    db = np.zeros_like(b)
+    dw = np.zeros_like(w)
+    dh0 = np.zeros((B, H, K, V))
+    for bi in range(B):
+        for h in range(H):
+            S = np.zeros((K, V)) if initial_state is None else np.array(initial_state[bi, h], dtype=np.float64)
+            Sdec, Ss, us = [], [], []
+            for t in range(T):
+                St = np.exp(g[bi, t, h])[:, None] * S
+                e = b[bi, t, h] * kn[bi, t, h]
+                u = w[bi, t, h] * v[bi, t, h] - St.T @ e
+                S = St + np.outer(kn[bi, t, h], u)
+                Sdec.append(St)
+                Ss.append(S)
+                us.append(u)
+            dS = np.zeros((K, V)) if dht is None else np.array(dht[bi, h], dtype=np.float64)
+            for t in range(T - 1, -1, -1):
+                qt, kt, et = qs[bi, t, h], kn[bi, t, h], b[bi, t, h] * kn[bi, t, h]
+                dS = dS + np.outer(qt, do[bi, t, h])
+                dq[bi, t, h] = Ss[t] @ do[bi, t, h]
+                dk_t = dS @ us[t]
+                du = dS.T @ kt
+                dw[bi, t, h] = du * v[bi, t, h]
+                dv[bi, t, h] = du * w[bi, t, h]
+                dr = -du
+                dSt = dS + np.outer(et, dr)
+                de = Sdec[t] @ dr
+                db[bi, t, h] = de * kt
+                dk_t = dk_t + de * b[bi, t, h]
+                dk[bi, t, h] = dk_t
+                dg[bi, t, h] = (dSt * Sdec[t]).sum(-1)
+                dS = np.exp(g[bi, t, h])[:, None] * dSt
+            dh0[bi, h] = dS
+    dq = dq * scale
+    if use_qk_l2norm_in_kernel:
+        dq = _l2norm_vjp(q_raw, dq)
+        dk = _l2norm_vjp(k_raw, dk)
+    return dq, dk, dv, dg, db, dw, dh0
+
+
+def make_inputs(cfg_index: int, B, T, H, K, V, seed=None, scalar_gates=True, state_std=0.0):
+    r"""Seeded synthetic inputs of the BASELINE configs (numpy float64).
+
+    Draw order (a fixed contract): q, k, v, beta_logit, g_pre, then the
+    initial state when ``state_std > 0``.  q and k ~ N(0,1) then L2-normalised
+    per head; v ~ N(0,1); beta = sigmoid(N(0,1)); g = -softplus(N(0,1) + 2).
+    With ``scalar_gates`` beta and g are drawn per (b, t, h) and broadcast to
+    the channel-wise API (``g, b`` over K and ``w`` over V, with b = w = beta).
+    """
+    rng = np.random.default_rng(cfg_index if seed is None else seed)
+    q = l2normalize(rng.standard_normal((B, T, H, K)))
+    k = l2normalize(rng.standard_normal((B, T, H, K)))
+    v = rng.standard_normal((B, T, H, V))
+    gshape = (B, T, H, 1) if scalar_gates else (B, T, H, K)
+    bl = rng.standard_normal(gshape)
+    gp = rng.standard_normal(gshape)
+    beta = 1.0 / (1.0 + np.exp(-bl))
+    g = -np.logaddexp(0.0, gp + 2.0)
+    if scalar_gates:
+        g = np.broadcast_to(g, (B, T, H, K)).copy()
+        bk = np.broadcast_to(beta, (B, T, H, K)).copy()
+        wv = np.broadcast_to(beta, (B, T, H, V)).copy()
+    else:
+        bk = beta
+        wv = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H, V))))
+    h0 = None
+    if state_std > 0:
+        h0 = rng.standard_normal((B, H, K, V)) * state_std
+    return dict(q=q, k=k, v=v, g=g, b=bk, w=wv, h0=h0)

@@ -1,0 +1,182 @@
+// extern "C" entry points of libgdn2_hip.so: argument validation and dispatch.
+// Declarations and the reference interfaces they replace: include/gdn2_hip.h.
+
+#include "gdn2_common.h"
+#include "gdn2_internal.h"
+
+using namespace gdn2;
+
+static bool valid_dtype(int d)
+{
+    return d == GDN2_DTYPE_F32 || d == GDN2_DTYPE_BF16 || d == GDN2_DTYPE_F16;
+}
+
+static int check_chunk_args(int io_dtype, int g_dtype, const int64_t *cu_seqlens,
+                            const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H,
+                            int K, int V, unsigned flags, const float *A_log)
+{
+    if (!valid_dtype(io_dtype) || !valid_dtype(g_dtype)) return GDN2_ERR_INVALID;
+    if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
+    if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND))
+        return GDN2_ERR_INVALID;
+    if ((flags & GDN2_FLAG_LOWER_BOUND) && !(flags & GDN2_FLAG_GATE_IN_KERNEL))
+        return GDN2_ERR_INVALID;
+    if ((flags & GDN2_FLAG_GATE_IN_KERNEL) && !A_log) return GDN2_ERR_INVALID;
+    if ((cu_seqlens == nullptr) != (cu_seqlens_host == nullptr)) return GDN2_ERR_INVALID;
+    if (cu_seqlens && (B != 1 || num_seqs < 0)) return GDN2_ERR_INVALID;
+    if (cu_seqlens_host) {
+        if (cu_seqlens_host[0] != 0 || cu_seqlens_host[num_seqs] != T) return GDN2_ERR_INVALID;
+        for (int i = 0; i < num_seqs; ++i)
+            if (cu_seqlens_host[i + 1] < cu_seqlens_host[i]) return GDN2_ERR_INVALID;
+    }
+    return GDN2_OK;
+}
+
+static void fill_chunk_args(ChunkFwdArgs &a, const void *q, const void *k, const void *v,
+                            const void *g, const void *b, const void *w, void *o,
+                            const float *h0, float *ht, const float *A_log, const float *dt_bias,
+                            float lower_bound, const int64_t *cu_seqlens, const int64_t *cu_host,
+                            int num_seqs, int B, int T, int H, int K, int V, float scale,
+                            unsigned flags, void *workspace, size_t workspace_bytes)
+{
+    a.q = q; a.k = k; a.v = v; a.g = g; a.b = b; a.w = w; a.o = o;
+    a.h0 = h0;
+    a.ht = ht;
+    a.A_log = A_log;
+    a.dt_bias = dt_bias;
+    a.lower_bound = lower_bound;
+    a.cu_seqlens = cu_seqlens;
+    a.cu_host = cu_host;
+    a.num_seqs = cu_seqlens ? num_seqs : B;
+    a.B = B; a.T = T; a.H = H; a.K = K; a.V = V;
+    a.scale = scale;
+    a.flags = flags;
+    a.workspace = workspace;
+    a.workspace_bytes = workspace_bytes;
+    a.stages = 3;
+}
+
+extern "C" {
+
+int gdn2_abi_version(void) { return GDN2_ABI_VERSION; }
+
+const char *gdn2_status_string(int status)
+{
+    switch (status) {
+    case GDN2_OK: return "ok";
+    case GDN2_ERR_INVALID: return "invalid argument";
+    case GDN2_ERR_UNSUPPORTED: return "unsupported shape, dtype or option";
+    case GDN2_ERR_LAUNCH: return "kernel launch failed";
+    case GDN2_ERR_WORKSPACE: return "workspace missing or too small";
+    default: return "unknown status";
+    }
+}
+
+int gdn2_recurrent_fwd(const void *q, const void *k, const void *v, const void *g,
+                       const void *b, const void *w, int io_dtype, int g_dtype, void *o,
+                       const float *initial_state, float *final_state, const float *A_log,
+                       const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
+                       int num_seqs, int B, int T, int H, int HV, int K, int V, float scale,
+                       unsigned flags, void *stream)
+{
+    if (!valid_dtype(io_dtype) || !valid_dtype(g_dtype)) return GDN2_ERR_INVALID;
+    if (B < 0 || T < 0 || H <= 0 || HV <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
+    if (HV % H != 0) return GDN2_ERR_INVALID;
+    if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND))
+        return GDN2_ERR_INVALID;
+    if ((flags & GDN2_FLAG_LOWER_BOUND) && !(flags & GDN2_FLAG_GATE_IN_KERNEL))
+        return GDN2_ERR_INVALID;
+    if ((flags & GDN2_FLAG_GATE_IN_KERNEL) && !A_log) return GDN2_ERR_INVALID;
+    if (K > 256 || (V % 4) != 0) return GDN2_ERR_UNSUPPORTED;
+    int N = B;
+    if (cu_seqlens) {
+        if (B != 1 || num_seqs < 0) return GDN2_ERR_INVALID;
+        N = num_seqs;
+    }
+    const int64_t ntok = static_cast<int64_t>(B) * T;
+    if (ntok > 0 && (!q || !k || !v || !g || !b || !w || !o)) return GDN2_ERR_INVALID;
+    if (N == 0) return GDN2_OK;
+    if (static_cast<int64_t>(N) * HV > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
+
+    RecurrentParams p;
+    p.q = q; p.k = k; p.v = v; p.g = g; p.b = b; p.w = w; p.o = o;
+    p.h0 = initial_state;
+    p.ht = final_state;
+    p.A_log = A_log;
+    p.dt_bias = dt_bias;
+    p.lower_bound = lower_bound;
+    p.cu_seqlens = cu_seqlens;
+    p.T = T; p.H = H; p.HV = HV; p.K = K; p.V = V;
+    p.scale = scale;
+    p.flags = flags;
+    const hipError_t err =
+        launch_recurrent_fwd(p, io_dtype, g_dtype, N, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+size_t gdn2_chunk_fwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,
+                                     const int64_t *cu_seqlens_host, int num_seqs)
+{
+    if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || !valid_dtype(io_dtype)) return 0;
+    return chunk_fwd_workspace_bytes(B, T, H, K, V, io_dtype, cu_seqlens_host, num_seqs);
+}
+
+int gdn2_chunk_fwd(const void *q, const void *k, const void *v, const void *g, const void *b,
+                   const void *w, int io_dtype, int g_dtype, void *o,
+                   const float *initial_state, float *final_state, const float *A_log,
+                   const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
+                   const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H, int K,
+                   int V, float scale, unsigned flags, void *workspace,
+                   size_t workspace_bytes, void *stream)
+{
+    ChunkFwdArgs a;
+    const int st = check_chunk_args(io_dtype, g_dtype, cu_seqlens, cu_seqlens_host, num_seqs, B,
+                                    T, H, K, V, flags, A_log);
+    if (st != GDN2_OK) return st;
+    if (static_cast<int64_t>(B) * T > 0 && (!q || !k || !v || !g || !b || !w || !o))
+        return GDN2_ERR_INVALID;
+    fill_chunk_args(a, q, k, v, g, b, w, o, initial_state, final_state, A_log, dt_bias,
+                    lower_bound, cu_seqlens, cu_seqlens_host, num_seqs, B, T, H, K, V, scale,
+                    flags, workspace, workspace_bytes);
+    a.stages = 3;
+    return launch_chunk_fwd(a, io_dtype, g_dtype, static_cast<hipStream_t>(stream));
+}
+
+int gdn2_chunk_fwd_prep(const void *q, const void *k, const void *g, const void *b,
+                        int io_dtype, int g_dtype, const float *A_log, const float *dt_bias,
+                        float lower_bound, const int64_t *cu_seqlens,
+                        const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H,
+                        int K, int V, float scale, unsigned flags, void *workspace,
+                        size_t workspace_bytes, void *stream)
+{
+    ChunkFwdArgs a;
+    const int st = check_chunk_args(io_dtype, g_dtype, cu_seqlens, cu_seqlens_host, num_seqs, B,
+                                    T, H, K, V, flags, A_log);
+    if (st != GDN2_OK) return st;
+    if (static_cast<int64_t>(B) * T > 0 && (!q || !k || !g || !b)) return GDN2_ERR_INVALID;
+    fill_chunk_args(a, q, k, nullptr, g, b, nullptr, nullptr, nullptr, nullptr, A_log, dt_bias,
+                    lower_bound, cu_seqlens, cu_seqlens_host, num_seqs, B, T, H, K, V, scale,
+                    flags, workspace, workspace_bytes);
+    a.stages = 1;
+    return launch_chunk_fwd(a, io_dtype, g_dtype, static_cast<hipStream_t>(stream));
+}
+
+int gdn2_chunk_fwd_scan(const void *v, const void *w, int io_dtype, void *o,
+                        const float *initial_state, float *final_state,
+                        const int64_t *cu_seqlens, const int64_t *cu_seqlens_host, int num_seqs,
+                        int B, int T, int H, int K, int V, void *workspace,
+                        size_t workspace_bytes, void *stream)
+{
+    ChunkFwdArgs a;
+    const int st = check_chunk_args(io_dtype, GDN2_DTYPE_F32, cu_seqlens, cu_seqlens_host,
+                                    num_seqs, B, T, H, K, V, 0u, nullptr);
+    if (st != GDN2_OK) return st;
+    if (static_cast<int64_t>(B) * T > 0 && (!v || !w || !o)) return GDN2_ERR_INVALID;
+    fill_chunk_args(a, nullptr, nullptr, v, nullptr, nullptr, w, o, initial_state, final_state,
+                    nullptr, nullptr, 0.f, cu_seqlens, cu_seqlens_host, num_seqs, B, T, H, K, V,
+                    1.f, 0u, workspace, workspace_bytes);
+    a.stages = 2;
+    return launch_chunk_fwd(a, io_dtype, GDN2_DTYPE_F32, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,94 @@
+// Shared device helpers for the gdn2 HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gdn2_hip.h"
+
+namespace gdn2 {
+
+constexpr int kWave = 64;
+
+// bf16 is handled as raw 16-bit patterns so that the kernels depend on no
+// vendor half/bf16 class: widening is a shift, narrowing is round-to-nearest-
+// even on the float bits (NaN kept quiet).
+struct bf16_t {
+    uint16_t bits;
+};
+struct f16_t {
+    _Float16 v;
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b)
+{
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T>
+struct io;
+
+template <>
+struct io<float> {
+    static __device__ __forceinline__ float ld(const float *p, int64_t i) { return p[i]; }
+    static __device__ __forceinline__ void st(float *p, int64_t i, float x) { p[i] = x; }
+};
+
+template <>
+struct io<bf16_t> {
+    static __device__ __forceinline__ float ld(const bf16_t *p, int64_t i)
+    {
+        return bf16_bits_to_f32(p[i].bits);
+    }
+    static __device__ __forceinline__ void st(bf16_t *p, int64_t i, float x)
+    {
+        p[i].bits = f32_to_bf16_bits(x);
+    }
+};
+
+template <>
+struct io<f16_t> {
+    static __device__ __forceinline__ float ld(const f16_t *p, int64_t i)
+    {
+        return static_cast<float>(p[i].v);
+    }
+    static __device__ __forceinline__ void st(f16_t *p, int64_t i, float x)
+    {
+        p[i].v = static_cast<_Float16>(x);
+    }
+};
+
+__device__ __forceinline__ float wave_sum(float x)
+{
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+    return x;
+}
+
+// torch.nn.functional.softplus with its default threshold of 20.
+__device__ __forceinline__ float softplus_f(float x)
+{
+    return x > 20.0f ? x : log1pf(expf(x));
+}
+
+// Decay activation applied in-kernel when GDN2_FLAG_GATE_IN_KERNEL is set:
+//   g = -exp(A_log[h]) * softplus(g_raw + dt_bias[h, d])         (default)
+//   g = lower_bound * sigmoid(exp(A_log[h]) * (g_raw + dt_bias))  (lower-bound form)
+__device__ __forceinline__ float gate_activation(float graw, float a_log, float dt_bias,
+                                                 int use_lower_bound, float lower_bound)
+{
+    const float x = graw + dt_bias;
+    const float a = expf(a_log);
+    if (use_lower_bound) return lower_bound / (1.0f + expf(-a * x));
+    return -a * softplus_f(x);
+}
+
+}  // namespace gdn2

@@ -1,0 +1,51 @@
+// Internal host-side interfaces between the C ABI (gdn2_api.hip) and the
+// kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gdn2 {
+
+struct RecurrentParams {
+    const void *q, *k, *v, *g, *b, *w;
+    void *o;
+    const float *h0;
+    float *ht;
+    const float *A_log;
+    const float *dt_bias;
+    float lower_bound;
+    const int64_t *cu_seqlens;
+    int T, H, HV, K, V;
+    float scale;
+    unsigned flags;
+};
+
+hipError_t launch_recurrent_fwd(const RecurrentParams &p, int io_dtype, int g_dtype, int N,
+                                hipStream_t stream);
+
+struct ChunkFwdArgs {
+    const void *q, *k, *v, *g, *b, *w;
+    void *o;
+    const float *h0;
+    float *ht;
+    const float *A_log;
+    const float *dt_bias;
+    float lower_bound;
+    const int64_t *cu_seqlens;
+    const int64_t *cu_host;
+    int num_seqs;
+    int B, T, H, K, V;
+    float scale;
+    unsigned flags;
+    void *workspace;
+    size_t workspace_bytes;
+    int stages;  // bit 0: prep, bit 1: scan
+};
+
+size_t chunk_fwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype,
+                                 const int64_t *cu_host, int num_seqs);
+int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream);
+
+}  // namespace gdn2

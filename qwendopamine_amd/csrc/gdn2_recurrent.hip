@@ -1,0 +1,305 @@
+// Token-serial gdn2 forward for decode steps and short prefills (gfx950).
+//
+// Arithmetic: reference models/gdn2/gdn2.py:156-179 (torch_recurrent_gdn2), per
+// token and (sequence, value head):
+//     S <- Diag(exp(g)) S ;  r = S^T (b*k) ;  u = w*v - r ;  S <- S + k u^T ;  o = S^T q
+// with q, k L2-normalised (F.normalize, eps 1e-6) and q scaled, fused in-kernel.
+// Interface: reference fused_recurrent_gdn2.py:344-458 (GVA, varlen, in-place
+// final state, optional in-kernel gate activation).
+//
+// Mapping.  One 256-thread workgroup owns the float32 state slab S[:, c0:c0+VB]
+// of one (sequence, value head) -- K rows of VB columns, V contiguous in HBM.
+// Thread t holds a float4 of columns 4*(t % TPR) for rows (t / TPR) + i*RG,
+// i < NR, in VGPRs for the whole token loop, so a decode step reads and
+// writes every state byte exactly once with 16-byte coalesced accesses
+// (one wavefront row = 2 x 512 B for VB = 128).  The two K-reductions of a
+// token (r = S^T e and the S^T q partial) are summed across the row groups of
+// a wave with xor-shuffles and across the 4 waves through 4 KB of LDS.
+// The output uses o = (Diag(a)S)^T q + u (k.q), so S is swept once per token.
+
+#include "gdn2_common.h"
+#include "gdn2_internal.h"
+
+namespace gdn2 {
+
+
+template <typename T>
+struct vec4io;
+
+template <>
+struct vec4io<float> {
+    static __device__ __forceinline__ float4 ld(const float *p, int64_t i)
+    {
+        return *reinterpret_cast<const float4 *>(p + i);
+    }
+    static __device__ __forceinline__ void st(float *p, int64_t i, float4 x)
+    {
+        *reinterpret_cast<float4 *>(p + i) = x;
+    }
+};
+
+template <>
+struct vec4io<bf16_t> {
+    static __device__ __forceinline__ float4 ld(const bf16_t *p, int64_t i)
+    {
+        const uint2 u = *reinterpret_cast<const uint2 *>(p + i);
+        return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                           __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+    }
+    static __device__ __forceinline__ void st(bf16_t *p, int64_t i, float4 x)
+    {
+        uint2 u;
+        u.x = static_cast<uint32_t>(f32_to_bf16_bits(x.x)) |
+              (static_cast<uint32_t>(f32_to_bf16_bits(x.y)) << 16);
+        u.y = static_cast<uint32_t>(f32_to_bf16_bits(x.z)) |
+              (static_cast<uint32_t>(f32_to_bf16_bits(x.w)) << 16);
+        *reinterpret_cast<uint2 *>(p + i) = u;
+    }
+};
+
+template <>
+struct vec4io<f16_t> {
+    static __device__ __forceinline__ float4 ld(const f16_t *p, int64_t i)
+    {
+        return make_float4(static_cast<float>(p[i].v), static_cast<float>(p[i + 1].v),
+                           static_cast<float>(p[i + 2].v), static_cast<float>(p[i + 3].v));
+    }
+    static __device__ __forceinline__ void st(f16_t *p, int64_t i, float4 x)
+    {
+        p[i].v = static_cast<_Float16>(x.x);
+        p[i + 1].v = static_cast<_Float16>(x.y);
+        p[i + 2].v = static_cast<_Float16>(x.z);
+        p[i + 3].v = static_cast<_Float16>(x.w);
+    }
+};
+
+__device__ __forceinline__ float4 f4_fma(float4 a, float s, float4 c)
+{
+    return make_float4(fmaf(a.x, s, c.x), fmaf(a.y, s, c.y), fmaf(a.z, s, c.z),
+                       fmaf(a.w, s, c.w));
+}
+
+__device__ __forceinline__ float4 shfl_xor4(float4 x, int off)
+{
+    return make_float4(__shfl_xor(x.x, off, kWave), __shfl_xor(x.y, off, kWave),
+                       __shfl_xor(x.z, off, kWave), __shfl_xor(x.w, off, kWave));
+}
+
+// TPR threads cover one state row of VB = 4*TPR columns; RG = 256/TPR row
+// groups; each thread keeps NR rows (NR*RG >= K).
+template <typename TI, typename TG, int NR, int TPR>
+__global__ __launch_bounds__(256) void recurrent_fwd_kernel(RecurrentParams p)
+{
+    constexpr int RG = 256 / TPR;
+    constexpr int VB = 4 * TPR;
+    static_assert(TPR <= 32 && (TPR & (TPR - 1)) == 0, "TPR must be a power of two <= 32");
+
+    const int K = p.K, V = p.V;
+    const int nh = blockIdx.x;
+    const int vs = blockIdx.y;
+    const int n = nh / p.HV, hv = nh % p.HV;
+    const int h = hv / (p.HV / p.H);
+
+    int64_t bos, len;
+    if (p.cu_seqlens) {
+        bos = p.cu_seqlens[n];
+        len = p.cu_seqlens[n + 1] - bos;
+    } else {
+        bos = static_cast<int64_t>(n) * p.T;
+        len = p.T;
+    }
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1), wid = tid / kWave;
+    const int cq = tid % TPR, rg = tid / TPR;
+    const int col = vs * VB + 4 * cq;
+    const bool col_ok = col < V;
+
+    __shared__ float s_q[256], s_k[256], s_e[256], s_a[256];
+    __shared__ float s_part[4][4];
+    __shared__ float4 s_red[4][2][TPR];
+
+    const TI *q = static_cast<const TI *>(p.q);
+    const TI *k = static_cast<const TI *>(p.k);
+    const TI *v = static_cast<const TI *>(p.v);
+    const TI *b = static_cast<const TI *>(p.b);
+    const TI *w = static_cast<const TI *>(p.w);
+    const TG *g = static_cast<const TG *>(p.g);
+    TI *o = static_cast<TI *>(p.o);
+    const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
+    const bool gate = (p.flags & GDN2_FLAG_GATE_IN_KERNEL) != 0;
+    const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
+
+    const int64_t soff = (static_cast<int64_t>(n) * p.HV + hv) * K * V;
+    float4 st[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int r = rg + i * RG;
+        st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (p.h0 && col_ok && r < K)
+            st[i] = *reinterpret_cast<const float4 *>(p.h0 + soff + static_cast<int64_t>(r) * V + col);
+    }
+
+    const float a_log = gate ? p.A_log[hv] : 0.0f;
+
+    for (int64_t t = 0; t < len; ++t) {
+        const int64_t tok = bos + t;
+        const int64_t qk_off = (tok * p.H + h) * K;
+        const int64_t gb_off = (tok * p.HV + hv) * K;
+        const int64_t vw_off = (tok * p.HV + hv) * V;
+
+        float qv = 0.f, kv = 0.f, gv = 0.f, bv = 0.f;
+        if (tid < K) {
+            qv = io<TI>::ld(q, qk_off + tid);
+            kv = io<TI>::ld(k, qk_off + tid);
+            gv = io<TG>::ld(g, gb_off + tid);
+            bv = io<TI>::ld(b, gb_off + tid);
+        }
+        float4 vv = make_float4(0.f, 0.f, 0.f, 0.f), ww = vv;
+        if (col_ok) {
+            vv = vec4io<TI>::ld(v, vw_off + col);
+            ww = vec4io<TI>::ld(w, vw_off + col);
+        }
+        float rq = wave_sum(qv * qv), rk = wave_sum(kv * kv), rqk = wave_sum(qv * kv);
+        if (lane == 0) {
+            s_part[wid][0] = rq;
+            s_part[wid][1] = rk;
+            s_part[wid][2] = rqk;
+        }
+        __syncthreads();
+        float qq = 0.f, kk = 0.f, qk = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qq += s_part[i][0];
+            kk += s_part[i][1];
+            qk += s_part[i][2];
+        }
+        const float invq = l2 ? 1.0f / fmaxf(sqrtf(qq), 1e-6f) : 1.0f;
+        const float invk = l2 ? 1.0f / fmaxf(sqrtf(kk), 1e-6f) : 1.0f;
+        if (tid < K) {
+            const float kn = kv * invk;
+            s_q[tid] = qv * invq * p.scale;
+            s_k[tid] = kn;
+            s_e[tid] = bv * kn;
+            float gk = gv;
+            if (gate) {
+                const float db = p.dt_bias ? p.dt_bias[hv * K + tid] : 0.0f;
+                gk = gate_activation(gv, a_log, db, use_lb, p.lower_bound);
+            }
+            s_a[tid] = expf(gk);
+        }
+        const float kq = qk * invq * invk * p.scale;
+        __syncthreads();
+
+        float4 pr = make_float4(0.f, 0.f, 0.f, 0.f), po = pr;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int r = rg + i * RG;
+            if (r < K) {
+                const float a = s_a[r];
+                st[i].x *= a;
+                st[i].y *= a;
+                st[i].z *= a;
+                st[i].w *= a;
+                pr = f4_fma(st[i], s_e[r], pr);
+                po = f4_fma(st[i], s_q[r], po);
+            }
+        }
+#pragma unroll
+        for (int off = TPR; off < kWave; off <<= 1) {
+            const float4 a = shfl_xor4(pr, off), c = shfl_xor4(po, off);
+            pr.x += a.x; pr.y += a.y; pr.z += a.z; pr.w += a.w;
+            po.x += c.x; po.y += c.y; po.z += c.z; po.w += c.w;
+        }
+        if (lane < TPR) {
+            s_red[wid][0][cq] = pr;
+            s_red[wid][1][cq] = po;
+        }
+        __syncthreads();
+        float4 R = s_red[0][0][cq], PO = s_red[0][1][cq];
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+            const float4 a = s_red[i][0][cq], c = s_red[i][1][cq];
+            R.x += a.x; R.y += a.y; R.z += a.z; R.w += a.w;
+            PO.x += c.x; PO.y += c.y; PO.z += c.z; PO.w += c.w;
+        }
+        const float4 u = make_float4(ww.x * vv.x - R.x, ww.y * vv.y - R.y, ww.z * vv.z - R.z,
+                                     ww.w * vv.w - R.w);
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int r = rg + i * RG;
+            if (r < K) {
+                const float kr = s_k[r];
+                st[i].x = fmaf(kr, u.x, st[i].x);
+                st[i].y = fmaf(kr, u.y, st[i].y);
+                st[i].z = fmaf(kr, u.z, st[i].z);
+                st[i].w = fmaf(kr, u.w, st[i].w);
+            }
+        }
+        if (rg == 0 && col_ok) vec4io<TI>::st(o, vw_off + col, f4_fma(u, kq, PO));
+        __syncthreads();
+    }
+
+    if (p.ht && col_ok) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int r = rg + i * RG;
+            if (r < K)
+                *reinterpret_cast<float4 *>(p.ht + soff + static_cast<int64_t>(r) * V + col) = st[i];
+        }
+    }
+}
+
+template <typename TI, typename TG, int TPR>
+static hipError_t launch_nr(const RecurrentParams &p, int N, hipStream_t stream)
+{
+    constexpr int RG = 256 / TPR;
+    const int need = (p.K + RG - 1) / RG;
+    const int nvs = (p.V + 4 * TPR - 1) / (4 * TPR);
+    dim3 grid(N * p.HV, nvs);
+    if (need <= 1)
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 1, TPR>), grid, dim3(256), 0, stream, p);
+    else if (need <= 2)
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 2, TPR>), grid, dim3(256), 0, stream, p);
+    else if (need <= 4)
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 4, TPR>), grid, dim3(256), 0, stream, p);
+    else if (need <= 8)
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 8, TPR>), grid, dim3(256), 0, stream, p);
+    else if (need <= 16)
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 16, TPR>), grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 32, TPR>), grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <typename TI, typename TG>
+static hipError_t launch_tpr(const RecurrentParams &p, int N, hipStream_t stream)
+{
+    // Narrowest row that still covers V with float4 lanes, capped at 128 columns.
+    if (p.V <= 16) return launch_nr<TI, TG, 4>(p, N, stream);
+    if (p.V <= 32) return launch_nr<TI, TG, 8>(p, N, stream);
+    if (p.V <= 64) return launch_nr<TI, TG, 16>(p, N, stream);
+    return launch_nr<TI, TG, 32>(p, N, stream);
+}
+
+template <typename TI>
+static hipError_t launch_g(const RecurrentParams &p, int g_dtype, int N, hipStream_t stream)
+{
+    switch (g_dtype) {
+    case GDN2_DTYPE_F32: return launch_tpr<TI, float>(p, N, stream);
+    case GDN2_DTYPE_BF16: return launch_tpr<TI, bf16_t>(p, N, stream);
+    default: return launch_tpr<TI, f16_t>(p, N, stream);
+    }
+}
+
+hipError_t launch_recurrent_fwd(const RecurrentParams &p, int io_dtype, int g_dtype, int N,
+                                hipStream_t stream)
+{
+    switch (io_dtype) {
+    case GDN2_DTYPE_F32: return launch_g<float>(p, g_dtype, N, stream);
+    case GDN2_DTYPE_BF16: return launch_g<bf16_t>(p, g_dtype, N, stream);
+    default: return launch_g<f16_t>(p, g_dtype, N, stream);
+    }
+}
+
+}  // namespace gdn2

@@ -1,0 +1,397 @@
+"""Kernel-level gdn2 ops on the MI355X HIP backend.
+
+Mirrors the reference op interfaces so callers can swap them in unchanged:
+
+* ``fused_recurrent_gdn2`` / ``fused_recurrent_gdn2_fwd`` -- reference
+  ``models/gdn2/gdn2_ops/fused_recurrent_gdn2.py:461-555`` / ``:344-458``
+  (token-serial forward: decode steps and short prefills, inference only).
+* ``chunk_gdn2`` (+ ``ChunkGDN2Function``) -- reference
+  ``models/gdn2/gdn2_ops/chunk_gdn2.py:1268-1434`` / ``:2328-2547``
+  (chunkwise prefill and training forward/backward).
+
+Both run the hand-written kernels of ``libgdn2_hip.so`` on the current HIP
+stream of the inputs' device.  Inputs must be ROCm GPU tensors: there is no
+CPU path, and a missing library raises.  Semantics follow the reference
+oracle ``torch_recurrent_gdn2`` (``gdn2.py:100-184``); the final state is
+float32 (as the reference's accelerated ops return it).
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from . import _native as nat
+
+__all__ = [
+    "fused_recurrent_gdn2",
+    "fused_recurrent_gdn2_fwd",
+    "chunk_gdn2",
+    "chunk_gdn2_fwd",
+    "ChunkGDN2Function",
+]
+
+
+def _require_gpu(name: str, *tensors: torch.Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                f"{name}: the gdn2 HIP kernels need ROCm GPU tensors (got a {t.device} "
+                "tensor); this package has no CPU path."
+            )
+
+
+def _check_shapes(name, q, k, v, g, b, w, same_heads: bool) -> None:
+    """Every tensor must match the dims passed to the kernels (they index by them)."""
+    if q.dim() != 4 or v.dim() != 4:
+        raise ValueError(f"{name}: q and v must be 4-D [B, T, H, D]")
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[3]
+    if tuple(k.shape) != (B, T, H, K):
+        raise ValueError(f"{name}: k shape {tuple(k.shape)} != q shape {tuple(q.shape)}")
+    if tuple(v.shape[:2]) != (B, T) or tuple(w.shape) != (B, T, HV, V):
+        raise ValueError(f"{name}: v / w must be [B, T, HV, V]; got {tuple(v.shape)}, {tuple(w.shape)}")
+    if tuple(g.shape) != (B, T, HV, K) or tuple(b.shape) != (B, T, HV, K):
+        raise ValueError(f"{name}: g / b must be [B, T, HV, K]; got {tuple(g.shape)}, {tuple(b.shape)}")
+    if HV % H != 0 or (same_heads and HV != H):
+        raise ValueError(f"{name}: value heads {HV} incompatible with key heads {H}")
+
+
+def _flags(use_qk_l2norm_in_kernel: bool, use_gate_in_kernel: bool, lower_bound) -> int:
+    f = 0
+    if use_qk_l2norm_in_kernel:
+        f |= nat.FLAG_L2NORM_QK
+    if use_gate_in_kernel:
+        f |= nat.FLAG_GATE_IN_KERNEL
+        if lower_bound is not None:
+            f |= nat.FLAG_LOWER_BOUND
+    return f
+
+
+def _io(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    return x.to(dtype).contiguous()
+
+
+def _gate_tensors(use_gate_in_kernel, A_log, dt_bias, heads: int, K: int):
+    """float32 device copies of the in-kernel gate parameters (A_log [heads], dt_bias [heads*K])."""
+    if not use_gate_in_kernel:
+        return None, None
+    if A_log is None:
+        raise AssertionError("A_log must be provided when use_gate_in_kernel=True.")
+    a = A_log.detach().float().contiguous()
+    if a.numel() != heads:
+        raise ValueError(f"A_log must have {heads} elements, got {a.numel()}")
+    d = None if dt_bias is None else dt_bias.detach().float().contiguous()
+    if d is not None and d.numel() != heads * K:
+        raise ValueError(f"dt_bias must have {heads * K} elements, got {d.numel()}")
+    return a, d
+
+
+def _cu(cu_seqlens, device, total_tokens: int):
+    """Device and host int64 copies of ``cu_seqlens``, validated on the host.
+
+    The kernels index tokens through these offsets, so they must start at 0,
+    be non-decreasing and end at the packed length.
+    """
+    if cu_seqlens is None:
+        return None, None
+    cu_host = torch.as_tensor(cu_seqlens).detach().to("cpu", torch.int64).contiguous()
+    if cu_host.dim() != 1 or cu_host.numel() < 1:
+        raise ValueError("cu_seqlens must be a 1-D tensor of N+1 offsets")
+    if int(cu_host[0]) != 0 or int(cu_host[-1]) != total_tokens or bool((cu_host[1:] < cu_host[:-1]).any()):
+        raise ValueError(
+            f"cu_seqlens must start at 0, be non-decreasing and end at {total_tokens}; "
+            f"got {cu_host.tolist()[:8]}..."
+        )
+    cu_dev = cu_host.to(device=device)
+    return cu_dev, cu_host
+
+
+def fused_recurrent_gdn2_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    b: torch.Tensor,
+    w: torch.Tensor,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    initial_state: torch.Tensor | None = None,
+    scale: float | None = None,
+    output_final_state: bool = False,
+    inplace_final_state: bool = True,
+    cu_seqlens: torch.LongTensor | None = None,
+    ssm_state_indices: torch.Tensor | None = None,
+    num_accepted_tokens: torch.Tensor | None = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    lower_bound: float | None = None,
+    out: torch.Tensor | None = None,
+    transpose_state_layout: bool = False,
+    **kwargs: Any,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Launch the token-serial HIP kernel (reference ``fused_recurrent_gdn2.py:344-458``).
+
+    ``inplace_final_state`` writes the final state back into ``initial_state``
+    (which must then be a contiguous float32 tensor); ``output_final_state``
+    allocates a new float32 ``[N, HV, K, V]`` state.
+    """
+    name = "fused_recurrent_gdn2"
+    if ssm_state_indices is not None or num_accepted_tokens is not None:
+        raise NotImplementedError(f"{name}: continuous batching / speculative decoding")
+    if transpose_state_layout:
+        raise NotImplementedError(f"{name}: transpose_state_layout")
+    _require_gpu(name, q, k, v, g, b, w, initial_state)
+    _check_shapes(name, q, k, v, g, b, w, same_heads=False)
+    B, T, H, K = k.shape
+    HV, V = v.shape[2], v.shape[3]
+    if scale is None:
+        scale = K**-0.5
+    dt = q.dtype
+    q, k, v, b, w = (_io(x, dt) for x in (q, k, v, b, w))
+    g = g.contiguous() if g.dtype in (torch.float32, dt) else g.float().contiguous()
+    cu_dev, cu_host = _cu(cu_seqlens, q.device, T)
+    N = B if cu_seqlens is None else cu_host.numel() - 1
+    if out is None:
+        out = torch.empty_like(v)
+    else:
+        assert out.shape == v.shape and out.dtype == dt and out.is_contiguous()
+    h0 = None
+    if initial_state is not None:
+        if inplace_final_state:
+            assert initial_state.dtype == torch.float32 and initial_state.is_contiguous(), (
+                "inplace_final_state needs a contiguous float32 initial_state"
+            )
+            h0 = initial_state
+        else:
+            h0 = initial_state.float().contiguous()
+        assert tuple(h0.shape) == (N, HV, K, V), f"initial_state must be {(N, HV, K, V)}"
+    if inplace_final_state:
+        assert initial_state is not None, "inplace_final_state=True requires an initial_state"
+        ht = h0
+    elif output_final_state:
+        ht = torch.empty(N, HV, K, V, dtype=torch.float32, device=q.device)
+    else:
+        ht = None
+    a_log, dtb = _gate_tensors(use_gate_in_kernel, A_log, dt_bias, HV, K)
+    lib = nat.load()
+    st = lib.gdn2_recurrent_fwd(
+        nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(g), nat.ptr(b), nat.ptr(w),
+        nat.dtype_code(dt), nat.dtype_code(g.dtype), nat.ptr(out),
+        nat.ptr(h0), nat.ptr(ht), nat.ptr(a_log), nat.ptr(dtb),
+        float(lower_bound) if lower_bound is not None else 0.0,
+        nat.ptr(cu_dev), N, B, T, H, HV, K, V, float(scale),
+        _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound),
+        nat.stream_handle(q.device),
+    )
+    nat.check(st, name)
+    return out, ht
+
+
+def fused_recurrent_gdn2(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    b: torch.Tensor,
+    w: torch.Tensor,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    lower_bound: float | None = None,
+    cu_seqlens: torch.LongTensor | None = None,
+    transpose_state_layout: bool = False,
+    **kwargs: Any,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Token-by-token gdn2 forward, inference only (reference ``fused_recurrent_gdn2.py:461-555``).
+
+    Shapes: ``q, k [B,T,H,K]``, ``v, w [B,T,HV,V]``, ``g, b [B,T,HV,K]``,
+    ``initial_state [N,HV,K,V]`` float32.  Returns ``(o [B,T,HV,V], final_state)``.
+    """
+    if cu_seqlens is not None:
+        if q.shape[0] != 1:
+            raise ValueError(
+                f"The batch size is expected to be 1 rather than {q.shape[0]} when using "
+                "`cu_seqlens`. Please flatten variable-length inputs before processing."
+            )
+        if initial_state is not None and initial_state.shape[0] != len(cu_seqlens) - 1:
+            raise ValueError(
+                "The number of initial states is expected to be equal to the number of "
+                f"input sequences, i.e., {len(cu_seqlens) - 1} rather than "
+                f"{initial_state.shape[0]}."
+            )
+    assert b.shape == (*q.shape[:2], v.shape[2], k.shape[-1]) or b.shape == (*q.shape[:3], k.shape[-1]), (
+        f"b must have shape [B, T, HV, K]; got {tuple(b.shape)}"
+    )
+    assert w.shape == v.shape, f"w must have shape [B, T, HV, V] matching v; got {tuple(w.shape)}"
+    return fused_recurrent_gdn2_fwd(
+        q=q, k=k, v=v, g=g, b=b, w=w, A_log=A_log, dt_bias=dt_bias, scale=scale,
+        initial_state=initial_state, inplace_final_state=False,
+        output_final_state=output_final_state,
+        use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
+        use_gate_in_kernel=use_gate_in_kernel, lower_bound=lower_bound,
+        cu_seqlens=cu_seqlens, transpose_state_layout=transpose_state_layout,
+    )
+
+
+def chunk_gdn2_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    b: torch.Tensor,
+    w: torch.Tensor,
+    scale: float,
+    initial_state: torch.Tensor | None,
+    output_final_state: bool,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    lower_bound: float | None = None,
+    cu_seqlens: torch.LongTensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Launch the chunkwise HIP forward (reference ``chunk_gdn2.py:1165-1264``)."""
+    name = "chunk_gdn2"
+    _require_gpu(name, q, k, v, g, b, w, initial_state)
+    _check_shapes(name, q, k, v, g, b, w, same_heads=True)
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    dt = q.dtype
+    q, k, v, b, w = (_io(x, dt) for x in (q, k, v, b, w))
+    g = g.contiguous() if g.dtype in (torch.float32, dt) else g.float().contiguous()
+    cu_dev, cu_host = _cu(cu_seqlens, q.device, T)
+    N = B if cu_seqlens is None else cu_host.numel() - 1
+    h0 = None if initial_state is None else initial_state.float().contiguous()
+    if h0 is not None and tuple(h0.shape) != (N, H, K, V):
+        raise ValueError(f"{name}: initial_state must be {(N, H, K, V)}, got {tuple(h0.shape)}")
+    ht = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) if output_final_state else None
+    o = torch.empty_like(v)
+    lib = nat.load()
+    cu_host_p = None if cu_host is None else cu_host.data_ptr()
+    ws_bytes = lib.gdn2_chunk_fwd_workspace_size(B, T, H, K, V, nat.dtype_code(dt), cu_host_p, N)
+    if ws_bytes == 0 and B * T > 0 and K > 128:
+        raise NotImplementedError(f"{name}: key head dim {K} > 128 is not supported by the chunk kernel")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    a_log, dtb = _gate_tensors(use_gate_in_kernel, A_log, dt_bias, H, K)
+    st = lib.gdn2_chunk_fwd(
+        nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(g), nat.ptr(b), nat.ptr(w),
+        nat.dtype_code(dt), nat.dtype_code(g.dtype), nat.ptr(o),
+        nat.ptr(h0), nat.ptr(ht), nat.ptr(a_log), nat.ptr(dtb),
+        float(lower_bound) if lower_bound is not None else 0.0,
+        nat.ptr(cu_dev), cu_host_p, N, B, T, H, K, V, float(scale),
+        _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound),
+        ws.data_ptr(), ws.numel(), nat.stream_handle(q.device),
+    )
+    nat.check(st, name)
+    return o, ht
+
+
+class ChunkGDN2Function(torch.autograd.Function):
+    """Autograd wrapper of the chunkwise HIP kernels (reference ``chunk_gdn2.py:2328-2547``)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, b, w, A_log, dt_bias, scale, initial_state, output_final_state,
+                use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound):
+        o, ht = chunk_gdn2_fwd(
+            q, k, v, g, b, w, scale, initial_state, output_final_state,
+            use_qk_l2norm_in_kernel, use_gate_in_kernel, A_log, dt_bias, lower_bound, cu_seqlens,
+        )
+        ctx.save_for_backward(q, k, v, g, b, w, initial_state, A_log, dt_bias, cu_seqlens)
+        ctx.scale = scale
+        ctx.flags = (use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound)
+        return o, ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        from .backward import chunk_gdn2_bwd
+
+        q, k, v, g, b, w, h0, A_log, dt_bias, cu_seqlens = ctx.saved_tensors
+        use_l2, use_gate, lower_bound = ctx.flags
+        grads = chunk_gdn2_bwd(
+            q, k, v, g, b, w, ctx.scale, h0, do, dht, use_l2, use_gate, A_log, dt_bias,
+            lower_bound, cu_seqlens,
+        )
+        dq, dk, dv, dg, db, dw, dh0, dA_log, ddt_bias = grads
+        return (dq, dk, dv, dg, db, dw, dA_log, ddt_bias, None, dh0, None, None, None, None, None)
+
+
+def chunk_gdn2(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    b: torch.Tensor,
+    w: torch.Tensor,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    cu_seqlens: torch.LongTensor | None = None,
+    cu_seqlens_cpu: torch.LongTensor | None = None,
+    safe_gate: bool = False,
+    lower_bound: float | None = None,
+    disable_recompute: bool = False,
+    return_intermediate_states: bool = False,
+    transpose_state_layout: bool = False,
+    **kwargs: Any,
+):
+    """Chunkwise gdn2 forward with autograd (reference ``chunk_gdn2.py:1268-1434``).
+
+    Shapes ``q, k, g, b [B,T,H,K]``, ``v, w [B,T,H,V]``; ``initial_state``
+    ``[N,H,K,V]`` float32.  Returns ``(o, final_state)``.  The chunk size is 64,
+    as in the reference accelerated op.
+    """
+    if cu_seqlens is not None:
+        if q.shape[0] != 1:
+            raise ValueError(
+                f"The batch size is expected to be 1 rather than {q.shape[0]} when using "
+                "`cu_seqlens`. Please flatten variable-length inputs before processing."
+            )
+        if initial_state is not None and initial_state.shape[0] != len(cu_seqlens) - 1:
+            raise ValueError(
+                "The number of initial states is expected to be equal to the number of "
+                f"input sequences, i.e., {len(cu_seqlens) - 1} rather than "
+                f"{initial_state.shape[0]}."
+            )
+    if initial_state is not None:
+        assert initial_state.dtype == torch.float32, "initial_state must be in float32."
+    A_log, dt_bias = None, None
+    if use_gate_in_kernel:
+        assert "A_log" in kwargs, "A_log must be provided when use_gate_in_kernel=True."
+        A_log, dt_bias = kwargs["A_log"], kwargs.get("dt_bias")
+    if safe_gate and use_gate_in_kernel:
+        if lower_bound is None:
+            raise ValueError("`lower_bound` must be specified when `safe_gate=True` and `use_gate_in_kernel=True`.")
+        if not (-5 <= lower_bound < 0):
+            raise ValueError(f"`lower_bound` must be in the safe range [-5, 0), got {lower_bound}.")
+    if not (safe_gate and use_gate_in_kernel):
+        lower_bound = None
+    assert q.shape == k.shape == g.shape, "q, k, g must have the same shape."
+    assert k.shape[-1] <= 256, "Currently we only support key headdim <=256 for GDN-2 :-("
+    assert b.shape == q.shape, (
+        "b (channel-wise erase gate) must have shape [B, T, H, K] matching q; "
+        f"got {tuple(b.shape)} vs q {tuple(q.shape)}."
+    )
+    assert w.shape == v.shape, (
+        "w (channel-wise write gate) must have shape [B, T, H, V] matching v; "
+        f"got {tuple(w.shape)} vs v {tuple(v.shape)}."
+    )
+    assert v.shape == (*q.shape[:3], v.shape[-1]), (
+        "v must be of shape (batch size, seq len, num of head, head dim)."
+    )
+    if return_intermediate_states or transpose_state_layout:
+        raise NotImplementedError("chunk_gdn2: return_intermediate_states / transpose_state_layout")
+    if scale is None:
+        scale = k.shape[-1] ** -0.5
+    _require_gpu("chunk_gdn2", q, k, v, g, b, w, initial_state)
+    return ChunkGDN2Function.apply(
+        q, k, v, g, b, w, A_log, dt_bias, scale, initial_state, output_final_state,
+        use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound,
+    )

@@ -1,0 +1,59 @@
+"""Shared helpers for the gdn2 tests (inputs, dtype rounding, error metric)."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import gdn2_oracle as orc
+
+REL_TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def rel_l2(x, ref) -> float:
+    if isinstance(x, torch.Tensor):
+        x = x.detach().double().cpu().numpy()
+    if isinstance(ref, torch.Tensor):
+        ref = ref.detach().double().cpu().numpy()
+    return orc.rel_l2(x, ref)
+
+
+def rand_inputs(B, T, H, K, V, HV=None, seed=0, decay="paper", h0_std=0.1, gate_scale=1.0):
+    """Channel-wise random inputs (numpy float64) in the reference tests' ranges.
+
+    decay="paper":   g = -softplus(N(0,1) + 2)        (BASELINE distribution)
+    decay="unit":    g = -|U(0,1)|                      (reference test_gdn2.py:122)
+    decay="extreme": g = -softplus(2 N(0,1) + 7)        (spans > 80 per 16 tokens)
+    """
+    HV = HV or H
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, T, H, K))
+    k = rng.standard_normal((B, T, H, K))
+    v = rng.standard_normal((B, T, HV, V))
+    if decay == "paper":
+        g = -np.logaddexp(0.0, rng.standard_normal((B, T, HV, K)) + 2.0)
+    elif decay == "unit":
+        g = -np.abs(rng.random((B, T, HV, K)))
+    elif decay == "extreme":
+        g = -np.logaddexp(0.0, 2.0 * rng.standard_normal((B, T, HV, K)) + 7.0)
+    else:
+        raise ValueError(decay)
+    g = g * gate_scale
+    b = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, HV, K))))
+    w = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, HV, V))))
+    h0 = rng.standard_normal((B, HV, K, V)) * h0_std if h0_std > 0 else None
+    return dict(q=q, k=k, v=v, g=g, b=b, w=w, h0=h0)
+
+
+def to_device(inp, device, dtype, g_dtype=torch.float32):
+    """Cast numpy inputs to device tensors; returns (tensors, the same values rounded, as numpy)."""
+    out, rounded = {}, {}
+    for name, x in inp.items():
+        if x is None:
+            out[name], rounded[name] = None, None
+            continue
+        dt = torch.float32 if name == "h0" else (g_dtype if name == "g" else dtype)
+        t = torch.from_numpy(np.ascontiguousarray(x)).to(dt)
+        rounded[name] = t.double().numpy()
+        out[name] = t.to(device)
+    return out, rounded
