@@ -1,0 +1,86 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol that
+include/gdn2_hip.h declares, and rejects bad arguments before launching."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "gdn2_hip.h"
+
+
+def _declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gdn2_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from qwendopamine_amd import _native as nat
+
+    if not nat.LIB_PATH.exists():
+        pytest.fail(f"{nat.LIB_PATH} not built (run python -m qwendopamine_amd.build)")
+    return nat.load()
+
+
+def test_header_declares_entry_points():
+    names = _declared_functions()
+    for n in ("gdn2_abi_version", "gdn2_status_string", "gdn2_recurrent_fwd",
+              "gdn2_chunk_fwd", "gdn2_chunk_fwd_workspace_size"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from qwendopamine_amd import _native as nat
+
+    raw = ctypes.CDLL(str(nat.LIB_PATH))
+    for name in _declared_functions():
+        assert hasattr(raw, name), f"{name} declared in gdn2_hip.h but not exported"
+        assert name in nat.SIGNATURES, f"{name} has no ctypes signature in _native.py"
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.gdn2_abi_version() == 1
+    assert lib.gdn2_status_string(0) == b"ok"
+    assert b"invalid" in lib.gdn2_status_string(-1)
+    assert b"workspace" in lib.gdn2_status_string(-4)
+
+
+def test_invalid_arguments_rejected_before_launch(lib):
+    from qwendopamine_amd import _native as nat
+
+    # bad dtype code
+    st = lib.gdn2_recurrent_fwd(None, None, None, None, None, None, 7, 0, None, None, None, None,
+                                None, 0.0, None, 1, 1, 1, 1, 1, 16, 16, 1.0, 0, None)
+    assert st == nat.ERR_INVALID
+    # value heads not a multiple of key heads
+    st = lib.gdn2_recurrent_fwd(None, None, None, None, None, None, 0, 0, None, None, None, None,
+                                None, 0.0, None, 1, 1, 1, 2, 3, 16, 16, 1.0, 0, None)
+    assert st == nat.ERR_INVALID
+    # key dim above 256 is unsupported (reference asserts K <= 256)
+    st = lib.gdn2_recurrent_fwd(None, None, None, None, None, None, 0, 0, None, None, None, None,
+                                None, 0.0, None, 1, 1, 1, 1, 1, 300, 16, 1.0, 0, None)
+    assert st == nat.ERR_UNSUPPORTED
+    # gate-in-kernel without A_log
+    st = lib.gdn2_recurrent_fwd(None, None, None, None, None, None, 0, 0, None, None, None, None,
+                                None, 0.0, None, 1, 1, 1, 1, 1, 16, 16, 1.0, nat.FLAG_GATE_IN_KERNEL, None)
+    assert st == nat.ERR_INVALID
+    # non-null tensors required when there are tokens
+    st = lib.gdn2_chunk_fwd(None, None, None, None, None, None, 1, 0, None, None, None, None, None,
+                            0.0, None, None, 1, 1, 8, 1, 16, 16, 1.0, 0, None, 0, None)
+    assert st == nat.ERR_INVALID
+
+
+def test_chunk_workspace_size(lib):
+    # bf16, K=V=128: 64 KiB of tiles + 512 B of decay per (chunk, head)
+    n = lib.gdn2_chunk_fwd_workspace_size(8, 4096, 16, 128, 128, 1, None, 8)
+    assert n == 8 * 64 * 16 * (65536 + 512)
+    cu = (ctypes.c_int64 * 4)(0, 10, 10, 75)
+    n2 = lib.gdn2_chunk_fwd_workspace_size(1, 75, 2, 64, 64, 0, ctypes.cast(cu, ctypes.c_void_p), 3)
+    assert n2 == (1 + 0 + 2) * 2 * ((192 * 64 + 8192) * 4 + 64 * 4)
+    assert lib.gdn2_chunk_fwd_workspace_size(1, 64, 1, 200, 64, 1, None, 1) == 0

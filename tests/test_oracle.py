@@ -1,0 +1,282 @@
+"""Pin the float64 oracle (CPU).
+
+The reference ships no golden tensors, so every oracle function is checked
+against something that does not restate its own formula:
+  * closed forms (linear attention, single token),
+  * an explicit (K x K) matrix form of the update (reference gdn2.py:10-11),
+  * the third-party scalar gated delta rule of ``transformers`` (qwen3_next),
+  * invariants the reference's own tests use (chunk-size and split/resume
+    invariance, test_gdn2.py:111-152 and 185-233; causality),
+  * central finite differences for the VJP,
+and planted mistakes are shown to fail at least one pin.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import gdn2_oracle as orc
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _rand(B, T, H, K, V, seed, decay="unit", h0=True):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, T, H, K))
+    k = rng.standard_normal((B, T, H, K))
+    v = rng.standard_normal((B, T, H, V))
+    if decay == "unit":
+        g = -np.abs(rng.random((B, T, H, K)))
+    else:
+        g = -np.logaddexp(0.0, rng.standard_normal((B, T, H, K)) + 2.0)
+    b = 1 / (1 + np.exp(-rng.standard_normal((B, T, H, K))))
+    w = 1 / (1 + np.exp(-rng.standard_normal((B, T, H, V))))
+    s0 = rng.standard_normal((B, H, K, V)) * 0.1 if h0 else None
+    return q, k, v, g, b, w, s0
+
+
+def _matrix_form(q, k, v, g, b, w, s0):
+    """S_t = (I - k (b*k)^T) Diag(e^g) S + k (w*v)^T ; o_t = S_t^T q  (explicit K x K matrices)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    qn = orc.l2normalize(q) * K**-0.5
+    kn = orc.l2normalize(k)
+    o = np.zeros((B, T, H, V))
+    S = np.zeros((B, H, K, V)) if s0 is None else s0.copy()
+    eye = np.eye(K)
+    for bi in range(B):
+        for h in range(H):
+            St = S[bi, h]
+            for t in range(T):
+                kk = kn[bi, t, h][:, None]
+                P = eye - kk @ (b[bi, t, h] * kn[bi, t, h])[None, :]
+                St = P @ np.diag(np.exp(g[bi, t, h])) @ St + kk @ (w[bi, t, h] * v[bi, t, h])[None, :]
+                o[bi, t, h] = St.T @ qn[bi, t, h]
+            S[bi, h] = St
+    return o, S
+
+
+def test_linear_attention_closed_form():
+    """b = 0, w = 1, g = 0: o = tril(q k^T) v with normalised, scaled q."""
+    q, k, v, _, _, _, _ = _rand(2, 13, 3, 8, 5, seed=1, h0=False)
+    z = np.zeros_like(q)
+    o, S = orc.recurrent_fwd(q, k, v, z, z, np.ones_like(v))
+    qn = orc.l2normalize(q) * 8**-0.5
+    kn = orc.l2normalize(k)
+    for bi in range(2):
+        for h in range(3):
+            A = np.tril(qn[bi, :, h] @ kn[bi, :, h].T)
+            np.testing.assert_allclose(o[bi, :, h], A @ v[bi, :, h], rtol=1e-12, atol=1e-12)
+            np.testing.assert_allclose(S[bi, h], kn[bi, :, h].T @ v[bi, :, h], atol=1e-12)
+
+
+def test_single_token_closed_form():
+    q, k, v, g, b, w, s0 = _rand(1, 1, 2, 6, 4, seed=2)
+    o, S = orc.recurrent_fwd(q, k, v, g, b, w, s0)
+    qn = orc.l2normalize(q)[0, 0] * 6**-0.5
+    kn = orc.l2normalize(k)[0, 0]
+    for h in range(2):
+        Sd = np.exp(g[0, 0, h])[:, None] * s0[0, h]
+        u = w[0, 0, h] * v[0, 0, h] - Sd.T @ (b[0, 0, h] * kn[h])
+        exp_o = Sd.T @ qn[h] + (qn[h] @ kn[h]) * u
+        np.testing.assert_allclose(o[0, 0, h], exp_o, atol=1e-13)
+        np.testing.assert_allclose(S[0, h], Sd + np.outer(kn[h], u), atol=1e-13)
+    # zero state: o = (q.k)(w*v)
+    o0, _ = orc.recurrent_fwd(q, k, v, g, b, w, None)
+    np.testing.assert_allclose(o0[0, 0], (qn * kn).sum(-1)[:, None] * (w * v)[0, 0], atol=1e-13)
+
+
+def test_matches_explicit_matrix_form():
+    args = _rand(2, 9, 2, 7, 5, seed=3, decay="paper")
+    o1, s1 = orc.recurrent_fwd(*args)
+    o2, s2 = _matrix_form(*args)
+    np.testing.assert_allclose(o1, o2, atol=1e-12)
+    np.testing.assert_allclose(s1, s2, atol=1e-12)
+
+
+def test_matches_transformers_scalar_gated_delta_rule():
+    """Broadcast scalar gates reduce gdn2 to the gated delta rule (third-party implementation)."""
+    torch = pytest.importorskip("torch")
+    qn3 = pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    rng = np.random.default_rng(4)
+    B, T, H, K, V = 2, 17, 3, 16, 12
+    q = orc.l2normalize(rng.standard_normal((B, T, H, K)))
+    k = orc.l2normalize(rng.standard_normal((B, T, H, K)))
+    v = rng.standard_normal((B, T, H, V))
+    beta = 1 / (1 + np.exp(-rng.standard_normal((B, T, H))))
+    gs = -np.logaddexp(0.0, rng.standard_normal((B, T, H)) + 2.0)
+    s0 = rng.standard_normal((B, H, K, V)) * 0.1
+    o, S = orc.recurrent_fwd(q, k, v, np.repeat(gs[..., None], K, -1), np.repeat(beta[..., None], K, -1),
+                             np.repeat(beta[..., None], V, -1), s0, use_qk_l2norm_in_kernel=False)
+    t = lambda x: torch.tensor(x, dtype=torch.float64)  # noqa: E731
+    ot, St = qn3.torch_recurrent_gated_delta_rule(t(q), t(k), t(v), t(gs), t(beta), t(s0), True,
+                                                  use_qk_l2norm_in_kernel=False)
+    # that implementation casts to float32 internally
+    assert orc.rel_l2(ot.numpy(), o) < 1e-6
+    assert orc.rel_l2(St.numpy(), S) < 1e-6
+
+
+@pytest.mark.parametrize("chunk", [1, 4, 8, 16, 33, 64])
+@pytest.mark.parametrize("T", [8, 41, 100])
+def test_chunk_form_equals_recurrence(chunk, T):
+    args = _rand(2, T, 2, 16, 12, seed=T + chunk, decay="paper")
+    o1, s1 = orc.recurrent_fwd(*args)
+    o2, s2 = orc.chunk_fwd(*args, chunk_size=chunk)
+    np.testing.assert_allclose(o2, o1, atol=1e-11)
+    np.testing.assert_allclose(s2, s1, atol=1e-11)
+
+
+def test_split_resume_and_causality():
+    q, k, v, g, b, w, s0 = _rand(2, 12, 3, 16, 16, seed=5)
+    o, s = orc.recurrent_fwd(q, k, v, g, b, w, s0)
+    _, s_pre = orc.recurrent_fwd(q[:, :5], k[:, :5], v[:, :5], g[:, :5], b[:, :5], w[:, :5], s0)
+    o_post, s_post = orc.chunk_fwd(q[:, 5:], k[:, 5:], v[:, 5:], g[:, 5:], b[:, 5:], w[:, 5:], s_pre,
+                                   chunk_size=4)
+    np.testing.assert_allclose(o[:, 5:], o_post, atol=1e-12)
+    np.testing.assert_allclose(s, s_post, atol=1e-12)
+    # appending tokens never changes earlier outputs
+    o_short, _ = orc.recurrent_fwd(q[:, :7], k[:, :7], v[:, :7], g[:, :7], b[:, :7], w[:, :7], s0)
+    np.testing.assert_allclose(o[:, :7], o_short, atol=1e-14)
+
+
+def test_varlen_equals_separate_sequences():
+    q, k, v, g, b, w, _ = _rand(1, 30, 2, 8, 8, seed=6)
+    cu = [0, 4, 4, 19, 30]
+    s0 = np.random.default_rng(7).standard_normal((4, 2, 8, 8)) * 0.1
+    o, s = orc.recurrent_fwd(q, k, v, g, b, w, s0, cu_seqlens=cu)
+    for n in range(4):
+        a, e = cu[n], cu[n + 1]
+        on, sn = orc.recurrent_fwd(q[:, a:e], k[:, a:e], v[:, a:e], g[:, a:e], b[:, a:e], w[:, a:e], s0[n:n + 1])
+        np.testing.assert_allclose(o[:, a:e], on, atol=1e-14)
+        np.testing.assert_allclose(s[n], sn[0], atol=1e-14)
+
+
+def test_gva_equals_repeated_heads():
+    rng = np.random.default_rng(8)
+    B, T, H, HV, K, V = 1, 9, 2, 4, 8, 8
+    q, k = rng.standard_normal((B, T, H, K)), rng.standard_normal((B, T, H, K))
+    v, w = rng.standard_normal((B, T, HV, V)), rng.random((B, T, HV, V))
+    g, b = -rng.random((B, T, HV, K)), rng.random((B, T, HV, K))
+    o1, s1 = orc.recurrent_fwd(q, k, v, g, b, w)
+    o2, s2 = orc.recurrent_fwd(np.repeat(q, 2, 2), np.repeat(k, 2, 2), v, g, b, w)
+    np.testing.assert_allclose(o1, o2, atol=1e-14)
+    np.testing.assert_allclose(s1, s2, atol=1e-14)
+
+
+def test_vjp_matches_finite_differences():
+    q, k, v, g, b, w, s0 = _rand(1, 11, 2, 6, 5, seed=9, decay="paper")
+    rng = np.random.default_rng(10)
+    do = rng.standard_normal(v.shape)
+    dht = rng.standard_normal(s0.shape)
+    grads = orc.recurrent_vjp(q, k, v, g, b, w, do, dht, s0)
+    args = [q, k, v, g, b, w, s0]
+
+    def loss(a):
+        o, s = orc.recurrent_fwd(*a)
+        return float((o * do).sum() + (s * dht).sum())
+
+    for i, gr in enumerate(grads):
+        d = rng.standard_normal(args[i].shape)
+        eps = 1e-6
+        ap = list(args)
+        ap[i] = args[i] + eps * d
+        am = list(args)
+        am[i] = args[i] - eps * d
+        fd = (loss(ap) - loss(am)) / (2 * eps)
+        assert abs(fd - float((gr * d).sum())) <= 1e-6 * max(1.0, abs(fd)), i
+
+
+def test_vjp_without_l2norm_matches_finite_differences():
+    q, k, v, g, b, w, s0 = _rand(1, 7, 1, 5, 4, seed=11)
+    rng = np.random.default_rng(12)
+    do = rng.standard_normal(v.shape)
+    grads = orc.recurrent_vjp(q, k, v, g, b, w, do, None, s0, use_qk_l2norm_in_kernel=False)
+    for i, name in enumerate("qk"):
+        d = rng.standard_normal(q.shape)
+        a = [q, k]
+
+        def L(x):
+            aa = list(a)
+            aa[i] = x
+            o, _ = orc.recurrent_fwd(aa[0], aa[1], v, g, b, w, s0, use_qk_l2norm_in_kernel=False)
+            return float((o * do).sum())
+
+        eps = 1e-6
+        fd = (L(a[i] + eps * d) - L(a[i] - eps * d)) / (2 * eps)
+        assert abs(fd - float((grads[i] * d).sum())) <= 1e-6 * max(1.0, abs(fd)), name
+
+
+def test_golden_fixtures_reproduce():
+    f = np.load(GOLDEN / "gdn2_fwd_T100_H2_K32_V16.npz")
+    x = {n: f[n].astype(np.float64) for n in ("q", "k", "v", "g", "b", "w", "h0")}
+    o, ht = orc.recurrent_fwd(x["q"], x["k"], x["v"], x["g"], x["b"], x["w"], x["h0"])
+    np.testing.assert_allclose(o, f["o"], atol=1e-12)
+    np.testing.assert_allclose(ht, f["ht"], atol=1e-12)
+    f = np.load(GOLDEN / "gdn2_varlen_T90_N4.npz")
+    x = {n: f[n].astype(np.float64) for n in ("q", "k", "v", "g", "b", "w", "h0")}
+    o, ht = orc.recurrent_fwd(x["q"], x["k"], x["v"], x["g"], x["b"], x["w"], x["h0"],
+                              cu_seqlens=f["cu_seqlens"])
+    np.testing.assert_allclose(o, f["o"], atol=1e-12)
+    f = np.load(GOLDEN / "gdn2_bwd_T24_H2_K8_V8.npz")
+    x = {n: f[n].astype(np.float64) for n in ("q", "k", "v", "g", "b", "w", "h0", "do", "dht")}
+    grads = orc.recurrent_vjp(x["q"], x["k"], x["v"], x["g"], x["b"], x["w"], x["do"], x["dht"], x["h0"])
+    for name, gr in zip(("dq", "dk", "dv", "dg", "db", "dw", "dh0"), grads):
+        np.testing.assert_allclose(gr, f[name], atol=1e-12, err_msg=name)
+
+
+def test_config0_recipe_and_fingerprint():
+    inp = orc.make_inputs(0, 1, 512, 4, 64, 64)
+    assert np.allclose(np.linalg.norm(inp["q"], axis=-1), 1.0)
+    assert (inp["g"] < 0).all() and (inp["b"][..., :1] == inp["w"][..., :1]).all()
+    f = np.load(GOLDEN / "gdn2_config0_fingerprint.npz")
+    sums = np.array([float(np.sum(inp[n])) for n in ("q", "k", "v", "g", "b", "w")])
+    np.testing.assert_allclose(sums, f["input_sums"], rtol=1e-12)
+    o, ht = orc.recurrent_fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["b"], inp["w"])
+    np.testing.assert_allclose(o[0, :64, 0], f["o_head0_first64"], atol=1e-12)
+    np.testing.assert_allclose(ht, f["ht"], atol=1e-12)
+
+
+def test_c_port_matches_oracle():
+    from oracle import cpu_lib
+
+    args = _rand(2, 37, 3, 24, 20, seed=13, decay="paper")
+    o1, s1 = orc.recurrent_fwd(*args)
+    o2, s2 = cpu_lib.recurrent_fwd_f32(*args[:6], h0=args[6], nthreads=2)
+    assert orc.rel_l2(o2, o1) < 1e-5 and orc.rel_l2(s2, s1) < 1e-5
+
+
+# ---------------------------------------------------------------- planted bugs
+def _mutant(kind, q, k, v, g, b, w, s0):
+    """The recurrence with one plausible mistake (used only to show the pins bite)."""
+    B, T, H, K = q.shape
+    qn = orc.l2normalize(q) * K**-0.5
+    kn = orc.l2normalize(k)
+    o = np.zeros((B, T, H, v.shape[-1]))
+    S = np.zeros((B, H, K, v.shape[-1])) if s0 is None else s0.copy()
+    for t in range(T):
+        a = np.exp(g[:, t])[..., None]
+        e = b[:, t] * kn[:, t]
+        if kind == "erase_before_decay":
+            r = np.einsum("bhkv,bhk->bhv", S, e)
+            S = S * a
+        else:
+            S = S * a
+            r = np.einsum("bhkv,bhk->bhv", S, kn[:, t] if kind == "erase_without_b" else e)
+        u = w[:, t] * v[:, t] - r
+        S_new = S + kn[:, t][..., None] * u[..., None, :]
+        o[:, t] = np.einsum("bhkv,bhk->bhv", S if kind == "read_before_write" else S_new, qn[:, t])
+        S = S_new
+    return o, S
+
+
+@pytest.mark.parametrize("kind", ["erase_before_decay", "erase_without_b", "read_before_write"])
+def test_planted_mistakes_fail_the_matrix_form_pin(kind):
+    args = _rand(1, 6, 2, 6, 4, seed=14, decay="paper")
+    o_ref, _ = _matrix_form(*args)
+    o_bad, _ = _mutant(kind, *args)
+    o_good, _ = _mutant("none", *args)
+    np.testing.assert_allclose(o_good, o_ref, atol=1e-12)
+    assert np.abs(o_bad - o_ref).max() > 1e-6
