@@ -12,25 +12,35 @@
 //   O = (q*exp(G)) S0 + Aqk U,   S1 = Diag(exp(G_last)) S0 + (k*exp(G_last-G))^T U
 //
 // Only relative decays appear.  The pair products are factored per 16-token
-// sub-block with references that keep every factor in [e^-D, e^D] (D = the
-// sub-block's decay span): row factors q*exp(G_r - G_start(R)), column factors
-// k*exp(G_end(I) - G_i) times the decay between the blocks (<= 1), and
-// exp(+span) for the diagonal block.  A diagonal block whose span exceeds
-// kDiagSpanLimit (factors would leave the fp32/bf16 range) is recomputed
-// exactly, pair by pair, on the VALU.
+// sub-block R with references that keep every factor in [2^-D, 2^D] (D = the
+// sub-block's decay span in log2 units): rows q*2^(G_r - G_start(R)), columns
+// k*2^(G_end(I) - G_i) times the decay between the blocks (<= 1), and 2^D on
+// the diagonal block.  A diagonal block whose span exceeds kDiagSpanLimit2
+// (factors would leave the normal fp32/bf16 range) is recomputed exactly,
+// pair by pair, on the VALU.  Decays are handled in log2 units so every
+// exponential is one v_exp_f32.
+//
+// Operands follow the K16 convention of gdn2_mfma.h: accumulators of one
+// product are B operands of the next without data movement, and a product
+// with the identity transposes a tile in registers.
 //
 // Two kernels:
-//  * chunk_prep_kernel  -- one workgroup per (chunk, head), all chunks in
-//    parallel.  Fused prologue (L2 norm, scale, in-kernel gate, in-chunk
-//    cumsum), the Aqk / L products on MFMA, the block-triangular inverse of
-//    I + L in fp32, and W = X Ebar.  Writes Qbar, -W, Ktilde^T, X, Aqk in the
-//    fragment-native layout of gdn2_mfma.h plus exp(G_last), so the scan
-//    reads each operand block with one coalesced access per lane.
-//  * chunk_scan_kernel  -- one workgroup per (sequence, head, 64-column value
-//    slice), walking the chunks in order with the fp32 state slab held as MFMA
-//    accumulators in VGPRs: U, O and the state update are five MFMA
-//    contractions per chunk.  Both slices of a head are mapped to the same
-//    XCD so the shared K-side operands are fetched from HBM once.
+//  * chunk_prep_kernel -- one workgroup (4 waves, wave R = 16-token block R)
+//    per (chunk, head), all chunks in parallel.  Fused prologue (L2 norm,
+//    scale, optional in-kernel gate, in-block prefix sums), Aqk^T and L^T on
+//    MFMA, the block-triangular inverse of I + L in fp32, and W^T = Ebar^T X^T.
+//    It writes one contiguous "blob" per (chunk, head): X, -W, Qbar, Aqk,
+//    Ktilde^T in K16 fragment-native order plus exp(G_last).
+//  * chunk_scan_kernel -- one workgroup per (sequence, head, 64-column value
+//    slice) walking the chunks in order.  Wave c owns 16 value columns and
+//    holds its fp32 state columns S[:, c] as accumulators; with the column
+//    split no wave needs another's U or S, so U, O and the state update run
+//    from registers.  Each chunk's blob is copied to LDS once per workgroup
+//    (double-buffered, the next blob prefetched into registers during the
+//    current chunk) and read by all four waves.  Both value slices of a head
+//    share an XCD, so the second blob read hits L2.
+
+#include <type_traits>
 
 #include "gdn2_internal.h"
 #include "gdn2_mfma.h"
@@ -40,7 +50,10 @@ namespace gdn2 {
 namespace {
 
 constexpr int kChunk = 64;
-constexpr float kDiagSpanLimit = 80.0f;
+constexpr float kLog2e = 1.4426950408889634f;
+// Largest in-block decay span (log2 units, ~ e^80) for which the factored
+// diagonal block keeps every factor inside the normal fp32/bf16 range.
+constexpr float kDiagSpanLimit2 = 115.0f;
 
 struct ChunkParams {
     const void *q, *k, *v, *g, *b, *w;
@@ -55,20 +68,23 @@ struct ChunkParams {
     int nt;  // chunks per sequence without cu_seqlens
     float scale;
     unsigned flags;
-    int vec_ok;  // K % 8 == 0: 16-byte input loads
-    void *ws_tiles;
-    float *ws_gl;
+    int vec_ok;  // K % 4 == 0: 4-wide input loads
+    void *ws;
 };
 
-// Per (chunk, head) tile offsets, in storage elements.
-template <int KP>
-struct TileLayout {
-    static constexpr int64_t QBAR = 0;
-    static constexpr int64_t WNEG = 64 * KP;
-    static constexpr int64_t KT = 128 * KP;
-    static constexpr int64_t X = 192 * KP;
-    static constexpr int64_t AQK = 192 * KP + 4096;
-    static constexpr int64_t SIZE = 192 * KP + 8192;
+// Per (chunk, head) blob, in storage elements.
+template <PrecKind PK, int KP>
+struct Blob {
+    using st = typename Prec<PK>::st;
+    static constexpr int64_t X = 0;                 // [64][64]   (I + L)^{-1}
+    static constexpr int64_t WN = 4096;             // [64][KP]   -W
+    static constexpr int64_t QB = 4096 + 64 * KP;   // [64][KP]   Qbar
+    static constexpr int64_t AQ = 4096 + 128 * KP;  // [64][64]   Aqk
+    static constexpr int64_t KT = 8192 + 128 * KP;  // [KP][64]   Ktilde^T
+    static constexpr int64_t GL = 8192 + 192 * KP;  // KP floats  exp(G_last)
+    static constexpr int64_t SIZE = GL + KP * 4 / static_cast<int64_t>(sizeof(st));
+    static constexpr int64_t BYTES = SIZE * static_cast<int64_t>(sizeof(st));
+    static_assert(BYTES % 16 == 0, "blob must be a whole number of 16-byte units");
 };
 
 __device__ __forceinline__ void locate_chunk(const ChunkParams &p, int gc, int &n, int &j,
@@ -116,77 +132,71 @@ __device__ __forceinline__ int seq_chunk_base(const ChunkParams &p, int n, int64
     return acc;
 }
 
+// 4 consecutive channels c0..c0+3 of one row, zero outside [0, K) or when !ok.
 template <typename T>
-__device__ __forceinline__ void load8(const T *base, int64_t off, int c0, int K, bool ok,
-                                      int vec_ok, float (&x)[8])
+__device__ __forceinline__ void load4(const T *base, int64_t off, int c0, int K, bool ok, int vec_ok,
+                                      float (&x)[4])
 {
-    if (ok && vec_ok && c0 + 8 <= K) {
-        if constexpr (sizeof(T) == 2) {
-            const uint4 u = *reinterpret_cast<const uint4 *>(base + off + c0);
-            const uint32_t wds[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const T lo{static_cast<uint16_t>(wds[i] & 0xffffu)};
-                const T hi{static_cast<uint16_t>(wds[i] >> 16)};
-                x[2 * i] = io<T>::ld(&lo, 0);
-                x[2 * i + 1] = io<T>::ld(&hi, 0);
-            }
-        } else {
+    if (ok && vec_ok && c0 + 4 <= K) {
+        if constexpr (std::is_same<T, float>::value) {
             const float4 a = *reinterpret_cast<const float4 *>(base + off + c0);
-            const float4 c = *reinterpret_cast<const float4 *>(base + off + c0 + 4);
             x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-            x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+        } else if constexpr (std::is_same<T, bf16_t>::value) {
+            const uint2 u = *reinterpret_cast<const uint2 *>(base + off + c0);
+            x[0] = __uint_as_float(u.x << 16);
+            x[1] = __uint_as_float(u.x & 0xffff0000u);
+            x[2] = __uint_as_float(u.y << 16);
+            x[3] = __uint_as_float(u.y & 0xffff0000u);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = io<T>::ld(base, off + c0 + i);
         }
         return;
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = (ok && c0 + j < K) ? io<T>::ld(base, off + c0 + j) : 0.0f;
+    for (int i = 0; i < 4; ++i) x[i] = (ok && c0 + i < K) ? io<T>::ld(base, off + c0 + i) : 0.0f;
 }
 
-// f16 needs a bit-level constructor for load8's 16-byte path.
-template <>
-__device__ __forceinline__ void load8<f16_t>(const f16_t *base, int64_t off, int c0, int K,
-                                             bool ok, int vec_ok, float (&x)[8])
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Inclusive prefix sum over the 16 lanes m of a 16-lane row.
+__device__ __forceinline__ float row16_scan(float x, int m)
 {
-    (void)vec_ok;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = (ok && c0 + j < K) ? io<f16_t>::ld(base, off + c0 + j) : 0.0f;
+    for (int d = 1; d < 16; d <<= 1) {
+        const float y = __shfl_up(x, d, 16);
+        if (m >= d) x += y;
+    }
+    return x;
 }
-
-template <int A, int B>
-struct cmax {
-    static constexpr int value = A > B ? A : B;
-};
 
 // ---------------------------------------------------------------------------
 // Prep: one workgroup (4 waves) per (chunk, head).  Wave R owns token rows
-// 16R..16R+15; lane (m, kg) holds row 16R+m, channels 32s + 8kg + j.
+// 16R..16R+15; lane (m, kg) holds row 16R+m and channels 16kt + 4kg + i.
 // ---------------------------------------------------------------------------
 template <PrecKind PK, int KP, typename TI, typename TG>
-__global__ __launch_bounds__(256, 2) void chunk_prep_kernel(ChunkParams p)
+__global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkParams p)
 {
     using P = Prec<PK>;
     using st = typename P::st;
-    using TL = TileLayout<KP>;
+    using BL = Blob<PK, KP>;
+    using Q = Q4<PK>;
+    constexpr int NKT = KP / 16;
     constexpr int NKS = KP / 32;
-    constexpr int LDK = KP + 8;  // row-major [64][KP] storage tiles
-    constexpr int LDT = 64 + 8;  // transposed [KP][64] storage tiles
+    constexpr int LDK = KP + 8;  // row-major [64][KP] keys (storage precision)
     constexpr int LDF = 64 + 4;  // fp32 [64][64]
-    constexpr int SZ1 = cmax<64 * LDK * (int)sizeof(st), 64 * LDF * 4>::value;
-    constexpr int SZ2 = cmax<KP * LDT * (int)sizeof(st), cmax<64 * LDT * (int)sizeof(st), 4096>::value>::value;
-    constexpr int SZ3 = KP * LDT * (int)sizeof(st);
-    constexpr int SZ4 = cmax<64 * LDF * 4, 64 * LDK * (int)sizeof(st)>::value;
-    __shared__ __align__(16) unsigned char smem[SZ1 + SZ2 + SZ3 + SZ4];
-    __shared__ float sT[4][KP];
-
-    st *sKend = reinterpret_cast<st *>(smem);                 // [64][LDK]  then sX
-    float *sX = reinterpret_cast<float *>(smem);              // [64][LDF]
-    st *sKt = reinterpret_cast<st *>(smem + SZ1);             // [KP][LDT]  then sAq, scratch
-    st *sAq = sKt;                                            // [64][LDT]
-    float *sScr = reinterpret_cast<float *>(smem + SZ1);      // 4 x 256 fp32
-    st *sEt = reinterpret_cast<st *>(smem + SZ1 + SZ2);       // [KP][LDT]
-    float *sL = reinterpret_cast<float *>(smem + SZ1 + SZ2 + SZ3);  // [64][LDF] then sW
-    st *sW = reinterpret_cast<st *>(smem + SZ1 + SZ2 + SZ3);        // [64][LDK]
+    constexpr int SZK = 64 * LDK * static_cast<int>(sizeof(st));
+    constexpr int SZ1 = SZK > 64 * LDF * 4 ? SZK : 64 * LDF * 4;
+    __shared__ __align__(16) unsigned char smem1[SZ1];   // Kend, then L (fp32)
+    __shared__ __align__(16) st sEt[NKT * 4 * 256];      // Ebar^T, K16 blocks (channel, token)
+    __shared__ __align__(16) float sX[64 * LDF];
+    __shared__ __align__(16) float sT[4][KP];            // in-block decay totals (log2)
+    __shared__ __align__(16) float sEr[4][KP];           // 2^(decay before block)
+    __shared__ __align__(16) float sEa[4][KP];           // 2^(decay after block)
+    __shared__ __align__(16) float sPf[4][4][KP];        // key scale of block pair (R, I)
+    __shared__ __align__(16) float sScr[4][256];
+    st *sKend = reinterpret_cast<st *>(smem1);
+    float *sL = reinterpret_cast<float *>(smem1);
 
     const int tid = threadIdx.x, R = tid >> 6, l = tid & 63, m = l & 15, kg = l >> 4;
     const int gc = blockIdx.x, h = blockIdx.y;
@@ -195,11 +205,9 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(ChunkParams p)
     int n, jc;
     int64_t bos, len;
     locate_chunk(p, gc, n, jc, bos, len);
-    (void)n;
     const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
-    const int lc = static_cast<int>(len - static_cast<int64_t>(jc) * kChunk < kChunk
-                                        ? len - static_cast<int64_t>(jc) * kChunk
-                                        : kChunk);
+    const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
+    const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
     const int r = 16 * R + m;
     const bool row_ok = r < lc;
     const int64_t roff = ((t0 + r) * H + h) * K;
@@ -209,24 +217,25 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(ChunkParams p)
     const TI *b = static_cast<const TI *>(p.b);
     const TG *g = static_cast<const TG *>(p.g);
 
-    float qv[NKS][8], kv[NKS][8], ev[NKS][8], gv[NKS][8];
+    float qv[NKT][4], kv[NKT][4], ev[NKT][4], gv[NKT][4];
 #pragma unroll
-    for (int s = 0; s < NKS; ++s) {
-        const int c0 = 32 * s + 8 * kg;
-        load8<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv[s]);
-        load8<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv[s]);
-        load8<TI>(b, roff, c0, K, row_ok, p.vec_ok, ev[s]);
-        load8<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv[s]);
+    for (int kt = 0; kt < NKT; ++kt) {
+        const int c0 = 16 * kt + 4 * kg;
+        load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv[kt]);
+        load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv[kt]);
+        load4<TI>(b, roff, c0, K, row_ok, p.vec_ok, ev[kt]);
+        load4<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv[kt]);
     }
 
-    // Fused prologue: L2 norm (F.normalize semantics), scale, erase vector.
+    // Fused prologue: L2 norm (F.normalize semantics), scale, erase vector,
+    // optional gate activation, decay in log2 units.
     float sq = 0.f, sk = 0.f;
 #pragma unroll
-    for (int s = 0; s < NKS; ++s)
+    for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            sq = fmaf(qv[s][j], qv[s][j], sq);
-            sk = fmaf(kv[s][j], kv[s][j], sk);
+        for (int i = 0; i < 4; ++i) {
+            sq = fmaf(qv[kt][i], qv[kt][i], sq);
+            sk = fmaf(kv[kt][i], kv[kt][i], sk);
         }
     sq += __shfl_xor(sq, 16, 64);
     sq += __shfl_xor(sq, 32, 64);
@@ -240,163 +249,185 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(ChunkParams p)
     const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
     const float a_log = gate ? p.A_log[h] : 0.0f;
 #pragma unroll
-    for (int s = 0; s < NKS; ++s)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int c = 32 * s + 8 * kg + j;
-            qv[s][j] *= qmul;
-            kv[s][j] *= invk;
-            ev[s][j] *= kv[s][j];
-            if (gate && row_ok && c < K) {
-                const float db = p.dt_bias ? p.dt_bias[h * K + c] : 0.0f;
-                gv[s][j] = gate_activation(gv[s][j], a_log, db, use_lb, p.lower_bound);
-            }
-        }
-
-    // In-block inclusive cumsum over the 16 rows of this wave (lanes m of a
-    // 16-lane row).  gv becomes G_r - G_{start of block}.
-#pragma unroll
-    for (int s = 0; s < NKS; ++s)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float x = gv[s][j];
-#pragma unroll
-            for (int d = 1; d < 16; d <<= 1) {
-                const float y = __shfl_up(x, d, 16);
-                if (m >= d) x += y;
-            }
-            gv[s][j] = x;
-        }
-    if (m == 15) {
-#pragma unroll
-        for (int s = 0; s < NKS; ++s)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) sT[R][32 * s + 8 * kg + j] = gv[s][j];
-    }
-    __syncthreads();
-
-    st *ws = static_cast<st *>(p.ws_tiles) + (static_cast<int64_t>(gc) * H + h) * TL::SIZE;
-    typename P::frag fqb[NKS], feb[NKS];
-    bool slow = false;
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) {
-        float qb[8], eb[8], ke[8], qbar[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int c = 32 * s + 8 * kg + j;
-            float cum = 0.f, after = 0.f;
-#pragma unroll
-            for (int R2 = 0; R2 < 4; ++R2) {
-                const float t = sT[R2][c];
-                if (R2 < R) cum += t;
-                if (R2 > R) after += t;
-            }
-            const float TR = sT[R][c];
-            const float G = gv[s][j];
-            const float e1 = expf(G);
-            const float e2 = expf(TR - G);
-            const float eR = expf(cum);
-            qb[j] = qv[s][j] * e1;
-            eb[j] = ev[s][j] * e1;
-            ke[j] = kv[s][j] * e2;
-            qbar[j] = qb[j] * eR;
-            const float ebar = eb[j] * eR;
-            const float ktil = ke[j] * expf(after);
-            sKt[c * LDT + r] = P::from_f32(ktil);
-            sEt[c * LDT + r] = P::from_f32(ebar);
-            slow = slow || (-TR > kDiagSpanLimit);
-        }
-        fqb[s] = pack_frag<PK>(qb);
-        feb[s] = pack_frag<PK>(eb);
-        st_frag<PK>(sKend + r * LDK + 32 * s + 8 * kg, pack_frag<PK>(ke));
-        st_frag<PK>(ws + TL::QBAR + fn_block(R, s, KP) + 8 * l, pack_frag<PK>(qbar));
-    }
-    const bool wave_slow = __ballot(slow) != 0;
-    __syncthreads();
-
-    // Ktilde^T -> workspace, fragment-native [KP][64].
-    for (int task = tid; task < (KP / 16) * 2 * 64; task += 256) {
-        const int blk = task >> 6, L = task & 63, mt = blk >> 1, kt = blk & 1;
-        const st *src = sKt + (16 * mt + (L & 15)) * LDT + 32 * kt + 8 * (L >> 4);
-        st_frag<PK>(ws + TL::KT + fn_block(mt, kt, 64) + 8 * L, ld_frag<PK>(src));
-    }
-    __syncthreads();
-
-    // Aqk and L row strips of block R on MFMA.
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-        f32x4 aq = zero4(), al = zero4();
-        if (I <= R) {
-#pragma unroll
-            for (int s = 0; s < NKS; ++s) {
-                float kb[8];
-                unpack_frag<PK>(ld_frag<PK>(sKend + (16 * I + m) * LDK + 32 * s + 8 * kg), kb);
-                if (I != R - 1) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int c = 32 * s + 8 * kg + j;
-                        float ex;
-                        if (I == R) {
-                            ex = -sT[R][c];
-                        } else {
-                            ex = 0.f;
-                            for (int R2 = I + 1; R2 < R; ++R2) ex += sT[R2][c];
-                        }
-                        kb[j] *= expf(ex);
-                    }
-                }
-                const typename P::frag fb = pack_frag<PK>(kb);
-                aq = P::mma(aq, fqb[s], fb);
-                al = P::mma(al, feb[s], fb);
-            }
-        }
+    for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int rr = 4 * kg + i, cc = m;
-            const bool below = I < R;
-            const float vq = (below || (I == R && cc <= rr)) ? aq[i] : 0.f;
-            const float vl = (below || (I == R && cc < rr)) ? al[i] : 0.f;
-            sAq[(16 * R + rr) * LDT + 16 * I + cc] = P::from_f32(vq);
-            sL[(16 * R + rr) * LDF + 16 * I + cc] = vl;
+            const int c = 16 * kt + 4 * kg + i;
+            qv[kt][i] *= qmul;
+            kv[kt][i] *= invk;
+            ev[kt][i] *= kv[kt][i];
+            float gg = gv[kt][i];
+            if (gate && row_ok && c < K) {
+                const float db = p.dt_bias ? p.dt_bias[h * K + c] : 0.0f;
+                gg = gate_activation(gg, a_log, db, use_lb, p.lower_bound);
+            }
+            gv[kt][i] = row16_scan(gg * kLog2e, m);  // G (log2) relative to block start
+        }
+    bool wide = false;
+    if (m == 15) {
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+            *reinterpret_cast<float4 *>(&sT[R][16 * kt + 4 * kg]) =
+                make_float4(gv[kt][0], gv[kt][1], gv[kt][2], gv[kt][3]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wide = wide || (-gv[kt][i] > kDiagSpanLimit2);
         }
     }
+    // A diagonal block whose decay span is too wide for the factored form is
+    // summed exactly, pair by pair (row m, column j of block R), here while
+    // the fp32 inputs are still live.
+    const bool wave_slow = __ballot(wide) != 0;
+    f32x4 dq = zero4(), dl = zero4();
     if (wave_slow) {
-        // Exact pair sums for the diagonal block when its decay span is too
-        // wide for the factored form.
-        for (int i = 0; i < 16; ++i) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
             float accq = 0.f, accl = 0.f;
 #pragma unroll
-            for (int s = 0; s < NKS; ++s)
+            for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float ki = __shfl(kv[s][j], 16 * kg + i, 64);
-                    const float Gi = __shfl(gv[s][j], 16 * kg + i, 64);
-                    const float ex = (i <= m) ? expf(gv[s][j] - Gi) : 0.f;
-                    accq = fmaf(qv[s][j] * ki, ex, accq);
-                    accl = fmaf(ev[s][j] * ki, ex, accl);
+                for (int i = 0; i < 4; ++i) {
+                    const float kj = __shfl(kv[kt][i], 16 * kg + j, 64);
+                    const float Gj = __shfl(gv[kt][i], 16 * kg + j, 64);
+                    const float ex = (j <= m) ? fexp2(gv[kt][i] - Gj) : 0.f;
+                    accq = fmaf(qv[kt][i] * kj, ex, accq);
+                    accl = fmaf(ev[kt][i] * kj, ex, accl);
                 }
             accq += __shfl_xor(accq, 16, 64);
             accq += __shfl_xor(accq, 32, 64);
             accl += __shfl_xor(accl, 16, 64);
             accl += __shfl_xor(accl, 32, 64);
-            if (kg == 0) {
-                sAq[(16 * R + m) * LDT + 16 * R + i] = P::from_f32(i <= m ? accq : 0.f);
-                sL[(16 * R + m) * LDF + 16 * R + i] = i < m ? accl : 0.f;
+            if (kg == (j >> 2)) {
+                dq[j & 3] = accq;
+                dl[j & 3] = accl;
             }
         }
     }
     __syncthreads();
 
-    // Aqk -> workspace, fragment-native [64][64].
-    for (int task = tid; task < 8 * 64; task += 256) {
-        const int blk = task >> 6, L = task & 63, mt = blk >> 1, kt = blk & 1;
-        const st *src = sAq + (16 * mt + (L & 15)) * LDT + 32 * kt + 8 * (L >> 4);
-        st_frag<PK>(ws + TL::AQK + fn_block(mt, kt, 64) + 8 * L, ld_frag<PK>(src));
+    st *ws = static_cast<st *>(p.ws) + (static_cast<int64_t>(gc) * H + h) * BL::SIZE;
+    // Per-channel block vectors.
+    for (int e = tid; e < 4 * KP; e += 256) {
+        const int Rb = e / KP, c = e % KP;
+        const float t[4] = {sT[0][c], sT[1][c], sT[2][c], sT[3][c]};
+        float cum = 0.f, after = 0.f;
+#pragma unroll
+        for (int R2 = 0; R2 < 4; ++R2) {
+            if (R2 < Rb) cum += t[R2];
+            if (R2 > Rb) after += t[R2];
+        }
+        sEr[Rb][c] = fexp2(cum);
+        sEa[Rb][c] = fexp2(after);
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+            float ex = 0.f;
+            if (I == Rb) {
+                ex = -t[Rb];
+            } else {
+#pragma unroll
+                for (int R2 = 0; R2 < 4; ++R2)
+                    if (R2 > I && R2 < Rb) ex += t[R2];
+            }
+            sPf[Rb][I][c] = I > Rb ? 0.f : fexp2(ex);
+        }
+        if (Rb == 0) reinterpret_cast<float *>(ws + BL::GL)[c] = fexp2(t[0] + t[1] + t[2] + t[3]);
     }
     __syncthreads();
 
+    // Factors.  Qb / Eb stay in registers as K16 operands of this row block;
+    // Qbar goes straight to the blob; Ktilde^T and Ebar^T are transposed by
+    // an identity product.
+    const Q ident = identity_q4<PK>(l);
+    Q fqb[NKT], feb[NKT];
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+        const int c0 = 16 * kt + 4 * kg;
+        const float4 er = *reinterpret_cast<const float4 *>(&sEr[R][c0]);
+        const float4 ea = *reinterpret_cast<const float4 *>(&sEa[R][c0]);
+        const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][c0]);
+        const float erv[4] = {er.x, er.y, er.z, er.w};
+        const float eav[4] = {ea.x, ea.y, ea.z, ea.w};
+        const float trv[4] = {tr.x, tr.y, tr.z, tr.w};
+        float qb[4], eb[4], ke[4], qbar[4], ebar[4], ktil[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float G = gv[kt][i];
+            const float e1 = fexp2(G), e2 = fexp2(trv[i] - G);
+            qb[i] = qv[kt][i] * e1;
+            eb[i] = ev[kt][i] * e1;
+            ke[i] = kv[kt][i] * e2;
+            qbar[i] = qb[i] * erv[i];
+            ebar[i] = eb[i] * erv[i];
+            ktil[i] = ke[i] * eav[i];
+        }
+        fqb[kt] = pack4<PK>(qb[0], qb[1], qb[2], qb[3]);
+        feb[kt] = pack4<PK>(eb[0], eb[1], eb[2], eb[3]);
+        st_q4<PK>(ws + BL::QB + k16_block(R, kt, KP) + 4 * l, pack4<PK>(qbar[0], qbar[1], qbar[2], qbar[3]));
+        st_q4<PK>(sKend + r * LDK + c0, pack4<PK>(ke[0], ke[1], ke[2], ke[3]));
+        const f32x4 dk = mma1<PK>(zero4(), pack4<PK>(ktil[0], ktil[1], ktil[2], ktil[3]), ident);
+        st_q4<PK>(ws + BL::KT + k16_block(kt, R, 64) + 4 * l, pack4<PK>(dk));
+        const f32x4 de = mma1<PK>(zero4(), pack4<PK>(ebar[0], ebar[1], ebar[2], ebar[3]), ident);
+        st_q4<PK>(sEt + k16_block(kt, R, 64) + 4 * l, pack4<PK>(de));
+    }
+    __syncthreads();
+
+    // Aqk^T(I, R) = Kend_I^T-scaled . Qb_R^T and L^T(I, R) likewise with Eb:
+    // A = scaled keys of block I (LDS), B = this block's Qb / Eb (registers).
+    // Lane (n, kg) of the result holds Aqk[16R+n][16I+4kg+i], which is the
+    // K16 A-operand order of Aqk, so it is stored as is.
+    f32x4 aq[4], al[4];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+        aq[I] = zero4();
+        al[I] = zero4();
+        if (I <= R) {
+#pragma unroll
+            for (int s = 0; s < NKS; ++s) {
+                Q a[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int c0 = 32 * s + 16 * hh + 4 * kg;
+                    Q raw = ld_q4<PK>(sKend + (16 * I + m) * LDK + c0);
+                    if (I != R - 1) {
+                        float x[4];
+                        unpack4<PK>(raw, x);
+                        const float4 sc = *reinterpret_cast<const float4 *>(&sPf[R][I][c0]);
+                        raw = pack4<PK>(x[0] * sc.x, x[1] * sc.y, x[2] * sc.z, x[3] * sc.w);
+                    }
+                    a[hh] = raw;
+                }
+                aq[I] = mma2<PK>(aq[I], a[0], a[1], fqb[2 * s], fqb[2 * s + 1]);
+                al[I] = mma2<PK>(al[I], a[0], a[1], feb[2 * s], feb[2 * s + 1]);
+            }
+        }
+    }
+    if (wave_slow) {
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+            if (I == R) {
+                aq[I] = dq;
+                al[I] = dl;
+            }
+    }
+    // Causal masks; Aqk to the blob.
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int col = 16 * I + 4 * kg + i, row = 16 * R + m;
+            if (!(col <= row)) aq[I][i] = 0.f;
+            if (!(col < row)) al[I][i] = 0.f;
+        }
+        st_q4<PK>(ws + BL::AQ + k16_block(R, I, 64) + 4 * l, pack4<PK>(aq[I]));
+    }
+    __syncthreads();  // all reads of sKend done; its space becomes L
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+        *reinterpret_cast<float4 *>(&sL[(16 * R + m) * LDF + 16 * I + 4 * kg]) =
+            make_float4(al[I][0], al[I][1], al[I][2], al[I][3]);
+    __syncthreads();
+
     // X = (I + L)^{-1} in fp32: diagonal 16x16 blocks by forward substitution
-    // (lane j = column j), zero strictly-upper blocks.
+    // (lane j = column j), strictly-upper blocks zero.
     if (l < 16) {
         const int j = l;
         float x[16];
@@ -413,15 +444,15 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(ChunkParams p)
     for (int I = R + 1; I < 4; ++I)
         for (int e = l; e < 256; e += 64) sX[(16 * R + (e >> 4)) * LDF + 16 * I + (e & 15)] = 0.f;
     __syncthreads();
-    // Off-diagonal blocks by block forward substitution, one sub-diagonal at
-    // a time:  X_RI = -X_RR * sum_{J=I}^{R-1} L_RJ X_JI.
+    // Off-diagonal blocks, one sub-diagonal at a time:
+    //   X_RI = -X_RR * sum_{J=I}^{R-1} L_RJ X_JI.
     for (int d = 1; d <= 3; ++d) {
         if (R < 4 - d) {
             const int Rr = R + d, I = R;
             f32x4 t = zero4();
             for (int J = I; J < Rr; ++J)
                 t = mm16_f32(t, sL + (16 * Rr) * LDF + 16 * J, LDF, sX + (16 * J) * LDF + 16 * I, LDF, l);
-            float *scr = sScr + R * 256;
+            float *scr = sScr[R];
 #pragma unroll
             for (int i = 0; i < 4; ++i) scr[(4 * kg + i) * 16 + m] = t[i];
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -433,46 +464,28 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(ChunkParams p)
         __syncthreads();
     }
 
-    // W = X Ebar (stored negated), rows of block R.
-    {
-        typename P::frag fa[2];
+    // X to the blob (row block R).
+    Q xt[4];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            float xs[8];
-            const float *src = sX + (16 * R + m) * LDF + 32 * kb + 8 * kg;
+    for (int J = 0; J < 4; ++J) {
+        const float4 xv = *reinterpret_cast<const float4 *>(&sX[(16 * R + m) * LDF + 16 * J + 4 * kg]);
+        xt[J] = pack4<PK>(xv.x, xv.y, xv.z, xv.w);
+        st_q4<PK>(ws + BL::X + k16_block(R, J, 64) + 4 * l, xt[J]);
+    }
+    // W^T(ct, R) = Ebar^T(ct, :) X^T(:, R): B operand X^T(J, R) is row 16R+m of
+    // X, i.e. xt[J]; result lane (n, kg) holds W[16R+n][16ct+4kg+i] -- the K16
+    // A-operand order of W.  Stored negated.
 #pragma unroll
-            for (int j = 0; j < 8; ++j) xs[j] = src[j];
-            fa[kb] = pack_frag<PK>(xs);
+    for (int ct = 0; ct < NKT; ++ct) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            if (2 * s <= R)
+                acc = mma2<PK>(acc, ld_q4<PK>(sEt + k16_block(ct, 2 * s, 64) + 4 * l),
+                               ld_q4<PK>(sEt + k16_block(ct, 2 * s + 1, 64) + 4 * l), xt[2 * s],
+                               xt[2 * s + 1]);
         }
-#pragma unroll
-        for (int ct = 0; ct < KP / 16; ++ct) {
-            f32x4 acc = zero4();
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-                acc = P::mma(acc, fa[kb], ld_frag<PK>(sEt + (16 * ct + m) * LDT + 32 * kb + 8 * kg));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sW[(16 * R + 4 * kg + i) * LDK + 16 * ct + m] = P::from_f32(-acc[i]);
-        }
-    }
-    // X -> workspace, fragment-native [64][64].
-    for (int task = tid; task < 8 * 64; task += 256) {
-        const int blk = task >> 6, L = task & 63, mt = blk >> 1, kt = blk & 1;
-        const float *src = sX + (16 * mt + (L & 15)) * LDF + 32 * kt + 8 * (L >> 4);
-        float xs[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xs[j] = src[j];
-        st_frag<PK>(ws + TL::X + fn_block(mt, kt, 64) + 8 * L, pack_frag<PK>(xs));
-    }
-    if (tid < KP) {
-        const float tot = sT[0][tid] + sT[1][tid] + sT[2][tid] + sT[3][tid];
-        p.ws_gl[(static_cast<int64_t>(gc) * H + h) * KP + tid] = expf(tot);
-    }
-    __syncthreads();
-    // -W -> workspace, fragment-native [64][KP].
-    for (int task = tid; task < 4 * NKS * 64; task += 256) {
-        const int blk = task >> 6, L = task & 63, mt = blk / NKS, kt = blk % NKS;
-        const st *src = sW + (16 * mt + (L & 15)) * LDK + 32 * kt + 8 * (L >> 4);
-        st_frag<PK>(ws + TL::WNEG + fn_block(mt, kt, KP) + 8 * L, ld_frag<PK>(src));
+        st_q4<PK>(ws + BL::WN + k16_block(R, ct, KP) + 4 * l, pack4<PK>(-acc[0], -acc[1], -acc[2], -acc[3]));
     }
 }
 
@@ -480,19 +493,18 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(ChunkParams p)
 // Scan: one workgroup per (sequence, head, value slice of BV columns).
 // ---------------------------------------------------------------------------
 template <PrecKind PK, int KP, int BV, typename TI>
-__global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkParams p, int NVB, int NP)
+__global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB, int NP)
 {
     using P = Prec<PK>;
     using st = typename P::st;
-    using TL = TileLayout<KP>;
-    constexpr int NKS = KP / 32, NCT = BV / 16, NRT = KP / 16;
-    constexpr int NS = NRT * NCT, NSW = (NS + 3) / 4;
-    constexpr int LDS_ = KP + 8;
-    constexpr int LDZ = 64 + 8;
-    __shared__ __align__(16) st sSt[BV * LDS_];
-    __shared__ __align__(16) st sZt[BV * LDZ];
-    __shared__ __align__(16) st sUt[BV * LDZ];
-    __shared__ float sGl[KP];
+    using BL = Blob<PK, KP>;
+    using Q = Q4<PK>;
+    constexpr bool DB = PK != PrecKind::F32;  // double-buffer the blob (fits only for 16-bit)
+    constexpr int NBUF = DB ? 2 : 1;
+    constexpr int NKT = KP / 16, NKS = KP / 32, NCT = BV / 16;
+    constexpr int U16 = static_cast<int>(BL::BYTES / 16);
+    constexpr int PF = (U16 + 255) / 256;
+    __shared__ __align__(16) st sB[NBUF][BL::SIZE];
 
     // XCD-aware order: all value slices of a (sequence, head) pair share
     // blockIdx % 8, hence one XCD and one L2.
@@ -503,9 +515,15 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkParams p, int NVB,
     if (pair >= NP) return;
     const int H = p.H, K = p.K, V = p.V;
     const int n = pair / H, h = pair % H;
-    const int v0 = vs * BV;
 
+    // Waves 0..3 compute (wave c owns value columns 16c..16c+15 of the
+    // slice); waves 4..7 only move the per-chunk blobs from HBM to LDS.
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, m = l & 15, kg = l >> 4;
+    const bool copier = wv >= 4;
+    const int ctid = tid - 256;
+    const bool active = wv < NCT;
+    const int col = vs * BV + 16 * wv + m;
+    const bool col_ok = active && col < V;
     int64_t bos, len;
     const int gc0 = seq_chunk_base(p, n, bos, len);
     const int nch = static_cast<int>((len + kChunk - 1) / kChunk);
@@ -513,124 +531,154 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkParams p, int NVB,
     const TI *vp = static_cast<const TI *>(p.v);
     const TI *wp = static_cast<const TI *>(p.w);
     TI *op = static_cast<TI *>(p.o);
+    const st *wsb = static_cast<const st *>(p.ws);
+    auto blob = [&](int gci) {
+        return reinterpret_cast<const uint4 *>(wsb + (static_cast<int64_t>(gci) * H + h) * BL::SIZE);
+    };
+    auto copy_blob = [&](int gci, int buf) {
+        const uint4 *src = blob(gci);
+        uint4 *dst = reinterpret_cast<uint4 *>(sB[buf]);
+        for (int u = ctid; u < U16; u += 256) dst[u] = src[u];
+    };
 
-    f32x4 S[NSW];
+    // State columns of this wave: S[kt] holds rows 16kt + 4kg + i, column col.
+    f32x4 S[NKT];
 #pragma unroll
-    for (int jj = 0; jj < NSW; ++jj) {
-        S[jj] = zero4();
-        const int t = wv + 4 * jj;
-        if (t < NS && p.h0) {
-            const int rt = t / NCT, ct = t % NCT;
+    for (int kt = 0; kt < NKT; ++kt) {
+        S[kt] = zero4();
+        if (p.h0 && col_ok) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int row = 16 * rt + 4 * kg + i, col = v0 + 16 * ct + m;
-                if (row < K && col < V)
-                    S[jj][i] = p.h0[((static_cast<int64_t>(n) * H + h) * K + row) * V + col];
+                const int row = 16 * kt + 4 * kg + i;
+                if (row < K) S[kt][i] = p.h0[((static_cast<int64_t>(n) * H + h) * K + row) * V + col];
             }
         }
     }
+
+    if (copier && nch > 0) copy_blob(gc0, 0);
+    __syncthreads();
 
     for (int jc = 0; jc < nch; ++jc) {
-        const int gci = gc0 + jc;
-        const st *ws = static_cast<const st *>(p.ws_tiles) + (static_cast<int64_t>(gci) * H + h) * TL::SIZE;
-        const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
-        const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
-        const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
-
-        // z = w * v, stored transposed [BV][64].
-        {
-            const int r = tid >> 2;
-            const int cb = (tid & 3) * (BV / 4);
-            const int64_t roff = ((t0 + r) * H + h) * V;
+        const int buf = DB ? (jc & 1) : 0;
+        if (copier) {
+            if constexpr (DB) {
+                // Next chunk's blob into the idle buffer (last read one chunk ago).
+                if (jc + 1 < nch) {
+                    const uint4 *src = blob(gc0 + jc + 1);
+                    uint4 *dst = reinterpret_cast<uint4 *>(sB[buf ^ 1]);
+                    uint4 pf[PF];
 #pragma unroll
-            for (int cc = 0; cc < BV / 4; ++cc) {
-                const int col = v0 + cb + cc;
-                float z = 0.f;
-                if (r < lc && col < V) z = io<TI>::ld(wp, roff + col) * io<TI>::ld(vp, roff + col);
-                sZt[(cb + cc) * LDZ + r] = P::from_f32(z);
-            }
-        }
-        if (tid < KP) sGl[tid] = p.ws_gl[(static_cast<int64_t>(gci) * H + h) * KP + tid];
-        // S^T (storage precision) for the B operand.
+                    for (int u = 0; u < PF; ++u) {
+                        const int idx = ctid + 256 * u;
+                        pf[u] = src[idx < U16 ? idx : U16 - 1];
+                    }
 #pragma unroll
-        for (int jj = 0; jj < NSW; ++jj) {
-            const int t = wv + 4 * jj;
-            if (t < NS) {
-                const int rt = t / NCT, ct = t % NCT;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    sSt[(16 * ct + m) * LDS_ + 16 * rt + 4 * kg + i] = P::from_f32(S[jj][i]);
-            }
-        }
-        __syncthreads();
-
-        // U = X z + (-W) S, rows of block wv; stored transposed [BV][64].
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) {
-            f32x4 acc = zero4();
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-                acc = P::mma(acc, ld_frag<PK>(ws + TL::X + fn_block(wv, kb, 64) + 8 * l),
-                             ld_frag<PK>(sZt + (16 * ct + m) * LDZ + 32 * kb + 8 * kg));
-#pragma unroll
-            for (int s = 0; s < NKS; ++s)
-                acc = P::mma(acc, ld_frag<PK>(ws + TL::WNEG + fn_block(wv, s, KP) + 8 * l),
-                             ld_frag<PK>(sSt + (16 * ct + m) * LDS_ + 32 * s + 8 * kg));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sUt[(16 * ct + m) * LDZ + 16 * wv + 4 * kg + i] = P::from_f32(acc[i]);
-        }
-        __syncthreads();
-
-        // O = Qbar S + Aqk U, rows of block wv.
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) {
-            f32x4 acc = zero4();
-#pragma unroll
-            for (int s = 0; s < NKS; ++s)
-                acc = P::mma(acc, ld_frag<PK>(ws + TL::QBAR + fn_block(wv, s, KP) + 8 * l),
-                             ld_frag<PK>(sSt + (16 * ct + m) * LDS_ + 32 * s + 8 * kg));
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-                acc = P::mma(acc, ld_frag<PK>(ws + TL::AQK + fn_block(wv, kb, 64) + 8 * l),
-                             ld_frag<PK>(sUt + (16 * ct + m) * LDZ + 32 * kb + 8 * kg));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = 16 * wv + 4 * kg + i, col = v0 + 16 * ct + m;
-                if (row < lc && col < V) io<TI>::st(op, ((t0 + row) * H + h) * V + col, acc[i]);
-            }
-        }
-
-        // S <- Diag(exp(G_last)) S + Ktilde^T U.
-#pragma unroll
-        for (int jj = 0; jj < NSW; ++jj) {
-            const int t = wv + 4 * jj;
-            if (t < NS) {
-                const int rt = t / NCT, ct = t % NCT;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) S[jj][i] *= sGl[16 * rt + 4 * kg + i];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-                    S[jj] = P::mma(S[jj], ld_frag<PK>(ws + TL::KT + fn_block(rt, kb, 64) + 8 * l),
-                                   ld_frag<PK>(sUt + (16 * ct + m) * LDZ + 32 * kb + 8 * kg));
-            }
-        }
-        __syncthreads();
-    }
-
-    if (p.ht) {
-#pragma unroll
-        for (int jj = 0; jj < NSW; ++jj) {
-            const int t = wv + 4 * jj;
-            if (t < NS) {
-                const int rt = t / NCT, ct = t % NCT;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int row = 16 * rt + 4 * kg + i, col = v0 + 16 * ct + m;
-                    if (row < K && col < V)
-                        p.ht[((static_cast<int64_t>(n) * H + h) * K + row) * V + col] = S[jj][i];
+                    for (int u = 0; u < PF; ++u) {
+                        const int idx = ctid + 256 * u;
+                        if (idx < U16) dst[idx] = pf[u];
+                    }
                 }
             }
+        } else if (active) {
+            const st *Bk = sB[buf];
+            const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
+            const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
+            const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
+
+            // z = w * v as B operand (contraction over tokens).
+            Q zf[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                float z[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tok = 16 * kt + 4 * kg + i;
+                    z[i] = 0.f;
+                    if (tok < lc && col_ok) {
+                        const int64_t off = ((t0 + tok) * H + h) * V + col;
+                        z[i] = io<TI>::ld(wp, off) * io<TI>::ld(vp, off);
+                    }
+                }
+                zf[kt] = pack4<PK>(z[0], z[1], z[2], z[3]);
+            }
+            Q sf[NKT];
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) sf[kt] = pack4<PK>(S[kt]);
+
+            // U = X z + (-W) S, token block rt.
+            Q uf[4];
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                f32x4 acc = zero4();
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    if (2 * s <= rt)
+                        acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::X + k16_block(rt, 2 * s, 64) + 4 * l),
+                                       ld_q4<PK>(Bk + BL::X + k16_block(rt, 2 * s + 1, 64) + 4 * l),
+                                       zf[2 * s], zf[2 * s + 1]);
+#pragma unroll
+                for (int s = 0; s < NKS; ++s)
+                    acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::WN + k16_block(rt, 2 * s, KP) + 4 * l),
+                                   ld_q4<PK>(Bk + BL::WN + k16_block(rt, 2 * s + 1, KP) + 4 * l),
+                                   sf[2 * s], sf[2 * s + 1]);
+                uf[rt] = pack4<PK>(acc);
+            }
+            // O = Qbar S + Aqk U.
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                f32x4 acc = zero4();
+#pragma unroll
+                for (int s = 0; s < NKS; ++s)
+                    acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::QB + k16_block(rt, 2 * s, KP) + 4 * l),
+                                   ld_q4<PK>(Bk + BL::QB + k16_block(rt, 2 * s + 1, KP) + 4 * l),
+                                   sf[2 * s], sf[2 * s + 1]);
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    if (2 * s <= rt)
+                        acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::AQ + k16_block(rt, 2 * s, 64) + 4 * l),
+                                       ld_q4<PK>(Bk + BL::AQ + k16_block(rt, 2 * s + 1, 64) + 4 * l),
+                                       uf[2 * s], uf[2 * s + 1]);
+                if (col_ok) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tok = 16 * rt + 4 * kg + i;
+                        if (tok < lc) io<TI>::st(op, ((t0 + tok) * H + h) * V + col, acc[i]);
+                    }
+                }
+            }
+            // S <- Diag(exp(G_last)) S + Ktilde^T U.
+            const float *gl = reinterpret_cast<const float *>(Bk + BL::GL);
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) {
+                const float4 gv = *reinterpret_cast<const float4 *>(gl + 16 * kt + 4 * kg);
+                S[kt][0] *= gv.x;
+                S[kt][1] *= gv.y;
+                S[kt][2] *= gv.z;
+                S[kt][3] *= gv.w;
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    S[kt] = mma2<PK>(S[kt], ld_q4<PK>(Bk + BL::KT + k16_block(kt, 2 * s, 64) + 4 * l),
+                                     ld_q4<PK>(Bk + BL::KT + k16_block(kt, 2 * s + 1, 64) + 4 * l),
+                                     uf[2 * s], uf[2 * s + 1]);
+            }
         }
+        __syncthreads();
+        if constexpr (!DB) {
+            if (jc + 1 < nch) {
+                if (copier) copy_blob(gc0 + jc + 1, 0);
+                __syncthreads();
+            }
+        }
+    }
+
+    if (p.ht && col_ok) {
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * kt + 4 * kg + i;
+                if (row < K) p.ht[((static_cast<int64_t>(n) * H + h) * K + row) * V + col] = S[kt][i];
+            }
     }
 }
 
@@ -645,9 +693,15 @@ int64_t count_chunks(int B, int T, const int64_t *cu_host, int num_seqs)
     return c;
 }
 
-size_t storage_bytes(int io_dtype) { return io_dtype == GDN2_DTYPE_F32 ? 4 : 2; }
-
-size_t tile_elems(int KP) { return static_cast<size_t>(192 * KP + 8192); }
+int64_t blob_bytes(int io_dtype, int KP)
+{
+    const bool f32 = io_dtype == GDN2_DTYPE_F32;
+    switch (KP) {
+    case 32: return f32 ? Blob<PrecKind::F32, 32>::BYTES : Blob<PrecKind::BF16, 32>::BYTES;
+    case 64: return f32 ? Blob<PrecKind::F32, 64>::BYTES : Blob<PrecKind::BF16, 64>::BYTES;
+    default: return f32 ? Blob<PrecKind::F32, 128>::BYTES : Blob<PrecKind::BF16, 128>::BYTES;
+    }
+}
 
 template <PrecKind PK, int KP, typename TI, typename TG>
 hipError_t launch_prep(const ChunkParams &p, int total_chunks, hipStream_t stream)
@@ -666,7 +720,7 @@ hipError_t launch_scan(const ChunkParams &p, int BVsel, hipStream_t stream)
     auto go = [&](auto bvtag) {
         constexpr int BV = decltype(bvtag)::value;
         const int NVB = (p.V + BV - 1) / BV;
-        hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI>), dim3(groups * 8 * NVB), dim3(256), 0,
+        hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI>), dim3(groups * 8 * NVB), dim3(512), 0,
                            stream, p, NVB, NP);
     };
     if (BVsel == 16) go(std::integral_constant<int, 16>{});
@@ -703,10 +757,8 @@ size_t chunk_fwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
 {
     (void)V;
     if (K > 128) return 0;
-    const int KP = kp_for(K);
     const int64_t nc = count_chunks(B, T, cu_host, num_seqs);
-    const size_t per = tile_elems(KP) * storage_bytes(io_dtype) + static_cast<size_t>(KP) * 4;
-    return static_cast<size_t>(nc) * H * per;
+    return static_cast<size_t>(nc) * H * static_cast<size_t>(blob_bytes(io_dtype, kp_for(K)));
 }
 
 int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream)
@@ -732,12 +784,8 @@ int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream
     p.nt = (a.T + kChunk - 1) / kChunk;
     p.scale = a.scale;
     p.flags = a.flags;
-    p.vec_ok = (a.K % 8) == 0;
-    const int KP = kp_for(a.K);
-    p.ws_tiles = a.workspace;
-    p.ws_gl = reinterpret_cast<float *>(static_cast<unsigned char *>(a.workspace) +
-                                        static_cast<size_t>(nc) * a.H * tile_elems(KP) *
-                                            storage_bytes(io_dtype));
+    p.vec_ok = (a.K % 4) == 0;
+    p.ws = a.workspace;
     const int total = static_cast<int>(nc);
 
     hipError_t e;
@@ -751,7 +799,7 @@ int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream
         break;
     default:
         // fp16 inputs use bf16 MFMA operands: the factored decay terms reach
-        // exp(+-kDiagSpanLimit/2), far outside the fp16 exponent range.
+        // 2^(+-kDiagSpanLimit2/2), far outside the fp16 exponent range.
         e = g_dtype == GDN2_DTYPE_F32 ? launch_kp<PrecKind::BF16, f16_t, float>(p, total, a.stages, stream)
                                       : launch_kp<PrecKind::BF16, f16_t, f16_t>(p, total, a.stages, stream);
         break;

@@ -250,6 +250,147 @@ __global__ __launch_bounds__(256) void recurrent_fwd_kernel(RecurrentParams p)
     }
 }
 
+// Decode step (T = 1, no cu_seqlens) specialised for d_k = d_v = 128.
+// Same arithmetic and thread mapping as recurrent_fwd_kernel, but each
+// workgroup walks two consecutive (sequence, value head) slabs and issues the
+// second slab's 64 KB of state loads before computing the first, so state
+// reads of one slab overlap the state writes of the other.  A decode step is
+// one pass over the whole state, so this overlap is what separates it from a
+// plain read-then-write of 2 x 64 KB per workgroup.
+template <typename TI, typename TG>
+__global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int nslabs)
+{
+    constexpr int KD = 128, VD = 128, TPR = 32, RG = 8, NR = KD / RG, SLABS = 2;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1), wid = tid / kWave;
+    const int cq = tid % TPR, rg = tid / TPR;
+    const int col = 4 * cq;
+
+    __shared__ float s_q[KD], s_k[KD], s_e[KD], s_a[KD];
+    __shared__ float s_part[4][4];
+    __shared__ float4 s_red[4][2][TPR];
+
+    const TI *q = static_cast<const TI *>(p.q);
+    const TI *k = static_cast<const TI *>(p.k);
+    const TI *v = static_cast<const TI *>(p.v);
+    const TI *b = static_cast<const TI *>(p.b);
+    const TI *w = static_cast<const TI *>(p.w);
+    const TG *g = static_cast<const TG *>(p.g);
+    TI *o = static_cast<TI *>(p.o);
+    const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
+    const bool gate = (p.flags & GDN2_FLAG_GATE_IN_KERNEL) != 0;
+    const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
+
+    float4 st[SLABS][NR];
+    const int slab0 = blockIdx.x * SLABS;
+    auto load_state = [&](float4 (&dst)[NR], int slab) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            dst[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (p.h0)
+                dst[i] = *reinterpret_cast<const float4 *>(p.h0 + static_cast<int64_t>(slab) * KD * VD +
+                                                           (rg + i * RG) * VD + col);
+        }
+    };
+    load_state(st[0], slab0);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+        const int slab = slab0 + s;
+        if (slab >= nslabs) break;
+        if (s + 1 < SLABS && slab + 1 < nslabs) load_state(st[s + 1], slab + 1);
+        const int n = slab / p.HV, hv = slab % p.HV;
+        const int h = hv / (p.HV / p.H);
+        const int64_t qk_off = (static_cast<int64_t>(n) * p.H + h) * KD;
+        const int64_t gb_off = static_cast<int64_t>(slab) * KD;
+        const int64_t vw_off = static_cast<int64_t>(slab) * VD;
+
+        float qv = 0.f, kv = 0.f, gv = 0.f, bv = 0.f;
+        if (tid < KD) {
+            qv = io<TI>::ld(q, qk_off + tid);
+            kv = io<TI>::ld(k, qk_off + tid);
+            gv = io<TG>::ld(g, gb_off + tid);
+            bv = io<TI>::ld(b, gb_off + tid);
+        }
+        const float4 vv = vec4io<TI>::ld(v, vw_off + col);
+        const float4 ww = vec4io<TI>::ld(w, vw_off + col);
+        const float rq = wave_sum(qv * qv), rk = wave_sum(kv * kv), rqk = wave_sum(qv * kv);
+        if (lane == 0) {
+            s_part[wid][0] = rq;
+            s_part[wid][1] = rk;
+            s_part[wid][2] = rqk;
+        }
+        __syncthreads();
+        float qq = 0.f, kk = 0.f, qk = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qq += s_part[i][0];
+            kk += s_part[i][1];
+            qk += s_part[i][2];
+        }
+        const float invq = l2 ? 1.0f / fmaxf(sqrtf(qq), 1e-6f) : 1.0f;
+        const float invk = l2 ? 1.0f / fmaxf(sqrtf(kk), 1e-6f) : 1.0f;
+        if (tid < KD) {
+            const float kn = kv * invk;
+            s_q[tid] = qv * invq * p.scale;
+            s_k[tid] = kn;
+            s_e[tid] = bv * kn;
+            float gk = gv;
+            if (gate) {
+                const float db = p.dt_bias ? p.dt_bias[hv * KD + tid] : 0.0f;
+                gk = gate_activation(gv, p.A_log[hv], db, use_lb, p.lower_bound);
+            }
+            s_a[tid] = expf(gk);
+        }
+        const float kq = qk * invq * invk * p.scale;
+        __syncthreads();
+
+        float4 pr = make_float4(0.f, 0.f, 0.f, 0.f), po = pr;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int r = rg + i * RG;
+            const float a = s_a[r];
+            st[s][i].x *= a;
+            st[s][i].y *= a;
+            st[s][i].z *= a;
+            st[s][i].w *= a;
+            pr = f4_fma(st[s][i], s_e[r], pr);
+            po = f4_fma(st[s][i], s_q[r], po);
+        }
+        {
+            const float4 a = shfl_xor4(pr, 32), c = shfl_xor4(po, 32);
+            pr.x += a.x; pr.y += a.y; pr.z += a.z; pr.w += a.w;
+            po.x += c.x; po.y += c.y; po.z += c.z; po.w += c.w;
+        }
+        if (lane < TPR) {
+            s_red[wid][0][cq] = pr;
+            s_red[wid][1][cq] = po;
+        }
+        __syncthreads();
+        float4 R = s_red[0][0][cq], PO = s_red[0][1][cq];
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+            const float4 a = s_red[i][0][cq], c = s_red[i][1][cq];
+            R.x += a.x; R.y += a.y; R.z += a.z; R.w += a.w;
+            PO.x += c.x; PO.y += c.y; PO.z += c.z; PO.w += c.w;
+        }
+        const float4 u = make_float4(ww.x * vv.x - R.x, ww.y * vv.y - R.y, ww.z * vv.z - R.z,
+                                     ww.w * vv.w - R.w);
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int r = rg + i * RG;
+            const float kr = s_k[r];
+            st[s][i].x = fmaf(kr, u.x, st[s][i].x);
+            st[s][i].y = fmaf(kr, u.y, st[s][i].y);
+            st[s][i].z = fmaf(kr, u.z, st[s][i].z);
+            st[s][i].w = fmaf(kr, u.w, st[s][i].w);
+            if (p.ht)
+                *reinterpret_cast<float4 *>(p.ht + static_cast<int64_t>(slab) * KD * VD + r * VD + col) = st[s][i];
+        }
+        if (rg == 0) vec4io<TI>::st(o, vw_off + col, f4_fma(u, kq, PO));
+        __syncthreads();
+    }
+}
+
 template <typename TI, typename TG, int TPR>
 static hipError_t launch_nr(const RecurrentParams &p, int N, hipStream_t stream)
 {
@@ -275,6 +416,12 @@ static hipError_t launch_nr(const RecurrentParams &p, int N, hipStream_t stream)
 template <typename TI, typename TG>
 static hipError_t launch_tpr(const RecurrentParams &p, int N, hipStream_t stream)
 {
+    if (p.T == 1 && !p.cu_seqlens && p.K == 128 && p.V == 128) {
+        const int nslabs = N * p.HV;
+        hipLaunchKernelGGL((decode_step_kernel<TI, TG>), dim3((nslabs + 1) / 2), dim3(256), 0, stream,
+                           p, nslabs);
+        return hipGetLastError();
+    }
     // Narrowest row that still covers V with float4 lanes, capped at 128 columns.
     if (p.V <= 16) return launch_nr<TI, TG, 4>(p, N, stream);
     if (p.V <= 32) return launch_nr<TI, TG, 8>(p, N, stream);
