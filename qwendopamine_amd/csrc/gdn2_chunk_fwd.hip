@@ -159,14 +159,22 @@ __device__ __forceinline__ void load4(const T *base, int64_t off, int c0, int K,
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Inclusive prefix sum over the 16 lanes m of a 16-lane row.
-__device__ __forceinline__ float row16_scan(float x, int m)
+// Inclusive prefix sum over the 16 lanes of each DPP row (lanes 16r..16r+15),
+// Hillis-Steele with row_shr:1,2,4,8; lanes shifted in from outside the row
+// read 0 (bound_ctrl), so no masking is needed.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_shr(float x)
 {
-#pragma unroll
-    for (int d = 1; d < 16; d <<= 1) {
-        const float y = __shfl_up(x, d, 16);
-        if (m >= d) x += y;
-    }
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                                 0xf, 0xf, true));
+}
+
+__device__ __forceinline__ float row16_scan(float x)
+{
+    x += dpp_row_shr<0x111>(x);
+    x += dpp_row_shr<0x112>(x);
+    x += dpp_row_shr<0x114>(x);
+    x += dpp_row_shr<0x118>(x);
     return x;
 }
 
@@ -261,7 +269,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkParams p)
                 const float db = p.dt_bias ? p.dt_bias[h * K + c] : 0.0f;
                 gg = gate_activation(gg, a_log, db, use_lb, p.lower_bound);
             }
-            gv[kt][i] = row16_scan(gg * kLog2e, m);  // G (log2) relative to block start
+            gv[kt][i] = row16_scan(gg * kLog2e);  // G (log2) relative to block start
         }
     bool wide = false;
     if (m == 15) {
@@ -505,6 +513,8 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     constexpr int U16 = static_cast<int>(BL::BYTES / 16);
     constexpr int PF = (U16 + 255) / 256;
     __shared__ __align__(16) st sB[NBUF][BL::SIZE];
+    // z = w * v of the chunk as K16 B operands: block (token tile kt, column tile c).
+    __shared__ __align__(16) st sZ[NBUF][16 * 256];
 
     // XCD-aware order: all value slices of a (sequence, head) pair share
     // blockIdx % 8, hence one XCD and one L2.
@@ -540,6 +550,40 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         uint4 *dst = reinterpret_cast<uint4 *>(sB[buf]);
         for (int u = ctid; u < U16; u += 256) dst[u] = src[u];
     };
+    // Copy waves: z = w * v of chunk jc for this value slice, scattered into
+    // the K16 B-operand order the compute waves read (zero past the sequence
+    // end and past V).
+    const int v0 = vs * BV;
+    auto stage_z = [&](int jc, int buf) {
+        const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
+        const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
+        const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
+        st *dst = sZ[buf];
+        for (int task = ctid; task < kChunk * (BV / 4); task += 256) {
+            const int tok = task / (BV / 4), c4 = 4 * (task % (BV / 4));
+            float z[4] = {0.f, 0.f, 0.f, 0.f};
+            if (tok < lc) {
+                const int64_t off = ((t0 + tok) * H + h) * V + v0 + c4;
+                if ((V & 3) == 0 && v0 + c4 + 4 <= V) {
+                    float vv[4], ww[4];
+                    load4<TI>(vp, off, 0, 4, true, 1, vv);
+                    load4<TI>(wp, off, 0, 4, true, 1, ww);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) z[i] = vv[i] * ww[i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (v0 + c4 + i < V) z[i] = io<TI>::ld(vp, off + i) * io<TI>::ld(wp, off + i);
+                }
+            }
+            const int kt = tok >> 4, kgz = (tok & 15) >> 2, iz = tok & 3;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int cl = c4 + i, ct = cl >> 4, nz = cl & 15;
+                dst[(kt * 4 + ct) * 256 + (nz + 16 * kgz) * 4 + iz] = P::from_f32(z[i]);
+            }
+        }
+    };
 
     // State columns of this wave: S[kt] holds rows 16kt + 4kg + i, column col.
     f32x4 S[NKT];
@@ -555,7 +599,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         }
     }
 
-    if (copier && nch > 0) copy_blob(gc0, 0);
+    if (copier && nch > 0) {
+        copy_blob(gc0, 0);
+        stage_z(0, 0);
+    }
     __syncthreads();
 
     for (int jc = 0; jc < nch; ++jc) {
@@ -572,6 +619,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                         const int idx = ctid + 256 * u;
                         pf[u] = src[idx < U16 ? idx : U16 - 1];
                     }
+                    stage_z(jc + 1, buf ^ 1);
 #pragma unroll
                     for (int u = 0; u < PF; ++u) {
                         const int idx = ctid + 256 * u;
@@ -585,22 +633,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
             const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
 
-            // z = w * v as B operand (contraction over tokens).
+            // z = w * v as B operand (contraction over tokens), staged in LDS.
             Q zf[4];
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                float z[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int tok = 16 * kt + 4 * kg + i;
-                    z[i] = 0.f;
-                    if (tok < lc && col_ok) {
-                        const int64_t off = ((t0 + tok) * H + h) * V + col;
-                        z[i] = io<TI>::ld(wp, off) * io<TI>::ld(vp, off);
-                    }
-                }
-                zf[kt] = pack4<PK>(z[0], z[1], z[2], z[3]);
-            }
+            for (int kt = 0; kt < 4; ++kt) zf[kt] = ld_q4<PK>(sZ[buf] + (kt * 4 + wv) * 256 + 4 * l);
             Q sf[NKT];
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) sf[kt] = pack4<PK>(S[kt]);
@@ -665,7 +701,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         __syncthreads();
         if constexpr (!DB) {
             if (jc + 1 < nch) {
-                if (copier) copy_blob(gc0 + jc + 1, 0);
+                if (copier) {
+                    copy_blob(gc0 + jc + 1, 0);
+                    stage_z(jc + 1, 0);
+                }
                 __syncthreads();
             }
         }
