@@ -47,6 +47,10 @@
 
 namespace gdn2 {
 
+// Native 16-byte vector: loads and stores of it stay single instructions and
+// arrays of it stay in registers (struct copies of uint4 lower to memcpy).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 namespace {
 
 constexpr int kChunk = 64;
@@ -543,44 +547,69 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     TI *op = static_cast<TI *>(p.o);
     const st *wsb = static_cast<const st *>(p.ws);
     auto blob = [&](int gci) {
-        return reinterpret_cast<const uint4 *>(wsb + (static_cast<int64_t>(gci) * H + h) * BL::SIZE);
+        return reinterpret_cast<const u32x4 *>(wsb + (static_cast<int64_t>(gci) * H + h) * BL::SIZE);
     };
-    auto copy_blob = [&](int gci, int buf) {
-        const uint4 *src = blob(gci);
-        uint4 *dst = reinterpret_cast<uint4 *>(sB[buf]);
+    auto copy_blob = [&](int gci, int buf) __attribute__((always_inline)) {
+        const u32x4 *src = blob(gci);
+        u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf]);
         for (int u = ctid; u < U16; u += 256) dst[u] = src[u];
     };
-    // Copy waves: z = w * v of chunk jc for this value slice, scattered into
-    // the K16 B-operand order the compute waves read (zero past the sequence
-    // end and past V).
+    // Copy waves: z = w * v of chunk jc for this value slice, in the K16
+    // B-operand order the compute waves read (zero past the sequence end and
+    // past V).  issue_z requests the raw rows (16-byte loads); land_z forms z
+    // and scatters it into LDS, so the two can sit a chunk apart.
     const int v0 = vs * BV;
-    auto stage_z = [&](int jc, int buf) {
-        const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
+    constexpr int EPV = 16 / static_cast<int>(sizeof(TI));  // values per 16-byte load
+    constexpr int ZT = kChunk * BV / EPV;                    // loads per tensor per chunk
+    constexpr int NZT = (ZT + 255) / 256;
+    const bool zvec = (V % EPV) == 0;
+    struct ZRaw {
+        u32x4 v[NZT], w[NZT];
+    };
+    auto chunk_rows = [&](int jc, int64_t &t0, int &lc) __attribute__((always_inline)) {
+        t0 = bos + static_cast<int64_t>(jc) * kChunk;
         const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
-        const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
+        lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
+    };
+    auto issue_z = [&](ZRaw &r, int jc) __attribute__((always_inline)) {
+        int64_t t0;
+        int lc;
+        chunk_rows(jc, t0, lc);
+#pragma unroll
+        for (int a = 0; a < NZT; ++a) {
+            const int task = ctid + 256 * a;
+            const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
+            const bool ok = task < ZT && tok < lc && zvec && v0 + c + EPV <= V;
+            const int64_t off = ((t0 + tok) * H + h) * V + v0 + c;
+            r.v[a] = ok ? *reinterpret_cast<const u32x4 *>(vp + off) : u32x4{0, 0, 0, 0};
+            r.w[a] = ok ? *reinterpret_cast<const u32x4 *>(wp + off) : u32x4{0, 0, 0, 0};
+        }
+    };
+    auto land_z = [&](const ZRaw &r, int jc, int buf) __attribute__((always_inline)) {
+        int64_t t0;
+        int lc;
+        chunk_rows(jc, t0, lc);
         st *dst = sZ[buf];
-        for (int task = ctid; task < kChunk * (BV / 4); task += 256) {
-            const int tok = task / (BV / 4), c4 = 4 * (task % (BV / 4));
-            float z[4] = {0.f, 0.f, 0.f, 0.f};
-            if (tok < lc) {
-                const int64_t off = ((t0 + tok) * H + h) * V + v0 + c4;
-                if ((V & 3) == 0 && v0 + c4 + 4 <= V) {
-                    float vv[4], ww[4];
-                    load4<TI>(vp, off, 0, 4, true, 1, vv);
-                    load4<TI>(wp, off, 0, 4, true, 1, ww);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) z[i] = vv[i] * ww[i];
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (v0 + c4 + i < V) z[i] = io<TI>::ld(vp, off + i) * io<TI>::ld(wp, off + i);
-                }
-            }
+        for (int a = 0; a < NZT; ++a) {
+            const int task = ctid + 256 * a;
+            if (task >= ZT) continue;
+            const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
+            const TI *rv = reinterpret_cast<const TI *>(&r.v[a]);
+            const TI *rw = reinterpret_cast<const TI *>(&r.w[a]);
+            const bool ok = tok < lc && zvec && v0 + c + EPV <= V;
             const int kt = tok >> 4, kgz = (tok & 15) >> 2, iz = tok & 3;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int cl = c4 + i, ct = cl >> 4, nz = cl & 15;
-                dst[(kt * 4 + ct) * 256 + (nz + 16 * kgz) * 4 + iz] = P::from_f32(z[i]);
+            for (int e = 0; e < EPV; ++e) {
+                float z = 0.f;
+                if (ok) {
+                    z = io<TI>::ld(rv, e) * io<TI>::ld(rw, e);
+                } else if (tok < lc && v0 + c + e < V) {
+                    const int64_t off = ((t0 + tok) * H + h) * V + v0 + c + e;
+                    z = io<TI>::ld(vp, off) * io<TI>::ld(wp, off);
+                }
+                const int cl = c + e, ct = cl >> 4, nz = cl & 15;
+                dst[(kt * 4 + ct) * 256 + (nz + 16 * kgz) * 4 + iz] = P::from_f32(z);
             }
         }
     };
@@ -599,35 +628,82 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         }
     }
 
-    if (copier && nch > 0) {
-        copy_blob(gc0, 0);
-        stage_z(0, 0);
-    }
-    __syncthreads();
-
-    for (int jc = 0; jc < nch; ++jc) {
-        const int buf = DB ? (jc & 1) : 0;
-        if (copier) {
-            if constexpr (DB) {
-                // Next chunk's blob into the idle buffer (last read one chunk ago).
+    // Copy waves (4..7) and compute waves (0..3) run separate loops with the
+    // same barrier schedule -- one barrier after the prologue, one per chunk,
+    // and in the single-buffer case one more per reload -- so the copy waves'
+    // prefetch registers never overlap the compute waves' live ranges.
+    if (copier) {
+        ZRaw zA, zB;
+        if (nch > 0) {
+            copy_blob(gc0, 0);
+            issue_z(zA, 0);
+            land_z(zA, 0, 0);
+        }
+        if constexpr (DB) {
+            u32x4 pA[PF], pB[PF];
+            auto issue = [&](u32x4 (&dst)[PF], int gci) __attribute__((always_inline)) {
+                const u32x4 *src = blob(gci);
+#pragma unroll
+                for (int u = 0; u < PF; ++u) {
+                    const int idx = ctid + 256 * u;
+                    dst[u] = src[idx < U16 ? idx : U16 - 1];
+                }
+            };
+            auto land = [&](const u32x4 (&src)[PF], int buf) __attribute__((always_inline)) {
+                u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf]);
+#pragma unroll
+                for (int u = 0; u < PF; ++u) {
+                    const int idx = ctid + 256 * u;
+                    if (idx < U16) dst[idx] = src[u];
+                }
+            };
+            if (nch > 1) {
+                issue(pA, gc0 + 1);
+                issue_z(zA, 1);
+            }
+            __syncthreads();
+            // Step jc: the blob and rows of chunk jc+1 (requested one step
+            // earlier) land in the idle buffer while chunk jc+2 is requested,
+            // so each request has two chunks of compute to arrive.  The loop
+            // is unrolled by two so that pA / pB swap roles at compile time.
+            for (int jc = 0; jc < nch; jc += 2) {
+                if (jc + 2 < nch) {
+                    issue(pB, gc0 + jc + 2);
+                    issue_z(zB, jc + 2);
+                }
                 if (jc + 1 < nch) {
-                    const uint4 *src = blob(gc0 + jc + 1);
-                    uint4 *dst = reinterpret_cast<uint4 *>(sB[buf ^ 1]);
-                    uint4 pf[PF];
-#pragma unroll
-                    for (int u = 0; u < PF; ++u) {
-                        const int idx = ctid + 256 * u;
-                        pf[u] = src[idx < U16 ? idx : U16 - 1];
-                    }
-                    stage_z(jc + 1, buf ^ 1);
-#pragma unroll
-                    for (int u = 0; u < PF; ++u) {
-                        const int idx = ctid + 256 * u;
-                        if (idx < U16) dst[idx] = pf[u];
-                    }
+                    land_z(zA, jc + 1, 1);
+                    land(pA, 1);
+                }
+                __syncthreads();
+                if (jc + 1 >= nch) break;
+                if (jc + 3 < nch) {
+                    issue(pA, gc0 + jc + 3);
+                    issue_z(zA, jc + 3);
+                }
+                if (jc + 2 < nch) {
+                    land_z(zB, jc + 2, 0);
+                    land(pB, 0);
+                }
+                __syncthreads();
+            }
+        } else {
+            __syncthreads();
+            for (int jc = 0; jc < nch; ++jc) {
+                __syncthreads();
+                if (jc + 1 < nch) {
+                    copy_blob(gc0 + jc + 1, 0);
+                    issue_z(zA, jc + 1);
+                    land_z(zA, jc + 1, 0);
+                    __syncthreads();
                 }
             }
-        } else if (active) {
+        }
+    } else {
+        __syncthreads();
+        for (int jc = 0; jc < nch; ++jc) {
+            const int buf = DB ? (jc & 1) : 0;
+            if (active) {
             const st *Bk = sB[buf];
             const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
             const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
@@ -697,15 +773,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                                      ld_q4<PK>(Bk + BL::KT + k16_block(kt, 2 * s + 1, 64) + 4 * l),
                                      uf[2 * s], uf[2 * s + 1]);
             }
-        }
-        __syncthreads();
-        if constexpr (!DB) {
-            if (jc + 1 < nch) {
-                if (copier) {
-                    copy_blob(gc0 + jc + 1, 0);
-                    stage_z(jc + 1, 0);
-                }
-                __syncthreads();
+            }
+            __syncthreads();
+            if constexpr (!DB) {
+                if (jc + 1 < nch) __syncthreads();
             }
         }
     }
