@@ -115,7 +115,7 @@ def bench_prefill(torch, nat, dev, steps, warmup):
                 inputs=(q, k, v, g, b, w))
 
 
-def bench_decode(torch, nat, dev, reps=3):
+def bench_decode(torch, nat, dev, reps=3, eager_steps=0):
     N, H, K, V, S = (DECODE[x] for x in ("N", "H", "K", "V", "steps"))
     F = torch.nn.functional
     gen = torch.Generator(device=dev).manual_seed(2)
@@ -143,6 +143,12 @@ def bench_decode(torch, nat, dev, reps=3):
             N, 1, H, H, K, V, scale, nat.FLAG_L2NORM_QK, sh)
         nat.check(st, "gdn2_recurrent_fwd")
 
+    if eager_steps:
+        sh = torch.cuda.current_stream(dev).cuda_stream
+        for i in range(eager_steps):
+            step(i, sh)
+        torch.cuda.synchronize(dev)
+        return None
     side = torch.cuda.Stream(dev)
     side.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(side):
@@ -177,6 +183,34 @@ def bench_decode(torch, nat, dev, reps=3):
                 frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4),
                 config={"workload": "C2 decode N64 H16 K128 V128, fp32 state in place, 1024 steps "
                                     "in one HIP graph", "dtype": "bf16 in / fp32 state"})
+
+
+def traffic_probe(torch, nat, dev):
+    """Short run for the rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE): first a
+    256 MiB device-to-device copy whose bytes are known, which calibrates the
+    counters, then two prefill ops and eight eager decode steps."""
+    a = torch.empty(64 << 20, dtype=torch.float32, device=dev).uniform_()
+    c = torch.empty_like(a)
+    c.copy_(a)
+    torch.cuda.synchronize(dev)
+    del a, c
+    bench_prefill(torch, nat, dev, steps=2, warmup=0)
+    bench_decode(torch, nat, dev, eager_steps=8)
+    print("traffic probe done", flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per prefill op from the committed counter summary (None if absent)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "chunk_fwd_C1_traffic.md")
+    try:
+        with open(path) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_op:"):
+                    return int(ln.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
 
 
 def cpu_baseline(torch, inputs, max_threads=16, reps=3):
@@ -217,6 +251,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="short run for rocprofv3 counter passes; prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (--gpus 1); multi-GPU sharding of the "
@@ -231,6 +267,9 @@ def main() -> int:
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda", 0)
+    if args.traffic_probe:
+        traffic_probe(torch, nat, dev)
+        return 0
     P = PREFILL
     res = bench_prefill(torch, nat, dev, args.steps, args.warmup)
     B, T, H, K, V, C = P["B"], P["T"], P["H"], P["K"], P["V"], P["C"]
@@ -263,7 +302,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "algorithmic_bytes": nbytes,
             "op_ms": round(t_op_ms, 4),
             "kernels_ms": {"chunk_prep_kernel": round(res["t_prep_ms"], 4),
