@@ -26,6 +26,12 @@ and chunks).  Functions and the reference code they restate:
                            (the gradients ``ChunkGDN2Function.backward`` returns,
                            ``chunk_gdn2.py:2461-2547``: dq, dk, dv, dg, db, dw,
                            dh0), including the L2-norm and scale chain rule.
+* ``chunk_vjp``         -- the same derivative computed chunk by chunk (the
+                           reverse state scan plus per-chunk products of the
+                           reference's chunk backward, ``chunk_gdn2.py:2170-2325``:
+                           recompute, dAv, dhu, wy_dqkg, intra, reverse cumsum
+                           of dg), restated with relative decays.  It is the
+                           algebra the HIP backward kernels implement.
 * ``make_inputs``       -- the seeded input recipe of BASELINE configs 0-4.
 
 How each function is pinned (tests/test_oracle.py):
@@ -37,6 +43,7 @@ How each function is pinned (tests/test_oracle.py):
                  zero-padding invariance.
   chunk_fwd      equals recurrent_fwd for chunk sizes 1..T incl. ragged tails.
   recurrent_vjp  central finite differences of recurrent_fwd in float64.
+  chunk_vjp      equals recurrent_vjp for several chunk sizes incl. ragged tails.
   make_inputs    distribution moments and l2-norms (cheap sanity only; it is a
                  recipe, not arithmetic of the reference).
 """
@@ -50,6 +57,7 @@ __all__ = [
     "recurrent_fwd",
     "chunk_fwd",
     "recurrent_vjp",
+    "chunk_vjp",
     "make_inputs",
     "rel_l2",
 ]
@@ -299,6 +307,105 @@ def recurrent_vjp(
                 dk[bi, t, h] = dk_t
                 dg[bi, t, h] = (dSt * Sdec[t]).sum(-1)
                 dS = np.exp(g[bi, t, h])[:, None] * dSt
+            dh0[bi, h] = dS
+    dq = dq * scale
+    if use_qk_l2norm_in_kernel:
+        dq = _l2norm_vjp(q_raw, dq)
+        dk = _l2norm_vjp(k_raw, dk)
+    return dq, dk, dv, dg, db, dw, dh0
+
+
+def chunk_vjp(
+    q,
+    k,
+    v,
+    g,
+    b,
+    w,
+    do,
+    dht=None,
+    initial_state=None,
+    scale=None,
+    use_qk_l2norm_in_kernel=True,
+    chunk_size=64,
+):
+    r"""Chunkwise reverse-mode derivative of ``chunk_fwd`` (no varlen, H == HV).
+
+    Returns ``(dq, dk, dv, dg, db, dw, dh0)`` like ``recurrent_vjp``.  For one
+    chunk (notation of ``chunk_fwd``; ``Qb = q*exp(G)``, ``Eb = e*exp(G)``,
+    ``Kt = k*exp(G_last - G)``) with ``dS1`` the gradient of its end state:
+
+        dU  = Aqk^T dO + Kt dS1,      dY = X^T dU     (dz = dY: dv = dY*w, dw = dY*v)
+        dQb = dO S0^T,  dEb = -dY S0^T,  dKt = U dS1^T
+        dA  = tril(dO U^T),  dL = strict_tril(-dY U^T)
+        dq_r = exp(G_r) dQb_r + sum_j dA[r,j] k_j exp(G_r - G_j)
+        de_r = exp(G_r) dEb_r + sum_j dL[r,j] k_j exp(G_r - G_j)
+        dk_j = exp(G_last - G_j) dKt_j + sum_r (dA[r,j] q_r + dL[r,j] e_r) exp(G_r - G_j)
+        dG_r = q_r dq_r + e_r de_r - k_r dk_r,   dG_last += rowsum(dS1 * S1)
+        dg   = reverse in-chunk cumulative sum of dG
+        dS0  = Qb^T dO + Diag(exp(G_last)) dS1 - Eb^T dY
+
+    ``rowsum(dS1 * S1)`` is the whole derivative of ``S1`` with respect to
+    ``G_last`` at fixed ``U`` (``S1 = exp(G_last) (S0 + sum_j exp(-G_j) k_j u_j^T)``).
+    """
+    B, T, H, K = np.shape(q)
+    V = np.shape(v)[-1]
+    q_raw = np.asarray(q, dtype=np.float64)
+    k_raw = np.asarray(k, dtype=np.float64)
+    if scale is None:
+        scale = K ** -0.5
+    qs, kn, v, g, b, w = _prep(q, k, v, g, b, w, scale, use_qk_l2norm_in_kernel)
+    do = np.asarray(do, dtype=np.float64)
+    dq, dk, dv = np.zeros_like(qs), np.zeros_like(kn), np.zeros_like(v)
+    dg, db, dw = np.zeros_like(g), np.zeros_like(b), np.zeros_like(w)
+    dh0 = np.zeros((B, H, K, V))
+    for bi in range(B):
+        for h in range(H):
+            S = np.zeros((K, V)) if initial_state is None else np.array(initial_state[bi, h], dtype=np.float64)
+            bounds = [(t0, min(T, t0 + chunk_size)) for t0 in range(0, T, chunk_size)]
+            saved = []
+            for t0, t1 in bounds:
+                qc, kc = qs[bi, t0:t1, h], kn[bi, t0:t1, h]
+                ec = b[bi, t0:t1, h] * kc
+                zc = w[bi, t0:t1, h] * v[bi, t0:t1, h]
+                G = np.cumsum(g[bi, t0:t1, h], axis=0)
+                C = t1 - t0
+                causal = np.tril(np.ones((C, C)))
+                expo = np.where(causal[:, :, None] > 0, G[:, None, :] - G[None, :, :], -np.inf)
+                rel = np.exp(expo)
+                Aqk = np.einsum("rd,id,rid->ri", qc, kc, rel)
+                L = np.einsum("rd,id,rid->ri", ec, kc, rel) * np.tril(np.ones((C, C)), -1)
+                X = np.linalg.inv(np.eye(C) + L)
+                Eb = ec * np.exp(G)
+                Kt = kc * np.exp(G[-1][None, :] - G)
+                U = X @ (zc - Eb @ S)
+                saved.append((qc, kc, ec, G, rel, Aqk, X, Eb, Kt, S, U))
+                S = np.exp(G[-1])[:, None] * S + Kt.T @ U
+            ends = [saved[i + 1][9] for i in range(len(saved) - 1)] + [S]
+            dS = np.zeros((K, V)) if dht is None else np.array(dht[bi, h], dtype=np.float64)
+            for ci in range(len(bounds) - 1, -1, -1):
+                t0, t1 = bounds[ci]
+                qc, kc, ec, G, rel, Aqk, X, Eb, Kt, S0, U = saved[ci]
+                dO = do[bi, t0:t1, h]
+                dU = Aqk.T @ dO + Kt @ dS
+                dY = X.T @ dU
+                dv[bi, t0:t1, h] = dY * w[bi, t0:t1, h]
+                dw[bi, t0:t1, h] = dY * v[bi, t0:t1, h]
+                dA = np.tril(dO @ U.T)
+                dL = np.tril(-dY @ U.T, -1)
+                eG = np.exp(G)
+                dqc = eG * (dO @ S0.T) + np.einsum("ri,id,rid->rd", dA, kc, rel)
+                de = eG * (-dY @ S0.T) + np.einsum("ri,id,rid->rd", dL, kc, rel)
+                dkc = (np.exp(G[-1][None, :] - G) * (U @ dS.T)
+                       + np.einsum("ri,rd,rid->id", dA, qc, rel)
+                       + np.einsum("ri,rd,rid->id", dL, ec, rel))
+                dG = qc * dqc + ec * de - kc * dkc
+                last = (dS * ends[ci]).sum(-1)
+                dg[bi, t0:t1, h] = np.cumsum(dG[::-1], axis=0)[::-1] + last
+                db[bi, t0:t1, h] = de * kc
+                dk[bi, t0:t1, h] = dkc + de * b[bi, t0:t1, h]
+                dq[bi, t0:t1, h] = dqc
+                dS = (qc * eG).T @ dO + np.exp(G[-1])[:, None] * dS - Eb.T @ dY
             dh0[bi, h] = dS
     dq = dq * scale
     if use_qk_l2norm_in_kernel:
