@@ -49,6 +49,8 @@ enum gdn2_status {
 #define GDN2_FLAG_L2NORM_QK 1u      /* q, k <- x / max(||x||, 1e-6) in-kernel  */
 #define GDN2_FLAG_GATE_IN_KERNEL 2u /* g is the raw gate pre-activation        */
 #define GDN2_FLAG_LOWER_BOUND 4u    /* with GATE_IN_KERNEL: bounded sigmoid    */
+#define GDN2_FLAG_SAVE_FOR_BWD 8u   /* gdn2_chunk_fwd: keep what the backward   *
+                                     * needs in a training-size workspace       */
 
 int gdn2_abi_version(void);
 const char *gdn2_status_string(int status);
@@ -126,6 +128,44 @@ int gdn2_chunk_fwd_scan(const void *v, const void *w, int io_dtype, void *o,
                         const int64_t *cu_seqlens, const int64_t *cu_seqlens_host, int num_seqs,
                         int B, int T, int H, int K, int V, void *workspace,
                         size_t workspace_bytes, void *stream);
+
+/*
+ * Bytes of the training workspace: gdn2_chunk_fwd with GDN2_FLAG_SAVE_FOR_BWD
+ * writes, next to its per-chunk blobs, the chunk start states and chunk
+ * values U (fp32 precision) that gdn2_chunk_bwd reads back (the tensors the
+ * reference forward saves for backward, chunk_gdn2.py:2424-2447).
+ * The same buffer is then passed unchanged to gdn2_chunk_bwd.
+ */
+size_t gdn2_chunk_train_workspace_size(int B, int T, int H, int K, int V, int io_dtype,
+                                       const int64_t *cu_seqlens_host, int num_seqs);
+
+/*
+ * Bytes of device scratch gdn2_chunk_bwd needs for this shape.
+ */
+size_t gdn2_chunk_bwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,
+                                     const int64_t *cu_seqlens_host, int num_seqs);
+
+/*
+ * Chunkwise backward.  Replaces chunk_gdn2_bwd and the gradient mapping of
+ * ChunkGDN2Function.backward (reference gdn2_ops/chunk_gdn2.py:2170-2325 and
+ * :2480-2547): given do [B,T,H,V] (io_dtype) and optionally dht [N,H,K,V]
+ * (float32, gradient of the final state), writes
+ *   dq, dk, db [B,T,H,K] (io_dtype), dg [B,T,H,K] (g_dtype),
+ *   dv, dw [B,T,H,V] (io_dtype), and dh0 [N,H,K,V] (float32, may be NULL),
+ * the gradients with respect to the raw inputs of the forward (through the
+ * in-kernel L2 norm when GDN2_FLAG_L2NORM_QK is set, and the scale).
+ * q, k, v, g, b, w, scale, flags and cu_seqlens must be those of the forward
+ * call, and `saved` the training workspace it filled.  The in-kernel gate
+ * (GDN2_FLAG_GATE_IN_KERNEL) is not differentiated here: callers that need
+ * gradients apply the gate before the op (GDN2_ERR_UNSUPPORTED otherwise).
+ */
+int gdn2_chunk_bwd(const void *q, const void *k, const void *v, const void *g, const void *b,
+                   const void *w, int io_dtype, int g_dtype, const void *dout,
+                   const float *dht, void *dq, void *dk, void *dv, void *dg, void *db, void *dw,
+                   float *dh0, const int64_t *cu_seqlens, const int64_t *cu_seqlens_host,
+                   int num_seqs, int B, int T, int H, int K, int V, float scale,
+                   unsigned flags, const void *saved, size_t saved_bytes, void *workspace,
+                   size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,7 @@ DTYPE_F16 = 2
 FLAG_L2NORM_QK = 1
 FLAG_GATE_IN_KERNEL = 2
 FLAG_LOWER_BOUND = 4
+FLAG_SAVE_FOR_BWD = 8
 
 OK = 0
 ERR_INVALID = -1
@@ -60,6 +61,13 @@ SIGNATURES: dict[str, tuple] = {
     "gdn2_chunk_fwd_scan": (
         _i,
         [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp],
+    ),
+    "gdn2_chunk_train_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _vp, _i]),
+    "gdn2_chunk_bwd_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _vp, _i]),
+    "gdn2_chunk_bwd": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+         _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _u, _vp, _sz, _vp, _sz, _vp],
     ),
 }
 

@@ -17,7 +17,8 @@ static int check_chunk_args(int io_dtype, int g_dtype, const int64_t *cu_seqlens
 {
     if (!valid_dtype(io_dtype) || !valid_dtype(g_dtype)) return GDN2_ERR_INVALID;
     if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
-    if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND))
+    if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND |
+                  GDN2_FLAG_SAVE_FOR_BWD))
         return GDN2_ERR_INVALID;
     if ((flags & GDN2_FLAG_LOWER_BOUND) && !(flags & GDN2_FLAG_GATE_IN_KERNEL))
         return GDN2_ERR_INVALID;
@@ -177,6 +178,53 @@ int gdn2_chunk_fwd_scan(const void *v, const void *w, int io_dtype, void *o,
                     1.f, 0u, workspace, workspace_bytes);
     a.stages = 2;
     return launch_chunk_fwd(a, io_dtype, GDN2_DTYPE_F32, static_cast<hipStream_t>(stream));
+}
+
+size_t gdn2_chunk_train_workspace_size(int B, int T, int H, int K, int V, int io_dtype,
+                                       const int64_t *cu_seqlens_host, int num_seqs)
+{
+    if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || !valid_dtype(io_dtype)) return 0;
+    return chunk_train_workspace_bytes(B, T, H, K, V, io_dtype, cu_seqlens_host, num_seqs);
+}
+
+size_t gdn2_chunk_bwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,
+                                     const int64_t *cu_seqlens_host, int num_seqs)
+{
+    if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || !valid_dtype(io_dtype)) return 0;
+    return chunk_bwd_workspace_bytes(B, T, H, K, V, io_dtype, cu_seqlens_host, num_seqs);
+}
+
+int gdn2_chunk_bwd(const void *q, const void *k, const void *v, const void *g, const void *b,
+                   const void *w, int io_dtype, int g_dtype, const void *dout,
+                   const float *dht, void *dq, void *dk, void *dv, void *dg, void *db, void *dw,
+                   float *dh0, const int64_t *cu_seqlens, const int64_t *cu_seqlens_host,
+                   int num_seqs, int B, int T, int H, int K, int V, float scale,
+                   unsigned flags, const void *saved, size_t saved_bytes, void *workspace,
+                   size_t workspace_bytes, void *stream)
+{
+    const int st = check_chunk_args(io_dtype, g_dtype, cu_seqlens, cu_seqlens_host, num_seqs, B,
+                                    T, H, K, V, flags & ~GDN2_FLAG_SAVE_FOR_BWD, nullptr);
+    if (st != GDN2_OK) return st;
+    if (flags & (GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND)) return GDN2_ERR_UNSUPPORTED;
+    if (static_cast<int64_t>(B) * T > 0 &&
+        (!q || !k || !v || !g || !b || !w || !dout || !dq || !dk || !dv || !dg || !db || !dw))
+        return GDN2_ERR_INVALID;
+    ChunkBwdArgs a;
+    a.q = q; a.k = k; a.v = v; a.g = g; a.b = b; a.w = w; a.dout = dout;
+    a.dht = dht;
+    a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.db = db; a.dw = dw;
+    a.dh0 = dh0;
+    a.cu_seqlens = cu_seqlens;
+    a.cu_host = cu_seqlens_host;
+    a.num_seqs = cu_seqlens ? num_seqs : B;
+    a.B = B; a.T = T; a.H = H; a.K = K; a.V = V;
+    a.scale = scale;
+    a.flags = flags;
+    a.saved = saved;
+    a.saved_bytes = saved_bytes;
+    a.workspace = workspace;
+    a.workspace_bytes = workspace_bytes;
+    return launch_chunk_bwd(a, io_dtype, g_dtype, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

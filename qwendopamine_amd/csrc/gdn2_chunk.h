@@ -1,0 +1,215 @@
+// Definitions shared by the chunkwise forward and backward kernels (gfx950).
+//
+// Chunk geometry: C = 64 tokens per chunk, 16-token sub-blocks, chunks of
+// all sequences numbered consecutively (gc), one workspace blob per
+// (chunk, head) written by the forward prep kernel.  The blob layout, the
+// chunk location helpers and the in-block decay scans live here so that the
+// backward kernels read exactly what the forward wrote.
+#pragma once
+
+#include "gdn2_mfma.h"
+
+namespace gdn2 {
+
+// Native 16-byte vector: loads and stores of it stay single instructions and
+// arrays of it stay in registers (struct copies of uint4 lower to memcpy).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kChunk = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+// Largest in-block decay span (log2 units, ~ e^80) for which the factored
+// diagonal block keeps every factor inside the normal fp32/bf16 range.
+constexpr float kDiagSpanLimit2 = 115.0f;
+
+struct ChunkParams {
+    const void *q, *k, *v, *g, *b, *w;
+    void *o;
+    const float *h0;
+    float *ht;
+    const float *A_log;
+    const float *dt_bias;
+    float lower_bound;
+    const int64_t *cu_seqlens;
+    int num_seqs, T, H, K, V;
+    int nt;  // chunks per sequence without cu_seqlens
+    float scale;
+    unsigned flags;
+    int vec_ok;  // K % 4 == 0: 4-wide input loads
+    void *ws;    // per-chunk blobs (prep writes, scan reads)
+    // Training mode (both null otherwise): the scan also writes, per chunk,
+    // its start state (hs) and its U (us), in K16 A-order blocks of width
+    // VP = V rounded up to 16.
+    void *hs, *us;
+    int VP;
+};
+
+// Per (chunk, head) blob, in storage elements.
+template <PrecKind PK, int KP>
+struct Blob {
+    using st = typename Prec<PK>::st;
+    static constexpr int64_t X = 0;                 // [64][64]   (I + L)^{-1}
+    static constexpr int64_t WN = 4096;             // [64][KP]   -W
+    static constexpr int64_t QB = 4096 + 64 * KP;   // [64][KP]   Qbar
+    static constexpr int64_t AQ = 4096 + 128 * KP;  // [64][64]   Aqk
+    static constexpr int64_t KT = 8192 + 128 * KP;  // [KP][64]   Ktilde^T
+    static constexpr int64_t GL = 8192 + 192 * KP;  // KP floats  exp(G_last)
+    static constexpr int64_t SIZE = GL + KP * 4 / static_cast<int64_t>(sizeof(st));
+    static constexpr int64_t BYTES = SIZE * static_cast<int64_t>(sizeof(st));
+    static_assert(BYTES % 16 == 0, "blob must be a whole number of 16-byte units");
+};
+
+template <class PP>
+__device__ __forceinline__ void locate_chunk(const PP &p, int gc, int &n, int &j,
+                                             int64_t &bos, int64_t &len)
+{
+    if (!p.cu_seqlens) {
+        n = gc / p.nt;
+        j = gc % p.nt;
+        bos = static_cast<int64_t>(n) * p.T;
+        len = p.T;
+        return;
+    }
+    int acc = 0;
+    n = 0;
+    j = 0;
+    bos = 0;
+    len = 0;
+    for (int s = 0; s < p.num_seqs; ++s) {
+        const int64_t b0 = p.cu_seqlens[s], e0 = p.cu_seqlens[s + 1];
+        const int c = static_cast<int>((e0 - b0 + kChunk - 1) / kChunk);
+        if (gc < acc + c) {
+            n = s;
+            j = gc - acc;
+            bos = b0;
+            len = e0 - b0;
+            return;
+        }
+        acc += c;
+    }
+}
+
+template <class PP>
+__device__ __forceinline__ int seq_chunk_base(const PP &p, int n, int64_t &bos,
+                                              int64_t &len)
+{
+    if (!p.cu_seqlens) {
+        bos = static_cast<int64_t>(n) * p.T;
+        len = p.T;
+        return n * p.nt;
+    }
+    int acc = 0;
+    for (int s = 0; s < n; ++s)
+        acc += static_cast<int>((p.cu_seqlens[s + 1] - p.cu_seqlens[s] + kChunk - 1) / kChunk);
+    bos = p.cu_seqlens[n];
+    len = p.cu_seqlens[n + 1] - bos;
+    return acc;
+}
+
+// 4 consecutive channels c0..c0+3 of one row, zero outside [0, K) or when !ok.
+template <typename T>
+__device__ __forceinline__ void load4(const T *base, int64_t off, int c0, int K, bool ok, int vec_ok,
+                                      float (&x)[4])
+{
+    if (ok && vec_ok && c0 + 4 <= K) {
+        if constexpr (std::is_same<T, float>::value) {
+            const float4 a = *reinterpret_cast<const float4 *>(base + off + c0);
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        } else if constexpr (std::is_same<T, bf16_t>::value) {
+            const uint2 u = *reinterpret_cast<const uint2 *>(base + off + c0);
+            x[0] = __uint_as_float(u.x << 16);
+            x[1] = __uint_as_float(u.x & 0xffff0000u);
+            x[2] = __uint_as_float(u.y << 16);
+            x[3] = __uint_as_float(u.y & 0xffff0000u);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = io<T>::ld(base, off + c0 + i);
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (ok && c0 + i < K) ? io<T>::ld(base, off + c0 + i) : 0.0f;
+}
+
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Inclusive prefix sum over the 16 lanes of each DPP row (lanes 16r..16r+15),
+// Hillis-Steele with row_shr:1,2,4,8; lanes shifted in from outside the row
+// read 0 (bound_ctrl), so no masking is needed.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_shr(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                                 0xf, 0xf, true));
+}
+
+__device__ __forceinline__ float row16_scan(float x)
+{
+    x += dpp_row_shr<0x111>(x);
+    x += dpp_row_shr<0x112>(x);
+    x += dpp_row_shr<0x114>(x);
+    x += dpp_row_shr<0x118>(x);
+    return x;
+}
+
+inline int kp_for(int K) { return K <= 32 ? 32 : (K <= 64 ? 64 : 128); }
+inline int bv_for(int V) { return V <= 16 ? 16 : (V <= 32 ? 32 : 64); }
+
+inline int64_t count_chunks(int B, int T, const int64_t *cu_host, int num_seqs)
+{
+    if (!cu_host) return static_cast<int64_t>(B) * ((T + kChunk - 1) / kChunk);
+    int64_t c = 0;
+    for (int i = 0; i < num_seqs; ++i) c += (cu_host[i + 1] - cu_host[i] + kChunk - 1) / kChunk;
+    return c;
+}
+
+inline int64_t blob_bytes(int io_dtype, int KP)
+{
+    const bool f32 = io_dtype == GDN2_DTYPE_F32;
+    switch (KP) {
+    case 32: return f32 ? Blob<PrecKind::F32, 32>::BYTES : Blob<PrecKind::BF16, 32>::BYTES;
+    case 64: return f32 ? Blob<PrecKind::F32, 64>::BYTES : Blob<PrecKind::BF16, 64>::BYTES;
+    default: return f32 ? Blob<PrecKind::F32, 128>::BYTES : Blob<PrecKind::BF16, 128>::BYTES;
+    }
+}
+
+inline int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+// Training workspace: the forward's blobs followed by what the backward
+// re-reads (per-chunk start states and U), each region 256-byte aligned.  These are kept at fp32 precision: one fp32
+// plane for fp32 inputs, two 16-bit planes (hi, lo) otherwise -- 4 bytes per
+// element either way.
+struct TrainLayout {
+    int64_t blob, hs, us, total;
+};
+
+inline TrainLayout train_layout(int64_t nc, int H, int K, int V, int io_dtype)
+{
+    const int KP = kp_for(K);
+    const int64_t VP = round_up(V, 16);
+    const int64_t es = 4;
+    TrainLayout t;
+    t.blob = 0;
+    t.hs = round_up(nc * H * blob_bytes(io_dtype, KP), 256);
+    t.us = t.hs + round_up(nc * H * KP * VP * es, 256);
+    t.total = t.us + round_up(nc * H * 64 * VP * es, 256);
+    return t;
+}
+
+// Backward scratch: per-chunk end-state gradients (dhs) and dY = X^T dU (dys).
+struct BwdLayout {
+    int64_t dhs, dys, total;
+};
+
+inline BwdLayout bwd_layout(int64_t nc, int H, int K, int V, int io_dtype)
+{
+    const int KP = kp_for(K);
+    const int64_t VP = round_up(V, 16);
+    const int64_t es = io_dtype == GDN2_DTYPE_F32 ? 4 : 2;
+    BwdLayout t;
+    t.dhs = 0;
+    t.dys = round_up(nc * H * KP * VP * es, 256);
+    t.total = t.dys + round_up(nc * H * 64 * VP * es, 256);
+    return t;
+}
+
+}  // namespace gdn2

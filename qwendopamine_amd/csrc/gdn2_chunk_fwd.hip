@@ -42,145 +42,12 @@
 
 #include <type_traits>
 
+#include "gdn2_chunk.h"
 #include "gdn2_internal.h"
-#include "gdn2_mfma.h"
 
 namespace gdn2 {
 
-// Native 16-byte vector: loads and stores of it stay single instructions and
-// arrays of it stay in registers (struct copies of uint4 lower to memcpy).
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
 namespace {
-
-constexpr int kChunk = 64;
-constexpr float kLog2e = 1.4426950408889634f;
-// Largest in-block decay span (log2 units, ~ e^80) for which the factored
-// diagonal block keeps every factor inside the normal fp32/bf16 range.
-constexpr float kDiagSpanLimit2 = 115.0f;
-
-struct ChunkParams {
-    const void *q, *k, *v, *g, *b, *w;
-    void *o;
-    const float *h0;
-    float *ht;
-    const float *A_log;
-    const float *dt_bias;
-    float lower_bound;
-    const int64_t *cu_seqlens;
-    int num_seqs, T, H, K, V;
-    int nt;  // chunks per sequence without cu_seqlens
-    float scale;
-    unsigned flags;
-    int vec_ok;  // K % 4 == 0: 4-wide input loads
-    void *ws;
-};
-
-// Per (chunk, head) blob, in storage elements.
-template <PrecKind PK, int KP>
-struct Blob {
-    using st = typename Prec<PK>::st;
-    static constexpr int64_t X = 0;                 // [64][64]   (I + L)^{-1}
-    static constexpr int64_t WN = 4096;             // [64][KP]   -W
-    static constexpr int64_t QB = 4096 + 64 * KP;   // [64][KP]   Qbar
-    static constexpr int64_t AQ = 4096 + 128 * KP;  // [64][64]   Aqk
-    static constexpr int64_t KT = 8192 + 128 * KP;  // [KP][64]   Ktilde^T
-    static constexpr int64_t GL = 8192 + 192 * KP;  // KP floats  exp(G_last)
-    static constexpr int64_t SIZE = GL + KP * 4 / static_cast<int64_t>(sizeof(st));
-    static constexpr int64_t BYTES = SIZE * static_cast<int64_t>(sizeof(st));
-    static_assert(BYTES % 16 == 0, "blob must be a whole number of 16-byte units");
-};
-
-__device__ __forceinline__ void locate_chunk(const ChunkParams &p, int gc, int &n, int &j,
-                                             int64_t &bos, int64_t &len)
-{
-    if (!p.cu_seqlens) {
-        n = gc / p.nt;
-        j = gc % p.nt;
-        bos = static_cast<int64_t>(n) * p.T;
-        len = p.T;
-        return;
-    }
-    int acc = 0;
-    n = 0;
-    j = 0;
-    bos = 0;
-    len = 0;
-    for (int s = 0; s < p.num_seqs; ++s) {
-        const int64_t b0 = p.cu_seqlens[s], e0 = p.cu_seqlens[s + 1];
-        const int c = static_cast<int>((e0 - b0 + kChunk - 1) / kChunk);
-        if (gc < acc + c) {
-            n = s;
-            j = gc - acc;
-            bos = b0;
-            len = e0 - b0;
-            return;
-        }
-        acc += c;
-    }
-}
-
-__device__ __forceinline__ int seq_chunk_base(const ChunkParams &p, int n, int64_t &bos,
-                                              int64_t &len)
-{
-    if (!p.cu_seqlens) {
-        bos = static_cast<int64_t>(n) * p.T;
-        len = p.T;
-        return n * p.nt;
-    }
-    int acc = 0;
-    for (int s = 0; s < n; ++s)
-        acc += static_cast<int>((p.cu_seqlens[s + 1] - p.cu_seqlens[s] + kChunk - 1) / kChunk);
-    bos = p.cu_seqlens[n];
-    len = p.cu_seqlens[n + 1] - bos;
-    return acc;
-}
-
-// 4 consecutive channels c0..c0+3 of one row, zero outside [0, K) or when !ok.
-template <typename T>
-__device__ __forceinline__ void load4(const T *base, int64_t off, int c0, int K, bool ok, int vec_ok,
-                                      float (&x)[4])
-{
-    if (ok && vec_ok && c0 + 4 <= K) {
-        if constexpr (std::is_same<T, float>::value) {
-            const float4 a = *reinterpret_cast<const float4 *>(base + off + c0);
-            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-        } else if constexpr (std::is_same<T, bf16_t>::value) {
-            const uint2 u = *reinterpret_cast<const uint2 *>(base + off + c0);
-            x[0] = __uint_as_float(u.x << 16);
-            x[1] = __uint_as_float(u.x & 0xffff0000u);
-            x[2] = __uint_as_float(u.y << 16);
-            x[3] = __uint_as_float(u.y & 0xffff0000u);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) x[i] = io<T>::ld(base, off + c0 + i);
-        }
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = (ok && c0 + i < K) ? io<T>::ld(base, off + c0 + i) : 0.0f;
-}
-
-__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Inclusive prefix sum over the 16 lanes of each DPP row (lanes 16r..16r+15),
-// Hillis-Steele with row_shr:1,2,4,8; lanes shifted in from outside the row
-// read 0 (bound_ctrl), so no masking is needed.
-template <int CTRL>
-__device__ __forceinline__ float dpp_row_shr(float x)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
-                                                                 0xf, 0xf, true));
-}
-
-__device__ __forceinline__ float row16_scan(float x)
-{
-    x += dpp_row_shr<0x111>(x);
-    x += dpp_row_shr<0x112>(x);
-    x += dpp_row_shr<0x114>(x);
-    x += dpp_row_shr<0x118>(x);
-    return x;
-}
 
 // ---------------------------------------------------------------------------
 // Prep: one workgroup (4 waves) per (chunk, head).  Wave R owns token rows
@@ -538,6 +405,25 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     const bool active = wv < NCT;
     const int col = vs * BV + 16 * wv + m;
     const bool col_ok = active && col < V;
+    // Training-mode emission: value tile vt of this wave, if inside V.
+    const int VP = p.VP, vt = vs * NCT + wv;
+    const bool emit = p.hs != nullptr && active && 16 * vt < V;
+    const Q ident = identity_q4<PK>(l);
+    // An fp32 accumulator tile (rows 4kg+i, column m) stored transposed, in
+    // A-order, at full precision: fp32 as is; 16-bit precisions as two planes
+    // (hi = x rounded, lo = x - hi rounded), each transposed exactly by an
+    // identity product.  The backward's products read both planes.
+    constexpr int NPL = PK == PrecKind::F32 ? 1 : 2;
+    auto emit_tile = [&](st *base, int plane, int64_t off, f32x4 x) __attribute__((always_inline)) {
+        const Q hi = pack4<PK>(x);
+        st_q4<PK>(base + off, pack4<PK>(mma1<PK>(zero4(), hi, ident)));
+        if constexpr (NPL == 2) {
+            float xh[4];
+            unpack4<PK>(hi, xh);
+            const Q lo = pack4<PK>(x[0] - xh[0], x[1] - xh[1], x[2] - xh[2], x[3] - xh[3]);
+            st_q4<PK>(base + plane + off, pack4<PK>(mma1<PK>(zero4(), lo, ident)));
+        }
+    };
     int64_t bos, len;
     const int gc0 = seq_chunk_base(p, n, bos, len);
     const int nch = static_cast<int>((len + kChunk - 1) / kChunk);
@@ -709,6 +595,13 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
             const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
 
+            // Training mode: this chunk's start state, A-order tiles (kt, vt).
+            if (emit) {
+                st *hsb = static_cast<st *>(p.hs) + (static_cast<int64_t>(gc0 + jc) * H + h) * (NPL * KP * VP);
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) emit_tile(hsb, KP * VP, k16_block(kt, vt, VP) + 4 * l, S[kt]);
+            }
+
             // z = w * v as B operand (contraction over tokens), staged in LDS.
             Q zf[4];
 #pragma unroll
@@ -734,6 +627,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                                    ld_q4<PK>(Bk + BL::WN + k16_block(rt, 2 * s + 1, KP) + 4 * l),
                                    sf[2 * s], sf[2 * s + 1]);
                 uf[rt] = pack4<PK>(acc);
+                if (emit) {
+                    st *usb = static_cast<st *>(p.us) + (static_cast<int64_t>(gc0 + jc) * H + h) * (NPL * 64 * VP);
+                    emit_tile(usb, 64 * VP, k16_block(rt, vt, VP) + 4 * l, acc);
+                }
             }
             // O = Qbar S + Aqk U.
 #pragma unroll
@@ -789,27 +686,6 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 const int row = 16 * kt + 4 * kg + i;
                 if (row < K) p.ht[((static_cast<int64_t>(n) * H + h) * K + row) * V + col] = S[kt][i];
             }
-    }
-}
-
-int kp_for(int K) { return K <= 32 ? 32 : (K <= 64 ? 64 : 128); }
-int bv_for(int V) { return V <= 16 ? 16 : (V <= 32 ? 32 : 64); }
-
-int64_t count_chunks(int B, int T, const int64_t *cu_host, int num_seqs)
-{
-    if (!cu_host) return static_cast<int64_t>(B) * ((T + kChunk - 1) / kChunk);
-    int64_t c = 0;
-    for (int i = 0; i < num_seqs; ++i) c += (cu_host[i + 1] - cu_host[i] + kChunk - 1) / kChunk;
-    return c;
-}
-
-int64_t blob_bytes(int io_dtype, int KP)
-{
-    const bool f32 = io_dtype == GDN2_DTYPE_F32;
-    switch (KP) {
-    case 32: return f32 ? Blob<PrecKind::F32, 32>::BYTES : Blob<PrecKind::BF16, 32>::BYTES;
-    case 64: return f32 ? Blob<PrecKind::F32, 64>::BYTES : Blob<PrecKind::BF16, 64>::BYTES;
-    default: return f32 ? Blob<PrecKind::F32, 128>::BYTES : Blob<PrecKind::BF16, 128>::BYTES;
     }
 }
 
@@ -877,8 +753,11 @@ int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream
     if (g_dtype != GDN2_DTYPE_F32 && g_dtype != io_dtype) return GDN2_ERR_UNSUPPORTED;
     const int64_t nc = count_chunks(a.B, a.T, a.cu_host, a.num_seqs);
     if (nc * a.H > 2147483647LL / 2) return GDN2_ERR_UNSUPPORTED;
-    const size_t need = chunk_fwd_workspace_bytes(a.B, a.T, a.H, a.K, a.V, io_dtype, a.cu_host,
-                                                  a.num_seqs);
+    const bool train = (a.flags & GDN2_FLAG_SAVE_FOR_BWD) != 0;
+    const TrainLayout tl = train_layout(nc, a.H, a.K, a.V, io_dtype);
+    const size_t need = train ? static_cast<size_t>(tl.total)
+                              : chunk_fwd_workspace_bytes(a.B, a.T, a.H, a.K, a.V, io_dtype,
+                                                          a.cu_host, a.num_seqs);
     if (need > 0 && (!a.workspace || a.workspace_bytes < need)) return GDN2_ERR_WORKSPACE;
 
     ChunkParams p;
@@ -896,6 +775,13 @@ int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream
     p.flags = a.flags;
     p.vec_ok = (a.K % 4) == 0;
     p.ws = a.workspace;
+    p.VP = static_cast<int>(round_up(a.V, 16));
+    p.hs = p.us = nullptr;
+    if (train) {
+        unsigned char *base = static_cast<unsigned char *>(a.workspace);
+        p.hs = base + tl.hs;
+        p.us = base + tl.us;
+    }
     const int total = static_cast<int>(nc);
 
     hipError_t e;

@@ -48,4 +48,27 @@ size_t chunk_fwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
                                  const int64_t *cu_host, int num_seqs);
 int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream);
 
+struct ChunkBwdArgs {
+    const void *q, *k, *v, *g, *b, *w, *dout;
+    const float *dht;
+    void *dq, *dk, *dv, *dg, *db, *dw;
+    float *dh0;
+    const int64_t *cu_seqlens;
+    const int64_t *cu_host;
+    int num_seqs;
+    int B, T, H, K, V;
+    float scale;
+    unsigned flags;
+    const void *saved;  // training workspace of the forward
+    size_t saved_bytes;
+    void *workspace;    // backward scratch
+    size_t workspace_bytes;
+};
+
+size_t chunk_train_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype,
+                                   const int64_t *cu_host, int num_seqs);
+size_t chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype,
+                                 const int64_t *cu_host, int num_seqs);
+int launch_chunk_bwd(const ChunkBwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream);
+
 }  // namespace gdn2

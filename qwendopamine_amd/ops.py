@@ -30,6 +30,7 @@ __all__ = [
     "chunk_gdn2",
     "chunk_gdn2_fwd",
     "ChunkGDN2Function",
+    "gate_activation",
 ]
 
 
@@ -70,7 +71,9 @@ def _flags(use_qk_l2norm_in_kernel: bool, use_gate_in_kernel: bool, lower_bound)
 
 
 def _io(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    return x.to(dtype).contiguous()
+    """Contiguous copy in ``dtype``, 16-byte aligned (the kernels use 16-byte loads)."""
+    x = x.to(dtype).contiguous()
+    return x if x.data_ptr() % 16 == 0 else x.clone()
 
 
 def _gate_tensors(use_gate_in_kernel, A_log, dt_bias, heads: int, K: int):
@@ -239,6 +242,25 @@ def fused_recurrent_gdn2(
     )
 
 
+def gate_activation(g: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor | None,
+                    lower_bound: float | None) -> torch.Tensor:
+    """The in-kernel decay activation as torch ops (differentiable), float32.
+
+    ``g = -exp(A_log[h]) * softplus(g + dt_bias[h, d])``, or with a lower bound
+    ``g = lower_bound * sigmoid(exp(A_log[h]) * (g + dt_bias[h, d]))``
+    (reference ``kda_gate`` forward, ``chunk_kda.py:3025-3053``; the same
+    formula the HIP kernels apply under ``GDN2_FLAG_GATE_IN_KERNEL``).
+    """
+    H, K = g.shape[-2], g.shape[-1]
+    x = g.float()
+    if dt_bias is not None:
+        x = x + dt_bias.float().reshape(H, K)
+    a = A_log.float().exp().reshape(H, 1)
+    if lower_bound is not None:
+        return lower_bound * torch.sigmoid(a * x)
+    return -a * torch.nn.functional.softplus(x)
+
+
 def chunk_gdn2_fwd(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -255,8 +277,14 @@ def chunk_gdn2_fwd(
     dt_bias: torch.Tensor | None = None,
     lower_bound: float | None = None,
     cu_seqlens: torch.LongTensor | None = None,
-) -> tuple[torch.Tensor, torch.Tensor | None]:
-    """Launch the chunkwise HIP forward (reference ``chunk_gdn2.py:1165-1264``)."""
+    save_for_bwd: bool = False,
+):
+    """Launch the chunkwise HIP forward (reference ``chunk_gdn2.py:1165-1264``).
+
+    Returns ``(o, final_state)``, or with ``save_for_bwd`` ``(o, final_state,
+    saved)`` where ``saved`` holds the inputs as the kernels read them and the
+    training workspace that ``chunk_gdn2_bwd`` consumes.
+    """
     name = "chunk_gdn2"
     _require_gpu(name, q, k, v, g, b, w, initial_state)
     _check_shapes(name, q, k, v, g, b, w, same_heads=True)
@@ -274,51 +302,70 @@ def chunk_gdn2_fwd(
     o = torch.empty_like(v)
     lib = nat.load()
     cu_host_p = None if cu_host is None else cu_host.data_ptr()
-    ws_bytes = lib.gdn2_chunk_fwd_workspace_size(B, T, H, K, V, nat.dtype_code(dt), cu_host_p, N)
+    size_fn = lib.gdn2_chunk_train_workspace_size if save_for_bwd else lib.gdn2_chunk_fwd_workspace_size
+    ws_bytes = size_fn(B, T, H, K, V, nat.dtype_code(dt), cu_host_p, N)
     if ws_bytes == 0 and B * T > 0 and K > 128:
         raise NotImplementedError(f"{name}: key head dim {K} > 128 is not supported by the chunk kernel")
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     a_log, dtb = _gate_tensors(use_gate_in_kernel, A_log, dt_bias, H, K)
+    flags = _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound)
+    if save_for_bwd:
+        if use_gate_in_kernel:
+            raise NotImplementedError(f"{name}: apply the gate before the op when gradients are needed")
+        flags |= nat.FLAG_SAVE_FOR_BWD
     st = lib.gdn2_chunk_fwd(
         nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(g), nat.ptr(b), nat.ptr(w),
         nat.dtype_code(dt), nat.dtype_code(g.dtype), nat.ptr(o),
         nat.ptr(h0), nat.ptr(ht), nat.ptr(a_log), nat.ptr(dtb),
         float(lower_bound) if lower_bound is not None else 0.0,
-        nat.ptr(cu_dev), cu_host_p, N, B, T, H, K, V, float(scale),
-        _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound),
+        nat.ptr(cu_dev), cu_host_p, N, B, T, H, K, V, float(scale), flags,
         ws.data_ptr(), ws.numel(), nat.stream_handle(q.device),
     )
     nat.check(st, name)
-    return o, ht
+    if not save_for_bwd:
+        return o, ht
+    saved = dict(q=q, k=k, v=v, g=g, b=b, w=w, ws=ws, cu_dev=cu_dev, cu_host=cu_host, N=N,
+                 scale=float(scale), flags=flags & ~nat.FLAG_SAVE_FOR_BWD)
+    return o, ht, saved
 
 
 class ChunkGDN2Function(torch.autograd.Function):
-    """Autograd wrapper of the chunkwise HIP kernels (reference ``chunk_gdn2.py:2328-2547``)."""
+    """Autograd wrapper of the chunkwise HIP kernels (reference ``chunk_gdn2.py:2328-2547``).
+
+    The training forward keeps its workspace (per-chunk blobs, chunk start
+    states and values, sequence end states) instead of recomputing them in
+    backward: MI355X has the HBM for it.
+    """
 
     @staticmethod
     def forward(ctx, q, k, v, g, b, w, A_log, dt_bias, scale, initial_state, output_final_state,
                 use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound):
-        o, ht = chunk_gdn2_fwd(
+        needs = any(ctx.needs_input_grad[i] for i in (0, 1, 2, 3, 4, 5, 9))
+        if use_gate_in_kernel and needs:
+            raise NotImplementedError(
+                "chunk_gdn2: gradients through the in-kernel gate are taken by applying the gate "
+                "before the op (chunk_gdn2 does this itself)"
+            )
+        res = chunk_gdn2_fwd(
             q, k, v, g, b, w, scale, initial_state, output_final_state,
             use_qk_l2norm_in_kernel, use_gate_in_kernel, A_log, dt_bias, lower_bound, cu_seqlens,
+            save_for_bwd=needs,
         )
-        ctx.save_for_backward(q, k, v, g, b, w, initial_state, A_log, dt_bias, cu_seqlens)
-        ctx.scale = scale
-        ctx.flags = (use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound)
-        return o, ht
+        ctx.in_dtypes = tuple(x.dtype for x in (q, k, v, g, b, w))
+        ctx.has_h0 = initial_state is not None
+        ctx.saved = res[2] if needs else None
+        return res[0], res[1]
 
     @staticmethod
     def backward(ctx, do, dht):
         from .backward import chunk_gdn2_bwd
 
-        q, k, v, g, b, w, h0, A_log, dt_bias, cu_seqlens = ctx.saved_tensors
-        use_l2, use_gate, lower_bound = ctx.flags
-        grads = chunk_gdn2_bwd(
-            q, k, v, g, b, w, ctx.scale, h0, do, dht, use_l2, use_gate, A_log, dt_bias,
-            lower_bound, cu_seqlens,
-        )
-        dq, dk, dv, dg, db, dw, dh0, dA_log, ddt_bias = grads
-        return (dq, dk, dv, dg, db, dw, dA_log, ddt_bias, None, dh0, None, None, None, None, None)
+        if ctx.saved is None:
+            raise RuntimeError("chunk_gdn2: backward called without a training forward")
+        dq, dk, dv, dg, db, dw, dh0 = chunk_gdn2_bwd(ctx.saved, do, dht, ctx.has_h0)
+        ctx.saved = None
+        dq, dk, dv, dg, db, dw = (x.to(d) for x, d in zip((dq, dk, dv, dg, db, dw), ctx.in_dtypes))
+        return (dq, dk, dv, dg, db, dw, None, None, None, dh0, None, None, None, None, None)
 
 
 def chunk_gdn2(
@@ -391,6 +438,12 @@ def chunk_gdn2(
     if scale is None:
         scale = k.shape[-1] ** -0.5
     _require_gpu("chunk_gdn2", q, k, v, g, b, w, initial_state)
+    if use_gate_in_kernel and torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (q, k, v, g, b, w, A_log, dt_bias, initial_state)
+    ):
+        # Differentiable gate in torch, then the kernels on the activated decay.
+        g = gate_activation(g, A_log, dt_bias, lower_bound)
+        use_gate_in_kernel, A_log, dt_bias, lower_bound = False, None, None, None
     return ChunkGDN2Function.apply(
         q, k, v, g, b, w, A_log, dt_bias, scale, initial_state, output_final_state,
         use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound,
