@@ -31,6 +31,7 @@ BF16_PEAK_TFLOPS = 2500.0
 
 PREFILL = dict(B=8, T=4096, H=16, K=128, V=128, C=64)
 DECODE = dict(N=64, H=16, K=128, V=128, steps=1024)
+TRAIN = dict(B=4, T=8192, H=16, K=128, V=128, C=64)
 
 
 def prefill_flops(B, T, H, K, V, C):
@@ -47,6 +48,21 @@ def prefill_bytes(B, T, H, K, V):
 def decode_bytes(N, H, K, V):
     """Per step: fp32 state read + write, q,k,b,v,w bf16 + g fp32 in, o bf16 out."""
     return 2 * N * H * K * V * 4 + N * H * (2 * (3 * K + 2 * V) + 4 * K + 2 * V)
+
+
+def train_bytes(B, T, H, K, V):
+    """Algorithmic HBM bytes of fwd+bwd: q,k,v,b,w bf16 + g fp32 read twice, dO read,
+    o written, dq,dk,dv,db,dw bf16 + dg fp32 written."""
+    fwd = 2 * (3 * K + 2 * V) + 4 * K + 2 * V
+    bwd = 2 * (3 * K + 2 * V) + 4 * K + 2 * V + 2 * (3 * K + 2 * V) + 4 * K
+    return B * T * H * (fwd + bwd)
+
+
+def train_flops(B, T, H, K, V, C):
+    """Dense chunkwise work per token-head: forward 6KV + 2C(3K+2V) + C^2/3, backward
+    16KV + 14CK + 10CV + 4C^2."""
+    return B * T * H * (6 * K * V + 2 * C * (3 * K + 2 * V) + C * C / 3.0
+                        + 16 * K * V + 14 * C * K + 10 * C * V + 4 * C * C)
 
 
 def make_prefill_inputs(torch, dev, B, T, H, K, V, seed=1):
@@ -113,6 +129,76 @@ def bench_prefill(torch, nat, dev, steps, warmup):
     ms_step = wall * 1e3 / steps
     return dict(ms_step=ms_step, t_prep_ms=t_prep, t_scan_ms=t_scan,
                 inputs=(q, k, v, g, b, w))
+
+
+def bench_train(torch, nat, dev, steps, warmup):
+    """C4: training forward (saving the backward's workspace) then backward, bf16."""
+    B, T, H, K, V = (TRAIN[x] for x in ("B", "T", "H", "K", "V"))
+    q, k, v, g, b, w = make_prefill_inputs(torch, dev, B, T, H, K, V, seed=4)
+    gen = torch.Generator(device=dev).manual_seed(40)
+    do = torch.randn(B, T, H, V, generator=gen, device=dev).to(torch.bfloat16)
+    lib = nat.load()
+    io, gd = nat.DTYPE_BF16, nat.DTYPE_F32
+    sv_bytes = lib.gdn2_chunk_train_workspace_size(B, T, H, K, V, io, None, B)
+    bw_bytes = lib.gdn2_chunk_bwd_workspace_size(B, T, H, K, V, io, None, B)
+    sv = torch.empty(sv_bytes, dtype=torch.uint8, device=dev)
+    bw = torch.empty(bw_bytes, dtype=torch.uint8, device=dev)
+    o = torch.empty_like(v)
+    dq, dk, db = torch.empty_like(q), torch.empty_like(k), torch.empty_like(b)
+    dv, dw, dg = torch.empty_like(v), torch.empty_like(w), torch.empty_like(g)
+    scale = K**-0.5
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def fwd():
+        st = lib.gdn2_chunk_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), b.data_ptr(),
+                                w.data_ptr(), io, gd, o.data_ptr(), None, None, None, None, 0.0, None,
+                                None, B, B, T, H, K, V, scale,
+                                nat.FLAG_L2NORM_QK | nat.FLAG_SAVE_FOR_BWD, sv.data_ptr(), sv_bytes, sh)
+        nat.check(st, "gdn2_chunk_fwd (training)")
+
+    def bwd():
+        st = lib.gdn2_chunk_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), b.data_ptr(),
+                                w.data_ptr(), io, gd, do.data_ptr(), None, dq.data_ptr(),
+                                dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), db.data_ptr(),
+                                dw.data_ptr(), None, None, None, B, B, T, H, K, V, scale,
+                                nat.FLAG_L2NORM_QK, sv.data_ptr(), sv_bytes, bw.data_ptr(), bw_bytes,
+                                sh)
+        nat.check(st, "gdn2_chunk_bwd")
+
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize(dev)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for e in evs:
+        e[0].record(stream)
+        fwd()
+        e[1].record(stream)
+        bwd()
+        e[2].record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    t_f = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    t_b = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    for x in (o, dq, dk, dv, db, dw, dg):
+        if not torch.isfinite(x.float()).all():
+            raise RuntimeError("non-finite training output")
+    ms = wall * 1e3 / steps
+    nbytes = train_bytes(B, T, H, K, V)
+    flops = train_flops(B, T, H, K, V, TRAIN["C"])
+    t_op = (t_f + t_b) * 1e-3
+    return {"tokens_per_s": round(B * T / (ms * 1e-3), 1), "ms_per_step": round(ms, 4),
+            "fwd_ms": round(t_f, 4), "bwd_ms": round(t_b, 4),
+            "algorithmic_bytes": nbytes, "achieved_GBps": round(nbytes / t_op / 1e9, 1),
+            "frac_hbm_peak": round(nbytes / t_op / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_flop": flops, "achieved_TFLOPs": round(flops / t_op / 1e12, 2),
+            "frac_mfma_peak": round(flops / t_op / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "config": {"workload": "C4 gdn2 chunkwise forward (training, workspace kept) + backward",
+                       "B": B, "T": T, "H": H, "d_k": K, "d_v": V, "chunk": TRAIN["C"],
+                       "dtype": "bf16 q,k,v,b,w,dO; fp32 g; fp32 accumulation",
+                       "grads": "dq, dk, dv, dg, db, dw"}}
 
 
 def bench_decode(torch, nat, dev, reps=3, eager_steps=0):
@@ -251,6 +337,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="short run for rocprofv3 counter passes; prints no JSON line")
     args = ap.parse_args()
@@ -315,6 +402,8 @@ def main() -> int:
     }
     if not args.no_decode:
         out["decode"] = bench_decode(torch, nat, dev)
+    if not args.no_train:
+        out["train"] = bench_train(torch, nat, dev, max(2, args.steps // 2), 1)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, res["inputs"])
     print(json.dumps(out), flush=True)

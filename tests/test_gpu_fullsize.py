@@ -7,6 +7,11 @@
   the reference update (gdn2.py:164-178); 256 decode steps equal the chunkwise
   prefill of the same 256 tokens.
 * C4 forward shape (B4 T8192 H16): chunk vs token-serial kernel.
+* C4 backward (B4 T8192 H16, bf16, dO ~ N(0,1)): the bf16 gradients equal the
+  float32 kernels' gradients on the same (upcast) inputs -- the float32
+  backward is itself pinned to the float64 oracle VJP at 1e-6 on small shapes
+  -- for dq, dk, dv, dbeta = sum_K db + sum_V dw (b = w = beta broadcast) and
+  the scalar dg = sum_K dg.
 """
 
 from __future__ import annotations
@@ -113,3 +118,32 @@ def test_decode_loop_equals_prefill(gpu_device):
     eo, es = rel_l2(oc.float(), od.float()), rel_l2(sc, state)
     print(f"  rel_l2 o={eo:.3e} state={es:.3e}", flush=True)
     assert eo <= 2e-2 and es <= 2e-2
+
+
+def _rel(a, b):
+    a, b = a.double(), b.double()
+    return float(torch.linalg.vector_norm(a - b) / torch.linalg.vector_norm(b))
+
+
+def test_backward_full_size_bf16_vs_fp32(gpu_device):
+    from qwendopamine_amd.ops import chunk_gdn2
+
+    B, T, H, K, V = 4, 8192, 16, 128, 128
+    print("[case] full-size C4 backward bf16 vs fp32 kernels", flush=True)
+    q, k, v, g, b, w = _inputs(gpu_device, B, T, H, K, V, seed=4)
+    gen = torch.Generator(device=gpu_device).manual_seed(41)
+    do = torch.randn(B, T, H, V, generator=gen, device=gpu_device).to(torch.bfloat16)
+    grads = {}
+    for dt in (torch.bfloat16, torch.float32):
+        leaves = [x.to(dt).detach().requires_grad_(True) for x in (q, k, v, g, b, w)]
+        o, _ = chunk_gdn2(*leaves, use_qk_l2norm_in_kernel=True)
+        (o.float() * do.float()).sum().backward()
+        torch.cuda.synchronize()
+        dq, dk, dv, dg, db, dw = (x.grad.float() for x in leaves)
+        grads[dt] = dict(dq=dq, dk=dk, dv=dv, dbeta=db.sum(-1) + dw.sum(-1), dg=dg.sum(-1))
+        del leaves, o
+    errs = {n: _rel(grads[torch.bfloat16][n], grads[torch.float32][n]) for n in grads[torch.float32]}
+    print("  rel_l2 " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
+    for n, e in errs.items():
+        assert e <= 2e-2, (n, e)
+        assert torch.isfinite(grads[torch.bfloat16][n]).all(), n
