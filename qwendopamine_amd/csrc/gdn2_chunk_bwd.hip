@@ -24,12 +24,13 @@
 //    copy waves land each forward blob in LDS with every matrix transposed
 //    (the backward contracts over the dimension the forward kept), so the
 //    compute waves issue the same K16 products as the forward scan.  Writes
-//    dv, dw, dh0 and, per chunk, dS1 and dY for the second kernel.
-//  * chunk_bwd_kside_kernel -- one workgroup (4 waves, wave R = token block R)
-//    per (chunk, head), all chunks in parallel: the V-contractions above on
-//    MFMA, the in-chunk pair terms with the forward's factored decays (exact
-//    VALU sums on diagonal blocks whose decay span is too wide), the reverse
-//    cumsum, and the chain rule to dq, dk, db, dg.
+//    dh0 and, per chunk, dS1 and dY for the second kernel.
+//  * chunk_bwd_kside_kernel -- one workgroup (8 waves, two per 16-token block)
+//    per (chunk, head), all chunks in parallel: dv, dw from dY, the
+//    V-contractions above on MFMA over LDS-staged value slices, the in-chunk
+//    pair terms with the forward's factored decays (exact VALU sums on
+//    diagonal blocks whose decay span is too wide), the reverse cumsum, and
+//    the chain rule to dq, dk, db, dg.
 
 #include <type_traits>
 
@@ -153,11 +154,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
     const int gc0 = seq_chunk_base(p, n, bos, len);
     const int nch = static_cast<int>((len + kChunk - 1) / kChunk);
 
-    const TI *vp = static_cast<const TI *>(p.v);
-    const TI *wp = static_cast<const TI *>(p.w);
     const TI *dop = static_cast<const TI *>(p.dout);
-    TI *dvp = static_cast<TI *>(p.dv);
-    TI *dwp = static_cast<TI *>(p.dw);
     const st *wsb = static_cast<const st *>(p.blob);
     auto blob = [&](int gci) {
         return reinterpret_cast<const u32x4 *>(wsb + (static_cast<int64_t>(gci) * H + h) * BL::SIZE);
@@ -347,19 +344,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
                                        sf[2 * s2], sf[2 * s2 + 1]);
                     duf[rt] = pack4<PK>(acc);
                 }
-                // dY = X^T dU; dv = dY * w, dw = dY * v.
-                // v and w at this wave's (token, column) positions, for dv, dw.
-                float vv[4][4], ww[4][4];
-#pragma unroll
-                for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int tok = 16 * rt + 4 * kg + i;
-                        const bool ok = col_ok && tok < lc;
-                        const int64_t off = ((t0 + tok) * H + h) * V + col;
-                        vv[rt][i] = ok ? io<TI>::ld(vp, off) : 0.f;
-                        ww[rt][i] = ok ? io<TI>::ld(wp, off) : 0.f;
-                    }
+                // dY = X^T dU (dv = dY * w and dw = dY * v are formed by the K-side kernel).
                 st *dyb = static_cast<st *>(p.dys) + cb * (64 * VP);
 #pragma unroll
                 for (int rt = 0; rt < 4; ++rt) {
@@ -370,17 +355,6 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
                             acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::X + k16_block(rt, 2 * s2, 64) + 4 * l),
                                            ld_q4<PK>(Bk + BL::X + k16_block(rt, 2 * s2 + 1, 64) + 4 * l),
                                            duf[2 * s2], duf[2 * s2 + 1]);
-                    if (col_ok) {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int tok = 16 * rt + 4 * kg + i;
-                            if (tok < lc) {
-                                const int64_t off = ((t0 + tok) * H + h) * V + col;
-                                io<TI>::st(dvp, off, acc[i] * ww[rt][i]);
-                                io<TI>::st(dwp, off, acc[i] * vv[rt][i]);
-                            }
-                        }
-                    }
                     if (emit)
                         st_q4<PK>(dyb + k16_block(rt, vt, VP) + 4 * l,
                                   pack4<PK>(mma1<PK>(zero4(), pack4<PK>(acc), ident)));
@@ -424,61 +398,97 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
 }
 
 
-// Decay factor of the (row block Rb, column block Ib) pair at channel c, in
-// the factored pair products: 2^(decay strictly between the blocks) below the
-// diagonal, 2^(-block span) on it, 0 above it (T = in-block decay totals).
-__device__ __forceinline__ float pair_factor(const float (*sT)[128 + 4], int Rb, int Ib, int c)
-{
-    if (Ib > Rb) return 0.f;
-    if (Ib == Rb) return __builtin_amdgcn_exp2f(-sT[Rb][c]);
-    float ex = 0.f;
-#pragma unroll
-    for (int R2 = 1; R2 < 3; ++R2)
-        if (R2 > Ib && R2 < Rb) ex += sT[R2][c];
-    return __builtin_amdgcn_exp2f(ex);
-}
+// Four input values kept in their input format (16-bit inputs: two packed
+// registers instead of four), widened to fp32 on use.
+template <typename T>
+struct Raw4 {
+    uint2 u;
+    __device__ __forceinline__ void set(const float (&x)[4])
+    {
+        u.x = raw16(x[0]) | (raw16(x[1]) << 16);
+        u.y = raw16(x[2]) | (raw16(x[3]) << 16);
+    }
+    __device__ __forceinline__ float operator[](int i) const
+    {
+        const uint32_t w = (i < 2 ? u.x : u.y) >> (16 * (i & 1));
+        return wide16(w & 0xffffu);
+    }
+    static __device__ __forceinline__ uint32_t raw16(float x)
+    {
+        if constexpr (std::is_same<T, bf16_t>::value)
+            return f32_to_bf16_bits(x);
+        else
+            return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+    }
+    static __device__ __forceinline__ float wide16(uint32_t b)
+    {
+        if constexpr (std::is_same<T, bf16_t>::value)
+            return bf16_bits_to_f32(static_cast<uint16_t>(b));
+        else
+            return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+    }
+};
+template <>
+struct Raw4<float> {
+    float4 f;
+    __device__ __forceinline__ void set(const float (&x)[4]) { f = make_float4(x[0], x[1], x[2], x[3]); }
+    __device__ __forceinline__ float operator[](int i) const
+    {
+        return i == 0 ? f.x : (i == 1 ? f.y : (i == 2 ? f.z : f.w));
+    }
+};
 
 // ---------------------------------------------------------------------------
-// K-side gradients: one workgroup (4 waves) per (chunk, head).  Wave R owns
-// token rows 16R..16R+15; lane (m, kg) holds row 16R+m, channels
-// 16kt + 4kg + i ("A-order", as in the forward prep kernel).
+// K-side gradients: one workgroup of 8 waves per (chunk, head).  Wave
+// w = 2R + hh owns token rows 16R..16R+15 (lane (m, kg): row 16R+m) and the
+// channel tiles hh*NKH .. hh*NKH+NKH-1 (channels 16dt + 4kg + i, "A-order",
+// as in the forward prep kernel).  Both waves of a token block compute the
+// block's in-chunk pair tiles (dA, dL over the value dimension), so no wave
+// waits on another for them.
 // ---------------------------------------------------------------------------
 template <PrecKind PK, int KP, typename TI, typename TG>
-__global__ __launch_bounds__(256) void chunk_bwd_kside_kernel(BwdParams p)
+__global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
 {
     using P = Prec<PK>;
     using st = typename P::st;
     using Q = Q4<PK>;
     constexpr int NKT = KP / 16;
-    constexpr int NVS = 4;  // value tiles per staged slice (64 columns)
+    constexpr int NKH = NKT / 2;  // channel tiles per wave
     // dg is a reverse cumulative sum in which the in-chunk pair terms cancel
     // in exact arithmetic; to keep that cancellation accurate, operands that
     // reach dg (chunk states and U from the forward, the factor tiles) carry
     // fp32 precision: for 16-bit MFMA operands as two planes, x = hi + lo.
     constexpr int NPL = PK == PrecKind::F32 ? 1 : 2;
+    constexpr int NVS = PK == PrecKind::F32 ? 1 : 2;  // value tiles per staged slice
+    constexpr int EPU = 16 / static_cast<int>(sizeof(st));
+    constexpr int BLK = 256;
     // Transposed (B-order) factor tiles of every token block, for the pair products.
-    __shared__ __align__(16) st sKT[NPL][4][NKT][256];  // k * 2^(T_R - G)       (kend)
-    __shared__ __align__(16) st sQT[NPL][4][NKT][256];  // q * 2^G               (qb)
-    __shared__ __align__(16) st sET[NPL][4][NKT][256];  // e * 2^G               (eb)
-    // dO, U, dY of one 64-column value slice: A-order blocks (token tile, value tile).
-    __shared__ __align__(16) st sO[4 * NVS * 256];
-    __shared__ __align__(16) st sU[NPL][4 * NVS * 256];
-    __shared__ __align__(16) st sY[4 * NVS * 256];
-    __shared__ __align__(16) float sT[4][128 + 4];  // in-block decay totals (log2)
+    __shared__ __align__(16) st sKT[NPL][4][NKT][BLK];  // k * 2^(T_R - G)   (kend)
+    __shared__ __align__(16) st sQT[NPL][4][NKT][BLK];  // q * 2^G           (qb)
+    __shared__ __align__(16) st sET[NPL][4][NKT][BLK];  // e * 2^G           (eb)
+    // One staged value slice (NVS value tiles), A-order blocks.
+    constexpr int NB_U = NPL * 4 * NVS, NB_Y = 4 * NVS, NB_H = NPL * NKT * NVS, NB_D = NKT * NVS;
+    constexpr int NB = NB_U + NB_Y + NB_H + NB_D;  // contiguous workspace blocks per slice
+    __shared__ __align__(16) st sW[NB * BLK];      // U planes, dY, h planes, dh
+    __shared__ __align__(16) st sO[4 * NVS * BLK];  // dO
+    __shared__ __align__(16) float sT[4][KP];       // in-block decay totals (log2)
     __shared__ __align__(16) float sEr[4][KP];      // 2^(decay before block)
     __shared__ __align__(16) float sEa[4][KP];      // 2^(decay after block)
+    __shared__ __align__(16) float sPf[4][4][KP];   // pair factor of (row block, column block)
     __shared__ __align__(16) float sDG[4][KP];      // per-block sums of dG
+    __shared__ __align__(16) float sKK[4][KP];      // per-block sums of dKt * Kt
     __shared__ __align__(16) float sLast[KP];       // exp(G_last) rowsum(dS1 * S0)
-    __shared__ __align__(16) float sKK[4][KP];      // per-block sum_j dKt_j * Kt_j
+    __shared__ float sRow[2][2][64];                // per-half row sums (norms, then L2 dots)
+    __shared__ int sWide[4][2];
 
-    const int tid = threadIdx.x, R = tid >> 6, l = tid & 63, m = l & 15, kg = l >> 4;
+    const int tid = threadIdx.x, wv = tid >> 6, R = wv >> 1, hh = wv & 1;
+    const int l = tid & 63, m = l & 15, kg = l >> 4;
     const int gc = blockIdx.x, h = blockIdx.y;
     const int H = p.H, K = p.K, V = p.V, VP = p.VP;
 
     int n, jc;
     int64_t bos, len;
     locate_chunk(p, gc, n, jc, bos, len);
-    const int nch = static_cast<int>((len + kChunk - 1) / kChunk);
     const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
     const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
     const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
@@ -486,227 +496,334 @@ __global__ __launch_bounds__(256) void chunk_bwd_kside_kernel(BwdParams p)
     const bool row_ok = r < lc;
     const int64_t roff = ((t0 + r) * H + h) * K;
     const int64_t cb = static_cast<int64_t>(gc) * H + h;
-
-    const TI *q = static_cast<const TI *>(p.q);
-    const TI *k = static_cast<const TI *>(p.k);
-    const TI *b = static_cast<const TI *>(p.b);
-    const TG *g = static_cast<const TG *>(p.g);
     const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
     const Q ident = identity_q4<PK>(l);
 
-    // Row norms (kept), in-block log2 decay prefix of channel tile kt.
-    float invq, invk;
-    bool bigq, bigk;  // ||x|| above the F.normalize epsilon
-    auto row_tile = [&](int kt, float (&qv)[4], float (&kv)[4], float (&bv)[4], float (&gv)[4])
-        __attribute__((always_inline)) {
-        const int c0 = 16 * kt + 4 * kg;
-        load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv);
-        load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv);
-        load4<TI>(b, roff, c0, K, row_ok, p.vec_ok, bv);
-        load4<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) gv[i] = row16_scan(gv[i] * kLog2e);
-    };
-    {
-        float sq = 0.f, sk = 0.f;
-#pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-            float qv[4], kv[4];
-            const int c0 = 16 * kt + 4 * kg;
-            load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv);
-            load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                sq = fmaf(qv[i], qv[i], sq);
-                sk = fmaf(kv[i], kv[i], sk);
-            }
-        }
-        sq += __shfl_xor(sq, 16, 64);
-        sq += __shfl_xor(sq, 32, 64);
-        sk += __shfl_xor(sk, 16, 64);
-        sk += __shfl_xor(sk, 32, 64);
-        invq = l2 ? 1.0f / fmaxf(sqrtf(sq), 1e-6f) : 1.0f;
-        invk = l2 ? 1.0f / fmaxf(sqrtf(sk), 1e-6f) : 1.0f;
-        bigq = sqrtf(sq) > 1e-6f;
-        bigk = sqrtf(sk) > 1e-6f;
-    }
-    const float qmul = invq * p.scale;
-
-    // Block totals and the wide-span flag of this wave's diagonal block.
-    bool wide = false;
-#pragma unroll
-    for (int kt = 0; kt < NKT; ++kt) {
-        float qv[4], kv[4], bv[4], gv[4];
-        row_tile(kt, qv, kv, bv, gv);
-        if (m == 15) {
-            *reinterpret_cast<float4 *>(&sT[R][16 * kt + 4 * kg]) = make_float4(gv[0], gv[1], gv[2], gv[3]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) wide = wide || (-gv[i] > kDiagSpanLimit2);
-        }
-    }
-    const bool wave_slow = __ballot(wide) != 0;
-    __syncthreads();
-    for (int e = tid; e < 4 * KP; e += 256) {
-        const int Rb = e / KP, c = e % KP;
-        float cum = 0.f, after = 0.f;
-#pragma unroll
-        for (int R2 = 0; R2 < 4; ++R2) {
-            if (R2 < Rb) cum += sT[R2][c];
-            if (R2 > Rb) after += sT[R2][c];
-        }
-        sEr[Rb][c] = fexp2(cum);
-        sEa[Rb][c] = fexp2(after);
-    }
-    // Factor tiles, transposed by an identity product.
-#pragma unroll
-    for (int kt = 0; kt < NKT; ++kt) {
-        float qv[4], kv[4], bv[4], gv[4];
-        row_tile(kt, qv, kv, bv, gv);
-        const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][16 * kt + 4 * kg]);
-        const float trv[4] = {tr.x, tr.y, tr.z, tr.w};
-        float qb[4], eb[4], ke[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float kn = kv[i] * invk;
-            const float e1 = fexp2(gv[i]);
-            qb[i] = qv[i] * qmul * e1;
-            eb[i] = bv[i] * kn * e1;
-            ke[i] = kn * fexp2(trv[i] - gv[i]);
-        }
-        auto put = [&](st (*dst)[4][NKT][256], const float (&x)[4]) __attribute__((always_inline)) {
-            const Q hi = pack4<PK>(x[0], x[1], x[2], x[3]);
-            st_q4<PK>(&dst[0][R][kt][4 * l], pack4<PK>(mma1<PK>(zero4(), hi, ident)));
-            if constexpr (NPL == 2) {
-                float xh[4];
-                unpack4<PK>(hi, xh);
-                const Q lo = pack4<PK>(x[0] - xh[0], x[1] - xh[1], x[2] - xh[2], x[3] - xh[3]);
-                st_q4<PK>(&dst[1][R][kt][4 * l], pack4<PK>(mma1<PK>(zero4(), lo, ident)));
-            }
-        };
-        put(sKT, ke);
-        put(sQT, qb);
-        put(sET, eb);
-    }
-
-    // G_last term, part 1: exp(G_last) rowsum(dS1 * S0).  (With part 2,
-    // sum_j dKt_j Kt_j, this is rowsum(dS1 * S1) written through the saved S0
-    // and U only, so it stays consistent with the other terms of dg.)  Wave R
-    // takes channel tiles R, R+4, ...
-    {
-        const st *dh = static_cast<const st *>(p.dhs) + cb * (KP * VP);
-        const st *s0 = static_cast<const st *>(p.hs) + cb * (NPL * KP * VP);
-        for (int dt = R; dt < NKT; dt += 4) {
-            float acc = 0.f;
-            for (int vt = 0; vt < VP / 16; ++vt) {
-                float a[4], c[4];
-                unpack4<PK>(ld_q4<PK>(dh + k16_block(dt, vt, VP) + 4 * l), a);
-#pragma unroll
-                for (int pl = 0; pl < NPL; ++pl) {
-                    unpack4<PK>(ld_q4<PK>(s0 + pl * (KP * VP) + k16_block(dt, vt, VP) + 4 * l), c);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc = fmaf(a[i], c[i], acc);
-                }
-            }
-            acc += __shfl_xor(acc, 16, 64);
-            acc += __shfl_xor(acc, 32, 64);
-            const int c = 16 * dt + m;
-            if (kg == 0) sLast[c] = acc * fexp2(sT[0][c] + sT[1][c] + sT[2][c] + sT[3][c]);
-        }
-    }
-
-    // V-contractions, one staged 64-column slice at a time:
-    //   aT[J] = dAqk^T tile (J, R)    lT[J] = -dL^T tile (J, R)     (J <= R)
-    //   aN[I] = dAqk tile (I, R)      lN[I] = -dL tile (I, R)       (I >= R)
-    //   cq[dt] = dQbar tile, ce[dt] = -dEbar tile, ck[dt] = dKtilde tile (row data)
-    f32x4 aT[4], lT[4], aN[4], lN[4], cq[NKT], ce[NKT], ck[NKT];
-#pragma unroll
-    for (int J = 0; J < 4; ++J) aT[J] = lT[J] = aN[J] = lN[J] = zero4();
-#pragma unroll
-    for (int dt = 0; dt < NKT; ++dt) cq[dt] = ce[dt] = ck[dt] = zero4();
     const st *hsb = static_cast<const st *>(p.hs) + cb * (NPL * KP * VP);
     const st *dhb = static_cast<const st *>(p.dhs) + cb * (KP * VP);
     const st *usb = static_cast<const st *>(p.us) + cb * (NPL * 64 * VP);
     const st *dyb = static_cast<const st *>(p.dys) + cb * (64 * VP);
     const TI *dop = static_cast<const TI *>(p.dout);
     const int NVT = VP / 16;
-    constexpr int EPU = 16 / static_cast<int>(sizeof(st));
-    for (int vt0 = 0; vt0 < NVT; vt0 += NVS) {
-        __syncthreads();  // previous slice fully consumed
-        // U and dY: contiguous A-order blocks, copied as 16-byte units.
-        for (int u = tid; u < 4 * NVS * 256 / EPU; u += 256) {
-            const int e = u * EPU, blk = e >> 8, rt = blk / NVS, vl = blk % NVS;
-            const bool ok = vt0 + vl < NVT;
-            const int64_t src = k16_block(rt, vt0 + vl, VP) + (e & 255);
-#pragma unroll
-            for (int pl = 0; pl < NPL; ++pl)
-                *reinterpret_cast<u32x4 *>(sU[pl] + e) =
-                    ok ? *reinterpret_cast<const u32x4 *>(usb + pl * (64 * VP) + src) : u32x4{0, 0, 0, 0};
-            *reinterpret_cast<u32x4 *>(sY + e) = ok ? *reinterpret_cast<const u32x4 *>(dyb + src) : u32x4{0, 0, 0, 0};
+
+    // ---- slice staging: workspace blocks as 16-byte units, dO rows as groups of 4 ----
+    constexpr int UPB = BLK / EPU;                  // units per block
+    constexpr int NUW = NB * UPB;                    // workspace units per slice
+    constexpr int NUO = 64 * 4 * NVS;                // dO groups of 4 values per slice
+    constexpr int NPRE_W = (NUW + 511) / 512, NPRE_O = (NUO + 511) / 512;
+    // Source of workspace unit u of slice vt0 (nullptr past V).
+    auto wsrc = [&](int u, int vt0) __attribute__((always_inline)) -> const st * {
+        const int b = u / UPB, e = (u % UPB) * EPU;
+        int rowt, vl;
+        const st *base;
+        if (b < NB_U) {
+            const int pl = b / (4 * NVS), rb = b % (4 * NVS);
+            rowt = rb / NVS; vl = rb % NVS;
+            base = usb + pl * (64 * VP);
+        } else if (b < NB_U + NB_Y) {
+            const int rb = b - NB_U;
+            rowt = rb / NVS; vl = rb % NVS;
+            base = dyb;
+        } else if (b < NB_U + NB_Y + NB_H) {
+            const int rb = b - NB_U - NB_Y, pl = rb / (NKT * NVS), r2 = rb % (NKT * NVS);
+            rowt = r2 / NVS; vl = r2 % NVS;
+            base = hsb + pl * (KP * VP);
+        } else {
+            const int rb = b - NB_U - NB_Y - NB_H;
+            rowt = rb / NVS; vl = rb % NVS;
+            base = dhb;
         }
-        // dO: rows of the chunk, 4 consecutive values per A-order group.
-        for (int task = tid; task < 64 * NVS * 4; task += 256) {
-            const int tok = task / (NVS * 4), grp = task % (NVS * 4);
-            const int c = 16 * vt0 + 4 * grp;
-            float x[4];
+        if (vt0 + vl >= NVT) return nullptr;
+        return base + k16_block(rowt, vt0 + vl, VP) + e;
+    };
+    struct Pre {
+        u32x4 w[NPRE_W];
+        float o[NPRE_O][4];
+    };
+    auto issue_slice = [&](Pre &pr, int vt0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int a = 0; a < NPRE_W; ++a) {
+            const int u = tid + 512 * a;
+            const st *src = u < NUW ? wsrc(u, vt0) : nullptr;
+            pr.w[a] = src ? *reinterpret_cast<const u32x4 *>(src) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int a = 0; a < NPRE_O; ++a) {
+            const int u = tid + 512 * a;
+            const int tok = u / (4 * NVS), c = 16 * vt0 + 4 * (u % (4 * NVS));
+            const bool ok = u < NUO && tok < lc;
             const int64_t off = ((t0 + tok) * H + h) * static_cast<int64_t>(V);
-            const bool ok = tok < lc;
             if (ok && (V % 4) == 0 && c + 4 <= V) {
-                load4<TI>(dop, off, c, V, true, 1, x);
+                load4<TI>(dop, off, c, V, true, 1, pr.o[a]);
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[i] = (ok && c + i < V) ? io<TI>::ld(dop, off + c + i) : 0.f;
+                for (int i = 0; i < 4; ++i) pr.o[a][i] = (ok && c + i < V) ? io<TI>::ld(dop, off + c + i) : 0.f;
             }
-            const int vl = grp >> 2, kgo = grp & 3;
-            st_q4<PK>(sO + k16_block(tok >> 4, vl, 16 * NVS) + 4 * ((tok & 15) + 16 * kgo),
-                      pack4<PK>(x[0], x[1], x[2], x[3]));
         }
+    };
+    auto land_slice = [&](const Pre &pr) __attribute__((always_inline)) {
+#pragma unroll
+        for (int a = 0; a < NPRE_W; ++a) {
+            const int u = tid + 512 * a;
+            if (u < NUW) *reinterpret_cast<u32x4 *>(sW + u * EPU) = pr.w[a];
+        }
+#pragma unroll
+        for (int a = 0; a < NPRE_O; ++a) {
+            const int u = tid + 512 * a;
+            if (u >= NUO) continue;
+            const int tok = u / (4 * NVS), grp = u % (4 * NVS);
+            st_q4<PK>(sO + k16_block(tok >> 4, grp >> 2, 16 * NVS) + 4 * ((tok & 15) + 16 * (grp & 3)),
+                      pack4<PK>(pr.o[a][0], pr.o[a][1], pr.o[a][2], pr.o[a][3]));
+        }
+    };
+    const st *sUb = sW;
+    const st *sYb = sW + NB_U * BLK;
+    const st *sHb = sW + (NB_U + NB_Y) * BLK;
+    const st *sDb = sW + (NB_U + NB_Y + NB_H) * BLK;
+    auto blkU = [&](int pl, int rt, int vl) { return sUb + ((pl * 4 + rt) * NVS + vl) * BLK + 4 * l; };
+    auto blkY = [&](int rt, int vl) { return sYb + (rt * NVS + vl) * BLK + 4 * l; };
+    auto blkH = [&](int pl, int dt, int vl) { return sHb + ((pl * NKT + dt) * NVS + vl) * BLK + 4 * l; };
+    auto blkD = [&](int dt, int vl) { return sDb + (dt * NVS + vl) * BLK + 4 * l; };
+    auto blkO = [&](int rt, int vl) { return sO + (rt * NVS + vl) * BLK + 4 * l; };
+    // acc += A . B^T over the staged value tiles (A, B given as tile loaders).
+    auto mmav = [&](f32x4 acc, const st *a0, const st *b0) __attribute__((always_inline)) {
+        if constexpr (NVS == 2)
+            return mma2<PK>(acc, ld_q4<PK>(a0), ld_q4<PK>(a0 + BLK), ld_q4<PK>(b0), ld_q4<PK>(b0 + BLK));
+        else
+            return mma1<PK>(acc, ld_q4<PK>(a0), ld_q4<PK>(b0));
+    };
+
+    Pre pre;
+    issue_slice(pre, 0);
+
+    // ---- rows of this wave: raw q, k, b (input format) and the in-block log2
+    // decay prefix G ----
+    // (Loaded here for the factor tiles and again after the V-contractions,
+    // so that they are not live across them.)
+    auto load_rows = [&](Raw4<TI> (&qv)[NKH], Raw4<TI> (&kv)[NKH], Raw4<TI> (&bv)[NKH],
+                         float (&gv)[NKH][4]) __attribute__((always_inline)) {
+        const TI *q = static_cast<const TI *>(p.q);
+        const TI *k = static_cast<const TI *>(p.k);
+        const TI *b = static_cast<const TI *>(p.b);
+        const TG *g = static_cast<const TG *>(p.g);
+#pragma unroll
+        for (int j = 0; j < NKH; ++j) {
+            const int c0 = 16 * (hh * NKH + j) + 4 * kg;
+            float x[4];
+            load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, x);
+            qv[j].set(x);
+            load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, x);
+            kv[j].set(x);
+            load4<TI>(b, roff, c0, K, row_ok, p.vec_ok, x);
+            bv[j].set(x);
+            load4<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv[j]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gv[j][i] = row16_scan(gv[j][i] * kLog2e);
+        }
+    };
+    float invq, invk, qmul;
+    bool bigq, bigk, wave_slow;
+    {
+    Raw4<TI> qv[NKH], kv[NKH], bv[NKH];
+    float gv[NKH][4];
+    load_rows(qv, kv, bv, gv);
+    {
+        float sq = 0.f, sk = 0.f;
+        bool wide = false;
+#pragma unroll
+        for (int j = 0; j < NKH; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sq = fmaf(qv[j][i], qv[j][i], sq);
+                sk = fmaf(kv[j][i], kv[j][i], sk);
+            }
+            if (m == 15) {
+                *reinterpret_cast<float4 *>(&sT[R][16 * (hh * NKH + j) + 4 * kg]) =
+                    make_float4(gv[j][0], gv[j][1], gv[j][2], gv[j][3]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wide = wide || (-gv[j][i] > kDiagSpanLimit2);
+            }
+        }
+        sq += __shfl_xor(sq, 16, 64);
+        sq += __shfl_xor(sq, 32, 64);
+        sk += __shfl_xor(sk, 16, 64);
+        sk += __shfl_xor(sk, 32, 64);
+        if (kg == 0) {
+            sRow[0][hh][r] = sq;
+            sRow[1][hh][r] = sk;
+        }
+        const bool w_any = __ballot(wide) != 0;
+        if (l == 0) sWide[R][hh] = w_any ? 1 : 0;
+    }
+    __syncthreads();
+    const float nq = sqrtf(sRow[0][0][r] + sRow[0][1][r]), nk = sqrtf(sRow[1][0][r] + sRow[1][1][r]);
+    invq = l2 ? 1.0f / fmaxf(nq, 1e-6f) : 1.0f;
+    invk = l2 ? 1.0f / fmaxf(nk, 1e-6f) : 1.0f;
+    bigq = nq > 1e-6f;
+    bigk = nk > 1e-6f;
+    qmul = invq * p.scale;
+    wave_slow = (sWide[R][0] | sWide[R][1]) != 0;
+    for (int e = tid; e < 4 * KP; e += 512) {
+        const int Rb = e / KP, c = e % KP;
+        const float t[4] = {sT[0][c], sT[1][c], sT[2][c], sT[3][c]};
+        float cum = 0.f, after = 0.f;
+#pragma unroll
+        for (int R2 = 0; R2 < 4; ++R2) {
+            if (R2 < Rb) cum += t[R2];
+            if (R2 > Rb) after += t[R2];
+        }
+        sEr[Rb][c] = fexp2(cum);
+        sEa[Rb][c] = fexp2(after);
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+            float ex = 0.f;
+            if (I == Rb) {
+                ex = -t[Rb];
+            } else {
+#pragma unroll
+                for (int R2 = 0; R2 < 4; ++R2)
+                    if (R2 > I && R2 < Rb) ex += t[R2];
+            }
+            sPf[Rb][I][c] = I > Rb ? 0.f : fexp2(ex);
+        }
+    }
+    // Factor tiles of this wave's rows and channels, transposed by an identity product.
+#pragma unroll
+    for (int j = 0; j < NKH; ++j) {
+        const int dt = hh * NKH + j;
+        const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][16 * dt + 4 * kg]);
+        const float trv[4] = {tr.x, tr.y, tr.z, tr.w};
+        float qb[4], eb[4], ke[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float kn = kv[j][i] * invk;
+            const float e1 = fexp2(gv[j][i]);
+            qb[i] = qv[j][i] * qmul * e1;
+            eb[i] = bv[j][i] * kn * e1;
+            ke[i] = kn * fexp2(trv[i] - gv[j][i]);
+        }
+        auto put = [&](st (*dst)[4][NKT][BLK], const float (&x)[4]) __attribute__((always_inline)) {
+            const Q hi = pack4<PK>(x[0], x[1], x[2], x[3]);
+            st_q4<PK>(&dst[0][R][dt][4 * l], pack4<PK>(mma1<PK>(zero4(), hi, ident)));
+            if constexpr (NPL == 2) {
+                float xh[4];
+                unpack4<PK>(hi, xh);
+                const Q lo = pack4<PK>(x[0] - xh[0], x[1] - xh[1], x[2] - xh[2], x[3] - xh[3]);
+                st_q4<PK>(&dst[1][R][dt][4 * l], pack4<PK>(mma1<PK>(zero4(), lo, ident)));
+            }
+        };
+        put(sKT, ke);
+        put(sQT, qb);
+        put(sET, eb);
+    }
+    }
+
+    // ---- V-contractions over staged slices ----
+    //   aT[J] = dAqk^T tile (J, R)    lT[J] = dY U^T tile^T (J, R)    (J <= R)
+    //   aN[I] = dAqk tile (I, R)      lN[I] = dY U^T tile (I, R)      (I >= R)
+    //   cq[j] = dQbar, ce[j] = dY S0^T, ck[j] = dKtilde (row data, channel tile hh*NKH+j)
+    f32x4 aT[4], lT[4], aN[4], lN[4], cq[NKH], ce[NKH], ck[NKH];
+#pragma unroll
+    for (int J = 0; J < 4; ++J) aT[J] = lT[J] = aN[J] = lN[J] = zero4();
+#pragma unroll
+    for (int j = 0; j < NKH; ++j) cq[j] = ce[j] = ck[j] = zero4();
+    TI *dvp = static_cast<TI *>(p.dv);
+    TI *dwp = static_cast<TI *>(p.dw);
+    const TI *vp = static_cast<const TI *>(p.v);
+    const TI *wp = static_cast<const TI *>(p.w);
+    for (int vt0 = 0; vt0 < NVT; vt0 += NVS) {
+        __syncthreads();  // previous slice fully consumed
+        land_slice(pre);
         __syncthreads();
+        if (vt0 + NVS < NVT) issue_slice(pre, vt0 + NVS);
+        // dv = dY * w, dw = dY * v for this slice (one group of 4 values per thread).
+        for (int u = tid; u < 64 * 4 * NVS; u += 512) {
+            const int tok = u / (4 * NVS), grp = u % (4 * NVS);
+            const int c = 16 * vt0 + 4 * grp;
+            if (tok >= lc || c >= V) continue;
+            float y[4];
+            unpack4<PK>(ld_q4<PK>(sYb + ((tok >> 4) * NVS + (grp >> 2)) * BLK + 4 * ((tok & 15) + 16 * (grp & 3))), y);
+            const int64_t off = ((t0 + tok) * H + h) * static_cast<int64_t>(V) + c;
 #pragma unroll
-        for (int s2 = 0; s2 < NVS / 2; ++s2) {
-            const int va = 2 * s2, vb = 2 * s2 + 1;
-            const Q oR0 = ld_q4<PK>(sO + k16_block(R, va, 16 * NVS) + 4 * l);
-            const Q oR1 = ld_q4<PK>(sO + k16_block(R, vb, 16 * NVS) + 4 * l);
-            const Q yR0 = ld_q4<PK>(sY + k16_block(R, va, 16 * NVS) + 4 * l);
-            const Q yR1 = ld_q4<PK>(sY + k16_block(R, vb, 16 * NVS) + 4 * l);
-            const bool oka = vt0 + va < NVT, okb = vt0 + vb < NVT;
-#pragma unroll
-            for (int pl = 0; pl < NPL; ++pl) {
-                const Q uR0 = ld_q4<PK>(sU[pl] + k16_block(R, va, 16 * NVS) + 4 * l);
-                const Q uR1 = ld_q4<PK>(sU[pl] + k16_block(R, vb, 16 * NVS) + 4 * l);
-#pragma unroll
-                for (int J = 0; J < 4; ++J) {
-                    if (J <= R) {
-                        const Q u0 = ld_q4<PK>(sU[pl] + k16_block(J, va, 16 * NVS) + 4 * l);
-                        const Q u1 = ld_q4<PK>(sU[pl] + k16_block(J, vb, 16 * NVS) + 4 * l);
-                        aT[J] = mma2<PK>(aT[J], u0, u1, oR0, oR1);
-                        lT[J] = mma2<PK>(lT[J], u0, u1, yR0, yR1);
-                    }
-                    if (J >= R) {
-                        aN[J] = mma2<PK>(aN[J], ld_q4<PK>(sO + k16_block(J, va, 16 * NVS) + 4 * l),
-                                         ld_q4<PK>(sO + k16_block(J, vb, 16 * NVS) + 4 * l), uR0, uR1);
-                        lN[J] = mma2<PK>(lN[J], ld_q4<PK>(sY + k16_block(J, va, 16 * NVS) + 4 * l),
-                                         ld_q4<PK>(sY + k16_block(J, vb, 16 * NVS) + 4 * l), uR0, uR1);
-                    }
+            for (int i = 0; i < 4; ++i) {
+                if (c + i < V) {
+                    const float vv = io<TI>::ld(vp, off + i), ww = io<TI>::ld(wp, off + i);
+                    io<TI>::st(dvp, off + i, y[i] * ww);
+                    io<TI>::st(dwp, off + i, y[i] * vv);
                 }
+            }
+        }
 #pragma unroll
-                for (int dt = 0; dt < NKT; ++dt) {
-                    const Q z = pack4<PK>(0.f, 0.f, 0.f, 0.f);
-                    const st *hp = hsb + pl * (KP * VP);
-                    const Q h0 = oka ? ld_q4<PK>(hp + k16_block(dt, vt0 + va, VP) + 4 * l) : z;
-                    const Q h1 = okb ? ld_q4<PK>(hp + k16_block(dt, vt0 + vb, VP) + 4 * l) : z;
-                    cq[dt] = mma2<PK>(cq[dt], h0, h1, oR0, oR1);
-                    ce[dt] = mma2<PK>(ce[dt], h0, h1, yR0, yR1);
-                    const Q d0 = oka ? ld_q4<PK>(dhb + k16_block(dt, vt0 + va, VP) + 4 * l) : z;
-                    const Q d1 = okb ? ld_q4<PK>(dhb + k16_block(dt, vt0 + vb, VP) + 4 * l) : z;
-                    ck[dt] = mma2<PK>(ck[dt], d0, d1, uR0, uR1);
+        for (int pl = 0; pl < NPL; ++pl) {
+#pragma unroll
+            for (int J = 0; J < 4; ++J) {
+                if (J <= R) {
+                    aT[J] = mmav(aT[J], blkU(pl, J, 0), blkO(R, 0));
+                    lT[J] = mmav(lT[J], blkU(pl, J, 0), blkY(R, 0));
                 }
+                if (J >= R) {
+                    aN[J] = mmav(aN[J], blkO(J, 0), blkU(pl, R, 0));
+                    lN[J] = mmav(lN[J], blkY(J, 0), blkU(pl, R, 0));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < NKH; ++j) {
+                const int dt = hh * NKH + j;
+                cq[j] = mmav(cq[j], blkH(pl, dt, 0), blkO(R, 0));
+                ce[j] = mmav(ce[j], blkH(pl, dt, 0), blkY(R, 0));
+                ck[j] = mmav(ck[j], blkD(dt, 0), blkU(pl, R, 0));
             }
         }
     }
 
-    // Causal masks (and the signs of dL); the diagonal tiles are kept for the
-    // exact path.  aT/lT lane values: row 16R+m, column 16J+4kg+i; aN/lN:
-    // row 16I+4kg+i, column 16R+m.
+    Raw4<TI> qv[NKH], kv[NKH], bv[NKH];
+    float gv[NKH][4];
+    load_rows(qv, kv, bv, gv);
+
+    // ---- G_last term: part 1 exp(G_last) rowsum(dS1 * S0) (channel tile wv),
+    // part 2 this block's sum of dKt * Kt (ck = dKt here).  Together they are
+    // rowsum(dS1 * S1) written through the saved S0 and U only. ----
+    if (wv < NKT) {
+        const int dt = wv;
+        float acc = 0.f;
+        for (int vt = 0; vt < NVT; ++vt) {
+            float a[4], c[4];
+            unpack4<PK>(ld_q4<PK>(dhb + k16_block(dt, vt, VP) + 4 * l), a);
+#pragma unroll
+            for (int pl = 0; pl < NPL; ++pl) {
+                unpack4<PK>(ld_q4<PK>(hsb + pl * (KP * VP) + k16_block(dt, vt, VP) + 4 * l), c);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc = fmaf(a[i], c[i], acc);
+            }
+        }
+        acc += __shfl_xor(acc, 16, 64);
+        acc += __shfl_xor(acc, 32, 64);
+        const int c = 16 * dt + m;
+        if (kg == 0) sLast[c] = acc * fexp2(sT[0][c] + sT[1][c] + sT[2][c] + sT[3][c]);
+    }
+#pragma unroll
+    for (int j = 0; j < NKH; ++j) {
+        const int dt = hh * NKH + j, c0 = 16 * dt + 4 * kg;
+        const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][c0]);
+        const float4 ea = *reinterpret_cast<const float4 *>(&sEa[R][c0]);
+        const float4 er = *reinterpret_cast<const float4 *>(&sEr[R][c0]);
+        const float trv[4] = {tr.x, tr.y, tr.z, tr.w}, eav[4] = {ea.x, ea.y, ea.z, ea.w};
+        const float erv[4] = {er.x, er.y, er.z, er.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float kt_ = kv[j][i] * invk * fexp2(trv[i] - gv[j][i]) * eav[i];
+            const float tot = row16_scan(ck[j][i] * kt_);
+            if (m == 15) sKK[R][c0 + i] = tot;
+            // Start the row-data accumulators from the V-contractions scaled by the
+            // decay before / after the block: Er * dQbar, Er * dEbar (= -Er dY S0^T),
+            // Ea * dKtilde.
+            cq[j][i] *= erv[i];
+            ce[j][i] *= -erv[i];
+            ck[j][i] *= eav[i];
+        }
+    }
+
+    // ---- causal masks and signs; diagonal tiles kept for the exact path ----
     f32x4 dAd = zero4(), dLd = zero4(), dANd = zero4(), dLNd = zero4();
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
@@ -726,38 +843,6 @@ __global__ __launch_bounds__(256) void chunk_bwd_kside_kernel(BwdParams p)
             dLNd = lN[J];
         }
     }
-
-    // G_last term, part 2: this block's rows of sum_j dKt_j Kt_j (ck = dKt here).
-#pragma unroll
-    for (int dt = 0; dt < NKT; ++dt) {
-        float qv[4], kv[4], bv[4], gv[4];
-        row_tile(dt, qv, kv, bv, gv);
-        const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][16 * dt + 4 * kg]);
-        const float4 ea = *reinterpret_cast<const float4 *>(&sEa[R][16 * dt + 4 * kg]);
-        const float trv[4] = {tr.x, tr.y, tr.z, tr.w}, eav[4] = {ea.x, ea.y, ea.z, ea.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float kt_ = kv[i] * invk * fexp2(trv[i] - gv[i]) * eav[i];
-            const float tot = row16_scan(ck[dt][i] * kt_);
-            if (m == 15) sKK[R][16 * dt + 4 * kg + i] = tot;
-        }
-    }
-
-    // Pair products.  The row-data accumulators start from the V-contractions
-    // scaled by the decay before / after the block: cq <- Er * dQbar,
-    // ce <- Er * dEbar (ce held +dY S0^T, hence the sign), ck <- Ea * dKtilde.
-#pragma unroll
-    for (int dt = 0; dt < NKT; ++dt) {
-        const float4 er = *reinterpret_cast<const float4 *>(&sEr[R][16 * dt + 4 * kg]);
-        const float4 ea = *reinterpret_cast<const float4 *>(&sEa[R][16 * dt + 4 * kg]);
-        const float erv[4] = {er.x, er.y, er.z, er.w}, eav[4] = {ea.x, ea.y, ea.z, ea.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            cq[dt][i] *= erv[i];
-            ce[dt][i] *= -erv[i];
-            ck[dt][i] *= eav[i];
-        }
-    }
     Q baT[4], blT[4], baN[4], blN[4];
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
@@ -766,12 +851,13 @@ __global__ __launch_bounds__(256) void chunk_bwd_kside_kernel(BwdParams p)
         baN[J] = pack4<PK>(aN[J]);
         blN[J] = pack4<PK>(lN[J]);
     }
-    // Factor tile (hi + lo planes) times a per-lane decay factor, split again
-    // into hi + lo operands.
+
+    // ---- pair products: factor tile (hi + lo) times the pair factor of its
+    // block pair, split again into hi + lo operands ----
     struct Q2 {
         Q hi, lo;
     };
-    auto scaled = [&](const st (*tile)[4][NKT][256], int blk, int dt, float f) __attribute__((always_inline)) {
+    auto scaled = [&](const st (*tile)[4][NKT][BLK], int blk, int dt, float f) __attribute__((always_inline)) {
         float x[4];
         unpack4<PK>(ld_q4<PK>(&tile[0][blk][dt][4 * l]), x);
         if constexpr (NPL == 2) {
@@ -780,16 +866,14 @@ __global__ __launch_bounds__(256) void chunk_bwd_kside_kernel(BwdParams p)
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[i] += y[i];
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] *= f;
-        Q2 r;
-        r.hi = pack4<PK>(x[0], x[1], x[2], x[3]);
+        Q2 res;
+        res.hi = pack4<PK>(x[0] * f, x[1] * f, x[2] * f, x[3] * f);
         if constexpr (NPL == 2) {
             float xh[4];
-            unpack4<PK>(r.hi, xh);
-            r.lo = pack4<PK>(x[0] - xh[0], x[1] - xh[1], x[2] - xh[2], x[3] - xh[3]);
+            unpack4<PK>(res.hi, xh);
+            res.lo = pack4<PK>(x[0] * f - xh[0], x[1] * f - xh[1], x[2] * f - xh[2], x[3] * f - xh[3]);
         }
-        return r;
+        return res;
     };
     auto mma2x = [&](f32x4 acc, const Q2 &a0, const Q2 &a1, Q b0, Q b1) __attribute__((always_inline)) {
         acc = mma2<PK>(acc, a0.hi, a1.hi, b0, b1);
@@ -797,111 +881,97 @@ __global__ __launch_bounds__(256) void chunk_bwd_kside_kernel(BwdParams p)
         return acc;
     };
 #pragma unroll
-    for (int dt = 0; dt < NKT; ++dt) {
+    for (int j = 0; j < NKH; ++j) {
+        const int dt = hh * NKH + j;
         const int c = 16 * dt + m;  // channel of this lane in the transposed tiles
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             const int J0 = 2 * s2, J1 = 2 * s2 + 1;
-            // Terms of dq, de: column blocks J <= R.
-            if (J0 <= R) {
-                const float f0 = (J0 == R && wave_slow) ? 0.f : pair_factor(sT, R, J0, c);
-                const float f1 = (J1 == R && wave_slow) ? 0.f : pair_factor(sT, R, J1, c);
+            if (J0 <= R) {  // dq, de: column blocks J <= R
+                const float f0 = (J0 == R && wave_slow) ? 0.f : sPf[R][J0][c];
+                const float f1 = (J1 == R && wave_slow) ? 0.f : sPf[R][J1][c];
                 const Q2 a0 = scaled(sKT, J0, dt, f0), a1 = scaled(sKT, J1, dt, f1);
-                cq[dt] = mma2x(cq[dt], a0, a1, baT[J0], baT[J1]);
-                ce[dt] = mma2x(ce[dt], a0, a1, blT[J0], blT[J1]);
+                cq[j] = mma2x(cq[j], a0, a1, baT[J0], baT[J1]);
+                ce[j] = mma2x(ce[j], a0, a1, blT[J0], blT[J1]);
             }
-            // Terms of dk: row blocks I >= R.
-            if (J1 >= R) {
-                const float f0 = (J0 == R && wave_slow) ? 0.f : pair_factor(sT, J0, R, c);
-                const float f1 = (J1 == R && wave_slow) ? 0.f : pair_factor(sT, J1, R, c);
-                ck[dt] = mma2x(ck[dt], scaled(sQT, J0, dt, f0), scaled(sQT, J1, dt, f1), baN[J0], baN[J1]);
-                ck[dt] = mma2x(ck[dt], scaled(sET, J0, dt, f0), scaled(sET, J1, dt, f1), blN[J0], blN[J1]);
+            if (J1 >= R) {  // dk: row blocks I >= R
+                const float f0 = (J0 == R && wave_slow) ? 0.f : sPf[J0][R][c];
+                const float f1 = (J1 == R && wave_slow) ? 0.f : sPf[J1][R][c];
+                ck[j] = mma2x(ck[j], scaled(sQT, J0, dt, f0), scaled(sQT, J1, dt, f1), baN[J0], baN[J1]);
+                ck[j] = mma2x(ck[j], scaled(sET, J0, dt, f0), scaled(sET, J1, dt, f1), blN[J0], blN[J1]);
             }
         }
     }
 
-    // Row data: dq = 2^G cq, de = 2^G ce, dk = 2^(T_R - G) ck, the exact
-    // diagonal terms of wide blocks, dG, and its per-block column sums.
-    float pq = 0.f, pk = 0.f;  // row sums for the L2-norm chain rule
+    // ---- row data: dq = 2^G cq, de = 2^G ce, dk = 2^(T_R - G) ck, exact
+    // diagonal terms of wide blocks, dG with its in-block suffix sums ----
+    float pq = 0.f, pk = 0.f;  // row dots for the L2-norm chain rule
 #pragma unroll
-    for (int dt = 0; dt < NKT; ++dt) {
-        float qv[4], kv[4], bv[4], gv[4];
-        row_tile(dt, qv, kv, bv, gv);
-        const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][16 * dt + 4 * kg]);
+    for (int j = 0; j < NKH; ++j) {
+        const int dt = hh * NKH + j, c0 = 16 * dt + 4 * kg;
+        const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][c0]);
         const float trv[4] = {tr.x, tr.y, tr.z, tr.w};
         float qn[4], kn[4], en[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            qn[i] = qv[i] * qmul;
-            kn[i] = kv[i] * invk;
-            en[i] = bv[i] * kn[i];
-            cq[dt][i] *= fexp2(gv[i]);
-            ce[dt][i] *= fexp2(gv[i]);
-            ck[dt][i] *= fexp2(trv[i] - gv[i]);
+            qn[i] = qv[j][i] * qmul;
+            kn[i] = kv[j][i] * invk;
+            en[i] = bv[j][i] * kn[i];
+            cq[j][i] *= fexp2(gv[j][i]);
+            ce[j][i] *= fexp2(gv[j][i]);
+            ck[j][i] *= fexp2(trv[i] - gv[j][i]);
         }
         if (wave_slow) {
-            // Diagonal block summed pair by pair: row m with rows j of this block.
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const float a = __shfl(dAd[j & 3], m + 16 * (j >> 2), 64);
-                const float lv = __shfl(dLd[j & 3], m + 16 * (j >> 2), 64);
-                const float aN2 = __shfl(dANd[j & 3], m + 16 * (j >> 2), 64);
-                const float lN2 = __shfl(dLNd[j & 3], m + 16 * (j >> 2), 64);
+            for (int jj = 0; jj < 16; ++jj) {
+                const int src_l = m + 16 * (jj >> 2);
+                const float a = __shfl(dAd[jj & 3], src_l, 64);
+                const float lv = __shfl(dLd[jj & 3], src_l, 64);
+                const float aN2 = __shfl(dANd[jj & 3], src_l, 64);
+                const float lN2 = __shfl(dLNd[jj & 3], src_l, 64);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int src = 16 * kg + j;
+                    const int src = 16 * kg + jj;
                     const float kj = __shfl(kn[i], src, 64), qj = __shfl(qn[i], src, 64);
-                    const float ej = __shfl(en[i], src, 64), Gj = __shfl(gv[i], src, 64);
-                    const float lo = (j <= m) ? fexp2(gv[i] - Gj) : 0.f;  // row m, column j
-                    const float hi = (j >= m) ? fexp2(Gj - gv[i]) : 0.f;  // row j, column m
-                    cq[dt][i] = fmaf(a * kj, lo, cq[dt][i]);
-                    ce[dt][i] = fmaf(lv * kj, lo, ce[dt][i]);
-                    ck[dt][i] = fmaf(aN2 * qj + lN2 * ej, hi, ck[dt][i]);
+                    const float ej = __shfl(en[i], src, 64), Gj = __shfl(gv[j][i], src, 64);
+                    const float lo = (jj <= m) ? fexp2(gv[j][i] - Gj) : 0.f;  // row m, column jj
+                    const float hi = (jj >= m) ? fexp2(Gj - gv[j][i]) : 0.f;  // row jj, column m
+                    cq[j][i] = fmaf(a * kj, lo, cq[j][i]);
+                    ce[j][i] = fmaf(lv * kj, lo, ce[j][i]);
+                    ck[j][i] = fmaf(aN2 * qj + lN2 * ej, hi, ck[j][i]);
                 }
             }
         }
-        float dG[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            dG[i] = qn[i] * cq[dt][i] + en[i] * ce[dt][i] - kn[i] * ck[dt][i];
-            // db = de * k; dk += de * b; dq <- scale * dq (w.r.t. the normalised q).
-            const float dbv = ce[dt][i] * kn[i];
-            ck[dt][i] = fmaf(ce[dt][i], bv[i], ck[dt][i]);
-            ce[dt][i] = dbv;
-            cq[dt][i] *= p.scale;
-            pq = fmaf(qv[i] * invq, cq[dt][i], pq);
-            pk = fmaf(kn[i], ck[dt][i], pk);
-            // In-block suffix sums of dG (reverse cumsum), block total to LDS.
-            const float pre = row16_scan(dG[i]);
-            const float tot = __shfl(pre, 16 * kg + 15, 64);
-            dG[i] = tot - pre + dG[i];
-            if (m == 0) sDG[R][16 * dt + 4 * kg + i] = tot;
+            const float dG = qn[i] * cq[j][i] + en[i] * ce[j][i] - kn[i] * ck[j][i];
+            const float dbv = ce[j][i] * kn[i];
+            ck[j][i] = fmaf(ce[j][i], bv[j][i], ck[j][i]);  // dk += de * b
+            cq[j][i] *= p.scale;                            // w.r.t. the normalised q
+            pq = fmaf(qv[j][i] * invq, cq[j][i], pq);
+            pk = fmaf(kn[i], ck[j][i], pk);
+            const float pre_s = row16_scan(dG);
+            const float tot = __shfl(pre_s, 16 * kg + 15, 64);
+            if (m == 0) sDG[R][c0 + i] = tot;
+            if (row_ok && c0 + i < K) io<TI>::st(static_cast<TI *>(p.db), roff + c0 + i, dbv);
+            ce[j][i] = tot - pre_s + dG;  // in-block suffix sum of dG
         }
-        if (row_ok) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int c = 16 * dt + 4 * kg + i;
-                if (c < K) io<TI>::st(static_cast<TI *>(p.db), roff + c, ce[dt][i]);
-            }
-        }
-        // ce now carries the in-block suffix sums of dG for the second pass.
-        ce[dt][0] = dG[0];
-        ce[dt][1] = dG[1];
-        ce[dt][2] = dG[2];
-        ce[dt][3] = dG[3];
     }
-    __syncthreads();
     pq += __shfl_xor(pq, 16, 64);
     pq += __shfl_xor(pq, 32, 64);
     pk += __shfl_xor(pk, 16, 64);
     pk += __shfl_xor(pk, 32, 64);
+    if (kg == 0) {
+        sRow[0][hh][r] = pq;
+        sRow[1][hh][r] = pk;
+    }
+    __syncthreads();
+    pq = sRow[0][0][r] + sRow[0][1][r];
+    pk = sRow[1][0][r] + sRow[1][1][r];
+    if (!row_ok) return;
 #pragma unroll
-    for (int dt = 0; dt < NKT; ++dt) {
-        float qv[4], kv[4];
-        const int c0 = 16 * dt + 4 * kg;
-        load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv);
-        load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv);
-        if (!row_ok) continue;
+    for (int j = 0; j < NKH; ++j) {
+        const int c0 = 16 * (hh * NKH + j) + 4 * kg;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = c0 + i;
@@ -910,12 +980,12 @@ __global__ __launch_bounds__(256) void chunk_bwd_kside_kernel(BwdParams p)
 #pragma unroll
             for (int R2 = 1; R2 < 4; ++R2)
                 if (R2 > R) later += sDG[R2][c];
-            io<TG>::st(static_cast<TG *>(p.dg), roff + c, ce[dt][i] + later);
-            float dq = cq[dt][i], dk = ck[dt][i];
+            io<TG>::st(static_cast<TG *>(p.dg), roff + c, ce[j][i] + later);
+            float dq = cq[j][i], dk = ck[j][i];
             if (l2) {
                 // d/dx of x / max(||x||, eps): (dy - y (y . dy)) / ||x|| above eps, dy / eps below.
-                dq = bigq ? (dq - qv[i] * invq * pq) * invq : dq * invq;
-                dk = bigk ? (dk - kv[i] * invk * pk) * invk : dk * invk;
+                dq = bigq ? (dq - qv[j][i] * invq * pq) * invq : dq * invq;
+                dk = bigk ? (dk - kv[j][i] * invk * pk) * invk : dk * invk;
             }
             io<TI>::st(static_cast<TI *>(p.dq), roff + c, dq);
             io<TI>::st(static_cast<TI *>(p.dk), roff + c, dk);
@@ -935,7 +1005,7 @@ hipError_t launch_bwd(const BwdParams &p, int total_chunks, hipStream_t stream)
                        stream, p, NVB, NP);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || total_chunks == 0) return e;
-    hipLaunchKernelGGL((chunk_bwd_kside_kernel<PK, KP, TI, TG>), dim3(total_chunks, p.H), dim3(256), 0,
+    hipLaunchKernelGGL((chunk_bwd_kside_kernel<PK, KP, TI, TG>), dim3(total_chunks, p.H), dim3(512), 0,
                        stream, p);
     return hipGetLastError();
 }
