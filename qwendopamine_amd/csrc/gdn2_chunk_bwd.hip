@@ -504,6 +504,10 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     const st *usb = static_cast<const st *>(p.us) + cb * (NPL * 64 * VP);
     const st *dyb = static_cast<const st *>(p.dys) + cb * (64 * VP);
     const TI *dop = static_cast<const TI *>(p.dout);
+    const TI *vp = static_cast<const TI *>(p.v);
+    const TI *wp = static_cast<const TI *>(p.w);
+    TI *dvp = static_cast<TI *>(p.dv);
+    TI *dwp = static_cast<TI *>(p.dw);
     const int NVT = VP / 16;
 
     // ---- slice staging: workspace blocks as 16-byte units, dO rows as groups of 4 ----
@@ -539,6 +543,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     struct Pre {
         u32x4 w[NPRE_W];
         float o[NPRE_O][4];
+        Raw4<TI> v[NPRE_O], w2[NPRE_O];  // v, w of the same groups, for dv and dw
     };
     auto issue_slice = [&](Pre &pr, int vt0) __attribute__((always_inline)) {
 #pragma unroll
@@ -553,12 +558,22 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
             const int tok = u / (4 * NVS), c = 16 * vt0 + 4 * (u % (4 * NVS));
             const bool ok = u < NUO && tok < lc;
             const int64_t off = ((t0 + tok) * H + h) * static_cast<int64_t>(V);
+            float xv[4], xw[4];
             if (ok && (V % 4) == 0 && c + 4 <= V) {
                 load4<TI>(dop, off, c, V, true, 1, pr.o[a]);
+                load4<TI>(vp, off, c, V, true, 1, xv);
+                load4<TI>(wp, off, c, V, true, 1, xw);
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) pr.o[a][i] = (ok && c + i < V) ? io<TI>::ld(dop, off + c + i) : 0.f;
+                for (int i = 0; i < 4; ++i) {
+                    const bool oki = ok && c + i < V;
+                    pr.o[a][i] = oki ? io<TI>::ld(dop, off + c + i) : 0.f;
+                    xv[i] = oki ? io<TI>::ld(vp, off + c + i) : 0.f;
+                    xw[i] = oki ? io<TI>::ld(wp, off + c + i) : 0.f;
+                }
             }
+            pr.v[a].set(xv);
+            pr.w2[a].set(xw);
         }
     };
     auto land_slice = [&](const Pre &pr) __attribute__((always_inline)) {
@@ -727,29 +742,46 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     for (int J = 0; J < 4; ++J) aT[J] = lT[J] = aN[J] = lN[J] = zero4();
 #pragma unroll
     for (int j = 0; j < NKH; ++j) cq[j] = ce[j] = ck[j] = zero4();
-    TI *dvp = static_cast<TI *>(p.dv);
-    TI *dwp = static_cast<TI *>(p.dw);
-    const TI *vp = static_cast<const TI *>(p.v);
-    const TI *wp = static_cast<const TI *>(p.w);
+    float last_acc = 0.f;  // this lane's part of rowsum(dS1 * S0) for channel tile wv
     for (int vt0 = 0; vt0 < NVT; vt0 += NVS) {
         __syncthreads();  // previous slice fully consumed
         land_slice(pre);
+        // dv = dY * w, dw = dY * v for this slice (v, w came with the prefetch).
+        Raw4<TI> pv[NPRE_O], pw[NPRE_O];
+#pragma unroll
+        for (int a = 0; a < NPRE_O; ++a) {
+            pv[a] = pre.v[a];
+            pw[a] = pre.w2[a];
+        }
         __syncthreads();
         if (vt0 + NVS < NVT) issue_slice(pre, vt0 + NVS);
-        // dv = dY * w, dw = dY * v for this slice (one group of 4 values per thread).
-        for (int u = tid; u < 64 * 4 * NVS; u += 512) {
+#pragma unroll
+        for (int a = 0; a < NPRE_O; ++a) {
+            const int u = tid + 512 * a;
             const int tok = u / (4 * NVS), grp = u % (4 * NVS);
             const int c = 16 * vt0 + 4 * grp;
-            if (tok >= lc || c >= V) continue;
+            if (u >= NUO || tok >= lc || c >= V) continue;
             float y[4];
             unpack4<PK>(ld_q4<PK>(sYb + ((tok >> 4) * NVS + (grp >> 2)) * BLK + 4 * ((tok & 15) + 16 * (grp & 3))), y);
             const int64_t off = ((t0 + tok) * H + h) * static_cast<int64_t>(V) + c;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if (c + i < V) {
-                    const float vv = io<TI>::ld(vp, off + i), ww = io<TI>::ld(wp, off + i);
-                    io<TI>::st(dvp, off + i, y[i] * ww);
-                    io<TI>::st(dwp, off + i, y[i] * vv);
+                    io<TI>::st(dvp, off + i, y[i] * pw[a][i]);
+                    io<TI>::st(dwp, off + i, y[i] * pv[a][i]);
+                }
+            }
+        }
+        if (wv < NKT) {
+#pragma unroll
+            for (int vl = 0; vl < NVS; ++vl) {
+                float a4[4], c4[4];
+                unpack4<PK>(ld_q4<PK>(blkD(wv, vl)), a4);
+#pragma unroll
+                for (int pl = 0; pl < NPL; ++pl) {
+                    unpack4<PK>(ld_q4<PK>(blkH(pl, wv, vl)), c4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) last_acc = fmaf(a4[i], c4[i], last_acc);
                 }
             }
         }
@@ -785,17 +817,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     // rowsum(dS1 * S1) written through the saved S0 and U only. ----
     if (wv < NKT) {
         const int dt = wv;
-        float acc = 0.f;
-        for (int vt = 0; vt < NVT; ++vt) {
-            float a[4], c[4];
-            unpack4<PK>(ld_q4<PK>(dhb + k16_block(dt, vt, VP) + 4 * l), a);
-#pragma unroll
-            for (int pl = 0; pl < NPL; ++pl) {
-                unpack4<PK>(ld_q4<PK>(hsb + pl * (KP * VP) + k16_block(dt, vt, VP) + 4 * l), c);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc = fmaf(a[i], c[i], acc);
-            }
-        }
+        float acc = last_acc;
         acc += __shfl_xor(acc, 16, 64);
         acc += __shfl_xor(acc, 32, 64);
         const int c = 16 * dt + m;
