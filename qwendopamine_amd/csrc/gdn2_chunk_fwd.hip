@@ -49,6 +49,49 @@ namespace gdn2 {
 
 namespace {
 
+// Rows 16R..16R+15 of one [.., K] input (K == KP) for the calling wave:
+// 16-byte loads that cover whole rows (lane l: row rr = j*RPI + l/LPR, bytes
+// 16*(l%LPR) of it), so every load instruction reads complete 128-byte lines.
+template <typename T, int KP>
+struct RowLoad {
+    static constexpr int RB = KP * static_cast<int>(sizeof(T));  // bytes per row
+    static constexpr int LPR = RB / 16;                           // lanes per row
+    static constexpr int RPI = 64 / LPR;                          // rows per instruction
+    static constexpr int NI = 16 / RPI;                           // instructions
+    u32x4 v[NI];
+    __device__ __forceinline__ void issue(const T *base, int64_t row0, int64_t stride, int nvalid, int l)
+    {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int rr = j * RPI + l / LPR;
+            const char *src = reinterpret_cast<const char *>(base + row0 + rr * stride) + 16 * (l % LPR);
+            v[j] = rr < nvalid ? *reinterpret_cast<const u32x4 *>(src) : u32x4{0, 0, 0, 0};
+        }
+    }
+    // Through the wave's LDS scratch into the A-order registers (row m,
+    // channels 16kt + 4kg + i).
+    __device__ __forceinline__ void land(unsigned char *stg, int l, int m, int kg, float (&out)[KP / 16][4])
+    {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int rr = j * RPI + l / LPR;
+            *reinterpret_cast<u32x4 *>(stg + rr * RB + 16 * (l % LPR)) = v[j];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        const T *row = reinterpret_cast<const T *>(stg + m * RB);
+#pragma unroll
+        for (int kt = 0; kt < KP / 16; ++kt) {
+            float x[4];
+            load4<T>(row, 0, 16 * kt + 4 * kg, KP, true, 1, x);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) out[kt][i] = x[i];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    }
+};
+
 // ---------------------------------------------------------------------------
 // Prep: one workgroup (4 waves) per (chunk, head).  Wave R owns token rows
 // 16R..16R+15; lane (m, kg) holds row 16R+m and channels 16kt + 4kg + i.
@@ -76,6 +119,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkParams p)
     __shared__ __align__(16) float sScr[4][256];
     st *sKend = reinterpret_cast<st *>(smem1);
     float *sL = reinterpret_cast<float *>(smem1);
+    static_assert(sizeof(sX) >= 2 * 16 * KP * 4 && sizeof(sEt) >= 2 * 16 * KP * 4,
+                  "row staging must fit in sX and sEt");
 
     const int tid = threadIdx.x, R = tid >> 6, l = tid & 63, m = l & 15, kg = l >> 4;
     const int gc = blockIdx.x, h = blockIdx.y;
@@ -97,13 +142,34 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkParams p)
     const TG *g = static_cast<const TG *>(p.g);
 
     float qv[NKT][4], kv[NKT][4], ev[NKT][4], gv[NKT][4];
+    if (K == KP) {
+        // Whole-row 16-byte loads, redistributed through a per-wave LDS
+        // scratch (sX for waves 0-1, sEt for waves 2-3; both are free until
+        // the first barrier).
+        unsigned char *stg = R < 2 ? reinterpret_cast<unsigned char *>(sX) + R * (16 * KP * 4)
+                                   : reinterpret_cast<unsigned char *>(sEt) + (R - 2) * (16 * KP * 4);
+        const int64_t row0 = ((t0 + 16 * R) * H + h) * static_cast<int64_t>(K);
+        const int64_t stride = static_cast<int64_t>(H) * K;
+        const int nvalid = lc - 16 * R;
+        RowLoad<TI, KP> lq, lk, lb;
+        RowLoad<TG, KP> lg;
+        lq.issue(q, row0, stride, nvalid, l);
+        lk.issue(k, row0, stride, nvalid, l);
+        lb.issue(b, row0, stride, nvalid, l);
+        lg.issue(g, row0, stride, nvalid, l);
+        lq.land(stg, l, m, kg, qv);
+        lk.land(stg, l, m, kg, kv);
+        lb.land(stg, l, m, kg, ev);
+        lg.land(stg, l, m, kg, gv);
+    } else {
 #pragma unroll
-    for (int kt = 0; kt < NKT; ++kt) {
-        const int c0 = 16 * kt + 4 * kg;
-        load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv[kt]);
-        load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv[kt]);
-        load4<TI>(b, roff, c0, K, row_ok, p.vec_ok, ev[kt]);
-        load4<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv[kt]);
+        for (int kt = 0; kt < NKT; ++kt) {
+            const int c0 = 16 * kt + 4 * kg;
+            load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv[kt]);
+            load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv[kt]);
+            load4<TI>(b, roff, c0, K, row_ok, p.vec_ok, ev[kt]);
+            load4<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv[kt]);
+        }
     }
 
     // Fused prologue: L2 norm (F.normalize semantics), scale, erase vector,

@@ -153,7 +153,7 @@ def fused_recurrent_gdn2_fwd(
         scale = K**-0.5
     dt = q.dtype
     q, k, v, b, w = (_io(x, dt) for x in (q, k, v, b, w))
-    g = g.contiguous() if g.dtype in (torch.float32, dt) else g.float().contiguous()
+    g = _io(g, g.dtype if g.dtype in (torch.float32, dt) else torch.float32)
     cu_dev, cu_host = _cu(cu_seqlens, q.device, T)
     N = B if cu_seqlens is None else cu_host.numel() - 1
     if out is None:
@@ -292,7 +292,7 @@ def chunk_gdn2_fwd(
     V = v.shape[-1]
     dt = q.dtype
     q, k, v, b, w = (_io(x, dt) for x in (q, k, v, b, w))
-    g = g.contiguous() if g.dtype in (torch.float32, dt) else g.float().contiguous()
+    g = _io(g, g.dtype if g.dtype in (torch.float32, dt) else torch.float32)
     cu_dev, cu_host = _cu(cu_seqlens, q.device, T)
     N = B if cu_seqlens is None else cu_host.numel() - 1
     h0 = None if initial_state is None else initial_state.float().contiguous()
