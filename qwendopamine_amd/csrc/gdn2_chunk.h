@@ -175,9 +175,8 @@ inline int64_t blob_bytes(int io_dtype, int KP)
 inline int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
 // Training workspace: the forward's blobs followed by what the backward
-// re-reads (per-chunk start states and U), each region 256-byte aligned.  These are kept at fp32 precision: one fp32
-// plane for fp32 inputs, two 16-bit planes (hi, lo) otherwise -- 4 bytes per
-// element either way.
+// re-reads (per-chunk start states and U in the MFMA operand precision),
+// each region 256-byte aligned.
 struct TrainLayout {
     int64_t blob, hs, us, total;
 };
@@ -186,7 +185,7 @@ inline TrainLayout train_layout(int64_t nc, int H, int K, int V, int io_dtype)
 {
     const int KP = kp_for(K);
     const int64_t VP = round_up(V, 16);
-    const int64_t es = 4;
+    const int64_t es = io_dtype == GDN2_DTYPE_F32 ? 4 : 2;
     TrainLayout t;
     t.blob = 0;
     t.hs = round_up(nc * H * blob_bytes(io_dtype, KP), 256);

@@ -455,9 +455,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     constexpr int NKT = KP / 16;
     constexpr int NKH = NKT / 2;  // channel tiles per wave
     // dg is a reverse cumulative sum in which the in-chunk pair terms cancel
-    // in exact arithmetic; to keep that cancellation accurate, operands that
-    // reach dg (chunk states and U from the forward, the factor tiles) carry
-    // fp32 precision: for 16-bit MFMA operands as two planes, x = hi + lo.
+    // in exact arithmetic; to keep that cancellation accurate, the factor
+    // tiles of the pair products carry fp32 precision: for 16-bit MFMA
+    // operands as two planes, x = hi + lo.
     constexpr int NPL = PK == PrecKind::F32 ? 1 : 2;
     constexpr int NVS = PK == PrecKind::F32 ? 1 : 2;  // value tiles per staged slice
     constexpr int EPU = 16 / static_cast<int>(sizeof(st));
@@ -467,9 +467,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     __shared__ __align__(16) st sQT[NPL][4][NKT][BLK];  // q * 2^G           (qb)
     __shared__ __align__(16) st sET[NPL][4][NKT][BLK];  // e * 2^G           (eb)
     // One staged value slice (NVS value tiles), A-order blocks.
-    constexpr int NB_U = NPL * 4 * NVS, NB_Y = 4 * NVS, NB_H = NPL * NKT * NVS, NB_D = NKT * NVS;
+    constexpr int NB_U = 4 * NVS, NB_Y = 4 * NVS, NB_H = NKT * NVS, NB_D = NKT * NVS;
     constexpr int NB = NB_U + NB_Y + NB_H + NB_D;  // contiguous workspace blocks per slice
-    __shared__ __align__(16) st sW[NB * BLK];      // U planes, dY, h planes, dh
+    __shared__ __align__(16) st sW[NB * BLK];      // U, dY, h, dh
     __shared__ __align__(16) st sO[4 * NVS * BLK];  // dO
     __shared__ __align__(16) float sT[4][KP];       // in-block decay totals (log2)
     __shared__ __align__(16) float sEr[4][KP];      // 2^(decay before block)
@@ -499,9 +499,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
     const Q ident = identity_q4<PK>(l);
 
-    const st *hsb = static_cast<const st *>(p.hs) + cb * (NPL * KP * VP);
+    const st *hsb = static_cast<const st *>(p.hs) + cb * (KP * VP);
     const st *dhb = static_cast<const st *>(p.dhs) + cb * (KP * VP);
-    const st *usb = static_cast<const st *>(p.us) + cb * (NPL * 64 * VP);
+    const st *usb = static_cast<const st *>(p.us) + cb * (64 * VP);
     const st *dyb = static_cast<const st *>(p.dys) + cb * (64 * VP);
     const TI *dop = static_cast<const TI *>(p.dout);
     const TI *vp = static_cast<const TI *>(p.v);
@@ -521,17 +521,16 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
         int rowt, vl;
         const st *base;
         if (b < NB_U) {
-            const int pl = b / (4 * NVS), rb = b % (4 * NVS);
-            rowt = rb / NVS; vl = rb % NVS;
-            base = usb + pl * (64 * VP);
+            rowt = b / NVS; vl = b % NVS;
+            base = usb;
         } else if (b < NB_U + NB_Y) {
             const int rb = b - NB_U;
             rowt = rb / NVS; vl = rb % NVS;
             base = dyb;
         } else if (b < NB_U + NB_Y + NB_H) {
-            const int rb = b - NB_U - NB_Y, pl = rb / (NKT * NVS), r2 = rb % (NKT * NVS);
-            rowt = r2 / NVS; vl = r2 % NVS;
-            base = hsb + pl * (KP * VP);
+            const int rb = b - NB_U - NB_Y;
+            rowt = rb / NVS; vl = rb % NVS;
+            base = hsb;
         } else {
             const int rb = b - NB_U - NB_Y - NB_H;
             rowt = rb / NVS; vl = rb % NVS;
@@ -595,9 +594,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     const st *sYb = sW + NB_U * BLK;
     const st *sHb = sW + (NB_U + NB_Y) * BLK;
     const st *sDb = sW + (NB_U + NB_Y + NB_H) * BLK;
-    auto blkU = [&](int pl, int rt, int vl) { return sUb + ((pl * 4 + rt) * NVS + vl) * BLK + 4 * l; };
+    auto blkU = [&](int rt, int vl) { return sUb + (rt * NVS + vl) * BLK + 4 * l; };
     auto blkY = [&](int rt, int vl) { return sYb + (rt * NVS + vl) * BLK + 4 * l; };
-    auto blkH = [&](int pl, int dt, int vl) { return sHb + ((pl * NKT + dt) * NVS + vl) * BLK + 4 * l; };
+    auto blkH = [&](int dt, int vl) { return sHb + (dt * NVS + vl) * BLK + 4 * l; };
     auto blkD = [&](int dt, int vl) { return sDb + (dt * NVS + vl) * BLK + 4 * l; };
     auto blkO = [&](int rt, int vl) { return sO + (rt * NVS + vl) * BLK + 4 * l; };
     // acc += A . B^T over the staged value tiles (A, B given as tile loaders).
@@ -777,34 +776,28 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
             for (int vl = 0; vl < NVS; ++vl) {
                 float a4[4], c4[4];
                 unpack4<PK>(ld_q4<PK>(blkD(wv, vl)), a4);
+                unpack4<PK>(ld_q4<PK>(blkH(wv, vl)), c4);
 #pragma unroll
-                for (int pl = 0; pl < NPL; ++pl) {
-                    unpack4<PK>(ld_q4<PK>(blkH(pl, wv, vl)), c4);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) last_acc = fmaf(a4[i], c4[i], last_acc);
-                }
+                for (int i = 0; i < 4; ++i) last_acc = fmaf(a4[i], c4[i], last_acc);
             }
         }
 #pragma unroll
-        for (int pl = 0; pl < NPL; ++pl) {
-#pragma unroll
-            for (int J = 0; J < 4; ++J) {
-                if (J <= R) {
-                    aT[J] = mmav(aT[J], blkU(pl, J, 0), blkO(R, 0));
-                    lT[J] = mmav(lT[J], blkU(pl, J, 0), blkY(R, 0));
-                }
-                if (J >= R) {
-                    aN[J] = mmav(aN[J], blkO(J, 0), blkU(pl, R, 0));
-                    lN[J] = mmav(lN[J], blkY(J, 0), blkU(pl, R, 0));
-                }
+        for (int J = 0; J < 4; ++J) {
+            if (J <= R) {
+                aT[J] = mmav(aT[J], blkU(J, 0), blkO(R, 0));
+                lT[J] = mmav(lT[J], blkU(J, 0), blkY(R, 0));
             }
-#pragma unroll
-            for (int j = 0; j < NKH; ++j) {
-                const int dt = hh * NKH + j;
-                cq[j] = mmav(cq[j], blkH(pl, dt, 0), blkO(R, 0));
-                ce[j] = mmav(ce[j], blkH(pl, dt, 0), blkY(R, 0));
-                ck[j] = mmav(ck[j], blkD(dt, 0), blkU(pl, R, 0));
+            if (J >= R) {
+                aN[J] = mmav(aN[J], blkO(J, 0), blkU(R, 0));
+                lN[J] = mmav(lN[J], blkY(J, 0), blkU(R, 0));
             }
+        }
+#pragma unroll
+        for (int j = 0; j < NKH; ++j) {
+            const int dt = hh * NKH + j;
+            cq[j] = mmav(cq[j], blkH(dt, 0), blkO(R, 0));
+            ce[j] = mmav(ce[j], blkH(dt, 0), blkY(R, 0));
+            ck[j] = mmav(ck[j], blkD(dt, 0), blkU(R, 0));
         }
     }
 

@@ -476,19 +476,9 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     const bool emit = p.hs != nullptr && active && 16 * vt < V;
     const Q ident = identity_q4<PK>(l);
     // An fp32 accumulator tile (rows 4kg+i, column m) stored transposed, in
-    // A-order, at full precision: fp32 as is; 16-bit precisions as two planes
-    // (hi = x rounded, lo = x - hi rounded), each transposed exactly by an
-    // identity product.  The backward's products read both planes.
-    constexpr int NPL = PK == PrecKind::F32 ? 1 : 2;
-    auto emit_tile = [&](st *base, int plane, int64_t off, f32x4 x) __attribute__((always_inline)) {
-        const Q hi = pack4<PK>(x);
-        st_q4<PK>(base + off, pack4<PK>(mma1<PK>(zero4(), hi, ident)));
-        if constexpr (NPL == 2) {
-            float xh[4];
-            unpack4<PK>(hi, xh);
-            const Q lo = pack4<PK>(x[0] - xh[0], x[1] - xh[1], x[2] - xh[2], x[3] - xh[3]);
-            st_q4<PK>(base + plane + off, pack4<PK>(mma1<PK>(zero4(), lo, ident)));
-        }
+    // A-order and the MFMA operand precision (an identity product transposes it).
+    auto emit_tile = [&](st *base, int64_t off, f32x4 x) __attribute__((always_inline)) {
+        st_q4<PK>(base + off, pack4<PK>(mma1<PK>(zero4(), pack4<PK>(x), ident)));
     };
     int64_t bos, len;
     const int gc0 = seq_chunk_base(p, n, bos, len);
@@ -663,9 +653,9 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
 
             // Training mode: this chunk's start state, A-order tiles (kt, vt).
             if (emit) {
-                st *hsb = static_cast<st *>(p.hs) + (static_cast<int64_t>(gc0 + jc) * H + h) * (NPL * KP * VP);
+                st *hsb = static_cast<st *>(p.hs) + (static_cast<int64_t>(gc0 + jc) * H + h) * (KP * VP);
 #pragma unroll
-                for (int kt = 0; kt < NKT; ++kt) emit_tile(hsb, KP * VP, k16_block(kt, vt, VP) + 4 * l, S[kt]);
+                for (int kt = 0; kt < NKT; ++kt) emit_tile(hsb, k16_block(kt, vt, VP) + 4 * l, S[kt]);
             }
 
             // z = w * v as B operand (contraction over tokens), staged in LDS.
@@ -694,8 +684,8 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                                    sf[2 * s], sf[2 * s + 1]);
                 uf[rt] = pack4<PK>(acc);
                 if (emit) {
-                    st *usb = static_cast<st *>(p.us) + (static_cast<int64_t>(gc0 + jc) * H + h) * (NPL * 64 * VP);
-                    emit_tile(usb, 64 * VP, k16_block(rt, vt, VP) + 4 * l, acc);
+                    st *usb = static_cast<st *>(p.us) + (static_cast<int64_t>(gc0 + jc) * H + h) * (64 * VP);
+                    emit_tile(usb, k16_block(rt, vt, VP) + 4 * l, acc);
                 }
             }
             // O = Qbar S + Aqk U.
