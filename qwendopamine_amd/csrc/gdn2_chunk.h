@@ -7,6 +7,8 @@
 // backward kernels read exactly what the forward wrote.
 #pragma once
 
+#include <type_traits>
+
 #include "gdn2_mfma.h"
 
 namespace gdn2 {
@@ -128,6 +130,29 @@ __device__ __forceinline__ void load4(const T *base, int64_t off, int c0, int K,
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = (ok && c0 + i < K) ? io<T>::ld(base, off + c0 + i) : 0.0f;
+}
+
+// Store 4 consecutive values x[0..3] at base[off + c0 ..]: one vector store
+// when all four are in [0, n) and the address is aligned, else element-wise.
+template <typename T>
+__device__ __forceinline__ void store4(T *base, int64_t off, int c0, int n, const float (&x)[4])
+{
+    T *p = base + off + c0;
+    if (c0 + 4 <= n && (reinterpret_cast<uintptr_t>(p) & (4 * sizeof(T) - 1)) == 0) {
+        if constexpr (std::is_same<T, float>::value) {
+            *reinterpret_cast<float4 *>(p) = make_float4(x[0], x[1], x[2], x[3]);
+        } else if constexpr (std::is_same<T, bf16_t>::value) {
+            *reinterpret_cast<uint2 *>(p) = make_uint2(f32x2_to_bf16x2_bits(x[0], x[1]),
+                                                       f32x2_to_bf16x2_bits(x[2], x[3]));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) io<T>::st(p, i, x[i]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (c0 + i < n) io<T>::st(p, i, x[i]);
 }
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }

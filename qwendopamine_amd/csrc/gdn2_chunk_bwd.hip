@@ -760,16 +760,16 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
             const int tok = u / (4 * NVS), grp = u % (4 * NVS);
             const int c = 16 * vt0 + 4 * grp;
             if (u >= NUO || tok >= lc || c >= V) continue;
-            float y[4];
+            float y[4], xv[4], xw[4];
             unpack4<PK>(ld_q4<PK>(sYb + ((tok >> 4) * NVS + (grp >> 2)) * BLK + 4 * ((tok & 15) + 16 * (grp & 3))), y);
-            const int64_t off = ((t0 + tok) * H + h) * static_cast<int64_t>(V) + c;
+            const int64_t off = ((t0 + tok) * H + h) * static_cast<int64_t>(V);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if (c + i < V) {
-                    io<TI>::st(dvp, off + i, y[i] * pw[a][i]);
-                    io<TI>::st(dwp, off + i, y[i] * pv[a][i]);
-                }
+                xv[i] = y[i] * pw[a][i];
+                xw[i] = y[i] * pv[a][i];
             }
+            store4<TI>(dvp, off, c, V, xv);
+            store4<TI>(dwp, off, c, V, xw);
         }
         if (wv < NKT) {
 #pragma unroll
@@ -957,10 +957,12 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
                 }
             }
         }
+        float dbv4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float dG = qn[i] * cq[j][i] + en[i] * ce[j][i] - kn[i] * ck[j][i];
             const float dbv = ce[j][i] * kn[i];
+            dbv4[i] = dbv;
             ck[j][i] = fmaf(ce[j][i], bv[j][i], ck[j][i]);  // dk += de * b
             cq[j][i] *= p.scale;                            // w.r.t. the normalised q
             pq = fmaf(qv[j][i] * invq, cq[j][i], pq);
@@ -968,9 +970,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
             const float pre_s = row16_scan(dG);
             const float tot = __shfl(pre_s, 16 * kg + 15, 64);
             if (m == 0) sDG[R][c0 + i] = tot;
-            if (row_ok && c0 + i < K) io<TI>::st(static_cast<TI *>(p.db), roff + c0 + i, dbv);
             ce[j][i] = tot - pre_s + dG;  // in-block suffix sum of dG
         }
+        if (row_ok) store4<TI>(static_cast<TI *>(p.db), roff, c0, K, dbv4);
     }
     pq += __shfl_xor(pq, 16, 64);
     pq += __shfl_xor(pq, 32, 64);
@@ -987,24 +989,27 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
 #pragma unroll
     for (int j = 0; j < NKH; ++j) {
         const int c0 = 16 * (hh * NKH + j) + 4 * kg;
+        float dg4[4], dq4[4], dk4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int c = c0 + i;
-            if (c >= K) continue;
+            const int c = c0 + i < KP ? c0 + i : KP - 1;
             float later = sLast[c] + sKK[0][c] + sKK[1][c] + sKK[2][c] + sKK[3][c];
 #pragma unroll
             for (int R2 = 1; R2 < 4; ++R2)
                 if (R2 > R) later += sDG[R2][c];
-            io<TG>::st(static_cast<TG *>(p.dg), roff + c, ce[j][i] + later);
+            dg4[i] = ce[j][i] + later;
             float dq = cq[j][i], dk = ck[j][i];
             if (l2) {
                 // d/dx of x / max(||x||, eps): (dy - y (y . dy)) / ||x|| above eps, dy / eps below.
                 dq = bigq ? (dq - qv[j][i] * invq * pq) * invq : dq * invq;
                 dk = bigk ? (dk - kv[j][i] * invk * pk) * invk : dk * invk;
             }
-            io<TI>::st(static_cast<TI *>(p.dq), roff + c, dq);
-            io<TI>::st(static_cast<TI *>(p.dk), roff + c, dk);
+            dq4[i] = dq;
+            dk4[i] = dk;
         }
+        store4<TG>(static_cast<TG *>(p.dg), roff, c0, K, dg4);
+        store4<TI>(static_cast<TI *>(p.dq), roff, c0, K, dq4);
+        store4<TI>(static_cast<TI *>(p.dk), roff, c0, K, dk4);
     }
 }
 
