@@ -474,7 +474,8 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     __shared__ __align__(16) float sT[4][KP];       // in-block decay totals (log2)
     __shared__ __align__(16) float sEr[4][KP];      // 2^(decay before block)
     __shared__ __align__(16) float sEa[4][KP];      // 2^(decay after block)
-    __shared__ __align__(16) float sPf[4][4][KP];   // pair factor of (row block, column block)
+    __shared__ __align__(16) float sE2[4][KP];      // 2^(T_J): decay across block J
+    __shared__ __align__(16) float sE2n[4][KP];     // 2^(-T_J)
     __shared__ __align__(16) float sDG[4][KP];      // per-block sums of dG
     __shared__ __align__(16) float sKK[4][KP];      // per-block sums of dKt * Kt
     __shared__ __align__(16) float sLast[KP];       // exp(G_last) rowsum(dS1 * S0)
@@ -516,7 +517,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     constexpr int NUO = 64 * 4 * NVS;                // dO groups of 4 values per slice
     constexpr int NPRE_W = (NUW + 511) / 512, NPRE_O = (NUO + 511) / 512;
     // Source of workspace unit u of slice vt0 (nullptr past V).
-    auto wsrc = [&](int u, int vt0) __attribute__((always_inline)) -> const st * {
+    auto wsrc = [=](int u, int vt0) __attribute__((always_inline)) -> const st * {
         const int b = u / UPB, e = (u % UPB) * EPU;
         int rowt, vl;
         const st *base;
@@ -594,11 +595,11 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     const st *sYb = sW + NB_U * BLK;
     const st *sHb = sW + (NB_U + NB_Y) * BLK;
     const st *sDb = sW + (NB_U + NB_Y + NB_H) * BLK;
-    auto blkU = [&](int rt, int vl) { return sUb + (rt * NVS + vl) * BLK + 4 * l; };
-    auto blkY = [&](int rt, int vl) { return sYb + (rt * NVS + vl) * BLK + 4 * l; };
-    auto blkH = [&](int dt, int vl) { return sHb + (dt * NVS + vl) * BLK + 4 * l; };
-    auto blkD = [&](int dt, int vl) { return sDb + (dt * NVS + vl) * BLK + 4 * l; };
-    auto blkO = [&](int rt, int vl) { return sO + (rt * NVS + vl) * BLK + 4 * l; };
+    auto blkU = [=](int rt, int vl) { return sUb + (rt * NVS + vl) * BLK + 4 * l; };
+    auto blkY = [=](int rt, int vl) { return sYb + (rt * NVS + vl) * BLK + 4 * l; };
+    auto blkH = [=](int dt, int vl) { return sHb + (dt * NVS + vl) * BLK + 4 * l; };
+    auto blkD = [=](int dt, int vl) { return sDb + (dt * NVS + vl) * BLK + 4 * l; };
+    auto blkO = [=](int rt, int vl) { return sO + (rt * NVS + vl) * BLK + 4 * l; };
     // acc += A . B^T over the staged value tiles (A, B given as tile loaders).
     auto mmav = [&](f32x4 acc, const st *a0, const st *b0) __attribute__((always_inline)) {
         if constexpr (NVS == 2)
@@ -688,18 +689,8 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
         }
         sEr[Rb][c] = fexp2(cum);
         sEa[Rb][c] = fexp2(after);
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-            float ex = 0.f;
-            if (I == Rb) {
-                ex = -t[Rb];
-            } else {
-#pragma unroll
-                for (int R2 = 0; R2 < 4; ++R2)
-                    if (R2 > I && R2 < Rb) ex += t[R2];
-            }
-            sPf[Rb][I][c] = I > Rb ? 0.f : fexp2(ex);
-        }
+        sE2[Rb][c] = fexp2(sT[Rb][c]);
+        sE2n[Rb][c] = fexp2(-sT[Rb][c]);
     }
     // Factor tiles of this wave's rows and channels, transposed by an identity product.
 #pragma unroll
@@ -821,20 +812,13 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
         const int dt = hh * NKH + j, c0 = 16 * dt + 4 * kg;
         const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][c0]);
         const float4 ea = *reinterpret_cast<const float4 *>(&sEa[R][c0]);
-        const float4 er = *reinterpret_cast<const float4 *>(&sEr[R][c0]);
         const float trv[4] = {tr.x, tr.y, tr.z, tr.w}, eav[4] = {ea.x, ea.y, ea.z, ea.w};
-        const float erv[4] = {er.x, er.y, er.z, er.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float kt_ = kv[j][i] * invk * fexp2(trv[i] - gv[j][i]) * eav[i];
             const float tot = row16_scan(ck[j][i] * kt_);
             if (m == 15) sKK[R][c0 + i] = tot;
-            // Start the row-data accumulators from the V-contractions scaled by the
-            // decay before / after the block: Er * dQbar, Er * dEbar (= -Er dY S0^T),
-            // Ea * dKtilde.
-            cq[j][i] *= erv[i];
-            ce[j][i] *= -erv[i];
-            ck[j][i] *= eav[i];
+            ce[j][i] = -ce[j][i];  // dEbar = -dY S0^T
         }
     }
 
@@ -867,53 +851,67 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
         blN[J] = pack4<PK>(lN[J]);
     }
 
-    // ---- pair products: factor tile (hi + lo) times the pair factor of its
-    // block pair, split again into hi + lo operands ----
-    struct Q2 {
-        Q hi, lo;
-    };
-    auto scaled = [&](const st (*tile)[4][NKT][BLK], int blk, int dt, float f) __attribute__((always_inline)) {
-        float x[4];
-        unpack4<PK>(ld_q4<PK>(&tile[0][blk][dt][4 * l]), x);
-        if constexpr (NPL == 2) {
-            float y[4];
-            unpack4<PK>(ld_q4<PK>(&tile[1][blk][dt][4 * l]), y);
+    // ---- pair products, Horner over blocks.  With P_J the product of block
+    // J's factor tiles with the pair tiles, the sums the factored form needs are
+    //   dq (and de):  Er dQbar + sum_{J<R} 2^(T_{J+1} + .. + T_{R-1}) P_J + 2^(-T_R) P_R
+    //   dk:           Ea dKt   + sum_{I>R} 2^(T_{R+1} + .. + T_{I-1}) P_I + 2^(-T_R) P_R
+    // (Er, Ea = decay before / after block R), so the running accumulator is
+    // scaled by 2^(T_J) per channel between blocks and the factor tiles are used
+    // as stored (hi + lo planes).  The diagonal block is skipped here when its
+    // span is too wide for 2^(-T_R) (the exact path below handles it). ----
+    auto pmma = [&](f32x4 acc, const st (*tile)[4][NKT][BLK], int blk, int dt, Q bop) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[i] += y[i];
-        }
-        Q2 res;
-        res.hi = pack4<PK>(x[0] * f, x[1] * f, x[2] * f, x[3] * f);
-        if constexpr (NPL == 2) {
-            float xh[4];
-            unpack4<PK>(res.hi, xh);
-            res.lo = pack4<PK>(x[0] * f - xh[0], x[1] * f - xh[1], x[2] * f - xh[2], x[3] * f - xh[3]);
-        }
-        return res;
-    };
-    auto mma2x = [&](f32x4 acc, const Q2 &a0, const Q2 &a1, Q b0, Q b1) __attribute__((always_inline)) {
-        acc = mma2<PK>(acc, a0.hi, a1.hi, b0, b1);
-        if constexpr (NPL == 2) acc = mma2<PK>(acc, a0.lo, a1.lo, b0, b1);
+        for (int pl = 0; pl < NPL; ++pl) acc = mma1<PK>(acc, ld_q4<PK>(&tile[pl][blk][dt][4 * l]), bop);
         return acc;
+    };
+    auto scale_by = [&](f32x4 &acc, const float *tab) __attribute__((always_inline)) {
+        const float4 f = *reinterpret_cast<const float4 *>(tab);
+        acc[0] *= f.x;
+        acc[1] *= f.y;
+        acc[2] *= f.z;
+        acc[3] *= f.w;
     };
 #pragma unroll
     for (int j = 0; j < NKH; ++j) {
-        const int dt = hh * NKH + j;
-        const int c = 16 * dt + m;  // channel of this lane in the transposed tiles
+        const int dt = hh * NKH + j, c0 = 16 * dt + 4 * kg;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            const int J0 = 2 * s2, J1 = 2 * s2 + 1;
-            if (J0 <= R) {  // dq, de: column blocks J <= R
-                const float f0 = (J0 == R && wave_slow) ? 0.f : sPf[R][J0][c];
-                const float f1 = (J1 == R && wave_slow) ? 0.f : sPf[R][J1][c];
-                const Q2 a0 = scaled(sKT, J0, dt, f0), a1 = scaled(sKT, J1, dt, f1);
-                cq[j] = mma2x(cq[j], a0, a1, baT[J0], baT[J1]);
-                ce[j] = mma2x(ce[j], a0, a1, blT[J0], blT[J1]);
+        for (int J = 0; J < 3; ++J) {  // dq, de: column blocks J < R
+            if (J < R) {
+                scale_by(cq[j], &sE2[J][c0]);
+                scale_by(ce[j], &sE2[J][c0]);
+                cq[j] = pmma(cq[j], sKT, J, dt, baT[J]);
+                ce[j] = pmma(ce[j], sKT, J, dt, blT[J]);
             }
-            if (J1 >= R) {  // dk: row blocks I >= R
-                const float f0 = (J0 == R && wave_slow) ? 0.f : sPf[J0][R][c];
-                const float f1 = (J1 == R && wave_slow) ? 0.f : sPf[J1][R][c];
-                ck[j] = mma2x(ck[j], scaled(sQT, J0, dt, f0), scaled(sQT, J1, dt, f1), baN[J0], baN[J1]);
-                ck[j] = mma2x(ck[j], scaled(sET, J0, dt, f0), scaled(sET, J1, dt, f1), blN[J0], blN[J1]);
+        }
+#pragma unroll
+        for (int I = 3; I > 0; --I) {  // dk: row blocks I > R
+            if (I > R) {
+                scale_by(ck[j], &sE2[I][c0]);
+                ck[j] = pmma(ck[j], sQT, I, dt, baN[I]);
+                ck[j] = pmma(ck[j], sET, I, dt, blN[I]);
+            }
+        }
+        if (!wave_slow) {  // diagonal block, factor 2^(-T_R)
+            Q dA_R = baT[0], dL_R = blT[0], dN_R = baN[0], dLN_R = blN[0];
+#pragma unroll
+            for (int J = 1; J < 4; ++J)
+                if (J == R) {
+                    dA_R = baT[J];
+                    dL_R = blT[J];
+                    dN_R = baN[J];
+                    dLN_R = blN[J];
+                }
+            f32x4 tq = pmma(zero4(), sKT, R, dt, dA_R);
+            f32x4 te = pmma(zero4(), sKT, R, dt, dL_R);
+            f32x4 tk = pmma(zero4(), sQT, R, dt, dN_R);
+            tk = pmma(tk, sET, R, dt, dLN_R);
+            const float4 f = *reinterpret_cast<const float4 *>(&sE2n[R][c0]);
+            const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                cq[j][i] = fmaf(tq[i], fv[i], cq[j][i]);
+                ce[j][i] = fmaf(te[i], fv[i], ce[j][i]);
+                ck[j][i] = fmaf(tk[i], fv[i], ck[j][i]);
             }
         }
     }
