@@ -179,6 +179,16 @@ __device__ __forceinline__ float row16_scan(float x)
 inline int kp_for(int K) { return K <= 32 ? 32 : (K <= 64 ? 64 : 128); }
 inline int bv_for(int V) { return V <= 16 ? 16 : (V <= 32 ? 32 : 64); }
 
+// Value-slice width of the sequential scans: the widest of 64/32/16 columns
+// whose (sequence, head, slice) workgroups still cover the 256 CUs, so that
+// few long sequences do not leave most of the chip idle.
+inline int scan_bv(int num_pairs, int V)
+{
+    int bv = bv_for(V);
+    while (bv > 16 && static_cast<int64_t>(num_pairs) * ((V + bv - 1) / bv) < 256) bv /= 2;
+    return bv;
+}
+
 inline int64_t count_chunks(int B, int T, const int64_t *cu_host, int num_seqs)
 {
     if (!cu_host) return static_cast<int64_t>(B) * ((T + kChunk - 1) / kChunk);

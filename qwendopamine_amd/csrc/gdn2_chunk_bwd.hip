@@ -1017,10 +1017,16 @@ hipError_t launch_bwd(const BwdParams &p, int total_chunks, hipStream_t stream)
     if (p.num_seqs == 0) return hipSuccess;
     const int NP = p.num_seqs * p.H;
     const int groups = (NP + 7) / 8;
-    constexpr int BV = 64;
-    const int NVB = (p.V + BV - 1) / BV;
-    hipLaunchKernelGGL((chunk_bwd_scan_kernel<PK, KP, BV, TI>), dim3(groups * 8 * NVB), dim3(512), 0,
-                       stream, p, NVB, NP);
+    auto go = [&](auto bvtag) {
+        constexpr int BV = decltype(bvtag)::value;
+        const int NVB = (p.V + BV - 1) / BV;
+        hipLaunchKernelGGL((chunk_bwd_scan_kernel<PK, KP, BV, TI>), dim3(groups * 8 * NVB), dim3(512), 0,
+                           stream, p, NVB, NP);
+    };
+    const int bv = scan_bv(NP, p.V);
+    if (bv == 16) go(std::integral_constant<int, 16>{});
+    else if (bv == 32) go(std::integral_constant<int, 32>{});
+    else go(std::integral_constant<int, 64>{});
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || total_chunks == 0) return e;
     hipLaunchKernelGGL((chunk_bwd_kside_kernel<PK, KP, TI, TG>), dim3(total_chunks, p.H), dim3(512), 0,

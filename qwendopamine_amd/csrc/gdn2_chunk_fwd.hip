@@ -779,7 +779,7 @@ hipError_t launch_all(const ChunkParams &p, int total_chunks, int stages, hipStr
         if (e != hipSuccess) return e;
     }
     if (!(stages & 2) || p.num_seqs == 0) return hipSuccess;
-    return launch_scan<PK, KP, TI>(p, bv_for(p.V), stream);
+    return launch_scan<PK, KP, TI>(p, scan_bv(p.num_seqs * p.H, p.V), stream);
 }
 
 template <PrecKind PK, typename TI, typename TG>
