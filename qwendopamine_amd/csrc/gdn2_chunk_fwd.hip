@@ -55,6 +55,7 @@ namespace {
 template <typename T, int KP>
 struct RowLoad {
     static constexpr int RB = KP * static_cast<int>(sizeof(T));  // bytes per row
+    static constexpr int RS = RB + 16;                            // LDS row stride (bank skew)
     static constexpr int LPR = RB / 16;                           // lanes per row
     static constexpr int RPI = 64 / LPR;                          // rows per instruction
     static constexpr int NI = 16 / RPI;                           // instructions
@@ -75,11 +76,11 @@ struct RowLoad {
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const int rr = j * RPI + l / LPR;
-            *reinterpret_cast<u32x4 *>(stg + rr * RB + 16 * (l % LPR)) = v[j];
+            *reinterpret_cast<u32x4 *>(stg + rr * RS + 16 * (l % LPR)) = v[j];
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
-        const T *row = reinterpret_cast<const T *>(stg + m * RB);
+        const T *row = reinterpret_cast<const T *>(stg + m * RS);
 #pragma unroll
         for (int kt = 0; kt < KP / 16; ++kt) {
             float x[4];
@@ -119,8 +120,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkParams p)
     __shared__ __align__(16) float sScr[4][256];
     st *sKend = reinterpret_cast<st *>(smem1);
     float *sL = reinterpret_cast<float *>(smem1);
-    static_assert(sizeof(sX) >= 2 * 16 * KP * 4 && sizeof(sEt) >= 2 * 16 * KP * 4,
-                  "row staging must fit in sX and sEt");
+    static_assert(sizeof(sX) >= 2 * 16 * (KP * 4 + 16) && sizeof(smem1) >= 2 * 16 * (KP * 4 + 16),
+                  "row staging must fit in sX and smem1");
 
     const int tid = threadIdx.x, R = tid >> 6, l = tid & 63, m = l & 15, kg = l >> 4;
     const int gc = blockIdx.x, h = blockIdx.y;
@@ -144,10 +145,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkParams p)
     float qv[NKT][4], kv[NKT][4], ev[NKT][4], gv[NKT][4];
     if (K == KP) {
         // Whole-row 16-byte loads, redistributed through a per-wave LDS
-        // scratch (sX for waves 0-1, sEt for waves 2-3; both are free until
+        // scratch (sX for waves 0-1, smem1 for waves 2-3; both are free until
         // the first barrier).
-        unsigned char *stg = R < 2 ? reinterpret_cast<unsigned char *>(sX) + R * (16 * KP * 4)
-                                   : reinterpret_cast<unsigned char *>(sEt) + (R - 2) * (16 * KP * 4);
+        unsigned char *stg = R < 2 ? reinterpret_cast<unsigned char *>(sX) + R * (16 * (KP * 4 + 16))
+                                   : smem1 + (R - 2) * (16 * (KP * 4 + 16));
         const int64_t row0 = ((t0 + 16 * R) * H + h) * static_cast<int64_t>(K);
         const int64_t stride = static_cast<int64_t>(H) * K;
         const int nvalid = lc - 16 * R;
