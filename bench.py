@@ -274,7 +274,8 @@ def bench_decode(torch, nat, dev, reps=3, eager_steps=0):
 def traffic_probe(torch, nat, dev):
     """Short run for the rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE): first a
     256 MiB device-to-device copy whose bytes are known, which calibrates the
-    counters, then two prefill ops and eight eager decode steps."""
+    counters, then two prefill ops, eight eager decode steps and two training
+    forward + backward steps."""
     a = torch.empty(64 << 20, dtype=torch.float32, device=dev).uniform_()
     c = torch.empty_like(a)
     c.copy_(a)
@@ -282,6 +283,7 @@ def traffic_probe(torch, nat, dev):
     del a, c
     bench_prefill(torch, nat, dev, steps=2, warmup=0)
     bench_decode(torch, nat, dev, eager_steps=8)
+    bench_train(torch, nat, dev, steps=2, warmup=0)
     print("traffic probe done", flush=True)
 
 
