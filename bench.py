@@ -201,12 +201,22 @@ def bench_train(torch, nat, dev, steps, warmup):
                        "grads": "dq, dk, dv, dg, db, dw"}}
 
 
-def bench_decode(torch, nat, dev, reps=3, eager_steps=0):
+def bench_decode(torch, nat, dev, reps=3, eager_steps=0, variant="plain"):
+    """Config-2 decode steps in one HIP graph.  ``variant``: "plain" (state [N,H,K,V] in place),
+    "pooled" (the states live in a pool of 2N slots addressed through int32
+    ssm_state_indices, updated in place) or "transposed" ([N,H,V,K] states)."""
     N, H, K, V, S = (DECODE[x] for x in ("N", "H", "K", "V", "steps"))
     F = torch.nn.functional
     gen = torch.Generator(device=dev).manual_seed(2)
     bf = torch.bfloat16
     state = torch.randn(N, H, K, V, generator=gen, device=dev) * 0.02
+    rows, slots = N, None
+    if variant == "pooled":
+        rows = 2 * N
+        state = torch.randn(rows, H, K, V, generator=gen, device=dev) * 0.02
+        slots = torch.randperm(rows, generator=gen, device=dev)[:N].to(torch.int32)
+    elif variant == "transposed":
+        state = state.transpose(-1, -2).contiguous()
     q = F.normalize(torch.randn(S, N, 1, H, K, generator=gen, device=dev), dim=-1).to(bf)
     k = F.normalize(torch.randn(S, N, 1, H, K, generator=gen, device=dev), dim=-1).to(bf)
     v = torch.randn(S, N, 1, H, V, generator=gen, device=dev).to(bf)
@@ -220,13 +230,29 @@ def bench_decode(torch, nat, dev, reps=3, eager_steps=0):
     scale = K**-0.5
     sz_k, sz_v, sz_g = N * H * K * 2, N * H * V * 2, N * H * K * 4
 
+    flags = nat.FLAG_L2NORM_QK
+    if variant == "pooled":
+        flags |= nat.FLAG_INPLACE_FINAL_STATE
+    if variant == "transposed":
+        flags |= nat.FLAG_TRANSPOSE_STATE
+    slab = H * K * V
+
     def step(i, sh):
-        st = lib.gdn2_recurrent_fwd(
-            q.data_ptr() + i * sz_k, k.data_ptr() + i * sz_k, v.data_ptr() + i * sz_v,
-            g.data_ptr() + i * sz_g, b.data_ptr() + i * sz_k, w.data_ptr() + i * sz_v,
-            nat.DTYPE_BF16, nat.DTYPE_F32, o.data_ptr() + i * sz_v,
-            state.data_ptr(), state.data_ptr(), None, None, 0.0, None, N,
-            N, 1, H, H, K, V, scale, nat.FLAG_L2NORM_QK, sh)
+        if variant == "plain":
+            st = lib.gdn2_recurrent_fwd(
+                q.data_ptr() + i * sz_k, k.data_ptr() + i * sz_k, v.data_ptr() + i * sz_v,
+                g.data_ptr() + i * sz_g, b.data_ptr() + i * sz_k, w.data_ptr() + i * sz_v,
+                nat.DTYPE_BF16, nat.DTYPE_F32, o.data_ptr() + i * sz_v,
+                state.data_ptr(), state.data_ptr(), None, None, 0.0, None, N,
+                N, 1, H, H, K, V, scale, flags, sh)
+        else:
+            st = lib.gdn2_recurrent_fwd_ex(
+                q.data_ptr() + i * sz_k, k.data_ptr() + i * sz_k, v.data_ptr() + i * sz_v,
+                g.data_ptr() + i * sz_g, b.data_ptr() + i * sz_k, w.data_ptr() + i * sz_v,
+                nat.DTYPE_BF16, nat.DTYPE_F32, o.data_ptr() + i * sz_v,
+                state.data_ptr(), rows, slab, state.data_ptr(), rows, slab, None, None, 0.0,
+                None, N, nat.ptr(slots), nat.DTYPE_I32, 0 if slots is None else N, 1, None,
+                nat.DTYPE_I32, N, 1, H, H, K, V, scale, flags, sh)
         nat.check(st, "gdn2_recurrent_fwd")
 
     if eager_steps:
@@ -268,7 +294,8 @@ def bench_decode(torch, nat, dev, reps=3, eager_steps=0):
                 bytes_per_step=nbytes, achieved_GBps=round(gbs, 1),
                 frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4),
                 config={"workload": "C2 decode N64 H16 K128 V128, fp32 state in place, 1024 steps "
-                                    "in one HIP graph", "dtype": "bf16 in / fp32 state"})
+                                    "in one HIP graph", "dtype": "bf16 in / fp32 state",
+                        "state": variant})
 
 
 def traffic_probe(torch, nat, dev):
@@ -404,6 +431,10 @@ def main() -> int:
     }
     if not args.no_decode:
         out["decode"] = bench_decode(torch, nat, dev)
+        for variant in ("pooled", "transposed"):
+            r = bench_decode(torch, nat, dev, variant=variant)
+            out["decode"][variant] = {x: r[x] for x in ("us_per_step", "achieved_GBps",
+                                                        "frac_hbm_peak")}
     if not args.no_train:
         out["train"] = bench_train(torch, nat, dev, max(2, args.steps // 2), 1)
     if not args.no_cpu_baseline:

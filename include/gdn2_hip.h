@@ -29,12 +29,14 @@
 extern "C" {
 #endif
 
-#define GDN2_ABI_VERSION 1
+#define GDN2_ABI_VERSION 2
 
 enum gdn2_dtype {
     GDN2_DTYPE_F32 = 0,
     GDN2_DTYPE_BF16 = 1,
     GDN2_DTYPE_F16 = 2,
+    GDN2_DTYPE_I32 = 3, /* index tensors only (ssm_state_indices, ...) */
+    GDN2_DTYPE_I64 = 4,
 };
 
 enum gdn2_status {
@@ -51,6 +53,11 @@ enum gdn2_status {
 #define GDN2_FLAG_LOWER_BOUND 4u    /* with GATE_IN_KERNEL: bounded sigmoid    */
 #define GDN2_FLAG_SAVE_FOR_BWD 8u   /* gdn2_chunk_fwd: keep what the backward   *
                                      * needs in a training-size workspace       */
+#define GDN2_FLAG_TRANSPOSE_STATE 16u     /* gdn2_recurrent_fwd_ex: states are  *
+                                           * [.., V, K] (K fastest)             */
+#define GDN2_FLAG_INPLACE_FINAL_STATE 32u /* gdn2_recurrent_fwd_ex with state  *
+                                           * indices: per-token states go to    *
+                                           * the indexed slots, not token rows  */
 
 int gdn2_abi_version(void);
 const char *gdn2_status_string(int status);
@@ -74,6 +81,46 @@ int gdn2_recurrent_fwd(const void *q, const void *k, const void *v, const void *
                        const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
                        int num_seqs, int B, int T, int H, int HV, int K, int V, float scale,
                        unsigned flags, void *stream);
+
+/*
+ * Token-serial forward with the serving options of fused_recurrent_gdn2_fwd
+ * (reference gdn2_ops/fused_recurrent_gdn2.py:344-458, kernel :129-341):
+ * a state pool addressed through ssm_state_indices (continuous batching),
+ * num_accepted_tokens (speculative decoding) and the transposed state layout.
+ * gdn2_recurrent_fwd is this call with rows = N, row strides = HV*K*V and no
+ * indices.
+ *
+ *   initial_state / final_state   float32 arrays of *_rows rows, row r of a
+ *       state at base + r*row_stride (elements; row_stride >= HV*K*V and a
+ *       multiple of 4), each row [HV, K, V] ([HV, V, K] with
+ *       GDN2_FLAG_TRANSPOSE_STATE, which then needs K % 4 == 0).
+ *   ssm_state_indices  NULL, or indices_numel int32/int64 (indices_dtype =
+ *       GDN2_DTYPE_I32/I64) slot numbers; sequence n, position t reads entry
+ *       n*indices_seq_stride + t (the reference's addressing, :215-224, 312-320).
+ *       With indices, sequence n starts from initial_state row
+ *       idx[n*stride + i0] (i0 = num_accepted_tokens[n] - 1, else 0), and the
+ *       state after each of its tokens t is stored
+ *         - to final_state row idx[n*stride + t] with GDN2_FLAG_INPLACE_FINAL_STATE,
+ *         - else to final_state row bos + t (the token's packed position).
+ *       Without indices the final state of sequence n goes to row n.
+ *       An index entry outside [0, indices_numel) or a slot outside
+ *       [0, rows) is a padded entry: that state is read as zero / not
+ *       stored (the reference does not guard these accesses).
+ *   num_accepted_tokens  NULL, or N int32/int64 counts (accepted_dtype);
+ *       used only with ssm_state_indices.
+ */
+int gdn2_recurrent_fwd_ex(const void *q, const void *k, const void *v, const void *g,
+                          const void *b, const void *w, int io_dtype, int g_dtype, void *o,
+                          const float *initial_state, int64_t initial_state_rows,
+                          int64_t initial_state_row_stride, float *final_state,
+                          int64_t final_state_rows, int64_t final_state_row_stride,
+                          const float *A_log, const float *dt_bias, float lower_bound,
+                          const int64_t *cu_seqlens, int num_seqs,
+                          const void *ssm_state_indices, int indices_dtype,
+                          int64_t indices_numel, int64_t indices_seq_stride,
+                          const void *num_accepted_tokens, int accepted_dtype, int B, int T,
+                          int H, int HV, int K, int V, float scale, unsigned flags,
+                          void *stream);
 
 /*
  * Bytes of device workspace gdn2_chunk_fwd needs for this shape.

@@ -22,6 +22,13 @@ and chunks).  Functions and the reference code they restate:
                            reference's own chunk form (``gdn2.py:243-369``) uses
                            absolute decays and underflows, so it is not
                            restated.
+* ``recurrent_fwd_pooled`` -- the serving options of the token-serial op
+                           (``fused_recurrent_gdn2.py:215-232, 311-333``): a state
+                           pool addressed through ``ssm_state_indices``
+                           (continuous batching), ``num_accepted_tokens``
+                           (speculative decoding), per-token state stores and
+                           the transposed ``[V, K]`` state layout, around
+                           ``recurrent_fwd``.
 * ``recurrent_vjp``     -- reverse-mode derivative of ``recurrent_fwd``
                            (the gradients ``ChunkGDN2Function.backward`` returns,
                            ``chunk_gdn2.py:2461-2547``: dq, dk, dv, dg, db, dw,
@@ -42,6 +49,11 @@ How each function is pinned (tests/test_oracle.py):
                  (qwen3_next) for broadcast scalar gates; split/resume and
                  zero-padding invariance.
   chunk_fwd      equals recurrent_fwd for chunk sizes 1..T incl. ragged tails.
+  recurrent_fwd_pooled  identity slots reduce it to recurrent_fwd; a speculative
+                 step resumed from slot num_accepted-1 equals the plain
+                 recurrence over the accepted tokens followed by the new ones;
+                 per-token stores equal the recurrence truncated at each token;
+                 the transposed layout is the swapped axes of the plain one.
   recurrent_vjp  central finite differences of recurrent_fwd in float64.
   chunk_vjp      equals recurrent_vjp for several chunk sizes incl. ragged tails.
   make_inputs    distribution moments and l2-norms (cheap sanity only; it is a
@@ -56,6 +68,7 @@ __all__ = [
     "l2normalize",
     "recurrent_fwd",
     "chunk_fwd",
+    "recurrent_fwd_pooled",
     "recurrent_vjp",
     "chunk_vjp",
     "make_inputs",
@@ -221,6 +234,95 @@ def chunk_fwd(
                 S = np.exp(G[-1])[:, None] * S + (kc * np.exp(G[-1][None, :] - G)).T @ U
             final[bi, h] = S
     return o, final
+
+
+def recurrent_fwd_pooled(
+    q,
+    k,
+    v,
+    g,
+    b,
+    w,
+    state_pool,
+    ssm_state_indices,
+    num_accepted_tokens=None,
+    inplace_final_state=True,
+    scale=None,
+    use_qk_l2norm_in_kernel=True,
+    cu_seqlens=None,
+    transpose_state_layout=False,
+    final_rows=None,
+):
+    r"""Token-serial forward over a state pool (continuous batching).
+
+    Restates the addressing of the reference kernel
+    (``fused_recurrent_gdn2.py:215-232`` and ``:311-326``). The index entry of
+    sequence ``n`` at position ``t`` is ``idx.flat[n * stride + t]``, where
+    ``stride`` is 1 for ``[N]`` indices and ``T_max`` for ``[N, T_max]``.
+
+    * **Initial state.** Sequence ``n`` starts from pool row ``idx[n, i0]``, with
+      ``i0 = num_accepted_tokens[n] - 1`` if given, else 0.
+    * **Per-token stores.** After each token ``t``, the state is stored to pool
+      row ``idx[n, t]`` when ``inplace_final_state``. Otherwise it goes to row
+      ``bos + t`` of a new array of ``final_rows`` rows.
+    * **Padded entries.** An entry outside the index array, or a slot outside the
+      pool, reads a zero state and stores nothing. The reference leaves that case
+      unguarded; this is the HIP op's documented behaviour.
+    * **Transposed layout.** With ``transpose_state_layout``, pool rows are
+      ``[HV, V, K]``.
+    * **Order.** All initial states are read before any store, so sequences must
+      not share slots, as on the GPU.
+
+    Returns ``(o, final, written)``:
+    * ``final`` is the updated pool (in place) or the new array;
+    * ``written`` is the sorted list of rows that were stored.
+    """
+    B, T = np.shape(q)[:2]
+    HV, V, K = np.shape(v)[2], np.shape(v)[3], np.shape(q)[3]
+    idx = np.asarray(ssm_state_indices)
+    stride = 1 if idx.ndim == 1 else idx.shape[1]
+    flat = idx.reshape(-1).astype(np.int64)
+    pool = np.array(state_pool, dtype=np.float64)
+    rows = pool.shape[0]
+    seqs = _seq_slices(B, T, cu_seqlens)
+
+    def slot(pos, nrows):
+        if pos < 0 or pos >= flat.size:
+            return -1
+        s_ = int(flat[pos])
+        return s_ if 0 <= s_ < nrows else -1
+
+    def to_kv(x):
+        return np.swapaxes(x, -1, -2) if transpose_state_layout else x
+
+    if inplace_final_state:
+        final = pool.copy()
+    else:
+        final = np.zeros((final_rows if final_rows is not None else len(seqs),) + pool.shape[1:])
+    o = np.zeros((B, T, HV, V))
+    written = set()
+    pending = []
+    for n, (bi, t0, t1) in enumerate(seqs):
+        if t1 == t0:
+            continue
+        i0 = int(num_accepted_tokens[n]) - 1 if num_accepted_tokens is not None else 0
+        s0 = slot(n * stride + i0, rows)
+        h0 = np.zeros((1, HV, K, V)) if s0 < 0 else to_kv(pool[s0])[None]
+        sl = (slice(bi, bi + 1), slice(t0, t1))
+        on, _, states = recurrent_fwd(q[sl], k[sl], v[sl], g[sl], b[sl], w[sl], h0, scale=scale,
+                                      use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
+                                      return_states=True)
+        o[bi, t0:t1] = on[0]
+        for t, S in enumerate(states[0]):
+            tok = bi * T + t0 + t  # packed token position (bos + t)
+            row = slot(n * stride + t, final.shape[0]) if inplace_final_state else (
+                tok if tok < final.shape[0] else -1)
+            if row >= 0:
+                pending.append((row, to_kv(S)))
+    for row, S in pending:
+        final[row] = S
+        written.add(row)
+    return o, final, sorted(written)
 
 
 def _l2norm_vjp(x_raw, dy, eps=L2_EPS):

@@ -15,16 +15,20 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede dlopen of the HIP library)
 
 LIB_PATH = Path(os.environ.get("GDN2_HIP_LIB", Path(__file__).with_name("libgdn2_hip.so")))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F16 = 2
+DTYPE_I32 = 3
+DTYPE_I64 = 4
 
 FLAG_L2NORM_QK = 1
 FLAG_GATE_IN_KERNEL = 2
 FLAG_LOWER_BOUND = 4
 FLAG_SAVE_FOR_BWD = 8
+FLAG_TRANSPOSE_STATE = 16
+FLAG_INPLACE_FINAL_STATE = 32
 
 OK = 0
 ERR_INVALID = -1
@@ -37,6 +41,7 @@ _i = ctypes.c_int
 _f = ctypes.c_float
 _u = ctypes.c_uint
 _sz = ctypes.c_size_t
+_i64 = ctypes.c_int64
 
 # Every exported symbol with its ctypes signature (restype, argtypes).
 SIGNATURES: dict[str, tuple] = {
@@ -46,6 +51,11 @@ SIGNATURES: dict[str, tuple] = {
         _i,
         [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _i,
          _i, _i, _i, _i, _i, _i, _f, _u, _vp],
+    ),
+    "gdn2_recurrent_fwd_ex": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp,
+         _f, _vp, _i, _vp, _i, _i64, _i64, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _u, _vp],
     ),
     "gdn2_chunk_fwd_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _vp, _i]),
     "gdn2_chunk_fwd": (
@@ -121,6 +131,15 @@ def dtype_code(dt: torch.dtype) -> int:
     if dt == torch.float16:
         return DTYPE_F16
     raise NotImplementedError(f"gdn2 HIP kernels support float32/bfloat16/float16, not {dt}")
+
+
+def index_dtype_code(t: torch.Tensor | None) -> int:
+    """Dtype code of an index tensor (int32 / int64); int64 when absent."""
+    if t is None or t.dtype == torch.int64:
+        return DTYPE_I64
+    if t.dtype == torch.int32:
+        return DTYPE_I32
+    raise NotImplementedError(f"gdn2 index tensors must be int32/int64, not {t.dtype}")
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

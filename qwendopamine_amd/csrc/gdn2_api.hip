@@ -73,22 +73,30 @@ const char *gdn2_status_string(int status)
     }
 }
 
-int gdn2_recurrent_fwd(const void *q, const void *k, const void *v, const void *g,
-                       const void *b, const void *w, int io_dtype, int g_dtype, void *o,
-                       const float *initial_state, float *final_state, const float *A_log,
-                       const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
-                       int num_seqs, int B, int T, int H, int HV, int K, int V, float scale,
-                       unsigned flags, void *stream)
+int gdn2_recurrent_fwd_ex(const void *q, const void *k, const void *v, const void *g,
+                          const void *b, const void *w, int io_dtype, int g_dtype, void *o,
+                          const float *initial_state, int64_t initial_state_rows,
+                          int64_t initial_state_row_stride, float *final_state,
+                          int64_t final_state_rows, int64_t final_state_row_stride,
+                          const float *A_log, const float *dt_bias, float lower_bound,
+                          const int64_t *cu_seqlens, int num_seqs,
+                          const void *ssm_state_indices, int indices_dtype,
+                          int64_t indices_numel, int64_t indices_seq_stride,
+                          const void *num_accepted_tokens, int accepted_dtype, int B, int T,
+                          int H, int HV, int K, int V, float scale, unsigned flags,
+                          void *stream)
 {
     if (!valid_dtype(io_dtype) || !valid_dtype(g_dtype)) return GDN2_ERR_INVALID;
     if (B < 0 || T < 0 || H <= 0 || HV <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
     if (HV % H != 0) return GDN2_ERR_INVALID;
-    if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND))
+    if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND |
+                  GDN2_FLAG_TRANSPOSE_STATE | GDN2_FLAG_INPLACE_FINAL_STATE))
         return GDN2_ERR_INVALID;
     if ((flags & GDN2_FLAG_LOWER_BOUND) && !(flags & GDN2_FLAG_GATE_IN_KERNEL))
         return GDN2_ERR_INVALID;
     if ((flags & GDN2_FLAG_GATE_IN_KERNEL) && !A_log) return GDN2_ERR_INVALID;
     if (K > 256 || (V % 4) != 0) return GDN2_ERR_UNSUPPORTED;
+    if ((flags & GDN2_FLAG_TRANSPOSE_STATE) && (K % 4) != 0) return GDN2_ERR_UNSUPPORTED;
     int N = B;
     if (cu_seqlens) {
         if (B != 1 || num_seqs < 0) return GDN2_ERR_INVALID;
@@ -96,6 +104,28 @@ int gdn2_recurrent_fwd(const void *q, const void *k, const void *v, const void *
     }
     const int64_t ntok = static_cast<int64_t>(B) * T;
     if (ntok > 0 && (!q || !k || !v || !g || !b || !w || !o)) return GDN2_ERR_INVALID;
+    // State rows: 16-byte aligned, non-overlapping heads.
+    const int64_t slab = static_cast<int64_t>(HV) * K * V;
+    const bool pooled = ssm_state_indices != nullptr;
+    if (initial_state) {
+        if (initial_state_row_stride < slab || (initial_state_row_stride % 4) != 0 ||
+            initial_state_rows < 0 || (reinterpret_cast<uintptr_t>(initial_state) & 15) != 0)
+            return GDN2_ERR_INVALID;
+        if (!pooled && initial_state_rows < N) return GDN2_ERR_INVALID;
+    }
+    if (final_state) {
+        if (final_state_row_stride < slab || (final_state_row_stride % 4) != 0 ||
+            final_state_rows < 0 || (reinterpret_cast<uintptr_t>(final_state) & 15) != 0)
+            return GDN2_ERR_INVALID;
+        if (!pooled && final_state_rows < N) return GDN2_ERR_INVALID;
+    }
+    if (pooled) {
+        if (indices_dtype != GDN2_DTYPE_I32 && indices_dtype != GDN2_DTYPE_I64) return GDN2_ERR_INVALID;
+        if (indices_numel < 0 || indices_seq_stride < 0) return GDN2_ERR_INVALID;
+        if (num_accepted_tokens && accepted_dtype != GDN2_DTYPE_I32 &&
+            accepted_dtype != GDN2_DTYPE_I64)
+            return GDN2_ERR_INVALID;
+    }
     if (N == 0) return GDN2_OK;
     if (static_cast<int64_t>(N) * HV > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
 
@@ -110,9 +140,35 @@ int gdn2_recurrent_fwd(const void *q, const void *k, const void *v, const void *
     p.T = T; p.H = H; p.HV = HV; p.K = K; p.V = V;
     p.scale = scale;
     p.flags = flags;
+    p.h0_rows = initial_state ? initial_state_rows : 0;
+    p.h0_stride = initial_state_row_stride;
+    p.ht_rows = final_state ? final_state_rows : 0;
+    p.ht_stride = final_state_row_stride;
+    p.state_indices = ssm_state_indices;
+    p.accepted = pooled ? num_accepted_tokens : nullptr;
+    p.idx_numel = pooled ? indices_numel : 0;
+    p.idx_seq_stride = pooled ? indices_seq_stride : 0;
+    p.idx_i64 = indices_dtype == GDN2_DTYPE_I64;
+    p.acc_i64 = accepted_dtype == GDN2_DTYPE_I64;
     const hipError_t err =
         launch_recurrent_fwd(p, io_dtype, g_dtype, N, static_cast<hipStream_t>(stream));
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_recurrent_fwd(const void *q, const void *k, const void *v, const void *g,
+                       const void *b, const void *w, int io_dtype, int g_dtype, void *o,
+                       const float *initial_state, float *final_state, const float *A_log,
+                       const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
+                       int num_seqs, int B, int T, int H, int HV, int K, int V, float scale,
+                       unsigned flags, void *stream)
+{
+    if (flags & (GDN2_FLAG_TRANSPOSE_STATE | GDN2_FLAG_INPLACE_FINAL_STATE)) return GDN2_ERR_INVALID;
+    const int64_t rows = cu_seqlens ? num_seqs : B;
+    const int64_t slab = static_cast<int64_t>(HV) * K * V;
+    return gdn2_recurrent_fwd_ex(q, k, v, g, b, w, io_dtype, g_dtype, o, initial_state, rows,
+                                 slab, final_state, rows, slab, A_log, dt_bias, lower_bound,
+                                 cu_seqlens, num_seqs, nullptr, GDN2_DTYPE_I64, 0, 0, nullptr,
+                                 GDN2_DTYPE_I64, B, T, H, HV, K, V, scale, flags, stream);
 }
 
 size_t gdn2_chunk_fwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,

@@ -20,6 +20,15 @@ struct RecurrentParams {
     int T, H, HV, K, V;
     float scale;
     unsigned flags;
+    // State rows: row r of a state array starts at base + r * stride (floats);
+    // row indices outside [0, rows) are padding (read as zero, not stored).
+    int64_t h0_rows, h0_stride, ht_rows, ht_stride;
+    // Continuous batching / speculative decoding (fused_recurrent_gdn2.py:215-224,
+    // 311-326): sequence n, position t uses slot state_indices[n * idx_seq_stride + t].
+    const void *state_indices;  // NULL = no state pool
+    const void *accepted;       // num_accepted_tokens, NULL = not speculative
+    int64_t idx_numel, idx_seq_stride;
+    int idx_i64, acc_i64;
 };
 
 hipError_t launch_recurrent_fwd(const RecurrentParams &p, int io_dtype, int g_dtype, int N,

@@ -85,6 +85,155 @@ __device__ __forceinline__ float4 shfl_xor4(float4 x, int off)
                        __shfl_xor(x.z, off, kWave), __shfl_xor(x.w, off, kWave));
 }
 
+__device__ __forceinline__ int64_t load_index(const void *p, int is64, int64_t i)
+{
+    return is64 ? static_cast<const int64_t *>(p)[i]
+                : static_cast<int64_t>(static_cast<const int32_t *>(p)[i]);
+}
+
+// State-pool slot of index entry `pos`, or -1 for a padded entry (entry or
+// slot out of range).
+__device__ __forceinline__ int64_t pool_slot(const RecurrentParams &p, int64_t pos, int64_t rows)
+{
+    if (pos < 0 || pos >= p.idx_numel) return -1;
+    const int64_t s = load_index(p.state_indices, p.idx_i64, pos);
+    return (s >= 0 && s < rows) ? s : -1;
+}
+
+// Start of the initial state of (sequence n, value head hv), or NULL (zero
+// state).  With a state pool the row is the slot of entry
+// n * idx_seq_stride + i0, i0 = num_accepted_tokens[n] - 1 when speculative
+// (fused_recurrent_gdn2.py:215-232).
+__device__ __forceinline__ const float *initial_row(const RecurrentParams &p, int n, int hv)
+{
+    if (!p.h0) return nullptr;
+    int64_t row = n;
+    if (p.state_indices) {
+        const int64_t i0 = p.accepted ? load_index(p.accepted, p.acc_i64, n) - 1 : 0;
+        row = pool_slot(p, static_cast<int64_t>(n) * p.idx_seq_stride + i0, p.h0_rows);
+        if (row < 0) return nullptr;
+    }
+    return p.h0 + row * p.h0_stride + static_cast<int64_t>(hv) * p.K * p.V;
+}
+
+// Where the state after token t (0-based within sequence n, packed position
+// tok) is stored, or NULL: with a state pool every token's state goes to the
+// slot of entry n * idx_seq_stride + t (in place) or to row tok
+// (fused_recurrent_gdn2.py:311-326); otherwise only the last token's state,
+// to row n (:328-333).
+__device__ __forceinline__ float *store_row(const RecurrentParams &p, int n, int hv, int64_t t,
+                                            int64_t tok)
+{
+    if (!p.ht) return nullptr;
+    int64_t row = n;
+    if (p.state_indices) {
+        row = (p.flags & GDN2_FLAG_INPLACE_FINAL_STATE)
+                  ? pool_slot(p, static_cast<int64_t>(n) * p.idx_seq_stride + t, p.ht_rows)
+                  : (tok < p.ht_rows ? tok : -1);
+        if (row < 0) return nullptr;
+    }
+    return p.ht + row * p.ht_stride + static_cast<int64_t>(hv) * p.K * p.V;
+}
+
+// Transposed state rows ([V, K] per head, element (k, v) at base[v*K + k]).
+// The slab (K rows x VB columns) moves through an LDS tile in blocks of KB
+// rows: 16-byte accesses run along k in HBM, and the registers keep the
+// layout of the [K, V] path (thread (rg, cq) holds row rg + i*RG, columns
+// c0 + 4cq .. +3).  Rows >= K and columns >= V read as zero and are not stored.
+template <int NR, int TPR>
+struct TransposedSlab {
+    static constexpr int RG = 256 / TPR, VB = 4 * TPR;
+    static constexpr int KB = RG > 32 ? RG : 32;  // rows per block
+    static constexpr int BI = KB / RG;            // register rows (i) per block
+    static constexpr int LD = KB + 1;             // tile row stride (floats)
+    static constexpr int Q = KB / 4;              // float4 per tile row
+    static constexpr int PER = VB * Q / 256;      // float4 per thread per block
+    static constexpr int TILE_FLOATS = VB * LD;
+    static_assert(VB * Q % 256 == 0, "tile must split evenly over 256 threads");
+
+    static __device__ void load(float4 (&st)[NR], const float *base, int K, int V, int c0,
+                                float *tile)
+    {
+        const int tid = threadIdx.x, cq = tid % TPR, rg = tid / TPR;
+#pragma unroll
+        for (int b0 = 0; b0 < NR; b0 += BI) {
+            const int k0 = b0 * RG;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int idx = tid + j * 256, vl = idx / Q, kq = idx % Q;
+                const int vv = c0 + vl, kk = k0 + 4 * kq;
+                float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (vv < V && kk < K)
+                    x = *reinterpret_cast<const float4 *>(base + static_cast<int64_t>(vv) * K + kk);
+                float *t = tile + vl * LD + 4 * kq;
+                t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int ii = 0; ii < BI; ++ii) {
+                if (b0 + ii < NR) {
+                    const int rl = rg + ii * RG;
+                    const float *t = tile + 4 * cq * LD + rl;
+                    st[b0 + ii] = make_float4(t[0], t[LD], t[2 * LD], t[3 * LD]);
+                }
+            }
+            __syncthreads();
+        }
+    }
+
+    static __device__ void store(const float4 (&st)[NR], float *base, int K, int V, int c0,
+                                 float *tile)
+    {
+        const int tid = threadIdx.x, cq = tid % TPR, rg = tid / TPR;
+#pragma unroll
+        for (int b0 = 0; b0 < NR; b0 += BI) {
+            const int k0 = b0 * RG;
+#pragma unroll
+            for (int ii = 0; ii < BI; ++ii) {
+                if (b0 + ii < NR) {
+                    const int rl = rg + ii * RG;
+                    float *t = tile + 4 * cq * LD + rl;
+                    t[0] = st[b0 + ii].x; t[LD] = st[b0 + ii].y;
+                    t[2 * LD] = st[b0 + ii].z; t[3 * LD] = st[b0 + ii].w;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int idx = tid + j * 256, vl = idx / Q, kq = idx % Q;
+                const int vv = c0 + vl, kk = k0 + 4 * kq;
+                if (vv < V && kk < K) {
+                    const float *t = tile + vl * LD + 4 * kq;
+                    *reinterpret_cast<float4 *>(base + static_cast<int64_t>(vv) * K + kk) =
+                        make_float4(t[0], t[1], t[2], t[3]);
+                }
+            }
+            __syncthreads();
+        }
+    }
+};
+
+// Stores the register slab (columns c0 + 4cq.., rows rg + i*RG) to the state
+// row at dst, in [K, V] or transposed [V, K] order.  Called by the whole
+// workgroup (the transposed path synchronises).
+template <int NR, int TPR>
+__device__ __forceinline__ void store_state(const float4 (&st)[NR], float *dst, int K, int V,
+                                            int c0, bool trans, float *tile)
+{
+    if (trans) {
+        TransposedSlab<NR, TPR>::store(st, dst, K, V, c0, tile);
+        return;
+    }
+    constexpr int RG = 256 / TPR;
+    const int cq = threadIdx.x % TPR, rg = threadIdx.x / TPR, col = c0 + 4 * cq;
+    if (col >= V) return;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int r = rg + i * RG;
+        if (r < K) *reinterpret_cast<float4 *>(dst + static_cast<int64_t>(r) * V + col) = st[i];
+    }
+}
+
 // TPR threads cover one state row of VB = 4*TPR columns; RG = 256/TPR row
 // groups; each thread keeps NR rows (NR*RG >= K).
 template <typename TI, typename TG, int NR, int TPR>
@@ -130,17 +279,27 @@ __global__ __launch_bounds__(256) void recurrent_fwd_kernel(RecurrentParams p)
     const bool gate = (p.flags & GDN2_FLAG_GATE_IN_KERNEL) != 0;
     const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
 
-    const int64_t soff = (static_cast<int64_t>(n) * p.HV + hv) * K * V;
+    using TS = TransposedSlab<NR, TPR>;
+    extern __shared__ float s_tile[];  // TS::TILE_FLOATS floats, transposed layout only
+    const bool trans = (p.flags & GDN2_FLAG_TRANSPOSE_STATE) != 0;
+    const bool per_token = p.state_indices != nullptr;
     float4 st[NR];
+    const float *h0row = initial_row(p, n, hv);
+    if (trans && h0row) {
+        TS::load(st, h0row, K, V, vs * VB, s_tile);
+    } else {
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-        const int r = rg + i * RG;
-        st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (p.h0 && col_ok && r < K)
-            st[i] = *reinterpret_cast<const float4 *>(p.h0 + soff + static_cast<int64_t>(r) * V + col);
+        for (int i = 0; i < NR; ++i) {
+            const int r = rg + i * RG;
+            st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (h0row && col_ok && r < K)
+                st[i] = *reinterpret_cast<const float4 *>(h0row + static_cast<int64_t>(r) * V + col);
+        }
     }
 
-    const float a_log = gate ? p.A_log[hv] : 0.0f;
+    // The gate parameters are indexed by key head, as the reference kernel does
+    // (fused_recurrent_gdn2.py:259-265); HV == H outside grouped value heads.
+    const float a_log = gate ? p.A_log[h] : 0.0f;
 
     for (int64_t t = 0; t < len; ++t) {
         const int64_t tok = bos + t;
@@ -183,7 +342,7 @@ __global__ __launch_bounds__(256) void recurrent_fwd_kernel(RecurrentParams p)
             s_e[tid] = bv * kn;
             float gk = gv;
             if (gate) {
-                const float db = p.dt_bias ? p.dt_bias[hv * K + tid] : 0.0f;
+                const float db = p.dt_bias ? p.dt_bias[h * K + tid] : 0.0f;
                 gk = gate_activation(gv, a_log, db, use_lb, p.lower_bound);
             }
             s_a[tid] = expf(gk);
@@ -238,15 +397,15 @@ __global__ __launch_bounds__(256) void recurrent_fwd_kernel(RecurrentParams p)
         }
         if (rg == 0 && col_ok) vec4io<TI>::st(o, vw_off + col, f4_fma(u, kq, PO));
         __syncthreads();
+        if (per_token) {
+            float *dst = store_row(p, n, hv, t, tok);
+            if (dst) store_state<NR, TPR>(st, dst, K, V, vs * VB, trans, s_tile);
+        }
     }
 
-    if (p.ht && col_ok) {
-#pragma unroll
-        for (int i = 0; i < NR; ++i) {
-            const int r = rg + i * RG;
-            if (r < K)
-                *reinterpret_cast<float4 *>(p.ht + soff + static_cast<int64_t>(r) * V + col) = st[i];
-        }
+    if (!per_token) {
+        float *dst = store_row(p, n, hv, len - 1, bos + len - 1);
+        if (dst) store_state<NR, TPR>(st, dst, K, V, vs * VB, trans, s_tile);
     }
 }
 
@@ -284,12 +443,11 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
     float4 st[SLABS][NR];
     const int slab0 = blockIdx.x * SLABS;
     auto load_state = [&](float4 (&dst)[NR], int slab) {
+        const float *row = initial_row(p, slab / p.HV, slab % p.HV);
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
             dst[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (p.h0)
-                dst[i] = *reinterpret_cast<const float4 *>(p.h0 + static_cast<int64_t>(slab) * KD * VD +
-                                                           (rg + i * RG) * VD + col);
+            if (row) dst[i] = *reinterpret_cast<const float4 *>(row + (rg + i * RG) * VD + col);
         }
     };
     load_state(st[0], slab0);
@@ -336,8 +494,8 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
             s_e[tid] = bv * kn;
             float gk = gv;
             if (gate) {
-                const float db = p.dt_bias ? p.dt_bias[hv * KD + tid] : 0.0f;
-                gk = gate_activation(gv, p.A_log[hv], db, use_lb, p.lower_bound);
+                const float db = p.dt_bias ? p.dt_bias[h * KD + tid] : 0.0f;
+                gk = gate_activation(gv, p.A_log[h], db, use_lb, p.lower_bound);
             }
             s_a[tid] = expf(gk);
         }
@@ -375,6 +533,8 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
         }
         const float4 u = make_float4(ww.x * vv.x - R.x, ww.y * vv.y - R.y, ww.z * vv.z - R.z,
                                      ww.w * vv.w - R.w);
+        // One token per sequence: its state is the final state (packed position n).
+        float *dst = store_row(p, n, hv, 0, n);
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
             const int r = rg + i * RG;
@@ -383,8 +543,7 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
             st[s][i].y = fmaf(kr, u.y, st[s][i].y);
             st[s][i].z = fmaf(kr, u.z, st[s][i].z);
             st[s][i].w = fmaf(kr, u.w, st[s][i].w);
-            if (p.ht)
-                *reinterpret_cast<float4 *>(p.ht + static_cast<int64_t>(slab) * KD * VD + r * VD + col) = st[s][i];
+            if (dst) *reinterpret_cast<float4 *>(dst + r * VD + col) = st[s][i];
         }
         if (rg == 0) vec4io<TI>::st(o, vw_off + col, f4_fma(u, kq, PO));
         __syncthreads();
@@ -398,25 +557,30 @@ static hipError_t launch_nr(const RecurrentParams &p, int N, hipStream_t stream)
     const int need = (p.K + RG - 1) / RG;
     const int nvs = (p.V + 4 * TPR - 1) / (4 * TPR);
     dim3 grid(N * p.HV, nvs);
+    // The LDS tile of the transposed state layout (same size for every NR).
+    const size_t lds = (p.flags & GDN2_FLAG_TRANSPOSE_STATE)
+                           ? TransposedSlab<1, TPR>::TILE_FLOATS * sizeof(float)
+                           : 0;
     if (need <= 1)
-        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 1, TPR>), grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 1, TPR>), grid, dim3(256), lds, stream, p);
     else if (need <= 2)
-        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 2, TPR>), grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 2, TPR>), grid, dim3(256), lds, stream, p);
     else if (need <= 4)
-        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 4, TPR>), grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 4, TPR>), grid, dim3(256), lds, stream, p);
     else if (need <= 8)
-        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 8, TPR>), grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 8, TPR>), grid, dim3(256), lds, stream, p);
     else if (need <= 16)
-        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 16, TPR>), grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 16, TPR>), grid, dim3(256), lds, stream, p);
     else
-        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 32, TPR>), grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((recurrent_fwd_kernel<TI, TG, 32, TPR>), grid, dim3(256), lds, stream, p);
     return hipGetLastError();
 }
 
 template <typename TI, typename TG>
 static hipError_t launch_tpr(const RecurrentParams &p, int N, hipStream_t stream)
 {
-    if (p.T == 1 && !p.cu_seqlens && p.K == 128 && p.V == 128) {
+    const bool trans = (p.flags & GDN2_FLAG_TRANSPOSE_STATE) != 0;
+    if (p.T == 1 && !p.cu_seqlens && p.K == 128 && p.V == 128 && !trans) {
         const int nslabs = N * p.HV;
         hipLaunchKernelGGL((decode_step_kernel<TI, TG>), dim3((nslabs + 1) / 2), dim3(256), 0, stream,
                            p, nslabs);

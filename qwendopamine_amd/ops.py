@@ -136,16 +136,28 @@ def fused_recurrent_gdn2_fwd(
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """Launch the token-serial HIP kernel (reference ``fused_recurrent_gdn2.py:344-458``).
 
-    ``inplace_final_state`` writes the final state back into ``initial_state``
-    (which must then be a contiguous float32 tensor); ``output_final_state``
-    allocates a new float32 ``[N, HV, K, V]`` state.
+    Final state (as the reference resolves it, ``:395-404``):
+
+    * ``inplace_final_state`` writes back into ``initial_state``, which must be
+      float32 with contiguous ``[HV, K, V]`` rows (any row stride).
+    * Otherwise ``output_final_state`` allocates a new float32 state,
+      ``[N, HV, K, V]`` (``[N, HV, V, K]`` with ``transpose_state_layout``).
+
+    Serving options (kernel ``:215-232, 311-333``):
+
+    * ``ssm_state_indices`` (``[N]`` or ``[N, T_max]``, int32/int64) makes
+      ``initial_state`` a state pool.  Sequence ``n`` starts from slot
+      ``idx[n, i0]``, where ``i0 = num_accepted_tokens[n] - 1`` when speculative
+      and 0 otherwise.
+    * The state after each of its tokens ``t`` is stored to slot ``idx[n, t]``
+      (in place), or else to row ``bos + t`` of the new final state.  That state
+      has ``max(N, tokens)`` rows, so every token's row exists.
+    * A negative or out-of-range slot marks a padded entry: it starts from a zero
+      state and its states are not stored.
+    * ``transpose_state_layout`` stores every state as ``[V, K]`` (K fastest).
     """
     name = "fused_recurrent_gdn2"
-    if ssm_state_indices is not None or num_accepted_tokens is not None:
-        raise NotImplementedError(f"{name}: continuous batching / speculative decoding")
-    if transpose_state_layout:
-        raise NotImplementedError(f"{name}: transpose_state_layout")
-    _require_gpu(name, q, k, v, g, b, w, initial_state)
+    _require_gpu(name, q, k, v, g, b, w, initial_state, ssm_state_indices, num_accepted_tokens)
     _check_shapes(name, q, k, v, g, b, w, same_heads=False)
     B, T, H, K = k.shape
     HV, V = v.shape[2], v.shape[3]
@@ -156,36 +168,86 @@ def fused_recurrent_gdn2_fwd(
     g = _io(g, g.dtype if g.dtype in (torch.float32, dt) else torch.float32)
     cu_dev, cu_host = _cu(cu_seqlens, q.device, T)
     N = B if cu_seqlens is None else cu_host.numel() - 1
+    state_shape = (HV, V, K) if transpose_state_layout else (HV, K, V)
     if out is None:
         out = torch.empty_like(v)
     else:
         assert out.shape == v.shape and out.dtype == dt and out.is_contiguous()
+
+    pooled = ssm_state_indices is not None
+    idx = acc = None
+    idx_stride = 0
+    if pooled:
+        idx = ssm_state_indices
+        if idx.dtype not in (torch.int32, torch.int64):
+            idx = idx.long()
+        idx = idx.contiguous()
+        assert idx.dim() in (1, 2) and idx.shape[0] >= N, (
+            f"ssm_state_indices must be [N] or [N, T] with N >= {N}; got {tuple(idx.shape)}"
+        )
+        idx_stride = 1 if idx.dim() == 1 else idx.shape[1]
+        if num_accepted_tokens is not None:
+            acc = num_accepted_tokens
+            if acc.dtype not in (torch.int32, torch.int64):
+                acc = acc.long()
+            acc = acc.contiguous()
+            assert acc.numel() >= N, f"num_accepted_tokens needs {N} entries; got {acc.numel()}"
+
+    def _rows(x):
+        assert tuple(x.shape[1:]) == state_shape, (
+            f"state rows must be {state_shape}; got {tuple(x.shape[1:])}"
+        )
+        assert x.stride()[1:] == (state_shape[1] * state_shape[2], state_shape[2], 1), (
+            "state rows must be contiguous"
+        )
+        return x.shape[0], x.stride(0)
+
     h0 = None
+    h0_rows = h0_stride = 0
     if initial_state is not None:
         if inplace_final_state:
-            assert initial_state.dtype == torch.float32 and initial_state.is_contiguous(), (
-                "inplace_final_state needs a contiguous float32 initial_state"
+            assert initial_state.dtype == torch.float32, (
+                "inplace_final_state needs a float32 initial_state"
             )
             h0 = initial_state
         else:
-            h0 = initial_state.float().contiguous()
-        assert tuple(h0.shape) == (N, HV, K, V), f"initial_state must be {(N, HV, K, V)}"
+            h0 = initial_state.float()
+            if h0.stride()[1:] != (state_shape[1] * state_shape[2], state_shape[2], 1):
+                h0 = h0.contiguous()
+        h0_rows, h0_stride = _rows(h0)
+        if not pooled:
+            assert h0_rows == N, f"initial_state must have {N} rows; got {h0_rows}"
     if inplace_final_state:
         assert initial_state is not None, "inplace_final_state=True requires an initial_state"
         ht = h0
     elif output_final_state:
-        ht = torch.empty(N, HV, K, V, dtype=torch.float32, device=q.device)
+        rows = max(N, B * T) if pooled else N
+        ht = torch.empty(rows, *state_shape, dtype=torch.float32, device=q.device)
     else:
         ht = None
-    a_log, dtb = _gate_tensors(use_gate_in_kernel, A_log, dt_bias, HV, K)
+    ht_rows, ht_stride = _rows(ht) if ht is not None else (0, 0)
+    for x in (h0, ht):
+        if x is not None and (x.data_ptr() % 16 or x.stride(0) % 4):
+            raise ValueError(f"{name}: state rows must be 16-byte aligned")
+
+    # Gate parameters per key head (fused_recurrent_gdn2.py:259-265).
+    a_log, dtb = _gate_tensors(use_gate_in_kernel, A_log, dt_bias, H, K)
+    flags = _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound)
+    if transpose_state_layout:
+        flags |= nat.FLAG_TRANSPOSE_STATE
+    if inplace_final_state:
+        flags |= nat.FLAG_INPLACE_FINAL_STATE
     lib = nat.load()
-    st = lib.gdn2_recurrent_fwd(
+    st = lib.gdn2_recurrent_fwd_ex(
         nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(g), nat.ptr(b), nat.ptr(w),
         nat.dtype_code(dt), nat.dtype_code(g.dtype), nat.ptr(out),
-        nat.ptr(h0), nat.ptr(ht), nat.ptr(a_log), nat.ptr(dtb),
+        nat.ptr(h0), h0_rows, h0_stride, nat.ptr(ht), ht_rows, ht_stride,
+        nat.ptr(a_log), nat.ptr(dtb),
         float(lower_bound) if lower_bound is not None else 0.0,
-        nat.ptr(cu_dev), N, B, T, H, HV, K, V, float(scale),
-        _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound),
+        nat.ptr(cu_dev), N,
+        nat.ptr(idx), nat.index_dtype_code(idx), 0 if idx is None else idx.numel(), idx_stride,
+        nat.ptr(acc), nat.index_dtype_code(acc),
+        B, T, H, HV, K, V, float(scale), flags,
         nat.stream_handle(q.device),
     )
     nat.check(st, name)

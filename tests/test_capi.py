@@ -45,7 +45,9 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gdn2_abi_version() == 1
+    from qwendopamine_amd import _native as nat
+
+    assert lib.gdn2_abi_version() == nat.ABI_VERSION == 2
     assert lib.gdn2_status_string(0) == b"ok"
     assert b"invalid" in lib.gdn2_status_string(-1)
     assert b"workspace" in lib.gdn2_status_string(-4)
@@ -73,6 +75,37 @@ def test_invalid_arguments_rejected_before_launch(lib):
     # non-null tensors required when there are tokens
     st = lib.gdn2_chunk_fwd(None, None, None, None, None, None, 1, 0, None, None, None, None, None,
                             0.0, None, None, 1, 1, 8, 1, 16, 16, 1.0, 0, None, 0, None)
+    assert st == nat.ERR_INVALID
+
+
+def test_serving_arguments_rejected_before_launch(lib):
+    from qwendopamine_amd import _native as nat
+
+    def call(h0=None, h0_rows=0, h0_stride=0, ht=None, ht_rows=0, ht_stride=0, idx=None,
+             idx_dtype=nat.DTYPE_I64, acc=None, acc_dtype=nat.DTYPE_I32, K=16, V=16, flags=0,
+             B=0, T=0):
+        return lib.gdn2_recurrent_fwd_ex(None, None, None, None, None, None, 0, 0, None, h0, h0_rows,
+                                         h0_stride, ht, ht_rows, ht_stride, None, None, 0.0, None, 0,
+                                         idx, idx_dtype, 4, 1, acc, acc_dtype, B, T, 1, 1, K, V, 1.0,
+                                         flags, None)
+
+    # No sequences, valid arguments: nothing to launch.
+    assert call(h0=256, h0_rows=1, h0_stride=256) == nat.OK
+    # State rows overlapping the next row, or not 16-byte aligned.
+    assert call(h0=256, h0_rows=1, h0_stride=128) == nat.ERR_INVALID
+    assert call(h0=264, h0_rows=1, h0_stride=256) == nat.ERR_INVALID
+    assert call(ht=256, ht_rows=1, ht_stride=258) == nat.ERR_INVALID
+    # Without a state pool every sequence needs a row.
+    assert call(h0=256, h0_rows=0, h0_stride=256, B=1) == nat.ERR_INVALID
+    # Index tensors must be int32 / int64.
+    assert call(idx=256, idx_dtype=nat.DTYPE_F32) == nat.ERR_INVALID
+    assert call(idx=256, acc=512, acc_dtype=nat.DTYPE_BF16) == nat.ERR_INVALID
+    # The transposed layout moves K in 16-byte groups.
+    assert call(K=18, flags=nat.FLAG_TRANSPOSE_STATE) == nat.ERR_UNSUPPORTED
+    # The plain entry point takes neither serving flag.
+    st = lib.gdn2_recurrent_fwd(None, None, None, None, None, None, 0, 0, None, None, None, None,
+                                None, 0.0, None, 1, 1, 0, 1, 1, 16, 16, 1.0,
+                                nat.FLAG_TRANSPOSE_STATE, None)
     assert st == nat.ERR_INVALID
 
 

@@ -166,6 +166,84 @@ def test_gva_equals_repeated_heads():
     np.testing.assert_allclose(s1, s2, atol=1e-14)
 
 
+def test_pooled_identity_slots_reduce_to_recurrence():
+    """Slots n -> n with one token per sequence: the pooled op is the plain op."""
+    q, k, v, g, b, w, s0 = _rand(5, 1, 2, 8, 6, seed=21)
+    o_ref, s_ref = orc.recurrent_fwd(q, k, v, g, b, w, s0)
+    o, pool, written = orc.recurrent_fwd_pooled(q, k, v, g, b, w, s0, np.arange(5))
+    np.testing.assert_allclose(o, o_ref, atol=1e-14)
+    np.testing.assert_allclose(pool, s_ref, atol=1e-14)
+    assert written == list(range(5))
+
+
+def test_pooled_permuted_slots_and_padding():
+    """Slots are a permutation into a larger pool; a padded entry (-1) starts from zero and
+    stores nothing; untouched slots keep their contents."""
+    q, k, v, g, b, w, _ = _rand(4, 3, 2, 8, 6, seed=22)
+    rng = np.random.default_rng(23)
+    pool = rng.standard_normal((9, 2, 8, 6))
+    slots = np.array([[7, 7, 7], [2, 2, 2], [-1, -1, -1], [5, 5, 5]])
+    o, new, written = orc.recurrent_fwd_pooled(q, k, v, g, b, w, pool, slots)
+    assert written == [2, 5, 7]
+    for n, sl in enumerate(slots[:, 0]):
+        h0 = np.zeros((1, 2, 8, 6)) if sl < 0 else pool[sl][None]
+        on, sn = orc.recurrent_fwd(q[n:n + 1], k[n:n + 1], v[n:n + 1], g[n:n + 1], b[n:n + 1],
+                                   w[n:n + 1], h0)
+        np.testing.assert_allclose(o[n], on[0], atol=1e-14)
+        if sl >= 0:
+            np.testing.assert_allclose(new[sl], sn[0], atol=1e-14)
+    for r in (0, 1, 3, 4, 6, 8):
+        np.testing.assert_array_equal(new[r], pool[r])
+
+
+def test_speculative_resume_equals_accepted_prefix():
+    """Speculative decoding: step 1 stores the state after each draft token t in slot
+    idx[n, t]; step 2 resumes from slot idx[n, a_n - 1].  Its outputs must equal the plain
+    recurrence over the a_n accepted tokens of step 1 followed by the step-2 tokens."""
+    H, K, V, Tm = 2, 8, 6, 4
+    rng = np.random.default_rng(24)
+    s0 = rng.standard_normal((3, H, K, V)) * 0.3
+    slots = np.array([[0, 1, 2, 3], [4, 5, 6, 7], [8, 9, 10, 11]])
+    pool = np.zeros((12, H, K, V))
+    pool[slots[:, 0]] = s0  # each sequence's current state sits in its first slot
+    acc1 = np.array([1, 1, 1])
+    step1 = _rand(1, 3 * Tm, H, K, V, seed=25)[:6]
+    cu1 = [0, Tm, 2 * Tm, 3 * Tm]
+    _, pool1, _ = orc.recurrent_fwd_pooled(*step1, pool, slots, acc1, cu_seqlens=cu1)
+    acc2 = np.array([3, 1, 4])
+    lens2 = [2, 3, 1]
+    cu2 = np.concatenate([[0], np.cumsum(lens2)])
+    step2 = _rand(1, int(cu2[-1]), H, K, V, seed=26)[:6]
+    o2, pool2, _ = orc.recurrent_fwd_pooled(*step2, pool1, slots, acc2, cu_seqlens=cu2)
+    for n in range(3):
+        a = acc2[n]
+        prefix = [x[:, cu1[n]:cu1[n] + a] for x in step1]
+        new = [x[:, cu2[n]:cu2[n + 1]] for x in step2]
+        joined = [np.concatenate([pa, pb], axis=1) for pa, pb in zip(prefix, new)]
+        o_ref, s_ref, states = orc.recurrent_fwd(*joined, s0[n:n + 1], return_states=True)
+        np.testing.assert_allclose(o2[:, cu2[n]:cu2[n + 1]], o_ref[:, a:], atol=1e-13)
+        for t in range(lens2[n]):
+            np.testing.assert_allclose(pool2[slots[n, t]], states[0][a + t], atol=1e-13)
+
+
+def test_pooled_token_rows_and_transposed_layout():
+    """Without in-place stores the state after token t goes to row bos + t, which equals the
+    recurrence truncated after that token; the transposed layout is the swapped axes."""
+    q, k, v, g, b, w, s0 = _rand(2, 3, 2, 8, 6, seed=27)
+    _, _, states = orc.recurrent_fwd(q, k, v, g, b, w, s0, return_states=True)
+    o, rows, written = orc.recurrent_fwd_pooled(q, k, v, g, b, w, s0, np.array([0, 1]),
+                                                inplace_final_state=False, final_rows=6)
+    assert written == list(range(6))
+    for n in range(2):
+        for t in range(3):
+            np.testing.assert_allclose(rows[n * 3 + t], states[n][t], atol=1e-14)
+    o_t, pool_t, _ = orc.recurrent_fwd_pooled(q, k, v, g, b, w, np.swapaxes(s0, -1, -2),
+                                              np.array([1, 0]), transpose_state_layout=True)
+    o_p, pool_p, _ = orc.recurrent_fwd_pooled(q, k, v, g, b, w, s0, np.array([1, 0]))
+    np.testing.assert_allclose(o_t, o_p, atol=1e-14)
+    np.testing.assert_allclose(pool_t, np.swapaxes(pool_p, -1, -2), atol=1e-14)
+
+
 def test_vjp_matches_finite_differences():
     q, k, v, g, b, w, s0 = _rand(1, 11, 2, 6, 5, seed=9, decay="paper")
     rng = np.random.default_rng(10)
