@@ -438,7 +438,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkParams p)
 // ---------------------------------------------------------------------------
 // Scan: one workgroup per (sequence, head, value slice of BV columns).
 // ---------------------------------------------------------------------------
-template <PrecKind PK, int KP, int BV, typename TI>
+template <PrecKind PK, int KP, int BV, typename TI, bool TRAIN>
 __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB, int NP)
 {
     using P = Prec<PK>;
@@ -474,7 +474,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     const bool col_ok = active && col < V;
     // Training-mode emission: value tile vt of this wave, if inside V.
     const int VP = p.VP, vt = vs * NCT + wv;
-    const bool emit = p.hs != nullptr && active && 16 * vt < V;
+    const bool emit = TRAIN && active && 16 * vt < V;
     const Q ident = identity_q4<PK>(l);
     // An fp32 accumulator tile (rows 4kg+i, column m) stored transposed, in
     // A-order and the MFMA operand precision (an identity product transposes it).
@@ -505,7 +505,8 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     constexpr int EPV = 16 / static_cast<int>(sizeof(TI));  // values per 16-byte load
     constexpr int ZT = kChunk * BV / EPV;                    // loads per tensor per chunk
     constexpr int NZT = (ZT + 255) / 256;
-    const bool zvec = (V % EPV) == 0;
+    // Whole 16-byte row pieces for every row of this slice (uniform per workgroup).
+    const bool zfast = (V % EPV) == 0 && v0 + BV <= V;
     struct ZRaw {
         u32x4 v[NZT], w[NZT];
     };
@@ -514,18 +515,48 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
         lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
     };
-    auto issue_z = [&](ZRaw &r, int jc) __attribute__((always_inline)) {
+    // Slices that do not allow 16-byte loads (ragged V, a slice past V) are
+    // assembled element by element here, zero-filled, so that land_z never
+    // touches global memory: a load there would make its wait also cover the
+    // prefetch of the chunk after.
+    using Raw = std::conditional_t<sizeof(TI) == 2, uint16_t, uint32_t>;
+    struct RawRow {
+        Raw e[EPV];
+    };
+    auto issue_z = [&](auto fastc, ZRaw &r, int jc) __attribute__((always_inline)) {
         int64_t t0;
         int lc;
         chunk_rows(jc, t0, lc);
+        if constexpr (decltype(fastc)::value) {
+            // Dead lanes load the chunk's first row piece (always valid) and
+            // are zeroed when landed: a select on the loaded value here would
+            // make the request wait for its own data.
 #pragma unroll
-        for (int a = 0; a < NZT; ++a) {
-            const int task = ctid + 256 * a;
-            const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
-            const bool ok = task < ZT && tok < lc && zvec && v0 + c + EPV <= V;
-            const int64_t off = ((t0 + tok) * H + h) * V + v0 + c;
-            r.v[a] = ok ? *reinterpret_cast<const u32x4 *>(vp + off) : u32x4{0, 0, 0, 0};
-            r.w[a] = ok ? *reinterpret_cast<const u32x4 *>(wp + off) : u32x4{0, 0, 0, 0};
+            for (int a = 0; a < NZT; ++a) {
+                const int task = ctid + 256 * a;
+                const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
+                const bool live = task < ZT && tok < lc;
+                const int64_t off = live ? ((t0 + tok) * H + h) * V + v0 + c : (t0 * H + h) * V + v0;
+                r.v[a] = *reinterpret_cast<const u32x4 *>(vp + off);
+                r.w[a] = *reinterpret_cast<const u32x4 *>(wp + off);
+            }
+        } else {
+#pragma unroll
+            for (int a = 0; a < NZT; ++a) {
+                const int task = ctid + 256 * a;
+                const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
+                const bool live = task < ZT && tok < lc;
+                const int64_t off = ((t0 + tok) * H + h) * V + v0 + c;
+                RawRow rv, rw;
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) {
+                    const bool in = live && v0 + c + e < V;
+                    rv.e[e] = in ? reinterpret_cast<const Raw *>(vp)[off + e] : Raw(0);
+                    rw.e[e] = in ? reinterpret_cast<const Raw *>(wp)[off + e] : Raw(0);
+                }
+                r.v[a] = __builtin_bit_cast(u32x4, rv);
+                r.w[a] = __builtin_bit_cast(u32x4, rw);
+            }
         }
     };
     auto land_z = [&](const ZRaw &r, int jc, int buf) __attribute__((always_inline)) {
@@ -540,17 +571,11 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
             const TI *rv = reinterpret_cast<const TI *>(&r.v[a]);
             const TI *rw = reinterpret_cast<const TI *>(&r.w[a]);
-            const bool ok = tok < lc && zvec && v0 + c + EPV <= V;
             const int kt = tok >> 4, kgz = (tok & 15) >> 2, iz = tok & 3;
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
-                float z = 0.f;
-                if (ok) {
-                    z = io<TI>::ld(rv, e) * io<TI>::ld(rw, e);
-                } else if (tok < lc && v0 + c + e < V) {
-                    const int64_t off = ((t0 + tok) * H + h) * V + v0 + c + e;
-                    z = io<TI>::ld(vp, off) * io<TI>::ld(wp, off);
-                }
+                // Zero past the sequence end (and past V, zero-filled by issue_z).
+                const float z = tok < lc ? io<TI>::ld(rv, e) * io<TI>::ld(rw, e) : 0.f;
                 const int cl = c + e, ct = cl >> 4, nz = cl & 15;
                 dst[(kt * 4 + ct) * 256 + (nz + 16 * kgz) * 4 + iz] = P::from_f32(z);
             }
@@ -576,72 +601,82 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     // and in the single-buffer case one more per reload -- so the copy waves'
     // prefetch registers never overlap the compute waves' live ranges.
     if (copier) {
-        ZRaw zA, zB;
-        if (nch > 0) {
-            copy_blob(gc0, 0);
-            issue_z(zA, 0);
-            land_z(zA, 0, 0);
-        }
-        if constexpr (DB) {
-            u32x4 pA[PF], pB[PF];
-            auto issue = [&](u32x4 (&dst)[PF], int gci) __attribute__((always_inline)) {
-                const u32x4 *src = blob(gci);
-#pragma unroll
-                for (int u = 0; u < PF; ++u) {
-                    const int idx = ctid + 256 * u;
-                    dst[u] = src[idx < U16 ? idx : U16 - 1];
-                }
-            };
-            auto land = [&](const u32x4 (&src)[PF], int buf) __attribute__((always_inline)) {
-                u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf]);
-#pragma unroll
-                for (int u = 0; u < PF; ++u) {
-                    const int idx = ctid + 256 * u;
-                    if (idx < U16) dst[idx] = src[u];
-                }
-            };
-            if (nch > 1) {
-                issue(pA, gc0 + 1);
-                issue_z(zA, 1);
+        // The copy loop is instantiated once for 16-byte value rows and once
+        // for the element-wise rows of ragged slices (uniform per workgroup),
+        // so that each loop body is straight-line and the compiler's
+        // load-completion waits stay exact.
+        auto copy_loop = [&](auto fastc) __attribute__((always_inline)) {
+            ZRaw zA, zB;
+            if (nch > 0) {
+                copy_blob(gc0, 0);
+                issue_z(fastc, zA, 0);
+                land_z(zA, 0, 0);
             }
-            __syncthreads();
-            // Step jc: the blob and rows of chunk jc+1 (requested one step
-            // earlier) land in the idle buffer while chunk jc+2 is requested,
-            // so each request has two chunks of compute to arrive.  The loop
-            // is unrolled by two so that pA / pB swap roles at compile time.
-            for (int jc = 0; jc < nch; jc += 2) {
-                if (jc + 2 < nch) {
-                    issue(pB, gc0 + jc + 2);
-                    issue_z(zB, jc + 2);
-                }
-                if (jc + 1 < nch) {
-                    land_z(zA, jc + 1, 1);
-                    land(pA, 1);
+            if constexpr (DB) {
+                u32x4 pA[PF], pB[PF];
+                auto issue = [&](u32x4 (&dst)[PF], int gci) __attribute__((always_inline)) {
+                    const u32x4 *src = blob(gci);
+#pragma unroll
+                    for (int u = 0; u < PF; ++u) {
+                        const int idx = ctid + 256 * u;
+                        dst[u] = src[idx < U16 ? idx : U16 - 1];
+                    }
+                };
+                auto land = [&](const u32x4 (&src)[PF], int buf) __attribute__((always_inline)) {
+                    u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf]);
+#pragma unroll
+                    for (int u = 0; u < PF; ++u) {
+                        const int idx = ctid + 256 * u;
+                        if (idx < U16) dst[idx] = src[u];
+                    }
+                };
+                // Two chunks in flight: at step jc the blob and rows of chunk
+                // jc+1 (requested two steps earlier) land in the idle buffer
+                // after chunk jc+2 has been requested.  Unrolled by two so the
+                // register sets A / B swap roles at compile time.
+                if (nch > 1) {
+                    issue(pA, gc0 + 1);
+                    issue_z(fastc, zA, 1);
                 }
                 __syncthreads();
-                if (jc + 1 >= nch) break;
-                if (jc + 3 < nch) {
-                    issue(pA, gc0 + jc + 3);
-                    issue_z(zA, jc + 3);
-                }
-                if (jc + 2 < nch) {
-                    land_z(zB, jc + 2, 0);
-                    land(pB, 0);
-                }
-                __syncthreads();
-            }
-        } else {
-            __syncthreads();
-            for (int jc = 0; jc < nch; ++jc) {
-                __syncthreads();
-                if (jc + 1 < nch) {
-                    copy_blob(gc0 + jc + 1, 0);
-                    issue_z(zA, jc + 1);
-                    land_z(zA, jc + 1, 0);
+                for (int jc = 0; jc < nch; jc += 2) {
+                    if (jc + 2 < nch) {
+                        issue(pB, gc0 + jc + 2);
+                        issue_z(fastc, zB, jc + 2);
+                    }
+                    if (jc + 1 < nch) {
+                        land_z(zA, jc + 1, 1);
+                        land(pA, 1);
+                    }
+                    __syncthreads();
+                    if (jc + 1 >= nch) break;
+                    if (jc + 3 < nch) {
+                        issue(pA, gc0 + jc + 3);
+                        issue_z(fastc, zA, jc + 3);
+                    }
+                    if (jc + 2 < nch) {
+                        land_z(zB, jc + 2, 0);
+                        land(pB, 0);
+                    }
                     __syncthreads();
                 }
+            } else {
+                __syncthreads();
+                for (int jc = 0; jc < nch; ++jc) {
+                    __syncthreads();
+                    if (jc + 1 < nch) {
+                        copy_blob(gc0 + jc + 1, 0);
+                        issue_z(fastc, zA, jc + 1);
+                        land_z(zA, jc + 1, 0);
+                        __syncthreads();
+                    }
+                }
             }
-        }
+        };
+        if (zfast)
+            copy_loop(std::true_type{});
+        else
+            copy_loop(std::false_type{});
     } else {
         __syncthreads();
         for (int jc = 0; jc < nch; ++jc) {
@@ -653,7 +688,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
 
             // Training mode: this chunk's start state, A-order tiles (kt, vt).
-            if (emit) {
+            if constexpr (TRAIN) if (emit) {
                 st *hsb = static_cast<st *>(p.hs) + (static_cast<int64_t>(gc0 + jc) * H + h) * (KP * VP);
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt) emit_tile(hsb, k16_block(kt, vt, VP) + 4 * l, S[kt]);
@@ -667,65 +702,128 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) sf[kt] = pack4<PK>(S[kt]);
 
-            // U = X z + (-W) S, token block rt.
+            // The chunk's products run as 12 steps -- U for token blocks 0-3,
+            // O for token blocks 0-3, the state update for pairs of key tiles
+            // -- whose LDS A operands are read one step ahead into a second
+            // register set (sched_barrier keeps that order), so the MFMAs do
+            // not wait on LDS latency.  Outputs and training tiles are stored
+            // after the last step.
+            f32x4 ua[4], oa[4];
             Q uf[4];
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                f32x4 acc = zero4();
-#pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    if (2 * s <= rt)
-                        acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::X + k16_block(rt, 2 * s, 64) + 4 * l),
-                                       ld_q4<PK>(Bk + BL::X + k16_block(rt, 2 * s + 1, 64) + 4 * l),
-                                       zf[2 * s], zf[2 * s + 1]);
-#pragma unroll
-                for (int s = 0; s < NKS; ++s)
-                    acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::WN + k16_block(rt, 2 * s, KP) + 4 * l),
-                                   ld_q4<PK>(Bk + BL::WN + k16_block(rt, 2 * s + 1, KP) + 4 * l),
-                                   sf[2 * s], sf[2 * s + 1]);
-                uf[rt] = pack4<PK>(acc);
-                if (emit) {
-                    st *usb = static_cast<st *>(p.us) + (static_cast<int64_t>(gc0 + jc) * H + h) * (64 * VP);
-                    emit_tile(usb, k16_block(rt, vt, VP) + 4 * l, acc);
+            const float *gl = reinterpret_cast<const float *>(Bk + BL::GL);
+            constexpr int NSU = 4, NSO = 4, NSS = (NKT + 1) / 2, NSTEP = NSU + NSO + NSS;
+            constexpr int MAXP = 2 + NKS > 4 ? 2 + NKS : 4;  // operand pairs per step
+            // Pair j of step st: blob offsets of its two K16 A blocks (or -1).
+            auto pair_off = [](int st_, int j, int &o0, int &o1) __attribute__((always_inline)) {
+                o0 = o1 = -1;
+                if (st_ < NSU + NSO) {
+                    const int rt = st_ % 4;
+                    const bool isu = st_ < NSU;
+                    if (j < NKS) {  // W (U) or Qbar (O) against the state
+                        const int base = isu ? BL::WN : BL::QB;
+                        o0 = base + k16_block(rt, 2 * j, KP);
+                        o1 = base + k16_block(rt, 2 * j + 1, KP);
+                    } else if (j - NKS < 2 && 2 * (j - NKS) <= rt) {  // X (U) or Aqk (O), causal
+                        const int base = isu ? BL::X : BL::AQ;
+                        o0 = base + k16_block(rt, 2 * (j - NKS), 64);
+                        o1 = base + k16_block(rt, 2 * (j - NKS) + 1, 64);
+                    }
+                } else {
+                    const int kt = 2 * (st_ - NSU - NSO) + j / 2, sx = j % 2;
+                    if (j < 4 && kt < NKT) {
+                        o0 = BL::KT + k16_block(kt, 2 * sx, 64);
+                        o1 = BL::KT + k16_block(kt, 2 * sx + 1, 64);
+                    }
                 }
-            }
-            // O = Qbar S + Aqk U.
+            };
+            auto load_step = [&](int st_, Q (&buf)[MAXP][2], float4 (&gb)[2]) __attribute__((always_inline)) {
+                if (st_ >= NSU + NSO) {
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                f32x4 acc = zero4();
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int kt = 2 * (st_ - NSU - NSO) + hh;
+                        if (kt < NKT) gb[hh] = *reinterpret_cast<const float4 *>(gl + 16 * kt + 4 * kg);
+                    }
+                }
 #pragma unroll
-                for (int s = 0; s < NKS; ++s)
-                    acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::QB + k16_block(rt, 2 * s, KP) + 4 * l),
-                                   ld_q4<PK>(Bk + BL::QB + k16_block(rt, 2 * s + 1, KP) + 4 * l),
-                                   sf[2 * s], sf[2 * s + 1]);
+                for (int j = 0; j < MAXP; ++j) {
+                    int o0, o1;
+                    pair_off(st_, j, o0, o1);
+                    if (o0 >= 0) {
+                        buf[j][0] = ld_q4<PK>(Bk + o0 + 4 * l);
+                        buf[j][1] = ld_q4<PK>(Bk + o1 + 4 * l);
+                    }
+                }
+            };
+            auto run_step = [&](int st_, const Q (&buf)[MAXP][2], const float4 (&gb)[2]) __attribute__((always_inline)) {
+                if (st_ < NSU + NSO) {
+                    const int rt = st_ % 4;
+                    const bool isu = st_ < NSU;
+                    f32x4 acc = zero4();
 #pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    if (2 * s <= rt)
-                        acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::AQ + k16_block(rt, 2 * s, 64) + 4 * l),
-                                       ld_q4<PK>(Bk + BL::AQ + k16_block(rt, 2 * s + 1, 64) + 4 * l),
-                                       uf[2 * s], uf[2 * s + 1]);
-                if (col_ok) {
+                    for (int j = 0; j < MAXP; ++j) {
+                        int o0, o1;
+                        pair_off(st_, j, o0, o1);
+                        if (o0 < 0) continue;
+                        if (j < NKS) {
+                            acc = mma2<PK>(acc, buf[j][0], buf[j][1], sf[2 * j], sf[2 * j + 1]);
+                        } else {
+                            const int sx = j - NKS;
+                            acc = isu ? mma2<PK>(acc, buf[j][0], buf[j][1], zf[2 * sx], zf[2 * sx + 1])
+                                      : mma2<PK>(acc, buf[j][0], buf[j][1], uf[2 * sx], uf[2 * sx + 1]);
+                        }
+                    }
+                    if (isu) {
+                        ua[rt] = acc;
+                        uf[rt] = pack4<PK>(acc);
+                    } else {
+                        oa[rt] = acc;
+                    }
+                } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int tok = 16 * rt + 4 * kg + i;
-                        if (tok < lc) io<TI>::st(op, ((t0 + tok) * H + h) * V + col, acc[i]);
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int kt = 2 * (st_ - NSU - NSO) + hh;
+                        if (kt >= NKT) continue;
+                        const float4 gv = gb[hh];
+                        S[kt][0] *= gv.x;
+                        S[kt][1] *= gv.y;
+                        S[kt][2] *= gv.z;
+                        S[kt][3] *= gv.w;
+                        S[kt] = mma2<PK>(S[kt], buf[2 * hh][0], buf[2 * hh][1], uf[0], uf[1]);
+                        S[kt] = mma2<PK>(S[kt], buf[2 * hh + 1][0], buf[2 * hh + 1][1], uf[2], uf[3]);
+                    }
+                }
+            };
+            {
+                Q bufA[MAXP][2], bufB[MAXP][2];
+                float4 gA[2], gB[2];
+                load_step(0, bufA, gA);
+#pragma unroll
+                for (int st_ = 0; st_ < NSTEP; st_ += 2) {
+                    if (st_ + 1 < NSTEP) load_step(st_ + 1, bufB, gB);
+                    __builtin_amdgcn_sched_barrier(0);
+                    run_step(st_, bufA, gA);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (st_ + 1 < NSTEP) {
+                        if (st_ + 2 < NSTEP) load_step(st_ + 2, bufA, gA);
+                        __builtin_amdgcn_sched_barrier(0);
+                        run_step(st_ + 1, bufB, gB);
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             }
-            // S <- Diag(exp(G_last)) S + Ktilde^T U.
-            const float *gl = reinterpret_cast<const float *>(Bk + BL::GL);
+            if (col_ok) {
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt) {
-                const float4 gv = *reinterpret_cast<const float4 *>(gl + 16 * kt + 4 * kg);
-                S[kt][0] *= gv.x;
-                S[kt][1] *= gv.y;
-                S[kt][2] *= gv.z;
-                S[kt][3] *= gv.w;
+                for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    S[kt] = mma2<PK>(S[kt], ld_q4<PK>(Bk + BL::KT + k16_block(kt, 2 * s, 64) + 4 * l),
-                                     ld_q4<PK>(Bk + BL::KT + k16_block(kt, 2 * s + 1, 64) + 4 * l),
-                                     uf[2 * s], uf[2 * s + 1]);
+                    for (int i = 0; i < 4; ++i) {
+                        const int tok = 16 * rt + 4 * kg + i;
+                        if (tok < lc) io<TI>::st(op, ((t0 + tok) * H + h) * V + col, oa[rt][i]);
+                    }
+            }
+            if constexpr (TRAIN) if (emit) {
+                st *usb = static_cast<st *>(p.us) + (static_cast<int64_t>(gc0 + jc) * H + h) * (64 * VP);
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) emit_tile(usb, k16_block(rt, vt, VP) + 4 * l, ua[rt]);
             }
             }
             __syncthreads();
@@ -763,8 +861,12 @@ hipError_t launch_scan(const ChunkParams &p, int BVsel, hipStream_t stream)
     auto go = [&](auto bvtag) {
         constexpr int BV = decltype(bvtag)::value;
         const int NVB = (p.V + BV - 1) / BV;
-        hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI>), dim3(groups * 8 * NVB), dim3(512), 0,
-                           stream, p, NVB, NP);
+        if (p.hs)
+            hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI, true>), dim3(groups * 8 * NVB),
+                               dim3(512), 0, stream, p, NVB, NP);
+        else
+            hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI, false>), dim3(groups * 8 * NVB),
+                               dim3(512), 0, stream, p, NVB, NP);
     };
     if (BVsel == 16) go(std::integral_constant<int, 16>{});
     else if (BVsel == 32) go(std::integral_constant<int, 32>{});
