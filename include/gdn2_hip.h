@@ -123,6 +123,36 @@ int gdn2_recurrent_fwd_ex(const void *q, const void *k, const void *v, const voi
                           void *stream);
 
 /*
+ * Short convolution of the mixer's prologue.  Replaces ShortConvolution.forward
+ * (reference src/qwendopamine/models/gdn2/gdn2.py:395-430) for up to three
+ * tensors (q, k, v) in one launch: for tensor i,
+ *   y_i[b, t, d] = act(bias_i[d] + sum_j weight_i[d, j] * x_i[b, t - W + 1 + j, d])
+ * with act = SiLU when `silu` is set; x_i, y_i [B, T, D_i] and weight_i
+ * [D_i, W] (the Conv1d weight [D, 1, W]), bias_i [D_i] or NULL, all io_dtype.
+ * Tokens before 0 are zero, or, on a single-token call (T == 1), the cache
+ * cache_in_i [B, D_i, W-1] (may be NULL).  cache_out_i (may be NULL) receives
+ * the last min(T, W-1) inputs as [B, D_i, min(T, W-1)] (W-1 columns when
+ * T == 1), as the reference's new conv state.  Like the reference, the
+ * convolution runs over the packed token axis (no cu_seqlens).
+ * 1 <= ntensors <= 3, 1 <= W <= 8.
+ */
+int gdn2_short_conv_fwd(int ntensors, const void *const *x, const void *const *weight,
+                        const void *const *bias, const void *const *cache_in,
+                        void *const *cache_out, void *const *y, const int *dims, int io_dtype,
+                        int B, int T, int W, int silu, void *stream);
+
+/*
+ * Gated RMS norm of the mixer's epilogue.  Replaces RMSNormGated.forward
+ * (reference gdn2.py:433-452): for each of `rows` rows of N values,
+ *   out = x * rsqrt(mean(x^2) + eps) * weight * silu(z)
+ * with the reference's rounding to io_dtype after every op.  weight [N] is
+ * io_dtype, or float32 (weight_dtype = GDN2_DTYPE_F32), in which case torch's
+ * promotion makes the last two products and `out` float32.
+ */
+int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int weight_dtype,
+                           void *out, int io_dtype, int64_t rows, int N, float eps, void *stream);
+
+/*
  * Bytes of device workspace gdn2_chunk_fwd needs for this shape.
  */
 size_t gdn2_chunk_fwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,

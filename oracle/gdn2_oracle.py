@@ -39,6 +39,13 @@ and chunks).  Functions and the reference code they restate:
                            recompute, dAv, dhu, wy_dqkg, intra, reverse cumsum
                            of dg), restated with relative decays.  It is the
                            algebra the HIP backward kernels implement.
+* ``short_conv``        -- ``ShortConvolution.forward`` (``gdn2.py:395-430``):
+                           causal depthwise conv1d + bias + SiLU with the conv
+                           cache of single-token calls and the new cache.
+* ``gated_rmsnorm``     -- ``RMSNormGated.forward`` (``gdn2.py:433-452``) in
+                           float64 (the reference rounds each op to the input
+                           dtype; the float64 value is what that rounding
+                           approximates).
 * ``make_inputs``       -- the seeded input recipe of BASELINE configs 0-4.
 
 How each function is pinned (tests/test_oracle.py):
@@ -56,6 +63,10 @@ How each function is pinned (tests/test_oracle.py):
                  the transposed layout is the swapped axes of the plain one.
   recurrent_vjp  central finite differences of recurrent_fwd in float64.
   chunk_vjp      equals recurrent_vjp for several chunk sizes incl. ragged tails.
+  short_conv     per channel equals numpy's full convolution (np.convolve, with
+                 the kernel flipped) truncated to T; a cached single-token call
+                 equals the last row of the prefill over cache + token.
+  gated_rmsnorm  equals torch.nn.functional.rms_norm (float64) times silu(z).
   make_inputs    distribution moments and l2-norms (cheap sanity only; it is a
                  recipe, not arithmetic of the reference).
 """
@@ -73,6 +84,8 @@ __all__ = [
     "chunk_vjp",
     "make_inputs",
     "rel_l2",
+    "short_conv",
+    "gated_rmsnorm",
 ]
 
 L2_EPS = 1e-6
@@ -323,6 +336,53 @@ def recurrent_fwd_pooled(
         final[row] = S
         written.add(row)
     return o, final, sorted(written)
+
+
+def short_conv(x, weight, bias=None, cache=None, output_final_state=False, activation="silu"):
+    r"""Causal depthwise conv1d of ``x [B, T, D]`` in float64 (gdn2.py:395-430).
+
+    ``weight`` is ``[D, W]`` (or the Conv1d ``[D, 1, W]``), ``bias`` ``[D]``.  Output
+    ``y[b, t, d] = bias[d] + sum_j weight[d, j] * xp[b, t + j, d]`` with ``xp`` the
+    inputs preceded by ``W-1`` tokens of history: the cache ``[B, D, W-1]`` on a
+    single-token call with a cache (gdn2.py:409-412), zeros otherwise
+    (padding=W-1, truncated to T, gdn2.py:414-424).  SiLU follows when
+    ``activation == "silu"``.  The new cache (with ``output_final_state``) is the
+    last ``W-1`` entries of the history + inputs on a single-token call, else
+    the last ``min(T, W-1)`` inputs, as ``[B, D, n]``.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    B, T, D = x.shape
+    w = np.asarray(weight, dtype=np.float64).reshape(D, -1)
+    W = w.shape[1]
+    if cache is not None and T == 1:
+        hist = np.transpose(np.asarray(cache, dtype=np.float64), (0, 2, 1))
+    else:
+        hist = np.zeros((B, W - 1, D))
+    xp = np.concatenate([hist, x], axis=1)
+    y = np.zeros((B, T, D))
+    for j in range(W):
+        y += w[:, j] * xp[:, j:j + T, :]
+    if bias is not None:
+        y += np.asarray(bias, dtype=np.float64)
+    if activation == "silu":
+        y = y / (1.0 + np.exp(-y))
+    new = None
+    if output_final_state:
+        if T == 1:
+            new = np.transpose(xp[:, -(W - 1):, :], (0, 2, 1)) if W > 1 else np.zeros((B, D, 0))
+        else:
+            keep = min(T, W - 1)
+            new = np.transpose(x[:, T - keep:, :], (0, 2, 1))
+    return y, new
+
+
+def gated_rmsnorm(x, z, weight, eps=1e-5):
+    r"""``x * rsqrt(mean(x^2) + eps) * weight * silu(z)`` over the last axis, float64
+    (gdn2.py:433-452)."""
+    x = np.asarray(x, dtype=np.float64)
+    z = np.asarray(z, dtype=np.float64)
+    inv = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
+    return x * inv * np.asarray(weight, dtype=np.float64) * (z / (1.0 + np.exp(-z)))
 
 
 def _l2norm_vjp(x_raw, dy, eps=L2_EPS):

@@ -171,6 +171,55 @@ int gdn2_recurrent_fwd(const void *q, const void *k, const void *v, const void *
                                  GDN2_DTYPE_I64, B, T, H, HV, K, V, scale, flags, stream);
 }
 
+int gdn2_short_conv_fwd(int ntensors, const void *const *x, const void *const *weight,
+                        const void *const *bias, const void *const *cache_in,
+                        void *const *cache_out, void *const *y, const int *dims, int io_dtype,
+                        int B, int T, int W, int silu, void *stream)
+{
+    if (!valid_dtype(io_dtype)) return GDN2_ERR_INVALID;
+    if (ntensors < 1 || ntensors > 3 || !x || !weight || !y || !dims) return GDN2_ERR_INVALID;
+    if (B < 0 || T < 0 || W < 1) return GDN2_ERR_INVALID;
+    if (W > 8) return GDN2_ERR_UNSUPPORTED;
+    ConvParams p;
+    p.B = B; p.T = T; p.W = W;
+    p.ncache = T == 1 ? W - 1 : (T < W - 1 ? T : W - 1);
+    p.silu = silu != 0;
+    int maxD = 0;
+    for (int i = 0; i < 3; ++i) {
+        const int j = i < ntensors ? i : 0;
+        ConvTensor &c = p.t[i];
+        c.D = dims[j];
+        if (c.D <= 0) return GDN2_ERR_INVALID;
+        if (B * static_cast<int64_t>(T) > 0 && (!x[j] || !weight[j] || !y[j])) return GDN2_ERR_INVALID;
+        c.x = x[j]; c.w = weight[j]; c.y = y[j];
+        c.bias = bias ? bias[j] : nullptr;
+        c.cache_in = cache_in ? cache_in[j] : nullptr;
+        c.cache_out = cache_out ? cache_out[j] : nullptr;
+        if (i < ntensors && c.D > maxD) maxD = c.D;
+    }
+    if (B == 0 || T == 0) return GDN2_OK;
+    const hipError_t err = launch_short_conv(p, io_dtype, maxD, ntensors, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int weight_dtype,
+                           void *out, int io_dtype, int64_t rows, int N, float eps, void *stream)
+{
+    if (!valid_dtype(io_dtype) || !valid_dtype(weight_dtype)) return GDN2_ERR_INVALID;
+    if (weight_dtype != io_dtype && weight_dtype != GDN2_DTYPE_F32) return GDN2_ERR_INVALID;
+    if (rows < 0 || N <= 0) return GDN2_ERR_INVALID;
+    if (N > 512) return GDN2_ERR_UNSUPPORTED;
+    if (rows == 0) return GDN2_OK;
+    if (!x || !z || !weight || !out) return GDN2_ERR_INVALID;
+    if ((rows + 3) / 4 > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
+    NormParams p;
+    p.x = x; p.z = z; p.weight = weight; p.out = out;
+    p.rows = rows; p.N = N; p.eps = eps;
+    p.w_f32 = weight_dtype == GDN2_DTYPE_F32 && io_dtype != GDN2_DTYPE_F32;
+    const hipError_t err = launch_gated_rmsnorm(p, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
 size_t gdn2_chunk_fwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,
                                      const int64_t *cu_seqlens_host, int num_seqs)
 {

@@ -80,4 +80,36 @@ size_t chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
                                  const int64_t *cu_host, int num_seqs);
 int launch_chunk_bwd(const ChunkBwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream);
 
+// Short convolution (prologue): up to three tensors per launch.
+struct ConvTensor {
+    const void *x;          // [B, T, D]
+    const void *w;          // [D, W]
+    const void *bias;       // [D] or NULL
+    const void *cache_in;   // [B, D, W-1] or NULL (read on single-token calls)
+    void *cache_out;        // [B, D, ncache] or NULL
+    void *y;                // [B, T, D]
+    int D;
+};
+
+struct ConvParams {
+    ConvTensor t[3];
+    int B, T, W, ncache;
+    int silu;
+};
+
+hipError_t launch_short_conv(const ConvParams &p, int io_dtype, int maxD, int ntensors,
+                             hipStream_t stream);
+
+// Gated RMS norm (epilogue).
+struct NormParams {
+    const void *x, *z, *weight;
+    void *out;
+    int64_t rows;
+    int N;
+    int w_f32;  // weight (and output) in float32 while x, z are 16-bit
+    float eps;
+};
+
+hipError_t launch_gated_rmsnorm(const NormParams &p, int io_dtype, hipStream_t stream);
+
 }  // namespace gdn2

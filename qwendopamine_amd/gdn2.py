@@ -84,6 +84,18 @@ def resolve_gdn2_backend(requested: str, *, training: bool, seq_len: int) -> str
     return "hip" if requested == "auto" else requested
 
 
+def _inference(*tensors: torch.Tensor | None) -> bool:
+    """True for GPU tensors through which no gradient flows.  The prologue and
+    epilogue then run on their HIP kernels, which are forward only.  Otherwise
+    they use torch's differentiable ops, as the reference does.  This covers
+    training, and standalone CPU use of these two nn.Modules.  The mixer's
+    recurrence itself has no CPU path."""
+    live = [t for t in tensors if t is not None]
+    if not all(t.is_cuda for t in live):
+        return False
+    return not (torch.is_grad_enabled() and any(t.requires_grad for t in live))
+
+
 class ShortConvolution(nn.Module):
     """Causal depthwise conv1d + optional SiLU with a rolling cache (reference ``gdn2.py:372-430``).
 
@@ -104,6 +116,12 @@ class ShortConvolution(nn.Module):
 
     def forward(self, x: torch.Tensor, cache: torch.Tensor | None = None,
                 output_final_state: bool = False, cu_seqlens: torch.Tensor | None = None):
+        if _inference(x, self.conv1d.weight):
+            ys, new = ops.short_convolution([x], [self.conv1d.weight], [self.conv1d.bias],
+                                            None if cache is None else [cache], output_final_state,
+                                            self.activation)
+            return ys[0], None if new is None else new[0]
+        # Differentiable path (training): torch's depthwise conv.
         bsz, seq, dim = x.shape
         xt = x.transpose(1, 2)
         wgt, bias = self.conv1d.weight, self.conv1d.bias
@@ -136,6 +154,9 @@ class RMSNormGated(nn.Module):
         self.weight = nn.Parameter(torch.ones(hidden_size))
 
     def forward(self, x: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
+        if _inference(x, z, self.weight):
+            return ops.gated_rmsnorm(x, z, self.weight, self.eps)
+        # Differentiable path (training): torch ops, same rounding.
         inv = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
         return x * inv * self.weight * F.silu(z)
 
@@ -409,7 +430,15 @@ class GatedDeltaNet2(nn.Module):
             hidden_states = _index_first_axis(hidden_states, indices).unsqueeze(0)
 
         x = hidden_states
-        if self.use_short_conv:
+        convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d) if self.use_short_conv else ()
+        if self.use_short_conv and _inference(x, *(c.conv1d.weight for c in convs)):
+            # q, k and v convolutions in one launch.
+            raw = [self.q_proj(x), self.k_proj(x), self.v_proj(x)]
+            (q, k, v), new = ops.short_convolution(
+                raw, [c.conv1d.weight for c in convs], [c.conv1d.bias for c in convs],
+                None if cq is None else [cq, ck, cv], want_state, self.q_conv1d.activation)
+            cq, ck, cv = new if new is not None else (None, None, None)
+        elif self.use_short_conv:
             q, cq = self.q_conv1d(self.q_proj(x), cache=cq, output_final_state=want_state, cu_seqlens=cu_seqlens)
             k, ck = self.k_conv1d(self.k_proj(x), cache=ck, output_final_state=want_state, cu_seqlens=cu_seqlens)
             v, cv = self.v_conv1d(self.v_proj(x), cache=cv, output_final_state=want_state, cu_seqlens=cu_seqlens)

@@ -20,6 +20,8 @@ from __future__ import annotations
 
 from typing import Any
 
+import ctypes
+
 import torch
 
 from . import _native as nat
@@ -31,6 +33,8 @@ __all__ = [
     "chunk_gdn2_fwd",
     "ChunkGDN2Function",
     "gate_activation",
+    "short_convolution",
+    "gated_rmsnorm",
 ]
 
 
@@ -510,3 +514,106 @@ def chunk_gdn2(
         q, k, v, g, b, w, A_log, dt_bias, scale, initial_state, output_final_state,
         use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound,
     )
+
+
+def _ptr_array(ptrs) -> int:
+    """Address of a C array of three ``void *`` (unused slots NULL)."""
+    arr = (ctypes.c_void_p * 3)(*(list(ptrs) + [None] * (3 - len(ptrs))))
+    _ptr_array.keep.append(arr)  # alive until the call returns
+    return ctypes.addressof(arr)
+
+
+_ptr_array.keep = []
+
+
+def short_convolution(
+    xs: list[torch.Tensor],
+    weights: list[torch.Tensor],
+    biases: list[torch.Tensor | None] | None = None,
+    caches: list[torch.Tensor | None] | None = None,
+    output_final_state: bool = False,
+    activation: str | None = "silu",
+) -> tuple[list[torch.Tensor], list[torch.Tensor] | None]:
+    """Causal depthwise conv1d (+ SiLU) of up to three ``[B, T, D]`` tensors in one launch.
+
+    Each tensor follows reference ``ShortConvolution.forward`` (``gdn2.py:395-430``):
+    * ``weights[i]`` is the Conv1d weight ``[D, 1, W]``;
+    * a single-token call convolves the cache ``[B, D, W-1]`` followed by the new token;
+    * with ``output_final_state`` the new cache holds the last ``min(T, W-1)`` inputs (``W-1`` when ``T == 1``).
+
+    Returns ``(ys, new_caches)``. Inference only: there is no backward.
+    """
+    name = "short_convolution"
+    n = len(xs)
+    if not 1 <= n <= 3 or len(weights) != n:
+        raise ValueError(f"{name}: 1 to 3 tensors with one weight each")
+    _require_gpu(name, *xs)
+    B, T = xs[0].shape[:2]
+    dt = xs[0].dtype
+    W = int(weights[0].shape[-1])
+    if activation not in (None, "silu"):
+        raise NotImplementedError(f"{name}: activation {activation!r}")
+    xs = [x.to(dt).contiguous() for x in xs]
+    for x in xs:
+        if x.dim() != 3 or tuple(x.shape[:2]) != (B, T):
+            raise ValueError(f"{name}: inputs must share [B, T, D]; got {tuple(x.shape)}")
+    dims = [x.shape[2] for x in xs]
+    ws = [w.detach().reshape(d, W).to(dt).contiguous() for w, d in zip(weights, dims)]
+    bs = None
+    if biases is not None and any(b_ is not None for b_ in biases):
+        bs = [None if b_ is None else b_.detach().to(dt).contiguous() for b_ in biases]
+    cs = None
+    if T == 1 and caches is not None and any(c is not None for c in caches):
+        cs = [None if c is None else c.to(dt).contiguous() for c in caches]
+        for c, d in zip(cs, dims):
+            if c is not None and tuple(c.shape) != (B, d, W - 1):
+                raise ValueError(f"{name}: cache must be {(B, d, W - 1)}; got {tuple(c.shape)}")
+    keep = W - 1 if T == 1 else min(T, W - 1)
+    new = [torch.empty(B, d, keep, dtype=dt, device=x.device) for x, d in zip(xs, dims)] \
+        if output_final_state else None
+    ys = [torch.empty_like(x) for x in xs]
+    dims_arr = (ctypes.c_int * 3)(*(dims + [dims[0]] * (3 - n)))
+    lib = nat.load()
+    st = lib.gdn2_short_conv_fwd(
+        n, _ptr_array([nat.ptr(x) for x in xs]), _ptr_array([nat.ptr(w) for w in ws]),
+        None if bs is None else _ptr_array([nat.ptr(b_) for b_ in bs]),
+        None if cs is None else _ptr_array([nat.ptr(c) for c in cs]),
+        None if new is None else _ptr_array([nat.ptr(c) for c in new]),
+        _ptr_array([nat.ptr(y) for y in ys]), ctypes.addressof(dims_arr),
+        nat.dtype_code(dt), B, T, W, int(activation == "silu"), nat.stream_handle(xs[0].device),
+    )
+    _ptr_array.keep.clear()
+    nat.check(st, name)
+    return ys, new
+
+
+def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """``x * rsqrt(mean(x^2) + eps) * weight * silu(z)`` over the last axis.
+
+    This is reference ``RMSNormGated.forward`` (``gdn2.py:433-452``), rounded to the input dtype after every op as the reference is.
+
+    Output dtype:
+    * the input dtype;
+    * float32 when ``weight`` is float32 and ``x`` is not (torch's promotion).
+
+    Inference only: there is no backward.
+    """
+    name = "gated_rmsnorm"
+    _require_gpu(name, x, z, weight)
+    if z.shape != x.shape or weight.numel() != x.shape[-1]:
+        raise ValueError(f"{name}: x, z must match and weight must have {x.shape[-1]} elements")
+    dt = x.dtype
+    N = x.shape[-1]
+    xc = x.contiguous()
+    zc = z.to(dt).contiguous()
+    wd = weight.detach()
+    wdt = torch.float32 if (wd.dtype == torch.float32 and dt != torch.float32) else dt
+    wc = wd.to(wdt).contiguous()
+    out = torch.empty(x.shape, dtype=wdt, device=x.device)
+    lib = nat.load()
+    st = lib.gdn2_gated_rmsnorm_fwd(
+        nat.ptr(xc), nat.ptr(zc), nat.ptr(wc), nat.dtype_code(wdt), nat.ptr(out), nat.dtype_code(dt),
+        xc.numel() // N, N, float(eps), nat.stream_handle(x.device),
+    )
+    nat.check(st, name)
+    return out

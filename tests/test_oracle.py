@@ -244,6 +244,49 @@ def test_pooled_token_rows_and_transposed_layout():
     np.testing.assert_allclose(pool_t, np.swapaxes(pool_p, -1, -2), atol=1e-14)
 
 
+def test_short_conv_equals_numpy_convolution():
+    """Per channel: the causal depthwise conv is numpy's full convolution with the kernel
+    flipped (conv1d is a correlation), truncated to the first T outputs."""
+    rng = np.random.default_rng(31)
+    B, T, D, W = 2, 11, 5, 4
+    x, w, bias = rng.standard_normal((B, T, D)), rng.standard_normal((D, W)), rng.standard_normal(D)
+    y, new = orc.short_conv(x, w, bias, activation=None, output_final_state=True)
+    for b in range(B):
+        for d in range(D):
+            ref = np.convolve(x[b, :, d], w[d, ::-1])[:T] + bias[d]
+            np.testing.assert_allclose(y[b, :, d], ref, atol=1e-12)
+    np.testing.assert_array_equal(new, np.transpose(x[:, -(W - 1):, :], (0, 2, 1)))
+    ys, _ = orc.short_conv(x, w, bias)
+    np.testing.assert_allclose(ys, y / (1 + np.exp(-y)), atol=1e-14)
+    # Shorter than the kernel: the new cache keeps every input.
+    _, new2 = orc.short_conv(x[:, :2], w, output_final_state=True)
+    np.testing.assert_array_equal(new2, np.transpose(x[:, :2], (0, 2, 1)))
+
+
+def test_short_conv_decode_step_continues_prefill():
+    """A single-token call with the cache of the previous W-1 tokens equals the last row of
+    the convolution over those tokens followed by the new one."""
+    rng = np.random.default_rng(32)
+    B, D, W = 3, 6, 4
+    prev, tok = rng.standard_normal((B, W - 1, D)), rng.standard_normal((B, 1, D))
+    w, bias = rng.standard_normal((D, W)), rng.standard_normal(D)
+    _, cache = orc.short_conv(prev, w, bias, output_final_state=True)
+    y1, new = orc.short_conv(tok, w, bias, cache=cache, output_final_state=True)
+    yfull, _ = orc.short_conv(np.concatenate([prev, tok], 1), w, bias)
+    np.testing.assert_allclose(y1[:, 0], yfull[:, -1], atol=1e-13)
+    np.testing.assert_array_equal(new, np.transpose(np.concatenate([prev, tok], 1)[:, 1:], (0, 2, 1)))
+
+
+def test_gated_rmsnorm_equals_torch_rms_norm():
+    import torch
+
+    rng = np.random.default_rng(33)
+    x, z, w = rng.standard_normal((7, 64)) * 3, rng.standard_normal((7, 64)), rng.standard_normal(64)
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(x), (64,), torch.from_numpy(w), eps=1e-5)
+    ref = ref * torch.nn.functional.silu(torch.from_numpy(z))
+    np.testing.assert_allclose(orc.gated_rmsnorm(x, z, w, 1e-5), ref.numpy(), rtol=1e-12, atol=1e-12)
+
+
 def test_vjp_matches_finite_differences():
     q, k, v, g, b, w, s0 = _rand(1, 11, 2, 6, 5, seed=9, decay="paper")
     rng = np.random.default_rng(10)
