@@ -32,6 +32,8 @@ BF16_PEAK_TFLOPS = 2500.0
 PREFILL = dict(B=8, T=4096, H=16, K=128, V=128, C=64)
 DECODE = dict(N=64, H=16, K=128, V=128, steps=1024)
 TRAIN = dict(B=4, T=8192, H=16, K=128, V=128, C=64)
+# Mixer prologue / epilogue at config 3's module shape (hidden 1024, 16 heads x 64).
+PROLOGUE = dict(B=4, T=2048, H=16, Dh=64, W=4)
 
 
 def prefill_flops(B, T, H, K, V, C):
@@ -298,6 +300,87 @@ def bench_decode(torch, nat, dev, reps=3, eager_steps=0, variant="plain"):
                         "state": variant})
 
 
+def bench_prologue(torch, dev, reps=20):
+    """The mixer's prologue and epilogue kernels at config 3's module shape.
+
+    * Prologue: the q/k/v short convolution + SiLU in one launch.
+    * Epilogue: the gated RMS norm.
+
+    Both are set against the torch ops of the reference module that they replace
+    (gdn2.py:395-452). Each is timed as a HIP-graph replay of `reps` calls. The HBM
+    bytes are algorithmic: each input read once, each output written once.
+    """
+    import torch.nn.functional as F
+
+    from qwendopamine_amd import ops
+
+    B, T, H, Dh, W = (PROLOGUE[x] for x in ("B", "T", "H", "Dh", "W"))
+    D = H * Dh
+    bf = torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(5)
+    xs = [torch.randn(B, T, D, generator=gen, device=dev).to(bf) for _ in range(3)]
+    ws = [(torch.randn(D, 1, W, generator=gen, device=dev) * 0.5).to(bf) for _ in range(3)]
+    o = torch.randn(B, T, H, Dh, generator=gen, device=dev).to(bf)
+    z = torch.randn(B, T, H, Dh, generator=gen, device=dev).to(bf)
+    nw = torch.randn(Dh, generator=gen, device=dev).to(bf)
+
+    def conv_hip():
+        ops.short_convolution(xs, ws, None, None, output_final_state=True)
+
+    def conv_torch():
+        for x, w in zip(xs, ws):
+            xt = x.transpose(1, 2)
+            F.silu(F.conv1d(xt, w, None, padding=W - 1, groups=D)[..., :T]).transpose(1, 2)
+            xt[:, :, -(W - 1):]
+
+    def norm_hip():
+        ops.gated_rmsnorm(o, z, nw, 1e-5)
+
+    def norm_torch():
+        (o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + 1e-5) * nw) * F.silu(z)
+
+    def timed(fn):
+        # `reps` calls captured in one HIP graph: the replay times the kernels,
+        # not the Python launch path of each call.
+        with torch.no_grad():
+            side = torch.cuda.Stream(dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    fn()
+            torch.cuda.current_stream(dev).wait_stream(side)
+            torch.cuda.synchronize(dev)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(reps):
+                    fn()
+            graph.replay()
+            torch.cuda.synchronize(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    conv_bytes = 6 * B * T * D * 2
+    norm_bytes = 3 * B * T * H * Dh * 2
+    t = {k: timed(f) for k, f in (("conv", conv_hip), ("conv_torch", conv_torch),
+                                  ("norm", norm_hip), ("norm_torch", norm_torch))}
+    return {
+        "config": {"workload": "C3 module shape: B4 T2048, q/k/v 1024 channels, conv width 4; "
+                               "norm over 16 heads x 64", "dtype": "bf16"},
+        "short_conv_qkv": {"us": round(t["conv"], 2), "torch_us": round(t["conv_torch"], 2),
+                           "algorithmic_bytes": conv_bytes,
+                           "achieved_GBps": round(conv_bytes / (t["conv"] * 1e-6) / 1e9, 1),
+                           "frac_hbm_peak": round(conv_bytes / (t["conv"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+        "gated_rmsnorm": {"us": round(t["norm"], 2), "torch_us": round(t["norm_torch"], 2),
+                          "algorithmic_bytes": norm_bytes,
+                          "achieved_GBps": round(norm_bytes / (t["norm"] * 1e-6) / 1e9, 1),
+                          "frac_hbm_peak": round(norm_bytes / (t["norm"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+    }
+
+
 def traffic_probe(torch, nat, dev):
     """Short run for the rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE): first a
     256 MiB device-to-device copy whose bytes are known, which calibrates the
@@ -367,6 +450,7 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true")
+    ap.add_argument("--no-prologue", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="short run for rocprofv3 counter passes; prints no JSON line")
     args = ap.parse_args()
@@ -437,6 +521,8 @@ def main() -> int:
                                                         "frac_hbm_peak")}
     if not args.no_train:
         out["train"] = bench_train(torch, nat, dev, max(2, args.steps // 2), 1)
+    if not args.no_prologue:
+        out["prologue_epilogue"] = bench_prologue(torch, dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, res["inputs"])
     print(json.dumps(out), flush=True)

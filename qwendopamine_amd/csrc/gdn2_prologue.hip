@@ -13,6 +13,8 @@
 // the SiLU; x^2, the mean, mean + eps, the rsqrt, and each product of the
 // norm), while each op itself runs in fp32 as torch's kernels do.
 
+#include <type_traits>
+
 #include "gdn2_common.h"
 #include "gdn2_internal.h"
 
@@ -38,7 +40,10 @@ __device__ __forceinline__ float round_to<f16_t>(float x)
     return static_cast<float>(static_cast<_Float16>(x));
 }
 
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+// x * sigmoid(x) with the hardware reciprocal (1 ulp in fp32) instead of an
+// IEEE divide: the divide dominated these passes' VALU time, and the result is
+// rounded to bf16 / fp16 right after for 16-bit inputs.
+__device__ __forceinline__ float silu_f32(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // One thread per (tensor, batch row, channel d, tile of TT tokens).  The
 // thread keeps the last W inputs of its channel in registers, so each input
@@ -138,9 +143,211 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(NormParams p)
     }
 }
 
-template <typename T, int W>
-hipError_t conv_w(const ConvParams &p, int maxD, int ntensors, hipStream_t s)
+// 16 bytes of T as floats and back (vector memory accesses of 8 bf16/fp16 or
+// 4 fp32 values).
+template <typename T>
+struct Vec16 {
+    static constexpr int N = 16 / static_cast<int>(sizeof(T));
+    static __device__ __forceinline__ void load(const T *p, float (&v)[N])
+    {
+        const uint4 u = *reinterpret_cast<const uint4 *>(p);
+        const unsigned w[4] = {u.x, u.y, u.z, u.w};
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(w[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint16_t b = static_cast<uint16_t>((i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu));
+                if constexpr (std::is_same<T, bf16_t>::value)
+                    v[i] = bf16_bits_to_f32(b);
+                else
+                    v[i] = static_cast<float>(__builtin_bit_cast(_Float16, b));
+            }
+        }
+    }
+    static __device__ __forceinline__ void store(T *p, const float (&v)[N])
+    {
+        unsigned w[4];
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(v[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint16_t lo, hi;
+                if constexpr (std::is_same<T, bf16_t>::value) {
+                    lo = f32_to_bf16_bits(v[2 * i]);
+                    hi = f32_to_bf16_bits(v[2 * i + 1]);
+                } else {
+                    lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * i]));
+                    hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * i + 1]));
+                }
+                w[i] = static_cast<unsigned>(lo) | (static_cast<unsigned>(hi) << 16);
+            }
+        }
+        *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+};
+
+// Vectorised short convolution: one thread per (16-byte group of CPT
+// channels, tile of TT tokens), one wave per workgroup.  All of a tile's
+// input rows are requested before any is used, so a wave keeps TT + W - 1
+// 16-byte loads in flight; each access is a contiguous 1 KB row segment.
+template <typename T, int W, int TT>
+__global__ __launch_bounds__(64) void short_conv_vec_kernel(ConvParams p)
 {
+    using VT = Vec16<T>;
+    constexpr int CPT = VT::N;
+    const ConvTensor ct = p.t[blockIdx.z];
+    const int D = ct.D, G = D / CPT;
+    const int g = blockIdx.x * 64 + static_cast<int>(threadIdx.x);
+    if (g >= G) return;  // no barriers below
+    const int tiles = (p.T + TT - 1) / TT;
+    const int b = blockIdx.y / tiles, tile = blockIdx.y % tiles;
+    const int t0 = tile * TT;
+    const int d0 = g * CPT;
+    const T *x = static_cast<const T *>(ct.x);
+    T *y = static_cast<T *>(ct.y);
+    const int64_t row0 = static_cast<int64_t>(b) * p.T;
+
+    // Rows t0-W+1 .. t0+TT-1 (clamped to valid rows; rows outside the
+    // sequence are replaced by history or zeros below).
+    float xin[W - 1 + TT][CPT];
+#pragma unroll
+    for (int r = 0; r < W - 1 + TT; ++r) {
+        const int tt = t0 - (W - 1) + r;
+        const int tc = tt < 0 ? 0 : (tt < p.T ? tt : p.T - 1);
+        VT::load(x + (row0 + tc) * D + d0, xin[r]);
+    }
+    // The group's weights [CPT][W] are W contiguous 16-byte pieces.
+    float wflat[W][CPT], wt[W][CPT], bias[CPT];
+#pragma unroll
+    for (int q = 0; q < W; ++q)
+        VT::load(static_cast<const T *>(ct.w) + static_cast<int64_t>(d0) * W + q * CPT, wflat[q]);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c)
+#pragma unroll
+        for (int j = 0; j < W; ++j) wt[j][c] = wflat[(c * W + j) / CPT][(c * W + j) % CPT];
+    if (ct.bias) {
+        VT::load(static_cast<const T *>(ct.bias) + d0, bias);
+    } else {
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) bias[c] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < W - 1; ++r) {
+        const int tt = t0 - (W - 1) + r;
+        if (tt < 0) {
+#pragma unroll
+            for (int c = 0; c < CPT; ++c)
+                xin[r][c] = (p.T == 1 && ct.cache_in)
+                                ? io<T>::ld(static_cast<const T *>(ct.cache_in),
+                                            (static_cast<int64_t>(b) * D + d0 + c) * (W - 1) + (W - 1 + tt))
+                                : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TT; ++i) {
+        const int t = t0 + i;
+        if (t >= p.T) break;
+        float out[CPT];
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < W; ++j) acc = fmaf(wt[j][c], xin[i + j][c], acc);
+            out[c] = round_to<T>(acc + bias[c]);
+            if (p.silu) out[c] = round_to<T>(silu_f32(out[c]));
+        }
+        VT::store(y + (row0 + t) * D + d0, out);
+    }
+    if (ct.cache_out && t0 + TT >= p.T) {
+        // The last W-1 inputs are rows (p.T - t0) .. (p.T - t0 + W - 2) of xin.
+        T *co = static_cast<T *>(ct.cache_out);
+        const int last = p.T - t0;  // index in xin of token p.T - (W - 1) ... shifted by W-1
+#pragma unroll
+        for (int r = 0; r < W - 1 + TT; ++r) {
+            const int k = r - last;  // position within the last W-1 inputs
+            const int c0 = k - (W - 1 - p.ncache);
+            if (k >= 0 && k < W - 1 && c0 >= 0) {
+#pragma unroll
+                for (int c = 0; c < CPT; ++c)
+                    io<T>::st(co, (static_cast<int64_t>(b) * D + d0 + c) * p.ncache + c0, xin[r][c]);
+            }
+        }
+    }
+}
+
+// Vectorised gated RMS norm: LPR lanes per row, 16 bytes (EPV values) per
+// lane, so a row of N = LPR * EPV values moves as LPR contiguous 16-byte
+// pieces and is reduced by xor-shuffles inside its lane group.  Each thread
+// takes RPT rows (RPB rows apart) and requests all of them before computing.
+template <typename T, int LPR, int RPT>
+__global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(NormParams p)
+{
+    using VT = Vec16<T>;
+    constexpr int EPV = VT::N, RPB = 256 / LPR;
+    const int N = LPR * EPV;
+    const int sub = threadIdx.x % LPR;
+    int64_t off[RPT];
+    bool live[RPT];
+    float xv[RPT][EPV], zv[RPT][EPV];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        int64_t row = (static_cast<int64_t>(blockIdx.x) * RPT + r) * RPB + threadIdx.x / LPR;
+        live[r] = row < p.rows;
+        if (!live[r]) row = p.rows - 1;  // stay in bounds; keep the shuffles uniform
+        off[r] = row * N + sub * EPV;
+        VT::load(static_cast<const T *>(p.x) + off[r], xv[r]);
+        VT::load(static_cast<const T *>(p.z) + off[r], zv[r]);
+    }
+    float wgt[EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+        const int c = sub * EPV + e;
+        wgt[e] = p.w_f32 ? static_cast<const float *>(p.weight)[c]
+                         : io<T>::ld(static_cast<const T *>(p.weight), c);
+    }
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) sq += round_to<T>(xv[r][e] * xv[r][e]);
+#pragma unroll
+        for (int o = 1; o < LPR; o <<= 1) sq += __shfl_xor(sq, o, 64);
+        const float var = round_to<T>(sq / static_cast<float>(N));
+        const float inv = round_to<T>(rsqrtf(round_to<T>(var + p.eps)));
+        float out[EPV];
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+            const float a = round_to<T>(xv[r][e] * inv);
+            const float gz = round_to<T>(silu_f32(zv[r][e]));
+            out[e] = p.w_f32 ? a * wgt[e] * gz : round_to<T>(round_to<T>(a * wgt[e]) * gz);
+        }
+        if (!live[r]) continue;
+        if (p.w_f32) {
+            float *o = static_cast<float *>(p.out) + off[r];
+#pragma unroll
+            for (int e = 0; e < EPV; e += 4)
+                *reinterpret_cast<float4 *>(o + e) = make_float4(out[e], out[e + 1], out[e + 2], out[e + 3]);
+        } else {
+            VT::store(static_cast<T *>(p.out) + off[r], out);
+        }
+    }
+}
+
+template <typename T, int W>
+hipError_t conv_w(const ConvParams &p, int maxD, int ntensors, bool vec, hipStream_t s)
+{
+    if (vec) {
+        constexpr int TT = 8, CPT = Vec16<T>::N;
+        const int tiles = (p.T + TT - 1) / TT;
+        const int groups = maxD / CPT;
+        hipLaunchKernelGGL((short_conv_vec_kernel<T, W, TT>), dim3((groups + 63) / 64, p.B * tiles, ntensors),
+                           dim3(64), 0, s, p);
+        return hipGetLastError();
+    }
     const int TT = 64;
     const int tiles = (p.T + TT - 1) / TT;
     hipLaunchKernelGGL((short_conv_kernel<T, W>), dim3((maxD + 255) / 256, p.B * tiles, ntensors),
@@ -151,21 +358,53 @@ hipError_t conv_w(const ConvParams &p, int maxD, int ntensors, hipStream_t s)
 template <typename T>
 hipError_t conv_t(const ConvParams &p, int maxD, int ntensors, hipStream_t s)
 {
-    switch (p.W) {
-    case 1: return conv_w<T, 1>(p, maxD, ntensors, s);
-    case 2: return conv_w<T, 2>(p, maxD, ntensors, s);
-    case 3: return conv_w<T, 3>(p, maxD, ntensors, s);
-    case 4: return conv_w<T, 4>(p, maxD, ntensors, s);
-    case 5: return conv_w<T, 5>(p, maxD, ntensors, s);
-    case 6: return conv_w<T, 6>(p, maxD, ntensors, s);
-    case 7: return conv_w<T, 7>(p, maxD, ntensors, s);
-    default: return conv_w<T, 8>(p, maxD, ntensors, s);
+    // 16-byte channel groups when every tensor's rows allow them.
+    constexpr int CPT = Vec16<T>::N;
+    bool vec = true;
+    for (int i = 0; i < ntensors; ++i) {
+        const ConvTensor &c = p.t[i];
+        vec = vec && c.D % CPT == 0 &&
+              ((reinterpret_cast<uintptr_t>(c.x) | reinterpret_cast<uintptr_t>(c.y) |
+                reinterpret_cast<uintptr_t>(c.w) | reinterpret_cast<uintptr_t>(c.bias)) & 15) == 0;
     }
+    switch (p.W) {
+    case 1: return conv_w<T, 1>(p, maxD, ntensors, vec, s);
+    case 2: return conv_w<T, 2>(p, maxD, ntensors, vec, s);
+    case 3: return conv_w<T, 3>(p, maxD, ntensors, vec, s);
+    case 4: return conv_w<T, 4>(p, maxD, ntensors, vec, s);
+    case 5: return conv_w<T, 5>(p, maxD, ntensors, vec, s);
+    case 6: return conv_w<T, 6>(p, maxD, ntensors, vec, s);
+    case 7: return conv_w<T, 7>(p, maxD, ntensors, vec, s);
+    default: return conv_w<T, 8>(p, maxD, ntensors, vec, s);
+    }
+}
+
+template <typename T, int LPR>
+hipError_t norm_vec(const NormParams &p, hipStream_t s)
+{
+    constexpr int RPT = 1, RPB = 256 / LPR;
+    hipLaunchKernelGGL((gated_rmsnorm_vec_kernel<T, LPR, RPT>),
+                       dim3(static_cast<unsigned>((p.rows + RPB * RPT - 1) / (RPB * RPT))), dim3(256), 0, s, p);
+    return hipGetLastError();
 }
 
 template <typename T>
 hipError_t norm_t(const NormParams &p, hipStream_t s)
 {
+    // Rows of N = LPR * (16 bytes of T), LPR a power of two <= 64, 16-byte aligned.
+    constexpr int EPV = Vec16<T>::N;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.z) |
+                           reinterpret_cast<uintptr_t>(p.out)) & 15) == 0;
+    if (aligned && p.N % EPV == 0) {
+        switch (p.N / EPV) {
+        case 4: return norm_vec<T, 4>(p, s);
+        case 8: return norm_vec<T, 8>(p, s);
+        case 16: return norm_vec<T, 16>(p, s);
+        case 32: return norm_vec<T, 32>(p, s);
+        case 64: return norm_vec<T, 64>(p, s);
+        default: break;
+        }
+    }
     const dim3 grid(static_cast<unsigned>((p.rows + 3) / 4));
     if (p.N <= 64) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 1>), grid, dim3(256), 0, s, p);
     else if (p.N <= 128) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 2>), grid, dim3(256), 0, s, p);
