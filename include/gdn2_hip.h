@@ -53,8 +53,8 @@ enum gdn2_status {
 #define GDN2_FLAG_LOWER_BOUND 4u    /* with GATE_IN_KERNEL: bounded sigmoid    */
 #define GDN2_FLAG_SAVE_FOR_BWD 8u   /* gdn2_chunk_fwd: keep what the backward   *
                                      * needs in a training-size workspace       */
-#define GDN2_FLAG_TRANSPOSE_STATE 16u     /* gdn2_recurrent_fwd_ex: states are  *
-                                           * [.., V, K] (K fastest)             */
+#define GDN2_FLAG_TRANSPOSE_STATE 16u     /* recurrent and chunk calls: states  *
+                                           * are [.., V, K] (K fastest)         */
 #define GDN2_FLAG_INPLACE_FINAL_STATE 32u /* gdn2_recurrent_fwd_ex with state  *
                                            * indices: per-token states go to    *
                                            * the indexed slots, not token rows  */
@@ -215,6 +215,20 @@ int gdn2_chunk_fwd_scan(const void *v, const void *w, int io_dtype, void *o,
  */
 size_t gdn2_chunk_train_workspace_size(int B, int T, int H, int K, int V, int io_dtype,
                                        const int64_t *cu_seqlens_host, int num_seqs);
+
+/*
+ * The per-chunk start states of a gdn2_chunk_fwd call made with
+ * GDN2_FLAG_SAVE_FOR_BWD, read from its training workspace `saved`: writes
+ * out [nc, H, K, V] (transpose = 0) or [nc, H, V, K] (transpose != 0) in
+ * io_dtype, nc = total chunks of 64 tokens (sequence-major, as the
+ * reference's chunk indices).  Replaces the `h` that chunk_gdn2 returns with
+ * return_intermediate_states (reference gdn2_ops/chunk_gdn2.py:1257-1263,
+ * 1415-1421; h from chunk_gated_delta_rule_fwd_h in the inputs' dtype,
+ * chunk_kda.py:2263).
+ */
+int gdn2_chunk_states(const void *saved, size_t saved_bytes, int io_dtype, void *out, int transpose,
+                      const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H, int K,
+                      int V, void *stream);
 
 /*
  * Bytes of device scratch gdn2_chunk_bwd needs for this shape.

@@ -31,13 +31,14 @@ def chunk_gdn2_bwd(saved: dict, do: torch.Tensor, dht: torch.Tensor | None, has_
     do = do.to(dt).contiguous()
     if do.data_ptr() % 16:
         do = do.clone()
+    sk = (V, K) if saved.get("transpose") else (K, V)
     dht = None if dht is None else dht.float().contiguous()
-    if dht is not None and tuple(dht.shape) != (N, H, K, V):
-        raise ValueError(f"chunk_gdn2 backward: dht must be {(N, H, K, V)}, got {tuple(dht.shape)}")
+    if dht is not None and tuple(dht.shape) != (N, H, *sk):
+        raise ValueError(f"chunk_gdn2 backward: dht must be {(N, H, *sk)}, got {tuple(dht.shape)}")
     dq, dk, db = torch.empty_like(q), torch.empty_like(k), torch.empty_like(b)
     dv, dw = torch.empty_like(v), torch.empty_like(w)
     dg = torch.empty_like(g)
-    dh0 = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) if has_h0 else None
+    dh0 = torch.empty(N, H, *sk, dtype=torch.float32, device=q.device) if has_h0 else None
     lib = nat.load()
     cu_host = saved["cu_host"]
     cu_host_p = None if cu_host is None else cu_host.data_ptr()

@@ -1,6 +1,7 @@
 // extern "C" entry points of libgdn2_hip.so: argument validation and dispatch.
 // Declarations and the reference interfaces they replace: include/gdn2_hip.h.
 
+#include "gdn2_chunk.h"
 #include "gdn2_common.h"
 #include "gdn2_internal.h"
 
@@ -18,7 +19,7 @@ static int check_chunk_args(int io_dtype, int g_dtype, const int64_t *cu_seqlens
     if (!valid_dtype(io_dtype) || !valid_dtype(g_dtype)) return GDN2_ERR_INVALID;
     if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
     if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND |
-                  GDN2_FLAG_SAVE_FOR_BWD))
+                  GDN2_FLAG_SAVE_FOR_BWD | GDN2_FLAG_TRANSPOSE_STATE))
         return GDN2_ERR_INVALID;
     if ((flags & GDN2_FLAG_LOWER_BOUND) && !(flags & GDN2_FLAG_GATE_IN_KERNEL))
         return GDN2_ERR_INVALID;
@@ -290,6 +291,23 @@ size_t gdn2_chunk_train_workspace_size(int B, int T, int H, int K, int V, int io
 {
     if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || !valid_dtype(io_dtype)) return 0;
     return chunk_train_workspace_bytes(B, T, H, K, V, io_dtype, cu_seqlens_host, num_seqs);
+}
+
+int gdn2_chunk_states(const void *saved, size_t saved_bytes, int io_dtype, void *out, int transpose,
+                      const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H, int K,
+                      int V, void *stream)
+{
+    if (!valid_dtype(io_dtype) || B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
+    if (cu_seqlens_host && (B != 1 || num_seqs < 0)) return GDN2_ERR_INVALID;
+    if (K > 128) return GDN2_ERR_UNSUPPORTED;
+    const int64_t nc = count_chunks(B, T, cu_seqlens_host, num_seqs);
+    if (nc == 0) return GDN2_OK;
+    if (!saved || !out) return GDN2_ERR_INVALID;
+    const TrainLayout tl = train_layout(nc, H, K, V, io_dtype);
+    if (saved_bytes < static_cast<size_t>(tl.total)) return GDN2_ERR_WORKSPACE;
+    const hipError_t err = launch_chunk_states(static_cast<const unsigned char *>(saved) + tl.hs, io_dtype, out,
+                                               transpose != 0, nc, H, K, V, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
 size_t gdn2_chunk_bwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,

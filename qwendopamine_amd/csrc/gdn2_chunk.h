@@ -155,6 +155,16 @@ __device__ __forceinline__ void store4(T *base, int64_t off, int c0, int n, cons
         if (c0 + i < n) io<T>::st(p, i, x[i]);
 }
 
+// Element (row k, column v) of the [K, V] state of (sequence n, head h) in a
+// [N, H, K, V] array, or [N, H, V, K] with GDN2_FLAG_TRANSPOSE_STATE (the
+// reference's transpose_state_layout).
+__device__ __forceinline__ int64_t state_index(unsigned flags, int n, int h, int row, int col, int H,
+                                               int K, int V)
+{
+    const int64_t base = static_cast<int64_t>(n) * H + h;
+    return (flags & GDN2_FLAG_TRANSPOSE_STATE) ? (base * V + col) * K + row : (base * K + row) * V + col;
+}
+
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Inclusive prefix sum over the 16 lanes of each DPP row (lanes 16r..16r+15),

@@ -230,7 +230,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = 16 * kt + 4 * kg + i;
-                if (row < K) dS[kt][i] = p.dht[((static_cast<int64_t>(n) * H + h) * K + row) * V + col];
+                if (row < K) dS[kt][i] = p.dht[state_index(p.flags, n, h, row, col, H, K, V)];
             }
         }
     }
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = 16 * kt + 4 * kg + i;
-                if (row < K) p.dh0[((static_cast<int64_t>(n) * H + h) * K + row) * V + col] = dS[kt][i];
+                if (row < K) p.dh0[state_index(p.flags, n, h, row, col, H, K, V)] = dS[kt][i];
             }
     }
 }
@@ -1110,6 +1110,50 @@ int launch_chunk_bwd(const ChunkBwdArgs &a, int io_dtype, int g_dtype, hipStream
         break;
     }
     return e == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+// Chunk start states of a training forward (K16 A-order tiles of the scan's
+// operand precision, the io dtype) rewritten as [nc, H, K, V] or [nc, H, V, K]
+// rows: a permutation of elements, one thread per output element so the
+// writes are coalesced.  This is the reference's return_intermediate_states
+// output (chunk_gdn2.py:1257-1263: h of chunk_gated_delta_rule_fwd_h, in the
+// inputs' dtype).
+template <typename E>
+__global__ __launch_bounds__(256) void chunk_states_kernel(const E *hs, E *out, int trans, int64_t total, int H,
+                                                           int K, int V, int KP, int VP)
+{
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const int inner = trans ? K : V, outer = trans ? V : K;
+    int64_t r = idx;
+    const int a = static_cast<int>(r % inner);
+    r /= inner;
+    const int b = static_cast<int>(r % outer);
+    r /= outer;
+    const int hh = static_cast<int>(r % H);
+    const int64_t gc = r / H;
+    const int k = trans ? a : b, v = trans ? b : a;
+    const int kt = k >> 4, m = k & 15, vt = v >> 4, c = v & 15;
+    const int64_t src = (gc * H + hh) * static_cast<int64_t>(KP) * VP + k16_block(kt, vt, VP) +
+                        4 * (m + 16 * (c >> 2)) + (c & 3);
+    out[idx] = hs[src];
+}
+
+hipError_t launch_chunk_states(const void *hs, int io_dtype, void *out, bool transpose, int64_t nc,
+                               int H, int K, int V, hipStream_t stream)
+{
+    const int KP = kp_for(K), VP = static_cast<int>(round_up(V, 16));
+    const int64_t total = nc * H * K * V;
+    const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+    if (io_dtype == GDN2_DTYPE_F32)
+        hipLaunchKernelGGL((chunk_states_kernel<uint32_t>), grid, dim3(256), 0, stream,
+                           static_cast<const uint32_t *>(hs), static_cast<uint32_t *>(out), int(transpose),
+                           total, H, K, V, KP, VP);
+    else
+        hipLaunchKernelGGL((chunk_states_kernel<uint16_t>), grid, dim3(256), 0, stream,
+                           static_cast<const uint16_t *>(hs), static_cast<uint16_t *>(out), int(transpose),
+                           total, H, K, V, KP, VP);
+    return hipGetLastError();
 }
 
 }  // namespace gdn2

@@ -591,7 +591,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = 16 * kt + 4 * kg + i;
-                if (row < K) S[kt][i] = p.h0[((static_cast<int64_t>(n) * H + h) * K + row) * V + col];
+                if (row < K) S[kt][i] = p.h0[state_index(p.flags, n, h, row, col, H, K, V)];
             }
         }
     }
@@ -839,7 +839,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = 16 * kt + 4 * kg + i;
-                if (row < K) p.ht[((static_cast<int64_t>(n) * H + h) * K + row) * V + col] = S[kt][i];
+                if (row < K) p.ht[state_index(p.flags, n, h, row, col, H, K, V)] = S[kt][i];
             }
     }
 }

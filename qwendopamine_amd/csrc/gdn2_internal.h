@@ -80,6 +80,11 @@ size_t chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
                                  const int64_t *cu_host, int num_seqs);
 int launch_chunk_bwd(const ChunkBwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream);
 
+// Chunk start states saved by a training forward -> [nc, H, K, V] (or
+// [nc, H, V, K]) in io_dtype.
+hipError_t launch_chunk_states(const void *hs, int io_dtype, void *out, bool transpose, int64_t nc,
+                               int H, int K, int V, hipStream_t stream);
+
 // Short convolution (prologue): up to three tensors per launch.
 struct ConvTensor {
     const void *x;          // [B, T, D]

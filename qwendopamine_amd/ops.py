@@ -344,12 +344,18 @@ def chunk_gdn2_fwd(
     lower_bound: float | None = None,
     cu_seqlens: torch.LongTensor | None = None,
     save_for_bwd: bool = False,
+    transpose_state_layout: bool = False,
+    return_intermediate_states: bool = False,
 ):
     """Launch the chunkwise HIP forward (reference ``chunk_gdn2.py:1165-1264``).
 
-    Returns ``(o, final_state)``, or with ``save_for_bwd`` ``(o, final_state,
-    saved)`` where ``saved`` holds the inputs as the kernels read them and the
-    training workspace that ``chunk_gdn2_bwd`` consumes.
+    Returns ``(o, final_state)``. Optional extras:
+    * ``return_intermediate_states`` appends ``h``: each chunk's start state, ``[B, NT, H, K, V]``
+      (``B = 1`` with ``cu_seqlens``, NT the total chunk count) in k's dtype (``chunk_kda.py:2257-2263``).
+    * ``save_for_bwd`` appends ``saved``: the inputs as the kernels read them, plus the training
+      workspace that ``chunk_gdn2_bwd`` consumes.
+
+    ``transpose_state_layout`` makes every state ``[.., V, K]``.
     """
     name = "chunk_gdn2"
     _require_gpu(name, q, k, v, g, b, w, initial_state)
@@ -361,23 +367,27 @@ def chunk_gdn2_fwd(
     g = _io(g, g.dtype if g.dtype in (torch.float32, dt) else torch.float32)
     cu_dev, cu_host = _cu(cu_seqlens, q.device, T)
     N = B if cu_seqlens is None else cu_host.numel() - 1
+    sk = (V, K) if transpose_state_layout else (K, V)
     h0 = None if initial_state is None else initial_state.float().contiguous()
-    if h0 is not None and tuple(h0.shape) != (N, H, K, V):
-        raise ValueError(f"{name}: initial_state must be {(N, H, K, V)}, got {tuple(h0.shape)}")
-    ht = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) if output_final_state else None
+    if h0 is not None and tuple(h0.shape) != (N, H, *sk):
+        raise ValueError(f"{name}: initial_state must be {(N, H, *sk)}, got {tuple(h0.shape)}")
+    ht = torch.empty(N, H, *sk, dtype=torch.float32, device=q.device) if output_final_state else None
+    keep = save_for_bwd or return_intermediate_states
     o = torch.empty_like(v)
     lib = nat.load()
     cu_host_p = None if cu_host is None else cu_host.data_ptr()
-    size_fn = lib.gdn2_chunk_train_workspace_size if save_for_bwd else lib.gdn2_chunk_fwd_workspace_size
+    size_fn = lib.gdn2_chunk_train_workspace_size if keep else lib.gdn2_chunk_fwd_workspace_size
     ws_bytes = size_fn(B, T, H, K, V, nat.dtype_code(dt), cu_host_p, N)
     if ws_bytes == 0 and B * T > 0 and K > 128:
         raise NotImplementedError(f"{name}: key head dim {K} > 128 is not supported by the chunk kernel")
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     a_log, dtb = _gate_tensors(use_gate_in_kernel, A_log, dt_bias, H, K)
     flags = _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound)
-    if save_for_bwd:
-        if use_gate_in_kernel:
-            raise NotImplementedError(f"{name}: apply the gate before the op when gradients are needed")
+    if transpose_state_layout:
+        flags |= nat.FLAG_TRANSPOSE_STATE
+    if save_for_bwd and use_gate_in_kernel:
+        raise NotImplementedError(f"{name}: apply the gate before the op when gradients are needed")
+    if keep:
         flags |= nat.FLAG_SAVE_FOR_BWD
     st = lib.gdn2_chunk_fwd(
         nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(g), nat.ptr(b), nat.ptr(w),
@@ -388,11 +398,23 @@ def chunk_gdn2_fwd(
         ws.data_ptr(), ws.numel(), nat.stream_handle(q.device),
     )
     nat.check(st, name)
+    res = (o, ht)
+    if return_intermediate_states:
+        nc = sum(-(-int(cu_host[i + 1] - cu_host[i]) // 64) for i in range(N)) if cu_host is not None \
+            else B * (-(-T // 64))
+        nb = 1 if cu_host is not None else B
+        h = torch.empty(nb, nc // max(nb, 1), H, *sk, dtype=dt, device=q.device)
+        st = lib.gdn2_chunk_states(ws.data_ptr(), ws.numel(), nat.dtype_code(dt), nat.ptr(h),
+                                   int(transpose_state_layout), cu_host_p, N, B, T, H, K, V,
+                                   nat.stream_handle(q.device))
+        nat.check(st, name)
+        res = res + (h,)
     if not save_for_bwd:
-        return o, ht
+        return res
     saved = dict(q=q, k=k, v=v, g=g, b=b, w=w, ws=ws, cu_dev=cu_dev, cu_host=cu_host, N=N,
-                 scale=float(scale), flags=flags & ~nat.FLAG_SAVE_FOR_BWD)
-    return o, ht, saved
+                 scale=float(scale), flags=flags & ~nat.FLAG_SAVE_FOR_BWD,
+                 transpose=transpose_state_layout)
+    return res + (saved,)
 
 
 class ChunkGDN2Function(torch.autograd.Function):
@@ -405,7 +427,8 @@ class ChunkGDN2Function(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, g, b, w, A_log, dt_bias, scale, initial_state, output_final_state,
-                use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound):
+                use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound,
+                transpose_state_layout=False):
         needs = any(ctx.needs_input_grad[i] for i in (0, 1, 2, 3, 4, 5, 9))
         if use_gate_in_kernel and needs:
             raise NotImplementedError(
@@ -415,11 +438,11 @@ class ChunkGDN2Function(torch.autograd.Function):
         res = chunk_gdn2_fwd(
             q, k, v, g, b, w, scale, initial_state, output_final_state,
             use_qk_l2norm_in_kernel, use_gate_in_kernel, A_log, dt_bias, lower_bound, cu_seqlens,
-            save_for_bwd=needs,
+            save_for_bwd=needs, transpose_state_layout=transpose_state_layout,
         )
         ctx.in_dtypes = tuple(x.dtype for x in (q, k, v, g, b, w))
         ctx.has_h0 = initial_state is not None
-        ctx.saved = res[2] if needs else None
+        ctx.saved = res[-1] if needs else None
         return res[0], res[1]
 
     @staticmethod
@@ -431,7 +454,7 @@ class ChunkGDN2Function(torch.autograd.Function):
         dq, dk, dv, dg, db, dw, dh0 = chunk_gdn2_bwd(ctx.saved, do, dht, ctx.has_h0)
         ctx.saved = None
         dq, dk, dv, dg, db, dw = (x.to(d) for x, d in zip((dq, dk, dv, dg, db, dw), ctx.in_dtypes))
-        return (dq, dk, dv, dg, db, dw, None, None, None, dh0, None, None, None, None, None)
+        return (dq, dk, dv, dg, db, dw, None, None, None, dh0, None, None, None, None, None, None)
 
 
 def chunk_gdn2(
@@ -457,9 +480,13 @@ def chunk_gdn2(
 ):
     """Chunkwise gdn2 forward with autograd (reference ``chunk_gdn2.py:1268-1434``).
 
-    Shapes ``q, k, g, b [B,T,H,K]``, ``v, w [B,T,H,V]``; ``initial_state``
-    ``[N,H,K,V]`` float32.  Returns ``(o, final_state)``.  The chunk size is 64,
-    as in the reference accelerated op.
+    Shapes: ``q, k, g, b [B,T,H,K]``, ``v, w [B,T,H,V]``, ``initial_state [N,H,K,V]`` float32
+    (``[N,H,V,K]`` with ``transpose_state_layout``). The chunk size is 64, as in the reference
+    accelerated op.
+
+    Returns ``(o, final_state)``. Under ``torch.inference_mode`` with
+    ``return_intermediate_states``, it returns ``(o, final_state, h)`` instead, with ``h`` the
+    per-chunk start states (``chunk_gdn2.py:1415-1421``).
     """
     if cu_seqlens is not None:
         if q.shape[0] != 1:
@@ -499,11 +526,22 @@ def chunk_gdn2(
     assert v.shape == (*q.shape[:3], v.shape[-1]), (
         "v must be of shape (batch size, seq len, num of head, head dim)."
     )
-    if return_intermediate_states or transpose_state_layout:
-        raise NotImplementedError("chunk_gdn2: return_intermediate_states / transpose_state_layout")
     if scale is None:
         scale = k.shape[-1] ** -0.5
     _require_gpu("chunk_gdn2", q, k, v, g, b, w, initial_state)
+    if return_intermediate_states:
+        assert torch.is_inference_mode_enabled(), (
+            "return_intermediate_states is only allowed in inference mode"
+        )
+        assert disable_recompute is False, (
+            "return_intermediate_states must be used with disable_recompute=False"
+        )
+        o, ht, h = chunk_gdn2_fwd(
+            q, k, v, g, b, w, scale, initial_state, output_final_state, use_qk_l2norm_in_kernel,
+            use_gate_in_kernel, A_log, dt_bias, lower_bound, cu_seqlens,
+            transpose_state_layout=transpose_state_layout, return_intermediate_states=True,
+        )
+        return o.type_as(q), ht, h
     if use_gate_in_kernel and torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (q, k, v, g, b, w, A_log, dt_bias, initial_state)
     ):
@@ -512,7 +550,7 @@ def chunk_gdn2(
         use_gate_in_kernel, A_log, dt_bias, lower_bound = False, None, None, None
     return ChunkGDN2Function.apply(
         q, k, v, g, b, w, A_log, dt_bias, scale, initial_state, output_final_state,
-        use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound,
+        use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound, transpose_state_layout,
     )
 
 
