@@ -25,9 +25,10 @@
 // with the identity transposes a tile in registers.
 //
 // Two kernels:
-//  * chunk_prep_kernel -- one workgroup (4 waves, wave R = 16-token block R)
-//    per (chunk, head), all chunks in parallel.  Fused prologue (L2 norm,
-//    scale, optional in-kernel gate, in-block prefix sums), Aqk^T and L^T on
+//  * chunk_prep_kernel -- a persistent grid of 4-wave workgroups (wave R =
+//    16-token block R), each walking (chunk, head) items with the next
+//    item's input rows in flight during the current one.  Fused prologue
+//    (L2 norm, scale, optional in-kernel gate, in-block prefix sums), Aqk^T and L^T on
 //    MFMA, the block-triangular inverse of I + L in fp32, and W^T = Ebar^T X^T.
 //    It writes one contiguous "blob" per (chunk, head): X, -W, Qbar, Aqk,
 //    Ktilde^T in K16 fragment-native order plus exp(G_last).
@@ -60,23 +61,36 @@ struct RowLoad {
     static constexpr int RPI = 64 / LPR;                          // rows per instruction
     static constexpr int NI = 16 / RPI;                           // instructions
     u32x4 v[NI];
-    __device__ __forceinline__ void issue(const T *base, int64_t row0, int64_t stride, int nvalid, int l)
+    // Rows first..first+15 of the chunk whose row 0 starts at element chunk0;
+    // rows at or beyond the chunk length lc read the chunk's row 0 instead
+    // (always in bounds) and are zeroed by land(), so no result of a load is
+    // selected on before it is needed.
+    __device__ __forceinline__ void issue(const T *base, int64_t chunk0, int64_t stride, int first, int lc,
+                                          int l)
     {
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
-            const int rr = j * RPI + l / LPR;
-            const char *src = reinterpret_cast<const char *>(base + row0 + rr * stride) + 16 * (l % LPR);
-            v[j] = rr < nvalid ? *reinterpret_cast<const u32x4 *>(src) : u32x4{0, 0, 0, 0};
+            const int row = first + j * RPI + l / LPR;
+            const int rc = row < lc ? row : 0;
+            const char *src = reinterpret_cast<const char *>(base + chunk0 + rc * stride) + 16 * (l % LPR);
+            v[j] = *reinterpret_cast<const u32x4 *>(src);
         }
     }
+    __device__ __forceinline__ void clear()
+    {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) v[j] = u32x4{0, 0, 0, 0};
+    }
     // Through the wave's LDS scratch into the A-order registers (row m,
-    // channels 16kt + 4kg + i).
-    __device__ __forceinline__ void land(unsigned char *stg, int l, int m, int kg, float (&out)[KP / 16][4])
+    // channels 16kt + 4kg + i); rows rr >= nvalid are zero.
+    __device__ __forceinline__ void land(unsigned char *stg, int l, int m, int kg, int nvalid,
+                                         float (&out)[KP / 16][4])
     {
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
             const int rr = j * RPI + l / LPR;
-            *reinterpret_cast<u32x4 *>(stg + rr * RS + 16 * (l % LPR)) = v[j];
+            *reinterpret_cast<u32x4 *>(stg + rr * RS + 16 * (l % LPR)) =
+                rr < nvalid ? v[j] : u32x4{0, 0, 0, 0};
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -93,12 +107,43 @@ struct RowLoad {
     }
 };
 
+// One prep work item: chunk gc (global index over all sequences) of head h;
+// item = gc * H + h, so neighbouring items read neighbouring rows of the
+// [tokens, H, K] inputs and write neighbouring blobs.
+struct PrepItem {
+    int gc, h, lc;   // lc = tokens in the chunk (<= kChunk)
+    int64_t chunk0;  // element offset of (token t0, head h, channel 0)
+};
+
+__device__ __forceinline__ PrepItem prep_item(const ChunkParams &p, int item)
+{
+    PrepItem it;
+    it.gc = item / p.H;
+    it.h = item - it.gc * p.H;
+    int n, jc;
+    int64_t bos, len;
+    locate_chunk(p, it.gc, n, jc, bos, len);
+    const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
+    const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
+    it.lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
+    it.chunk0 = (t0 * p.H + it.h) * static_cast<int64_t>(p.K);
+    return it;
+}
+
 // ---------------------------------------------------------------------------
-// Prep: one workgroup (4 waves) per (chunk, head).  Wave R owns token rows
+// Prep: a persistent grid of workgroups (4 waves each) walking the items
+// blockIdx.x, blockIdx.x + gridDim.x, ...  Wave R owns token rows
 // 16R..16R+15; lane (m, kg) holds row 16R+m and channels 16kt + 4kg + i.
+// When K == KP the next item's input rows are requested as soon as the
+// current item's inputs are dead (after the factors), so their HBM latency
+// overlaps the products and the inverse.
 // ---------------------------------------------------------------------------
+// Two workgroups per CU (the LDS limit for 16-bit storage) need <= 256
+// registers; fp32 storage at KP = 128 fits one workgroup per CU in LDS.
 template <PrecKind PK, int KP, typename TI, typename TG>
-__global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkParams p)
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(PK == PrecKind::F32 && KP == 128 ? 1 : 2))) void
+chunk_prep_kernel(ChunkParams p, int items)
 {
     using P = Prec<PK>;
     using st = typename P::st;
@@ -123,315 +168,348 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkParams p)
     static_assert(sizeof(sX) >= 2 * 16 * (KP * 4 + 16) && sizeof(smem1) >= 2 * 16 * (KP * 4 + 16),
                   "row staging must fit in sX and smem1");
 
-    const int tid = threadIdx.x, R = tid >> 6, l = tid & 63, m = l & 15, kg = l >> 4;
-    const int gc = blockIdx.x, h = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int R0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, uniform
     const int H = p.H, K = p.K;
-
-    int n, jc;
-    int64_t bos, len;
-    locate_chunk(p, gc, n, jc, bos, len);
-    const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
-    const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
-    const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
-    const int r = 16 * R + m;
-    const bool row_ok = r < lc;
-    const int64_t roff = ((t0 + r) * H + h) * K;
+    const bool rows_whole = K == KP;  // whole-row 16-byte loads, prefetched one item ahead
+    const int64_t stride = static_cast<int64_t>(H) * K;
 
     const TI *q = static_cast<const TI *>(p.q);
     const TI *k = static_cast<const TI *>(p.k);
     const TI *b = static_cast<const TI *>(p.b);
     const TG *g = static_cast<const TG *>(p.g);
 
-    float qv[NKT][4], kv[NKT][4], ev[NKT][4], gv[NKT][4];
-    if (K == KP) {
-        // Whole-row 16-byte loads, redistributed through a per-wave LDS
-        // scratch (sX for waves 0-1, smem1 for waves 2-3; both are free until
-        // the first barrier).
-        unsigned char *stg = R < 2 ? reinterpret_cast<unsigned char *>(sX) + R * (16 * (KP * 4 + 16))
-                                   : smem1 + (R - 2) * (16 * (KP * 4 + 16));
-        const int64_t row0 = ((t0 + 16 * R) * H + h) * static_cast<int64_t>(K);
-        const int64_t stride = static_cast<int64_t>(H) * K;
-        const int nvalid = lc - 16 * R;
-        RowLoad<TI, KP> lq, lk, lb;
-        RowLoad<TG, KP> lg;
-        lq.issue(q, row0, stride, nvalid, l);
-        lk.issue(k, row0, stride, nvalid, l);
-        lb.issue(b, row0, stride, nvalid, l);
-        lg.issue(g, row0, stride, nvalid, l);
-        lq.land(stg, l, m, kg, qv);
-        lk.land(stg, l, m, kg, kv);
-        lb.land(stg, l, m, kg, ev);
-        lg.land(stg, l, m, kg, gv);
-    } else {
-#pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-            const int c0 = 16 * kt + 4 * kg;
-            load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv[kt]);
-            load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv[kt]);
-            load4<TI>(b, roff, c0, K, row_ok, p.vec_ok, ev[kt]);
-            load4<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv[kt]);
-        }
+    // Rows staged through a per-wave LDS scratch: sX for waves 0-1, smem1
+    // for waves 2-3; both are free from the end of one item (after its last
+    // barrier) until the first barrier of the next.
+    unsigned char *stg = R0 < 2 ? reinterpret_cast<unsigned char *>(sX) + R0 * (16 * (KP * 4 + 16))
+                                : smem1 + (R0 - 2) * (16 * (KP * 4 + 16));
+    RowLoad<TI, KP> lq, lk, lb;
+    RowLoad<TG, KP> lg;
+    PrepItem it = prep_item(p, blockIdx.x);
+    if (rows_whole) {
+        lq.issue(q, it.chunk0, stride, 16 * R0, it.lc, lane);
+        lk.issue(k, it.chunk0, stride, 16 * R0, it.lc, lane);
+        lb.issue(b, it.chunk0, stride, 16 * R0, it.lc, lane);
+        lg.issue(g, it.chunk0, stride, 16 * R0, it.lc, lane);
     }
 
-    // Fused prologue: L2 norm (F.normalize semantics), scale, erase vector,
-    // optional gate activation, decay in log2 units.
-    float sq = 0.f, sk = 0.f;
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+        // The lane and wave indices are made opaque per item so that the
+        // compiler does not hoist the many per-lane LDS and blob addresses out
+        // of the loop, where they would hold registers through every phase.
+        int l = lane, R = R0;
+        asm volatile("" : "+v"(l));
+        asm volatile("" : "+s"(R));
+        const int tid = 64 * R + l, m = l & 15, kg = l >> 4;
+        const int gc = it.gc, h = it.h, lc = it.lc;
+        const int r = 16 * R + m;
+        const bool row_ok = r < lc;
+        const int64_t roff = it.chunk0 + r * stride;
+
+        float qv[NKT][4], kv[NKT][4], ev[NKT][4], gv[NKT][4];
+        if (rows_whole) {
+            const int nvalid = lc - 16 * R;
+            lq.land(stg, l, m, kg, nvalid, qv);
+            lk.land(stg, l, m, kg, nvalid, kv);
+            lb.land(stg, l, m, kg, nvalid, ev);
+            lg.land(stg, l, m, kg, nvalid, gv);
+        } else {
 #pragma unroll
-    for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sq = fmaf(qv[kt][i], qv[kt][i], sq);
-            sk = fmaf(kv[kt][i], kv[kt][i], sk);
-        }
-    sq += __shfl_xor(sq, 16, 64);
-    sq += __shfl_xor(sq, 32, 64);
-    sk += __shfl_xor(sk, 16, 64);
-    sk += __shfl_xor(sk, 32, 64);
-    const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
-    const float invq = l2 ? 1.0f / fmaxf(sqrtf(sq), 1e-6f) : 1.0f;
-    const float invk = l2 ? 1.0f / fmaxf(sqrtf(sk), 1e-6f) : 1.0f;
-    const float qmul = invq * p.scale;
-    const bool gate = (p.flags & GDN2_FLAG_GATE_IN_KERNEL) != 0;
-    const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
-    const float a_log = gate ? p.A_log[h] : 0.0f;
-#pragma unroll
-    for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = 16 * kt + 4 * kg + i;
-            qv[kt][i] *= qmul;
-            kv[kt][i] *= invk;
-            ev[kt][i] *= kv[kt][i];
-            float gg = gv[kt][i];
-            if (gate && row_ok && c < K) {
-                const float db = p.dt_bias ? p.dt_bias[h * K + c] : 0.0f;
-                gg = gate_activation(gg, a_log, db, use_lb, p.lower_bound);
+            for (int kt = 0; kt < NKT; ++kt) {
+                const int c0 = 16 * kt + 4 * kg;
+                load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv[kt]);
+                load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv[kt]);
+                load4<TI>(b, roff, c0, K, row_ok, p.vec_ok, ev[kt]);
+                load4<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv[kt]);
             }
-            gv[kt][i] = row16_scan(gg * kLog2e);  // G (log2) relative to block start
         }
-    bool wide = false;
-    if (m == 15) {
+
+        // Fused prologue: L2 norm (F.normalize semantics), scale, erase vector,
+        // optional gate activation, decay in log2 units.
+        float sq = 0.f, sk = 0.f;
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-            *reinterpret_cast<float4 *>(&sT[R][16 * kt + 4 * kg]) =
-                make_float4(gv[kt][0], gv[kt][1], gv[kt][2], gv[kt][3]);
+        for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) wide = wide || (-gv[kt][i] > kDiagSpanLimit2);
-        }
-    }
-    // A diagonal block whose decay span is too wide for the factored form is
-    // summed exactly, pair by pair (row m, column j of block R), here while
-    // the fp32 inputs are still live.
-    const bool wave_slow = __ballot(wide) != 0;
-    f32x4 dq = zero4(), dl = zero4();
-    if (wave_slow) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            float accq = 0.f, accl = 0.f;
+            for (int i = 0; i < 4; ++i) {
+                sq = fmaf(qv[kt][i], qv[kt][i], sq);
+                sk = fmaf(kv[kt][i], kv[kt][i], sk);
+            }
+        sq += __shfl_xor(sq, 16, 64);
+        sq += __shfl_xor(sq, 32, 64);
+        sk += __shfl_xor(sk, 16, 64);
+        sk += __shfl_xor(sk, 32, 64);
+        const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
+        const float invq = l2 ? 1.0f / fmaxf(sqrtf(sq), 1e-6f) : 1.0f;
+        const float invk = l2 ? 1.0f / fmaxf(sqrtf(sk), 1e-6f) : 1.0f;
+        const float qmul = invq * p.scale;
+        if (p.flags & GDN2_FLAG_GATE_IN_KERNEL) {
+            const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
+            const float a_log = p.A_log[h];
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float kj = __shfl(kv[kt][i], 16 * kg + j, 64);
-                    const float Gj = __shfl(gv[kt][i], 16 * kg + j, 64);
-                    const float ex = (j <= m) ? fexp2(gv[kt][i] - Gj) : 0.f;
-                    accq = fmaf(qv[kt][i] * kj, ex, accq);
-                    accl = fmaf(ev[kt][i] * kj, ex, accl);
-                }
-            accq += __shfl_xor(accq, 16, 64);
-            accq += __shfl_xor(accq, 32, 64);
-            accl += __shfl_xor(accl, 16, 64);
-            accl += __shfl_xor(accl, 32, 64);
-            if (kg == (j >> 2)) {
-                dq[j & 3] = accq;
-                dl[j & 3] = accl;
-            }
-        }
-    }
-    __syncthreads();
-
-    st *ws = static_cast<st *>(p.ws) + (static_cast<int64_t>(gc) * H + h) * BL::SIZE;
-    // Per-channel block vectors.
-    for (int e = tid; e < 4 * KP; e += 256) {
-        const int Rb = e / KP, c = e % KP;
-        const float t[4] = {sT[0][c], sT[1][c], sT[2][c], sT[3][c]};
-        float cum = 0.f, after = 0.f;
-#pragma unroll
-        for (int R2 = 0; R2 < 4; ++R2) {
-            if (R2 < Rb) cum += t[R2];
-            if (R2 > Rb) after += t[R2];
-        }
-        sEr[Rb][c] = fexp2(cum);
-        sEa[Rb][c] = fexp2(after);
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-            float ex = 0.f;
-            if (I == Rb) {
-                ex = -t[Rb];
-            } else {
-#pragma unroll
-                for (int R2 = 0; R2 < 4; ++R2)
-                    if (R2 > I && R2 < Rb) ex += t[R2];
-            }
-            sPf[Rb][I][c] = I > Rb ? 0.f : fexp2(ex);
-        }
-        if (Rb == 0) reinterpret_cast<float *>(ws + BL::GL)[c] = fexp2(t[0] + t[1] + t[2] + t[3]);
-    }
-    __syncthreads();
-
-    // Factors.  Qb / Eb stay in registers as K16 operands of this row block;
-    // Qbar goes straight to the blob; Ktilde^T and Ebar^T are transposed by
-    // an identity product.
-    const Q ident = identity_q4<PK>(l);
-    Q fqb[NKT], feb[NKT];
-#pragma unroll
-    for (int kt = 0; kt < NKT; ++kt) {
-        const int c0 = 16 * kt + 4 * kg;
-        const float4 er = *reinterpret_cast<const float4 *>(&sEr[R][c0]);
-        const float4 ea = *reinterpret_cast<const float4 *>(&sEa[R][c0]);
-        const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][c0]);
-        const float erv[4] = {er.x, er.y, er.z, er.w};
-        const float eav[4] = {ea.x, ea.y, ea.z, ea.w};
-        const float trv[4] = {tr.x, tr.y, tr.z, tr.w};
-        float qb[4], eb[4], ke[4], qbar[4], ebar[4], ktil[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float G = gv[kt][i];
-            const float e1 = fexp2(G), e2 = fexp2(trv[i] - G);
-            qb[i] = qv[kt][i] * e1;
-            eb[i] = ev[kt][i] * e1;
-            ke[i] = kv[kt][i] * e2;
-            qbar[i] = qb[i] * erv[i];
-            ebar[i] = eb[i] * erv[i];
-            ktil[i] = ke[i] * eav[i];
-        }
-        fqb[kt] = pack4<PK>(qb[0], qb[1], qb[2], qb[3]);
-        feb[kt] = pack4<PK>(eb[0], eb[1], eb[2], eb[3]);
-        st_q4<PK>(ws + BL::QB + k16_block(R, kt, KP) + 4 * l, pack4<PK>(qbar[0], qbar[1], qbar[2], qbar[3]));
-        st_q4<PK>(sKend + r * LDK + c0, pack4<PK>(ke[0], ke[1], ke[2], ke[3]));
-        const f32x4 dk = mma1<PK>(zero4(), pack4<PK>(ktil[0], ktil[1], ktil[2], ktil[3]), ident);
-        st_q4<PK>(ws + BL::KT + k16_block(kt, R, 64) + 4 * l, pack4<PK>(dk));
-        const f32x4 de = mma1<PK>(zero4(), pack4<PK>(ebar[0], ebar[1], ebar[2], ebar[3]), ident);
-        st_q4<PK>(sEt + k16_block(kt, R, 64) + 4 * l, pack4<PK>(de));
-    }
-    __syncthreads();
-
-    // Aqk^T(I, R) = Kend_I^T-scaled . Qb_R^T and L^T(I, R) likewise with Eb:
-    // A = scaled keys of block I (LDS), B = this block's Qb / Eb (registers).
-    // Lane (n, kg) of the result holds Aqk[16R+n][16I+4kg+i], which is the
-    // K16 A-operand order of Aqk, so it is stored as is.
-    f32x4 aq[4], al[4];
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-        aq[I] = zero4();
-        al[I] = zero4();
-        if (I <= R) {
-#pragma unroll
-            for (int s = 0; s < NKS; ++s) {
-                Q a[2];
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int c0 = 32 * s + 16 * hh + 4 * kg;
-                    Q raw = ld_q4<PK>(sKend + (16 * I + m) * LDK + c0);
-                    if (I != R - 1) {
-                        float x[4];
-                        unpack4<PK>(raw, x);
-                        const float4 sc = *reinterpret_cast<const float4 *>(&sPf[R][I][c0]);
-                        raw = pack4<PK>(x[0] * sc.x, x[1] * sc.y, x[2] * sc.z, x[3] * sc.w);
+                    const int c = 16 * kt + 4 * kg + i;
+                    if (row_ok && c < K) {
+                        const float db = p.dt_bias ? p.dt_bias[h * K + c] : 0.0f;
+                        gv[kt][i] = gate_activation(gv[kt][i], a_log, db, use_lb, p.lower_bound);
                     }
-                    a[hh] = raw;
                 }
-                aq[I] = mma2<PK>(aq[I], a[0], a[1], fqb[2 * s], fqb[2 * s + 1]);
-                al[I] = mma2<PK>(al[I], a[0], a[1], feb[2 * s], feb[2 * s + 1]);
+        }
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                qv[kt][i] *= qmul;
+                kv[kt][i] *= invk;
+                ev[kt][i] *= kv[kt][i];
+                gv[kt][i] = row16_scan(gv[kt][i] * kLog2e);  // G (log2) relative to block start
+            }
+        bool wide = false;
+        if (m == 15) {
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) {
+                *reinterpret_cast<float4 *>(&sT[R][16 * kt + 4 * kg]) =
+                    make_float4(gv[kt][0], gv[kt][1], gv[kt][2], gv[kt][3]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wide = wide || (-gv[kt][i] > kDiagSpanLimit2);
             }
         }
-    }
-    if (wave_slow) {
+        // A diagonal block whose decay span is too wide for the factored form is
+        // summed exactly, pair by pair (row m, column j of block R), here while
+        // the fp32 inputs are still live.
+        const bool wave_slow = __ballot(wide) != 0;
+        f32x4 dq = zero4(), dl = zero4();
+        if (wave_slow) {
 #pragma unroll
-        for (int I = 0; I < 4; ++I)
-            if (I == R) {
-                aq[I] = dq;
-                al[I] = dl;
+            for (int j = 0; j < 16; ++j) {
+                float accq = 0.f, accl = 0.f;
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float kj = __shfl(kv[kt][i], 16 * kg + j, 64);
+                        const float Gj = __shfl(gv[kt][i], 16 * kg + j, 64);
+                        const float ex = (j <= m) ? fexp2(gv[kt][i] - Gj) : 0.f;
+                        accq = fmaf(qv[kt][i] * kj, ex, accq);
+                        accl = fmaf(ev[kt][i] * kj, ex, accl);
+                    }
+                accq += __shfl_xor(accq, 16, 64);
+                accq += __shfl_xor(accq, 32, 64);
+                accl += __shfl_xor(accl, 16, 64);
+                accl += __shfl_xor(accl, 32, 64);
+                if (kg == (j >> 2)) {
+                    dq[j & 3] = accq;
+                    dl[j & 3] = accl;
+                }
             }
-    }
-    // Causal masks; Aqk to the blob.
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int col = 16 * I + 4 * kg + i, row = 16 * R + m;
-            if (!(col <= row)) aq[I][i] = 0.f;
-            if (!(col < row)) al[I][i] = 0.f;
-        }
-        st_q4<PK>(ws + BL::AQ + k16_block(R, I, 64) + 4 * l, pack4<PK>(aq[I]));
-    }
-    __syncthreads();  // all reads of sKend done; its space becomes L
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-        *reinterpret_cast<float4 *>(&sL[(16 * R + m) * LDF + 16 * I + 4 * kg]) =
-            make_float4(al[I][0], al[I][1], al[I][2], al[I][3]);
-    __syncthreads();
-
-    // X = (I + L)^{-1} in fp32: diagonal 16x16 blocks by forward substitution
-    // (lane j = column j), strictly-upper blocks zero.
-    if (l < 16) {
-        const int j = l;
-        float x[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float acc = (i == j) ? 1.f : 0.f;
-#pragma unroll
-            for (int mm = 0; mm < i; ++mm) acc = fmaf(-sL[(16 * R + i) * LDF + 16 * R + mm], x[mm], acc);
-            x[i] = acc;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sX[(16 * R + i) * LDF + 16 * R + j] = x[i];
-    }
-    for (int I = R + 1; I < 4; ++I)
-        for (int e = l; e < 256; e += 64) sX[(16 * R + (e >> 4)) * LDF + 16 * I + (e & 15)] = 0.f;
-    __syncthreads();
-    // Off-diagonal blocks, one sub-diagonal at a time:
-    //   X_RI = -X_RR * sum_{J=I}^{R-1} L_RJ X_JI.
-    for (int d = 1; d <= 3; ++d) {
-        if (R < 4 - d) {
-            const int Rr = R + d, I = R;
-            f32x4 t = zero4();
-            for (int J = I; J < Rr; ++J)
-                t = mm16_f32(t, sL + (16 * Rr) * LDF + 16 * J, LDF, sX + (16 * J) * LDF + 16 * I, LDF, l);
-            float *scr = sScr[R];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) scr[(4 * kg + i) * 16 + m] = t[i];
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            const f32x4 xr = mm16_f32(zero4(), sX + (16 * Rr) * LDF + 16 * Rr, LDF, scr, 16, l);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sX[(16 * Rr + 4 * kg + i) * LDF + 16 * I + m] = -xr[i];
         }
         __syncthreads();
-    }
 
-    // X to the blob (row block R).
-    Q xt[4];
+        st *ws = static_cast<st *>(p.ws) + (static_cast<int64_t>(gc) * H + h) * BL::SIZE;
+        // Per-channel block vectors.
+        for (int e = tid; e < 4 * KP; e += 256) {
+            const int Rb = e / KP, c = e % KP;
+            const float t[4] = {sT[0][c], sT[1][c], sT[2][c], sT[3][c]};
+            float cum = 0.f, after = 0.f;
 #pragma unroll
-    for (int J = 0; J < 4; ++J) {
-        const float4 xv = *reinterpret_cast<const float4 *>(&sX[(16 * R + m) * LDF + 16 * J + 4 * kg]);
-        xt[J] = pack4<PK>(xv.x, xv.y, xv.z, xv.w);
-        st_q4<PK>(ws + BL::X + k16_block(R, J, 64) + 4 * l, xt[J]);
-    }
-    // W^T(ct, R) = Ebar^T(ct, :) X^T(:, R): B operand X^T(J, R) is row 16R+m of
-    // X, i.e. xt[J]; result lane (n, kg) holds W[16R+n][16ct+4kg+i] -- the K16
-    // A-operand order of W.  Stored negated.
+            for (int R2 = 0; R2 < 4; ++R2) {
+                if (R2 < Rb) cum += t[R2];
+                if (R2 > Rb) after += t[R2];
+            }
+            sEr[Rb][c] = fexp2(cum);
+            sEa[Rb][c] = fexp2(after);
 #pragma unroll
-    for (int ct = 0; ct < NKT; ++ct) {
-        f32x4 acc = zero4();
+            for (int I = 0; I < 4; ++I) {
+                float ex = 0.f;
+                if (I == Rb) {
+                    ex = -t[Rb];
+                } else {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            if (2 * s <= R)
-                acc = mma2<PK>(acc, ld_q4<PK>(sEt + k16_block(ct, 2 * s, 64) + 4 * l),
-                               ld_q4<PK>(sEt + k16_block(ct, 2 * s + 1, 64) + 4 * l), xt[2 * s],
-                               xt[2 * s + 1]);
+                    for (int R2 = 0; R2 < 4; ++R2)
+                        if (R2 > I && R2 < Rb) ex += t[R2];
+                }
+                sPf[Rb][I][c] = I > Rb ? 0.f : fexp2(ex);
+            }
+            if (Rb == 0) reinterpret_cast<float *>(ws + BL::GL)[c] = fexp2(t[0] + t[1] + t[2] + t[3]);
         }
-        st_q4<PK>(ws + BL::WN + k16_block(R, ct, KP) + 4 * l, pack4<PK>(-acc[0], -acc[1], -acc[2], -acc[3]));
+        __syncthreads();
+
+        // Factors.  Qb / Eb stay in registers as K16 operands of this row block;
+        // Qbar goes straight to the blob; Ktilde^T and Ebar^T are transposed by
+        // an identity product.
+        const Q ident = identity_q4<PK>(l);
+        Q fqb[NKT], feb[NKT];
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+            const int c0 = 16 * kt + 4 * kg;
+            const float4 er = *reinterpret_cast<const float4 *>(&sEr[R][c0]);
+            const float4 ea = *reinterpret_cast<const float4 *>(&sEa[R][c0]);
+            const float4 tr = *reinterpret_cast<const float4 *>(&sT[R][c0]);
+            const float erv[4] = {er.x, er.y, er.z, er.w};
+            const float eav[4] = {ea.x, ea.y, ea.z, ea.w};
+            const float trv[4] = {tr.x, tr.y, tr.z, tr.w};
+            float qb[4], eb[4], ke[4], qbar[4], ebar[4], ktil[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float G = gv[kt][i];
+                const float e1 = fexp2(G), e2 = fexp2(trv[i] - G);
+                qb[i] = qv[kt][i] * e1;
+                eb[i] = ev[kt][i] * e1;
+                ke[i] = kv[kt][i] * e2;
+                qbar[i] = qb[i] * erv[i];
+                ebar[i] = eb[i] * erv[i];
+                ktil[i] = ke[i] * eav[i];
+            }
+            fqb[kt] = pack4<PK>(qb[0], qb[1], qb[2], qb[3]);
+            feb[kt] = pack4<PK>(eb[0], eb[1], eb[2], eb[3]);
+            st_q4<PK>(ws + BL::QB + k16_block(R, kt, KP) + 4 * l,
+                      pack4<PK>(qbar[0], qbar[1], qbar[2], qbar[3]));
+            st_q4<PK>(sKend + r * LDK + c0, pack4<PK>(ke[0], ke[1], ke[2], ke[3]));
+            const f32x4 dk = mma1<PK>(zero4(), pack4<PK>(ktil[0], ktil[1], ktil[2], ktil[3]), ident);
+            st_q4<PK>(ws + BL::KT + k16_block(kt, R, 64) + 4 * l, pack4<PK>(dk));
+            const f32x4 de = mma1<PK>(zero4(), pack4<PK>(ebar[0], ebar[1], ebar[2], ebar[3]), ident);
+            st_q4<PK>(sEt + k16_block(kt, R, 64) + 4 * l, pack4<PK>(de));
+        }
+        // The inputs of this item are dead: request the next item's rows.
+        const int next = item + gridDim.x;
+        const PrepItem nit = prep_item(p, next < items ? next : item);
+        if (rows_whole && next < items) {
+            lq.issue(q, nit.chunk0, stride, 16 * R, nit.lc, l);
+            lk.issue(k, nit.chunk0, stride, 16 * R, nit.lc, l);
+            lb.issue(b, nit.chunk0, stride, 16 * R, nit.lc, l);
+            lg.issue(g, nit.chunk0, stride, 16 * R, nit.lc, l);
+        } else {
+            // Defined on both paths: otherwise the landed rows of this item
+            // would stay live (as the merge's other input) through the item.
+            lq.clear();
+            lk.clear();
+            lb.clear();
+            lg.clear();
+        }
+        __syncthreads();
+
+        // Aqk^T(I, R) = Kend_I^T-scaled . Qb_R^T and L^T(I, R) likewise with Eb:
+        // A = scaled keys of block I (LDS), B = this block's Qb / Eb (registers).
+        // Lane (n, kg) of the result holds Aqk[16R+n][16I+4kg+i], which is the
+        // K16 A-operand order of Aqk, so it is stored as is.
+        f32x4 aq[4], al[4];
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+            aq[I] = zero4();
+            al[I] = zero4();
+            if (I <= R) {
+#pragma unroll
+                for (int s = 0; s < NKS; ++s) {
+                    Q a[2];
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int c0 = 32 * s + 16 * hh + 4 * kg;
+                        Q raw = ld_q4<PK>(sKend + (16 * I + m) * LDK + c0);
+                        if (I != R - 1) {
+                            float x[4];
+                            unpack4<PK>(raw, x);
+                            const float4 sc = *reinterpret_cast<const float4 *>(&sPf[R][I][c0]);
+                            raw = pack4<PK>(x[0] * sc.x, x[1] * sc.y, x[2] * sc.z, x[3] * sc.w);
+                        }
+                        a[hh] = raw;
+                    }
+                    aq[I] = mma2<PK>(aq[I], a[0], a[1], fqb[2 * s], fqb[2 * s + 1]);
+                    al[I] = mma2<PK>(al[I], a[0], a[1], feb[2 * s], feb[2 * s + 1]);
+                }
+            }
+        }
+        if (wave_slow) {
+#pragma unroll
+            for (int I = 0; I < 4; ++I)
+                if (I == R) {
+                    aq[I] = dq;
+                    al[I] = dl;
+                }
+        }
+        // Causal masks; Aqk to the blob.
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int col = 16 * I + 4 * kg + i, row = 16 * R + m;
+                if (!(col <= row)) aq[I][i] = 0.f;
+                if (!(col < row)) al[I][i] = 0.f;
+            }
+            st_q4<PK>(ws + BL::AQ + k16_block(R, I, 64) + 4 * l, pack4<PK>(aq[I]));
+        }
+        __syncthreads();  // all reads of sKend done; its space becomes L
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+            *reinterpret_cast<float4 *>(&sL[(16 * R + m) * LDF + 16 * I + 4 * kg]) =
+                make_float4(al[I][0], al[I][1], al[I][2], al[I][3]);
+        __syncthreads();
+
+        // X = (I + L)^{-1} in fp32: diagonal 16x16 blocks by forward substitution
+        // (lane j = column j), strictly-upper blocks zero.
+        if (l < 16) {
+            const int j = l;
+            float x[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float acc = (i == j) ? 1.f : 0.f;
+#pragma unroll
+                for (int mm = 0; mm < i; ++mm) acc = fmaf(-sL[(16 * R + i) * LDF + 16 * R + mm], x[mm], acc);
+                x[i] = acc;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sX[(16 * R + i) * LDF + 16 * R + j] = x[i];
+        }
+        for (int I = R + 1; I < 4; ++I)
+            for (int e = l; e < 256; e += 64) sX[(16 * R + (e >> 4)) * LDF + 16 * I + (e & 15)] = 0.f;
+        __syncthreads();
+        // Off-diagonal blocks, one sub-diagonal at a time:
+        //   X_RI = -X_RR * sum_{J=I}^{R-1} L_RJ X_JI.
+        for (int d = 1; d <= 3; ++d) {
+            if (R < 4 - d) {
+                const int Rr = R + d, I = R;
+                f32x4 t = zero4();
+                for (int J = I; J < Rr; ++J)
+                    t = mm16_f32(t, sL + (16 * Rr) * LDF + 16 * J, LDF, sX + (16 * J) * LDF + 16 * I, LDF, l);
+                float *scr = sScr[R];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) scr[(4 * kg + i) * 16 + m] = t[i];
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                const f32x4 xr = mm16_f32(zero4(), sX + (16 * Rr) * LDF + 16 * Rr, LDF, scr, 16, l);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sX[(16 * Rr + 4 * kg + i) * LDF + 16 * I + m] = -xr[i];
+            }
+            __syncthreads();
+        }
+
+        // X to the blob (row block R).
+        Q xt[4];
+#pragma unroll
+        for (int J = 0; J < 4; ++J) {
+            const float4 xv = *reinterpret_cast<const float4 *>(&sX[(16 * R + m) * LDF + 16 * J + 4 * kg]);
+            xt[J] = pack4<PK>(xv.x, xv.y, xv.z, xv.w);
+            st_q4<PK>(ws + BL::X + k16_block(R, J, 64) + 4 * l, xt[J]);
+        }
+        // W^T(ct, R) = Ebar^T(ct, :) X^T(:, R): B operand X^T(J, R) is row 16R+m of
+        // X, i.e. xt[J]; result lane (n, kg) holds W[16R+n][16ct+4kg+i] -- the K16
+        // A-operand order of W.  Stored negated.
+#pragma unroll
+        for (int ct = 0; ct < NKT; ++ct) {
+            f32x4 acc = zero4();
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                if (2 * s <= R)
+                    acc = mma2<PK>(acc, ld_q4<PK>(sEt + k16_block(ct, 2 * s, 64) + 4 * l),
+                                   ld_q4<PK>(sEt + k16_block(ct, 2 * s + 1, 64) + 4 * l), xt[2 * s],
+                                   xt[2 * s + 1]);
+            }
+            st_q4<PK>(ws + BL::WN + k16_block(R, ct, KP) + 4 * l,
+                      pack4<PK>(-acc[0], -acc[1], -acc[2], -acc[3]));
+        }
+        it = nit;
+        __syncthreads();  // sX / smem1 are read up to here; the next item stages its rows there
     }
 }
 
@@ -848,8 +926,27 @@ template <PrecKind PK, int KP, typename TI, typename TG>
 hipError_t launch_prep(const ChunkParams &p, int total_chunks, hipStream_t stream)
 {
     if (total_chunks == 0) return hipSuccess;
-    hipLaunchKernelGGL((chunk_prep_kernel<PK, KP, TI, TG>), dim3(total_chunks, p.H), dim3(256), 0,
-                       stream, p);
+    const auto kern = chunk_prep_kernel<PK, KP, TI, TG>;
+    // One resident wave of workgroups (occupancy x CUs of the current device,
+    // looked up once per device), each walking items with a stride of the grid.
+    static int resident[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    int slots = dev < 64 ? resident[dev] : 0;
+    if (slots == 0) {
+        int cus = 0, per_cu = 0;
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0);
+        if (e != hipSuccess) return e;
+        slots = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+        if (dev < 64) resident[dev] = slots;
+    }
+    const int64_t items = static_cast<int64_t>(total_chunks) * p.H;
+    if (items > (int64_t{1} << 30)) return hipErrorInvalidValue;  // item indices stay in int
+    const int grid = static_cast<int>(items < slots ? items : slots);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, stream, p, static_cast<int>(items));
     return hipGetLastError();
 }
 
