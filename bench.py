@@ -10,6 +10,10 @@ Also measured: the single-token decode step, N=64
 sequences x 16 heads, fp32 state [64,16,128,128] updated in place, 1024
 consecutive steps captured in one HIP graph.
 
+Also measured: a 0.68 B-parameter hybrid decoder (18 gdn2
++ 6 attention layers) prefilling 4 x 2048 tokens and decoding 256 greedily, with
+the decode step replayed as one HIP graph.
+
 Prints one JSON line: value = prefill tokens/s, with the roofline of the
 prefill kernels (HBM-bound), the decode figures, and the CPU baseline (the C
 restatement of the reference recurrence, oracle/gdn2_cpu.c, timed on this
@@ -381,6 +385,64 @@ def bench_prologue(torch, dev, reps=20):
     }
 
 
+def bench_e2e(torch, dev, n_prompt=2048, n_new=256, batch=4):
+    """Config 3 end to end: the hybrid decoder host (qwendopamine_amd.hybrid, 24 layers,
+    18 gdn2 + 6 attention, about 0.68 B parameters, random init, bf16) prefills
+    `batch` random prompts of `n_prompt` tokens, then decodes `n_new` tokens greedily.
+
+    * Prefill: eager (the gdn2 layers run the chunk kernels).
+    * Decode: the step is captured once as a HIP graph and replayed (the gdn2 layers run
+      the decode kernel).
+    * The first decode step (eager, before capture) is timed separately.
+    * The reported rates count prompt tokens for prefill and generated tokens for decode;
+      e2e counts both over the total time.
+    """
+    from qwendopamine_amd.hybrid import GreedyDecoder, HybridConfig, HybridDecoder
+
+    torch.manual_seed(3)
+    cfg = HybridConfig.c3()
+    model = HybridDecoder(cfg).to(dev, torch.bfloat16).eval()
+    gen = torch.Generator(device=dev).manual_seed(3)
+    prompt = torch.randint(0, cfg.vocab_size, (batch, n_prompt), generator=gen, device=dev)
+    dec = GreedyDecoder(model, use_graph=True)
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    # Warm-up run (library handles, kernel selection, graph capture), then the timed run.
+    dec.generate(prompt[:, :256], 4)
+    torch.cuda.synchronize(dev)
+    e = [ev() for _ in range(4)]
+    t0 = time.perf_counter()
+    e[0].record()
+    dec.prefill(prompt, n_new)
+    e[1].record()
+    dec.step()  # eager first step + capture
+    e[2].record()
+    for _ in range(n_new - 2):
+        dec.step()
+    e[3].record()
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    t_pre, t_first, t_dec = (e[i].elapsed_time(e[i + 1]) for i in range(3))
+    n_rep = n_new - 2
+    total_ms = t_pre + t_first + t_dec
+    return {
+        "config": {"workload": "C3 hybrid decoder, prefill B4 x 2048 then greedy decode 256",
+                   "layers": "24 (18 gdn2 + 6 attention)", "hidden": cfg.n_embd,
+                   "heads": f"{cfg.n_head} x {cfg.head_size}", "ffn": cfg.intermediate_size,
+                   "vocab": cfg.vocab_size, "params": sum(p.numel() for p in model.parameters()),
+                   "dtype": "bf16", "data": "random init, random token ids"},
+        "prefill_ms": round(t_pre, 3),
+        "prefill_tokens_per_s": round(batch * n_prompt / (t_pre * 1e-3), 1),
+        "decode_first_step_ms": round(t_first, 3),
+        "decode_ms_per_step": round(t_dec / n_rep, 4),
+        "decode_tokens_per_s": round(batch * n_rep / (t_dec * 1e-3), 1),
+        "e2e_tokens_per_s": round(batch * (n_prompt + n_new) / (total_ms * 1e-3), 1),
+        "wall_s": round(wall, 3),
+    }
+
+
 def traffic_probe(torch, nat, dev):
     """Short run for the rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE): first a
     256 MiB device-to-device copy whose bytes are known, which calibrates the
@@ -451,6 +513,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--no-prologue", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the config-3 end-to-end decoder run")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="short run for rocprofv3 counter passes; prints no JSON line")
     args = ap.parse_args()
@@ -523,6 +586,8 @@ def main() -> int:
         out["train"] = bench_train(torch, nat, dev, max(2, args.steps // 2), 1)
     if not args.no_prologue:
         out["prologue_epilogue"] = bench_prologue(torch, dev)
+    if not args.no_e2e:
+        out["e2e_c3"] = bench_e2e(torch, dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch, res["inputs"])
     print(json.dumps(out), flush=True)
