@@ -29,6 +29,7 @@ FLAG_LOWER_BOUND = 4
 FLAG_SAVE_FOR_BWD = 8
 FLAG_TRANSPOSE_STATE = 16
 FLAG_INPLACE_FINAL_STATE = 32
+FLAG_SIGMOID_BW = 64
 
 OK = 0
 ERR_INVALID = -1

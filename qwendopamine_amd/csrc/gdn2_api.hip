@@ -91,7 +91,7 @@ int gdn2_recurrent_fwd_ex(const void *q, const void *k, const void *v, const voi
     if (B < 0 || T < 0 || H <= 0 || HV <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
     if (HV % H != 0) return GDN2_ERR_INVALID;
     if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND |
-                  GDN2_FLAG_TRANSPOSE_STATE | GDN2_FLAG_INPLACE_FINAL_STATE))
+                  GDN2_FLAG_TRANSPOSE_STATE | GDN2_FLAG_INPLACE_FINAL_STATE | GDN2_FLAG_SIGMOID_BW))
         return GDN2_ERR_INVALID;
     if ((flags & GDN2_FLAG_LOWER_BOUND) && !(flags & GDN2_FLAG_GATE_IN_KERNEL))
         return GDN2_ERR_INVALID;

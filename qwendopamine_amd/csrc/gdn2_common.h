@@ -84,6 +84,9 @@ __device__ __forceinline__ float softplus_f(float x)
     return x > 20.0f ? x : log1pf(expf(x));
 }
 
+// torch.sigmoid in fp32 (GDN2_FLAG_SIGMOID_BW): 1 / (1 + e^-x), 0 for x -> -inf.
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
 // Decay activation applied in-kernel when GDN2_FLAG_GATE_IN_KERNEL is set:
 //   g = -exp(A_log[h]) * softplus(g_raw + dt_bias[h, d])         (default)
 //   g = lower_bound * sigmoid(exp(A_log[h]) * (g_raw + dt_bias))  (lower-bound form)

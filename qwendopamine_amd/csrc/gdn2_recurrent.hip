@@ -278,6 +278,7 @@ __global__ __launch_bounds__(256) void recurrent_fwd_kernel(RecurrentParams p)
     const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
     const bool gate = (p.flags & GDN2_FLAG_GATE_IN_KERNEL) != 0;
     const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
+    const bool sig_bw = (p.flags & GDN2_FLAG_SIGMOID_BW) != 0;
 
     using TS = TransposedSlab<NR, TPR>;
     extern __shared__ float s_tile[];  // TS::TILE_FLOATS floats, transposed layout only
@@ -318,6 +319,10 @@ __global__ __launch_bounds__(256) void recurrent_fwd_kernel(RecurrentParams p)
         if (col_ok) {
             vv = vec4io<TI>::ld(v, vw_off + col);
             ww = vec4io<TI>::ld(w, vw_off + col);
+        }
+        if (sig_bw) {
+            bv = sigmoid_f(bv);
+            ww = make_float4(sigmoid_f(ww.x), sigmoid_f(ww.y), sigmoid_f(ww.z), sigmoid_f(ww.w));
         }
         float rq = wave_sum(qv * qv), rk = wave_sum(kv * kv), rqk = wave_sum(qv * kv);
         if (lane == 0) {
@@ -439,6 +444,7 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
     const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
     const bool gate = (p.flags & GDN2_FLAG_GATE_IN_KERNEL) != 0;
     const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
+    const bool sig_bw = (p.flags & GDN2_FLAG_SIGMOID_BW) != 0;
 
     float4 st[SLABS][NR];
     const int slab0 = blockIdx.x * SLABS;
@@ -470,7 +476,11 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
             bv = io<TI>::ld(b, gb_off + tid);
         }
         const float4 vv = vec4io<TI>::ld(v, vw_off + col);
-        const float4 ww = vec4io<TI>::ld(w, vw_off + col);
+        float4 ww = vec4io<TI>::ld(w, vw_off + col);
+        if (sig_bw) {
+            bv = sigmoid_f(bv);
+            ww = make_float4(sigmoid_f(ww.x), sigmoid_f(ww.y), sigmoid_f(ww.z), sigmoid_f(ww.w));
+        }
         const float rq = wave_sum(qv * qv), rk = wave_sum(kv * kv), rqk = wave_sum(qv * kv);
         if (lane == 0) {
             s_part[wid][0] = rq;

@@ -383,6 +383,22 @@ class GatedDeltaNet2(nn.Module):
                     lc.conv_state = conv_state
 
     # ---------------------------------------------------------------- forward
+    def _gate_params(self, rep: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """float32 ``A_log [HV]`` and ``dt_bias [HV * d_k]`` for the in-kernel gate, each
+        key head's parameters repeated for its ``rep`` value heads.  Cached until either
+        parameter changes, so a decode step launches no conversion kernels."""
+        key = (self.A_log.data_ptr(), self.A_log._version, self.dt_bias.data_ptr(), self.dt_bias._version,
+               self.A_log.dtype, self.dt_bias.dtype, rep)
+        cached = getattr(self, "_gate_cache", None)
+        if cached is None or cached[0] != key:
+            a = self.A_log.detach().float()
+            d = self.dt_bias.detach().float().view(self.num_heads, self.head_k_dim)
+            if rep > 1:
+                a, d = a.repeat_interleave(rep), d.repeat_interleave(rep, dim=0)
+            cached = (key, a.contiguous(), d.reshape(-1).contiguous())
+            self._gate_cache = cached
+        return cached[1], cached[2]
+
     def _algorithm(self, mode: str, backend: str, needs_grad: bool) -> str:
         if backend in ("torch-chunk", "compiled"):
             algo = "chunk"
@@ -445,18 +461,28 @@ class GatedDeltaNet2(nn.Module):
         else:
             q, k, v = F.silu(self.q_proj(x)), F.silu(self.k_proj(x)), F.silu(self.v_proj(x))
 
-        # Decay g = -exp(A_log) * softplus(f_proj(x) + dt_bias), always in fp32.
-        A = self.A_log.float().exp().repeat_interleave(self.head_k_dim)
-        g = -A * F.softplus(self.f_proj(x).float() + self.dt_bias)
-        if not self.fp32_decay:
-            g = g.to(x.dtype)
-        b = self.b_proj(x).sigmoid()
-        w = self.w_proj(x).sigmoid()
+        # Decay g = -exp(A_log) * softplus(f_proj(x) + dt_bias), always in fp32;
+        # b = sigmoid(b_proj(x)), w = sigmoid(w_proj(x)) (gdn2.py:840-866).  In
+        # inference these activations run inside the kernels on the raw
+        # projections (same fp32 formula for g; b and w are not rounded to the
+        # input dtype in between).
+        fuse = (_inference(x, self.A_log, self.dt_bias, self.f_proj[1].weight, self.b_proj.weight,
+                           self.w_proj.weight)
+                and self.fp32_decay and not self.allow_neg_eigval)
+        if fuse:
+            g, b, w = self.f_proj(x), self.b_proj(x), self.w_proj(x)
+        else:
+            A = self.A_log.float().exp().repeat_interleave(self.head_k_dim)
+            g = -A * F.softplus(self.f_proj(x).float() + self.dt_bias)
+            if not self.fp32_decay:
+                g = g.to(x.dtype)
+            b = self.b_proj(x).sigmoid()
+            w = self.w_proj(x).sigmoid()
 
         q, k, g, b = (_split_heads(t, self.head_k_dim) for t in (q, k, g, b))
         v, w = _split_heads(v, self.head_v_dim), _split_heads(w, self.head_v_dim)
-        if self.num_v_heads > self.num_heads:
-            rep = self.num_v_heads // self.num_heads
+        rep = self.num_v_heads // self.num_heads
+        if rep > 1:
             q, k, g, b = (t.repeat_interleave(rep, dim=-2) for t in (q, k, g, b))
         if self.allow_neg_eigval:
             b = b * 2.0
@@ -466,16 +492,26 @@ class GatedDeltaNet2(nn.Module):
         algo = self._algorithm(mode, backend, needs_grad)
         h0 = None if recurrent_state is None else recurrent_state.float()
         dt = q.dtype
+        gate_kw: dict = {}
+        if fuse:
+            A_log, dt_bias = self._gate_params(rep)
+            gate_kw = dict(use_gate_in_kernel=True, A_log=A_log, dt_bias=dt_bias)
+            if algo == "chunk":
+                # The chunk kernels take activated b and w (one elementwise pass
+                # each, small next to a prefill).
+                b, w = b.sigmoid(), w.sigmoid()
+            else:
+                gate_kw["bw_logits"] = True
         b, w, v, k = b.to(dt), w.to(dt), v.to(dt), k.to(dt)
         if algo == "chunk":
             o, recurrent_state = ops.chunk_gdn2(
                 q, k, v, g, b, w, initial_state=h0, output_final_state=want_state,
-                use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens,
+                use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens, **gate_kw,
             )
         else:
             o, recurrent_state = ops.fused_recurrent_gdn2(
                 q, k, v, g, b, w, initial_state=h0, output_final_state=want_state,
-                use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens,
+                use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens, **gate_kw,
             )
 
         if use_cache or past_key_values is not None:

@@ -136,9 +136,13 @@ def fused_recurrent_gdn2_fwd(
     lower_bound: float | None = None,
     out: torch.Tensor | None = None,
     transpose_state_layout: bool = False,
+    bw_logits: bool = False,
     **kwargs: Any,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """Launch the token-serial HIP kernel (reference ``fused_recurrent_gdn2.py:344-458``).
+
+    ``bw_logits`` (an extension of this backend) passes ``b`` and ``w`` as the
+    pre-activation logits; the kernel applies the sigmoid in fp32.
 
     Final state (as the reference resolves it, ``:395-404``):
 
@@ -241,6 +245,8 @@ def fused_recurrent_gdn2_fwd(
         flags |= nat.FLAG_TRANSPOSE_STATE
     if inplace_final_state:
         flags |= nat.FLAG_INPLACE_FINAL_STATE
+    if bw_logits:
+        flags |= nat.FLAG_SIGMOID_BW
     lib = nat.load()
     st = lib.gdn2_recurrent_fwd_ex(
         nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(g), nat.ptr(b), nat.ptr(w),
@@ -275,6 +281,7 @@ def fused_recurrent_gdn2(
     lower_bound: float | None = None,
     cu_seqlens: torch.LongTensor | None = None,
     transpose_state_layout: bool = False,
+    bw_logits: bool = False,
     **kwargs: Any,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """Token-by-token gdn2 forward, inference only (reference ``fused_recurrent_gdn2.py:461-555``).
@@ -304,7 +311,7 @@ def fused_recurrent_gdn2(
         output_final_state=output_final_state,
         use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
         use_gate_in_kernel=use_gate_in_kernel, lower_bound=lower_bound,
-        cu_seqlens=cu_seqlens, transpose_state_layout=transpose_state_layout,
+        cu_seqlens=cu_seqlens, transpose_state_layout=transpose_state_layout, bw_logits=bw_logits,
     )
 
 

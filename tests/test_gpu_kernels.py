@@ -115,6 +115,37 @@ def test_recurrent_gate_in_kernel(gpu_device):
     assert rel_l2(o, o_ref) <= 1e-4 and rel_l2(ht, s_ref) <= 1e-4
 
 
+@pytest.mark.parametrize("T,K,V", [(9, 32, 32), (1, 128, 128)])
+def test_recurrent_sigmoid_bw_logits(gpu_device, T, K, V):
+    """b and w passed as logits (GDN2_FLAG_SIGMOID_BW), with the in-kernel gate: the
+    module's fused decode path. T = 1 with K = V = 128 runs the decode-step kernel,
+    the other case the generic one. The oracle gets sigmoid(b), sigmoid(w) in float64."""
+    from qwendopamine_amd.ops import fused_recurrent_gdn2
+
+    print(f"[case] recurrent sigmoid b/w T={T} K={K} V={V}", flush=True)
+    B, H = 3, 2
+    inp = rand_inputs(B, T, H, K, V, seed=11)
+    rng = np.random.default_rng(12)
+    bl, wl = rng.standard_normal((B, T, H, K)) * 2, rng.standard_normal((B, T, H, V)) * 2
+    graw = rng.standard_normal((B, T, H, K))
+    A_log = np.log(rng.uniform(1, 16, H))
+    dt_bias = rng.standard_normal(H * K) * 0.5
+    g = -np.exp(A_log)[:, None] * np.logaddexp(0.0, graw + dt_bias.reshape(H, K))
+    inp.update(b=bl, w=wl, g=graw)
+    t, r = to_device(inp, gpu_device, torch.float32)
+    o, ht = fused_recurrent_gdn2(
+        t["q"], t["k"], t["v"], t["g"], t["b"], t["w"],
+        A_log=torch.tensor(A_log, dtype=torch.float32, device=gpu_device),
+        dt_bias=torch.tensor(dt_bias, dtype=torch.float32, device=gpu_device),
+        initial_state=t["h0"], output_final_state=True, use_qk_l2norm_in_kernel=True,
+        use_gate_in_kernel=True, bw_logits=True,
+    )
+    torch.cuda.synchronize()
+    sig = lambda x: 1.0 / (1.0 + np.exp(-x))  # noqa: E731
+    o_ref, s_ref = orc.recurrent_fwd(r["q"], r["k"], r["v"], g, sig(r["b"]), sig(r["w"]), r["h0"])
+    assert rel_l2(o, o_ref) <= 1e-4 and rel_l2(ht, s_ref) <= 1e-4
+
+
 def _chunk(dev, dtype, B, T, H, K, V, seed=0, decay="paper", h0_std=0.1, g_dtype=torch.float32):
     from qwendopamine_amd.ops import chunk_gdn2
 
