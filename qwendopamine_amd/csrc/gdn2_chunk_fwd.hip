@@ -50,6 +50,71 @@ namespace gdn2 {
 
 namespace {
 
+// Four consecutive input values kept as the input dtype's bits (two registers
+// for 16-bit inputs, half of what fp32 values take) and widened to fp32 where
+// they are used.
+template <typename T>
+struct Raw4 {
+    static constexpr int W = sizeof(T) == 2 ? 2 : 4;
+    uint32_t u[W];
+    __device__ __forceinline__ void zero()
+    {
+#pragma unroll
+        for (int w = 0; w < W; ++w) u[w] = 0u;
+    }
+    // p: 4 values, 8-byte (16-bit T) or 16-byte (fp32) aligned.
+    __device__ __forceinline__ void load(const T *p)
+    {
+        if constexpr (W == 2) {
+            const uint2 a = *reinterpret_cast<const uint2 *>(p);
+            u[0] = a.x;
+            u[1] = a.y;
+        } else {
+            const uint4 a = *reinterpret_cast<const uint4 *>(p);
+            u[0] = a.x;
+            u[1] = a.y;
+            u[2] = a.z;
+            u[3] = a.w;
+        }
+    }
+    // Channels c0..c0+3 of the row at element off; zero outside [0, K) or when !ok.
+    __device__ __forceinline__ void load_checked(const T *base, int64_t off, int c0, int K, bool ok, int vec_ok)
+    {
+        if (ok && vec_ok && c0 + 4 <= K) {
+            load(base + off + c0);
+            return;
+        }
+        zero();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (!(ok && c0 + i < K)) continue;
+            if constexpr (W == 2) {
+                const uint32_t bits = reinterpret_cast<const uint16_t *>(base)[off + c0 + i];
+                u[i >> 1] |= bits << (16 * (i & 1));
+            } else {
+                u[i] = reinterpret_cast<const uint32_t *>(base)[off + c0 + i];
+            }
+        }
+    }
+    __device__ __forceinline__ void unpack(float (&x)[4]) const
+    {
+        if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(u[i]);
+        } else if constexpr (std::is_same<T, bf16_t>::value) {
+            x[0] = __uint_as_float(u[0] << 16);
+            x[1] = __uint_as_float(u[0] & 0xffff0000u);
+            x[2] = __uint_as_float(u[1] << 16);
+            x[3] = __uint_as_float(u[1] & 0xffff0000u);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                x[i] = static_cast<float>(
+                    __builtin_bit_cast(_Float16, static_cast<uint16_t>(u[i >> 1] >> (16 * (i & 1)))));
+        }
+    }
+};
+
 // Rows 16R..16R+15 of one [.., K] input (K == KP) for the calling wave:
 // 16-byte loads that cover whole rows (lane l: row rr = j*RPI + l/LPR, bytes
 // 16*(l%LPR) of it), so every load instruction reads complete 128-byte lines.
@@ -105,6 +170,24 @@ struct RowLoad {
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }
+    // The same, keeping the input dtype's bits.
+    __device__ __forceinline__ void land_raw(unsigned char *stg, int l, int m, int kg, int nvalid,
+                                             Raw4<T> (&out)[KP / 16])
+    {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int rr = j * RPI + l / LPR;
+            *reinterpret_cast<u32x4 *>(stg + rr * RS + 16 * (l % LPR)) =
+                rr < nvalid ? v[j] : u32x4{0, 0, 0, 0};
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        const T *row = reinterpret_cast<const T *>(stg + m * RS);
+#pragma unroll
+        for (int kt = 0; kt < KP / 16; ++kt) out[kt].load(row + 16 * kt + 4 * kg);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    }
 };
 
 // One prep work item: chunk gc (global index over all sequences) of head h;
@@ -134,15 +217,16 @@ __device__ __forceinline__ PrepItem prep_item(const ChunkParams &p, int item)
 // Prep: a persistent grid of workgroups (4 waves each) walking the items
 // blockIdx.x, blockIdx.x + gridDim.x, ...  Wave R owns token rows
 // 16R..16R+15; lane (m, kg) holds row 16R+m and channels 16kt + 4kg + i.
-// When K == KP the next item's input rows are requested as soon as the
-// current item's inputs are dead (after the factors), so their HBM latency
-// overlaps the products and the inverse.
+//
+// Sized for three workgroups per CU with 16-bit storage: 52 KB of LDS (the
+// block vectors live in the X matrix's space until X is formed, and the
+// off-diagonal inverse steps use L's unused upper blocks as scratch) and at
+// most 168 registers (q, k, b stay in their 16-bit input form until the
+// factors).  fp32 storage at KP = 128 fits one workgroup per CU.
 // ---------------------------------------------------------------------------
-// Two workgroups per CU (the LDS limit for 16-bit storage) need <= 256
-// registers; fp32 storage at KP = 128 fits one workgroup per CU in LDS.
 template <PrecKind PK, int KP, typename TI, typename TG>
 __global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(PK == PrecKind::F32 && KP == 128 ? 1 : 2))) void
+__attribute__((amdgpu_waves_per_eu(PK == PrecKind::F32 && KP == 128 ? 1 : 3))) void
 chunk_prep_kernel(ChunkParams p, int items)
 {
     using P = Prec<PK>;
@@ -155,23 +239,24 @@ chunk_prep_kernel(ChunkParams p, int items)
     constexpr int LDF = 64 + 4;  // fp32 [64][64]
     constexpr int SZK = 64 * LDK * static_cast<int>(sizeof(st));
     constexpr int SZ1 = SZK > 64 * LDF * 4 ? SZK : 64 * LDF * 4;
-    __shared__ __align__(16) unsigned char smem1[SZ1];   // Kend, then L (fp32)
-    __shared__ __align__(16) st sEt[NKT * 4 * 256];      // Ebar^T, K16 blocks (channel, token)
-    __shared__ __align__(16) float sX[64 * LDF];
-    __shared__ __align__(16) float sT[4][KP];            // in-block decay totals (log2)
-    __shared__ __align__(16) float sEr[4][KP];           // 2^(decay before block)
-    __shared__ __align__(16) float sEa[4][KP];           // 2^(decay after block)
-    __shared__ __align__(16) float sPf[4][4][KP];        // key scale of block pair (R, I)
-    __shared__ __align__(16) float sScr[4][256];
+    __shared__ __align__(16) unsigned char smem1[SZ1];  // Kend, then L (fp32)
+    __shared__ __align__(16) st sEt[NKT * 4 * 256];     // Ebar^T, K16 blocks (channel, token)
+    __shared__ __align__(16) float sX[64 * LDF];        // row staging, block vectors, then X
+    __shared__ __align__(16) float sT[4][KP];           // in-block decay totals (log2)
     st *sKend = reinterpret_cast<st *>(smem1);
     float *sL = reinterpret_cast<float *>(smem1);
+    // Block vectors, in sX until the inverse writes X there.
+    float(*sEr)[KP] = reinterpret_cast<float(*)[KP]>(sX);              // 2^(decay before block)
+    float(*sEa)[KP] = reinterpret_cast<float(*)[KP]>(sX + 4 * KP);     // 2^(decay after block)
+    float(*sPf)[4][KP] = reinterpret_cast<float(*)[4][KP]>(sX + 8 * KP);  // key scale of block pair (R, I)
+    static_assert(24 * KP <= 64 * LDF, "block vectors must fit in sX");
     static_assert(sizeof(sX) >= 2 * 16 * (KP * 4 + 16) && sizeof(smem1) >= 2 * 16 * (KP * 4 + 16),
                   "row staging must fit in sX and smem1");
 
     const int lane = threadIdx.x & 63;
     const int R0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, uniform
     const int H = p.H, K = p.K;
-    const bool rows_whole = K == KP;  // whole-row 16-byte loads, prefetched one item ahead
+    const bool rows_whole = K == KP;  // whole-row 16-byte loads through LDS
     const int64_t stride = static_cast<int64_t>(H) * K;
 
     const TI *q = static_cast<const TI *>(p.q);
@@ -184,15 +269,7 @@ chunk_prep_kernel(ChunkParams p, int items)
     // barrier) until the first barrier of the next.
     unsigned char *stg = R0 < 2 ? reinterpret_cast<unsigned char *>(sX) + R0 * (16 * (KP * 4 + 16))
                                 : smem1 + (R0 - 2) * (16 * (KP * 4 + 16));
-    RowLoad<TI, KP> lq, lk, lb;
-    RowLoad<TG, KP> lg;
     PrepItem it = prep_item(p, blockIdx.x);
-    if (rows_whole) {
-        lq.issue(q, it.chunk0, stride, 16 * R0, it.lc, lane);
-        lk.issue(k, it.chunk0, stride, 16 * R0, it.lc, lane);
-        lb.issue(b, it.chunk0, stride, 16 * R0, it.lc, lane);
-        lg.issue(g, it.chunk0, stride, 16 * R0, it.lc, lane);
-    }
 
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
         // The lane and wave indices are made opaque per item so that the
@@ -207,34 +284,45 @@ chunk_prep_kernel(ChunkParams p, int items)
         const bool row_ok = r < lc;
         const int64_t roff = it.chunk0 + r * stride;
 
-        float qv[NKT][4], kv[NKT][4], ev[NKT][4], gv[NKT][4];
+        Raw4<TI> qr[NKT], kr[NKT], br[NKT];
+        float gv[NKT][4];
         if (rows_whole) {
+            RowLoad<TI, KP> lq, lk, lb;
+            RowLoad<TG, KP> lg;
+            lq.issue(q, it.chunk0, stride, 16 * R, lc, l);
+            lk.issue(k, it.chunk0, stride, 16 * R, lc, l);
+            lb.issue(b, it.chunk0, stride, 16 * R, lc, l);
+            lg.issue(g, it.chunk0, stride, 16 * R, lc, l);
             const int nvalid = lc - 16 * R;
-            lq.land(stg, l, m, kg, nvalid, qv);
-            lk.land(stg, l, m, kg, nvalid, kv);
-            lb.land(stg, l, m, kg, nvalid, ev);
+            lq.land_raw(stg, l, m, kg, nvalid, qr);
+            lk.land_raw(stg, l, m, kg, nvalid, kr);
+            lb.land_raw(stg, l, m, kg, nvalid, br);
             lg.land(stg, l, m, kg, nvalid, gv);
         } else {
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) {
                 const int c0 = 16 * kt + 4 * kg;
-                load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, qv[kt]);
-                load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, kv[kt]);
-                load4<TI>(b, roff, c0, K, row_ok, p.vec_ok, ev[kt]);
+                qr[kt].load_checked(q, roff, c0, K, row_ok, p.vec_ok);
+                kr[kt].load_checked(k, roff, c0, K, row_ok, p.vec_ok);
+                br[kt].load_checked(b, roff, c0, K, row_ok, p.vec_ok);
                 load4<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv[kt]);
             }
         }
 
-        // Fused prologue: L2 norm (F.normalize semantics), scale, erase vector,
-        // optional gate activation, decay in log2 units.
+        // Fused prologue: L2 norms (F.normalize semantics) and scale, applied
+        // in the factors below; optional gate activation; decay in log2 units.
         float sq = 0.f, sk = 0.f;
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt)
+        for (int kt = 0; kt < NKT; ++kt) {
+            float xq[4], xk[4];
+            qr[kt].unpack(xq);
+            kr[kt].unpack(xk);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                sq = fmaf(qv[kt][i], qv[kt][i], sq);
-                sk = fmaf(kv[kt][i], kv[kt][i], sk);
+                sq = fmaf(xq[i], xq[i], sq);
+                sk = fmaf(xk[i], xk[i], sk);
             }
+        }
         sq += __shfl_xor(sq, 16, 64);
         sq += __shfl_xor(sq, 32, 64);
         sk += __shfl_xor(sk, 16, 64);
@@ -243,6 +331,18 @@ chunk_prep_kernel(ChunkParams p, int items)
         const float invq = l2 ? 1.0f / fmaxf(sqrtf(sq), 1e-6f) : 1.0f;
         const float invk = l2 ? 1.0f / fmaxf(sqrtf(sk), 1e-6f) : 1.0f;
         const float qmul = invq * p.scale;
+        // Normalised q (scaled), k and the erase vector e = b * k of tile kt.
+        auto qke = [&](int kt, float (&xq)[4], float (&xk)[4], float (&xe)[4]) __attribute__((always_inline)) {
+            qr[kt].unpack(xq);
+            kr[kt].unpack(xk);
+            br[kt].unpack(xe);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xq[i] *= qmul;
+                xk[i] *= invk;
+                xe[i] *= xk[i];
+            }
+        };
         if (p.flags & GDN2_FLAG_GATE_IN_KERNEL) {
             const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
             const float a_log = p.A_log[h];
@@ -260,12 +360,7 @@ chunk_prep_kernel(ChunkParams p, int items)
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                qv[kt][i] *= qmul;
-                kv[kt][i] *= invk;
-                ev[kt][i] *= kv[kt][i];
-                gv[kt][i] = row16_scan(gv[kt][i] * kLog2e);  // G (log2) relative to block start
-            }
+            for (int i = 0; i < 4; ++i) gv[kt][i] = row16_scan(gv[kt][i] * kLog2e);  // G (log2) from block start
         bool wide = false;
         if (m == 15) {
 #pragma unroll
@@ -277,31 +372,40 @@ chunk_prep_kernel(ChunkParams p, int items)
             }
         }
         // A diagonal block whose decay span is too wide for the factored form is
-        // summed exactly, pair by pair (row m, column j of block R), here while
-        // the fp32 inputs are still live.
+        // summed exactly, pair by pair (row m, column j of block R).
         const bool wave_slow = __ballot(wide) != 0;
         f32x4 dq = zero4(), dl = zero4();
         if (wave_slow) {
+            // Channel tiles outer, so that one tile's normalised values are
+            // live at a time; each column j still sums over (kt, i) in order.
+            float accq[16], accl[16];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                float accq = 0.f, accl = 0.f;
+            for (int j = 0; j < 16; ++j) accq[j] = accl[j] = 0.f;
 #pragma unroll
-                for (int kt = 0; kt < NKT; ++kt)
+            for (int kt = 0; kt < NKT; ++kt) {
+                float xq[4], xk[4], xe[4];
+                qke(kt, xq, xk, xe);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float kj = __shfl(kv[kt][i], 16 * kg + j, 64);
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const float kj = __shfl(xk[i], 16 * kg + j, 64);
                         const float Gj = __shfl(gv[kt][i], 16 * kg + j, 64);
                         const float ex = (j <= m) ? fexp2(gv[kt][i] - Gj) : 0.f;
-                        accq = fmaf(qv[kt][i] * kj, ex, accq);
-                        accl = fmaf(ev[kt][i] * kj, ex, accl);
+                        accq[j] = fmaf(xq[i] * kj, ex, accq[j]);
+                        accl[j] = fmaf(xe[i] * kj, ex, accl[j]);
                     }
-                accq += __shfl_xor(accq, 16, 64);
-                accq += __shfl_xor(accq, 32, 64);
-                accl += __shfl_xor(accl, 16, 64);
-                accl += __shfl_xor(accl, 32, 64);
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                float aq_ = accq[j], al_ = accl[j];
+                aq_ += __shfl_xor(aq_, 16, 64);
+                aq_ += __shfl_xor(aq_, 32, 64);
+                al_ += __shfl_xor(al_, 16, 64);
+                al_ += __shfl_xor(al_, 32, 64);
                 if (kg == (j >> 2)) {
-                    dq[j & 3] = accq;
-                    dl[j & 3] = accl;
+                    dq[j & 3] = aq_;
+                    dl[j & 3] = al_;
                 }
             }
         }
@@ -350,14 +454,16 @@ chunk_prep_kernel(ChunkParams p, int items)
             const float erv[4] = {er.x, er.y, er.z, er.w};
             const float eav[4] = {ea.x, ea.y, ea.z, ea.w};
             const float trv[4] = {tr.x, tr.y, tr.z, tr.w};
+            float xq[4], xk[4], xe[4];
+            qke(kt, xq, xk, xe);
             float qb[4], eb[4], ke[4], qbar[4], ebar[4], ktil[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float G = gv[kt][i];
                 const float e1 = fexp2(G), e2 = fexp2(trv[i] - G);
-                qb[i] = qv[kt][i] * e1;
-                eb[i] = ev[kt][i] * e1;
-                ke[i] = kv[kt][i] * e2;
+                qb[i] = xq[i] * e1;
+                eb[i] = xe[i] * e1;
+                ke[i] = xk[i] * e2;
                 qbar[i] = qb[i] * erv[i];
                 ebar[i] = eb[i] * erv[i];
                 ktil[i] = ke[i] * eav[i];
@@ -371,22 +477,6 @@ chunk_prep_kernel(ChunkParams p, int items)
             st_q4<PK>(ws + BL::KT + k16_block(kt, R, 64) + 4 * l, pack4<PK>(dk));
             const f32x4 de = mma1<PK>(zero4(), pack4<PK>(ebar[0], ebar[1], ebar[2], ebar[3]), ident);
             st_q4<PK>(sEt + k16_block(kt, R, 64) + 4 * l, pack4<PK>(de));
-        }
-        // The inputs of this item are dead: request the next item's rows.
-        const int next = item + gridDim.x;
-        const PrepItem nit = prep_item(p, next < items ? next : item);
-        if (rows_whole && next < items) {
-            lq.issue(q, nit.chunk0, stride, 16 * R, nit.lc, l);
-            lk.issue(k, nit.chunk0, stride, 16 * R, nit.lc, l);
-            lb.issue(b, nit.chunk0, stride, 16 * R, nit.lc, l);
-            lg.issue(g, nit.chunk0, stride, 16 * R, nit.lc, l);
-        } else {
-            // Defined on both paths: otherwise the landed rows of this item
-            // would stay live (as the merge's other input) through the item.
-            lq.clear();
-            lk.clear();
-            lb.clear();
-            lg.clear();
         }
         __syncthreads();
 
@@ -440,10 +530,13 @@ chunk_prep_kernel(ChunkParams p, int items)
             st_q4<PK>(ws + BL::AQ + k16_block(R, I, 64) + 4 * l, pack4<PK>(aq[I]));
         }
         __syncthreads();  // all reads of sKend done; its space becomes L
+        // Blocks I <= R only: the upper blocks are never read as L and serve as
+        // scratch below.
 #pragma unroll
         for (int I = 0; I < 4; ++I)
-            *reinterpret_cast<float4 *>(&sL[(16 * R + m) * LDF + 16 * I + 4 * kg]) =
-                make_float4(al[I][0], al[I][1], al[I][2], al[I][3]);
+            if (I <= R)
+                *reinterpret_cast<float4 *>(&sL[(16 * R + m) * LDF + 16 * I + 4 * kg]) =
+                    make_float4(al[I][0], al[I][1], al[I][2], al[I][3]);
         __syncthreads();
 
         // X = (I + L)^{-1} in fp32: diagonal 16x16 blocks by forward substitution
@@ -472,12 +565,13 @@ chunk_prep_kernel(ChunkParams p, int items)
                 f32x4 t = zero4();
                 for (int J = I; J < Rr; ++J)
                     t = mm16_f32(t, sL + (16 * Rr) * LDF + 16 * J, LDF, sX + (16 * J) * LDF + 16 * I, LDF, l);
-                float *scr = sScr[R];
+                // Transposing scratch of wave R (<= 2): L's upper block (0, R + 1).
+                float *scr = sL + 16 * (R + 1);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) scr[(4 * kg + i) * 16 + m] = t[i];
+                for (int i = 0; i < 4; ++i) scr[(4 * kg + i) * LDF + m] = t[i];
                 __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
                 __builtin_amdgcn_wave_barrier();
-                const f32x4 xr = mm16_f32(zero4(), sX + (16 * Rr) * LDF + 16 * Rr, LDF, scr, 16, l);
+                const f32x4 xr = mm16_f32(zero4(), sX + (16 * Rr) * LDF + 16 * Rr, LDF, scr, LDF, l);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sX[(16 * Rr + 4 * kg + i) * LDF + 16 * I + m] = -xr[i];
             }
@@ -508,7 +602,7 @@ chunk_prep_kernel(ChunkParams p, int items)
             st_q4<PK>(ws + BL::WN + k16_block(R, ct, KP) + 4 * l,
                       pack4<PK>(-acc[0], -acc[1], -acc[2], -acc[3]));
         }
-        it = nit;
+        if (item + static_cast<int>(gridDim.x) < items) it = prep_item(p, item + gridDim.x);
         __syncthreads();  // sX / smem1 are read up to here; the next item stages its rows there
     }
 }
