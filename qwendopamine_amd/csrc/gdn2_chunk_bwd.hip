@@ -403,6 +403,8 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
 template <typename T>
 struct Raw4 {
     uint2 u;
+    __device__ __forceinline__ void load(const T *p) { u = *reinterpret_cast<const uint2 *>(p); }
+    __device__ __forceinline__ void zero() { u = make_uint2(0u, 0u); }
     __device__ __forceinline__ void set(const float (&x)[4])
     {
         u.x = raw16(x[0]) | (raw16(x[1]) << 16);
@@ -431,6 +433,8 @@ struct Raw4 {
 template <>
 struct Raw4<float> {
     float4 f;
+    __device__ __forceinline__ void load(const float *p) { f = *reinterpret_cast<const float4 *>(p); }
+    __device__ __forceinline__ void zero() { f = make_float4(0.f, 0.f, 0.f, 0.f); }
     __device__ __forceinline__ void set(const float (&x)[4]) { f = make_float4(x[0], x[1], x[2], x[3]); }
     __device__ __forceinline__ float operator[](int i) const
     {
@@ -518,77 +522,79 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     constexpr int NPRE_W = (NUW + 511) / 512, NPRE_O = (NUO + 511) / 512;
     // Source of workspace unit u of slice vt0 (nullptr past V).
     auto wsrc = [=](int u, int vt0) __attribute__((always_inline)) -> const st * {
+        // Selects, not branches or a table: this runs per lane while the
+        // slice's requests are being issued.
         const int b = u / UPB, e = (u % UPB) * EPU;
-        int rowt, vl;
-        const st *base;
-        if (b < NB_U) {
-            rowt = b / NVS; vl = b % NVS;
-            base = usb;
-        } else if (b < NB_U + NB_Y) {
-            const int rb = b - NB_U;
-            rowt = rb / NVS; vl = rb % NVS;
-            base = dyb;
-        } else if (b < NB_U + NB_Y + NB_H) {
-            const int rb = b - NB_U - NB_Y;
-            rowt = rb / NVS; vl = rb % NVS;
-            base = hsb;
-        } else {
-            const int rb = b - NB_U - NB_Y - NB_H;
-            rowt = rb / NVS; vl = rb % NVS;
-            base = dhb;
-        }
+        const bool inU = b < NB_U, inY = b < NB_U + NB_Y, inH = b < NB_U + NB_Y + NB_H;
+        const int rb = b - (inU ? 0 : (inY ? NB_U : (inH ? NB_U + NB_Y : NB_U + NB_Y + NB_H)));
+        const st *base = inU ? usb : (inY ? dyb : (inH ? hsb : dhb));
+        const int rowt = rb / NVS, vl = rb % NVS;
         if (vt0 + vl >= NVT) return nullptr;
         return base + k16_block(rowt, vt0 + vl, VP) + e;
     };
+    // Requests never wait on their own data: invalid units and groups read a
+    // valid address and are zeroed when landed (validity bits in wok / ook).
     struct Pre {
         u32x4 w[NPRE_W];
-        float o[NPRE_O][4];
-        Raw4<TI> v[NPRE_O], w2[NPRE_O];  // v, w of the same groups, for dv and dw
+        Raw4<TI> o[NPRE_O], v[NPRE_O], w2[NPRE_O];  // dO, and v, w of the same groups for dv and dw
+        uint32_t wok, ook;
     };
     auto issue_slice = [&](Pre &pr, int vt0) __attribute__((always_inline)) {
+        pr.wok = pr.ook = 0u;
 #pragma unroll
         for (int a = 0; a < NPRE_W; ++a) {
             const int u = tid + 512 * a;
             const st *src = u < NUW ? wsrc(u, vt0) : nullptr;
-            pr.w[a] = src ? *reinterpret_cast<const u32x4 *>(src) : u32x4{0, 0, 0, 0};
+            pr.wok |= (src != nullptr ? 1u : 0u) << a;
+            pr.w[a] = *reinterpret_cast<const u32x4 *>(src != nullptr ? src : usb);
         }
 #pragma unroll
         for (int a = 0; a < NPRE_O; ++a) {
             const int u = tid + 512 * a;
             const int tok = u / (4 * NVS), c = 16 * vt0 + 4 * (u % (4 * NVS));
-            const bool ok = u < NUO && tok < lc;
-            const int64_t off = ((t0 + tok) * H + h) * static_cast<int64_t>(V);
-            float xv[4], xw[4];
-            if (ok && (V % 4) == 0 && c + 4 <= V) {
-                load4<TI>(dop, off, c, V, true, 1, pr.o[a]);
-                load4<TI>(vp, off, c, V, true, 1, xv);
-                load4<TI>(wp, off, c, V, true, 1, xw);
+            const bool ok = u < NUO && tok < lc && c < V;
+            pr.ook |= (ok ? 1u : 0u) << a;
+            if ((V % 4) == 0) {
+                // Whole groups of 4 (c < V implies c + 4 <= V): row 0 of the
+                // chunk, column 0, for invalid groups.
+                const int64_t off = ((t0 + (ok ? tok : 0)) * H + h) * static_cast<int64_t>(V) + (ok ? c : 0);
+                pr.o[a].load(dop + off);
+                pr.v[a].load(vp + off);
+                pr.w2[a].load(wp + off);
             } else {
+                const int64_t off = ((t0 + tok) * H + h) * static_cast<int64_t>(V);
+                float xo[4], xv[4], xw[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const bool oki = ok && c + i < V;
-                    pr.o[a][i] = oki ? io<TI>::ld(dop, off + c + i) : 0.f;
+                    xo[i] = oki ? io<TI>::ld(dop, off + c + i) : 0.f;
                     xv[i] = oki ? io<TI>::ld(vp, off + c + i) : 0.f;
                     xw[i] = oki ? io<TI>::ld(wp, off + c + i) : 0.f;
                 }
+                pr.o[a].set(xo);
+                pr.v[a].set(xv);
+                pr.w2[a].set(xw);
             }
-            pr.v[a].set(xv);
-            pr.w2[a].set(xw);
         }
     };
     auto land_slice = [&](const Pre &pr) __attribute__((always_inline)) {
 #pragma unroll
         for (int a = 0; a < NPRE_W; ++a) {
             const int u = tid + 512 * a;
-            if (u < NUW) *reinterpret_cast<u32x4 *>(sW + u * EPU) = pr.w[a];
+            if (u < NUW)
+                *reinterpret_cast<u32x4 *>(sW + u * EPU) = ((pr.wok >> a) & 1u) ? pr.w[a] : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int a = 0; a < NPRE_O; ++a) {
             const int u = tid + 512 * a;
             if (u >= NUO) continue;
             const int tok = u / (4 * NVS), grp = u % (4 * NVS);
+            const bool ok = ((pr.ook >> a) & 1u) != 0;
+            float x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = ok ? pr.o[a][i] : 0.f;
             st_q4<PK>(sO + k16_block(tok >> 4, grp >> 2, 16 * NVS) + 4 * ((tok & 15) + 16 * (grp & 3)),
-                      pack4<PK>(pr.o[a][0], pr.o[a][1], pr.o[a][2], pr.o[a][3]));
+                      pack4<PK>(x[0], x[1], x[2], x[3]));
         }
     };
     const st *sUb = sW;
@@ -609,18 +615,44 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     };
 
     Pre pre;
-    issue_slice(pre, 0);
 
     // ---- rows of this wave: raw q, k, b (input format) and the in-block log2
     // decay prefix G ----
     // (Loaded here for the factor tiles and again after the V-contractions,
     // so that they are not live across them.)
     auto load_rows = [&](Raw4<TI> (&qv)[NKH], Raw4<TI> (&kv)[NKH], Raw4<TI> (&bv)[NKH],
-                         float (&gv)[NKH][4]) __attribute__((always_inline)) {
+                         float (&gv)[NKH][4], auto between) __attribute__((always_inline)) {
         const TI *q = static_cast<const TI *>(p.q);
         const TI *k = static_cast<const TI *>(p.k);
         const TI *b = static_cast<const TI *>(p.b);
         const TG *g = static_cast<const TG *>(p.g);
+        if (K == KP) {
+            // Every channel tile is inside K: all loads are requested before any
+            // is used (rows past the chunk end read its first row and are zeroed).
+            const int64_t off = row_ok ? roff : (t0 * H + h) * static_cast<int64_t>(K);
+            Raw4<TG> rg[NKH];
+#pragma unroll
+            for (int j = 0; j < NKH; ++j) {
+                const int c0 = 16 * (hh * NKH + j) + 4 * kg;
+                qv[j].load(q + off + c0);
+                kv[j].load(k + off + c0);
+                bv[j].load(b + off + c0);
+                rg[j].load(g + off + c0);
+            }
+            between();  // more requests, issued before these rows are used
+#pragma unroll
+            for (int j = 0; j < NKH; ++j) {
+                if (!row_ok) {
+                    qv[j].zero();
+                    kv[j].zero();
+                    bv[j].zero();
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) gv[j][i] = row16_scan((row_ok ? rg[j][i] : 0.f) * kLog2e);
+            }
+            return;
+        }
+        between();
 #pragma unroll
         for (int j = 0; j < NKH; ++j) {
             const int c0 = 16 * (hh * NKH + j) + 4 * kg;
@@ -641,7 +673,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     {
     Raw4<TI> qv[NKH], kv[NKH], bv[NKH];
     float gv[NKH][4];
-    load_rows(qv, kv, bv, gv);
+    load_rows(qv, kv, bv, gv, [&]() __attribute__((always_inline)) { issue_slice(pre, 0); });
     {
         float sq = 0.f, sk = 0.f;
         bool wide = false;
@@ -794,7 +826,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
 
     Raw4<TI> qv[NKH], kv[NKH], bv[NKH];
     float gv[NKH][4];
-    load_rows(qv, kv, bv, gv);
+    load_rows(qv, kv, bv, gv, []() {});
 
     // ---- G_last term: part 1 exp(G_last) rowsum(dS1 * S0) (channel tile wv),
     // part 2 this block's sum of dKt * Kt (ck = dKt here).  Together they are
