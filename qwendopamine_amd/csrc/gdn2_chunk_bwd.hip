@@ -171,24 +171,33 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
     constexpr int EPV = 16 / static_cast<int>(sizeof(TI));
     constexpr int ZT = kChunk * BV / EPV;
     constexpr int NZT = (ZT + 255) / 256;
-    const bool dvec = (V % EPV) == 0;
+    // Whole 16-byte row pieces for every row of this slice (uniform per workgroup).
+    const bool dfast = (V % EPV) == 0 && v0 + BV <= V;
     struct DRaw {
         u32x4 d[NZT];
     };
-    auto issue_d = [&](DRaw &r, int jc) __attribute__((always_inline)) {
-        int64_t t0;
-        int lc;
-        chunk_rows(jc, t0, lc);
+    // issue_d requests the raw rows, land_d scatters them into LDS, so the two
+    // can sit a chunk apart.  On the fast path dead lanes load the chunk's
+    // first row piece (always valid) and are zeroed when landed, and land_d
+    // touches no global memory: a select on a loaded value, or a load in
+    // land_d, would make the request wait for its own data.  Ragged slices
+    // load element by element in land_d.
+    auto issue_d = [&](auto fastc, DRaw &r, int jc) __attribute__((always_inline)) {
+        if constexpr (decltype(fastc)::value) {
+            int64_t t0;
+            int lc;
+            chunk_rows(jc, t0, lc);
 #pragma unroll
-        for (int a = 0; a < NZT; ++a) {
-            const int task = ctid + 256 * a;
-            const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
-            const bool ok = task < ZT && tok < lc && dvec && v0 + c + EPV <= V;
-            const int64_t off = ((t0 + tok) * H + h) * V + v0 + c;
-            r.d[a] = ok ? *reinterpret_cast<const u32x4 *>(dop + off) : u32x4{0, 0, 0, 0};
+            for (int a = 0; a < NZT; ++a) {
+                const int task = ctid + 256 * a;
+                const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
+                const bool live = task < ZT && tok < lc;
+                const int64_t off = live ? ((t0 + tok) * H + h) * V + v0 + c : (t0 * H + h) * V + v0;
+                r.d[a] = *reinterpret_cast<const u32x4 *>(dop + off);
+            }
         }
     };
-    auto land_d = [&](const DRaw &r, int jc, int buf) __attribute__((always_inline)) {
+    auto land_d = [&](auto fastc, const DRaw &r, int jc, int buf) __attribute__((always_inline)) {
         int64_t t0;
         int lc;
         chunk_rows(jc, t0, lc);
@@ -199,15 +208,15 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
             if (task >= ZT) continue;
             const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
             const TI *rd = reinterpret_cast<const TI *>(&r.d[a]);
-            const bool ok = tok < lc && dvec && v0 + c + EPV <= V;
             const int kt = tok >> 4, kgz = (tok & 15) >> 2, iz = tok & 3;
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
                 float x = 0.f;
-                if (ok)
-                    x = io<TI>::ld(rd, e);
-                else if (tok < lc && v0 + c + e < V)
-                    x = io<TI>::ld(dop, ((t0 + tok) * H + h) * V + v0 + c + e);
+                if constexpr (decltype(fastc)::value) {
+                    x = tok < lc ? io<TI>::ld(rd, e) : 0.f;
+                } else {
+                    if (tok < lc && v0 + c + e < V) x = io<TI>::ld(dop, ((t0 + tok) * H + h) * V + v0 + c + e);
+                }
                 const int cl = c + e, ct = cl >> 4, nz = cl & 15;
                 dst[(kt * 4 + ct) * 256 + (nz + 16 * kgz) * 4 + iz] = P::from_f32(x);
             }
@@ -237,66 +246,74 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
 
     // Step s handles chunk nch-1-s.  Barrier schedule as in the forward scan.
     if (copier) {
-        DRaw dA, dB;
-        if (nch > 0) {
-            land_all(blob(gc0 + nch - 1));
-            issue_d(dA, nch - 1);
-            land_d(dA, nch - 1, 0);
-        }
-        if constexpr (DB) {
-            u32x4 pA[PF], pB[PF];
-            auto issue = [&](u32x4 (&dst)[PF], int gci) __attribute__((always_inline)) {
-                const u32x4 *src = blob(gci);
-#pragma unroll
-                for (int u = 0; u < PF; ++u) {
-                    const int idx = ctid + 256 * u;
-                    dst[u] = src[idx < U16 ? idx : U16 - 1];
-                }
-            };
-            auto land = [&](const u32x4 (&src)[PF], int buf) __attribute__((always_inline)) {
-#pragma unroll
-                for (int u = 0; u < PF; ++u)
-                    if (ctid + 256 * u < U16) land_transposed<PK, KP>(sB[buf], src[u], u, ctid);
-            };
-            if (nch > 1) {
-                issue(pA, gc0 + nch - 2);
-                issue_d(dA, nch - 2);
+        // Instantiated for whole-row and for ragged dO slices (uniform per
+        // workgroup), so that each loop body is straight-line.
+        auto copy_loop = [&](auto fastc) __attribute__((always_inline)) {
+            DRaw dA, dB;
+            if (nch > 0) {
+                land_all(blob(gc0 + nch - 1));
+                issue_d(fastc, dA, nch - 1);
+                land_d(fastc, dA, nch - 1, 0);
             }
-            __syncthreads();
-            for (int s = 0; s < nch; s += 2) {
-                if (s + 2 < nch) {
-                    issue(pB, gc0 + nch - 3 - s);
-                    issue_d(dB, nch - 3 - s);
-                }
-                if (s + 1 < nch) {
-                    land_d(dA, nch - 2 - s, 1);
-                    land(pA, 1);
+            if constexpr (DB) {
+                u32x4 pA[PF], pB[PF];
+                auto issue = [&](u32x4 (&dst)[PF], int gci) __attribute__((always_inline)) {
+                    const u32x4 *src = blob(gci);
+#pragma unroll
+                    for (int u = 0; u < PF; ++u) {
+                        const int idx = ctid + 256 * u;
+                        dst[u] = src[idx < U16 ? idx : U16 - 1];
+                    }
+                };
+                auto land = [&](const u32x4 (&src)[PF], int buf) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int u = 0; u < PF; ++u)
+                        if (ctid + 256 * u < U16) land_transposed<PK, KP>(sB[buf], src[u], u, ctid);
+                };
+                if (nch > 1) {
+                    issue(pA, gc0 + nch - 2);
+                    issue_d(fastc, dA, nch - 2);
                 }
                 __syncthreads();
-                if (s + 1 >= nch) break;
-                if (s + 3 < nch) {
-                    issue(pA, gc0 + nch - 4 - s);
-                    issue_d(dA, nch - 4 - s);
-                }
-                if (s + 2 < nch) {
-                    land_d(dB, nch - 3 - s, 0);
-                    land(pB, 0);
-                }
-                __syncthreads();
-            }
-        } else {
-            __syncthreads();
-            for (int s = 0; s < nch; ++s) {
-                __syncthreads();
-                if (s + 1 < nch) {
-                    const int jn = nch - 2 - s;
-                    land_all(blob(gc0 + jn));
-                    issue_d(dA, jn);
-                    land_d(dA, jn, 0);
+                for (int s = 0; s < nch; s += 2) {
+                    if (s + 2 < nch) {
+                        issue(pB, gc0 + nch - 3 - s);
+                        issue_d(fastc, dB, nch - 3 - s);
+                    }
+                    if (s + 1 < nch) {
+                        land_d(fastc, dA, nch - 2 - s, 1);
+                        land(pA, 1);
+                    }
+                    __syncthreads();
+                    if (s + 1 >= nch) break;
+                    if (s + 3 < nch) {
+                        issue(pA, gc0 + nch - 4 - s);
+                        issue_d(fastc, dA, nch - 4 - s);
+                    }
+                    if (s + 2 < nch) {
+                        land_d(fastc, dB, nch - 3 - s, 0);
+                        land(pB, 0);
+                    }
                     __syncthreads();
                 }
+            } else {
+                __syncthreads();
+                for (int s = 0; s < nch; ++s) {
+                    __syncthreads();
+                    if (s + 1 < nch) {
+                        const int jn = nch - 2 - s;
+                        land_all(blob(gc0 + jn));
+                        issue_d(fastc, dA, jn);
+                        land_d(fastc, dA, jn, 0);
+                        __syncthreads();
+                    }
+                }
             }
-        }
+        };
+        if (dfast)
+            copy_loop(std::true_type{});
+        else
+            copy_loop(std::false_type{});
     } else {
         const Q ident = identity_q4<PK>(l);
         __syncthreads();
