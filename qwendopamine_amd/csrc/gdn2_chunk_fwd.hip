@@ -664,10 +664,25 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     auto blob = [&](int gci) {
         return reinterpret_cast<const u32x4 *>(wsb + (static_cast<int64_t>(gci) * H + h) * BL::SIZE);
     };
+    // Whole blob into LDS, CB requests in flight per copy wave lane at a time
+    // (a plain element loop would wait for each load before its store).
     auto copy_blob = [&](int gci, int buf) __attribute__((always_inline)) {
+        constexpr int CB = 8;
         const u32x4 *src = blob(gci);
         u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf]);
-        for (int u = ctid; u < U16; u += 256) dst[u] = src[u];
+        for (int u0 = 0; u0 < U16; u0 += 256 * CB) {
+            u32x4 t[CB];
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                const int u = u0 + ctid + 256 * c;
+                t[c] = src[u < U16 ? u : U16 - 1];
+            }
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                const int u = u0 + ctid + 256 * c;
+                if (u < U16) dst[u] = t[c];
+            }
+        }
     };
     // Copy waves: z = w * v of chunk jc for this value slice, in the K16
     // B-operand order the compute waves read (zero past the sequence end and
