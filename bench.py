@@ -473,8 +473,9 @@ def measured_traffic():
     return None
 
 
-def cpu_baseline(torch, inputs, max_threads=16, reps=3):
-    """Time the C port of the reference recurrence on this host's cores, same prefill inputs."""
+def cpu_baseline(torch, inputs, max_threads=16, target_s=10.0, max_reps=200):
+    """Time the C port of the reference recurrence on this host's cores, same prefill inputs:
+    repeated passes over the full config-1 batch for about `target_s` seconds of CPU work."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import cpu_lib
 
@@ -484,10 +485,12 @@ def cpu_baseline(torch, inputs, max_threads=16, reps=3):
     cpu_lib.recurrent_fwd_f32(q[:, :64], k[:, :64], v[:, :64], g[:, :64], b[:, :64], w[:, :64],
                               nthreads=threads)
     times = []
-    for _ in range(reps):
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < target_s and len(times) < max_reps):
         t0 = time.perf_counter()
         cpu_lib.recurrent_fwd_f32(q, k, v, g, b, w, nthreads=threads)
         times.append(time.perf_counter() - t0)
+    reps = len(times)
     t = statistics.median(times)
     model = ""
     try:

@@ -546,10 +546,12 @@ chunk_prep_kernel(ChunkParams p, int items)
             float x[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float acc = (i == j) ? 1.f : 0.f;
+                // Four partial sums: the dependent FMA chain of row i is i / 4 long.
+                float acc[4] = {(i == j) ? 1.f : 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int mm = 0; mm < i; ++mm) acc = fmaf(-sL[(16 * R + i) * LDF + 16 * R + mm], x[mm], acc);
-                x[i] = acc;
+                for (int mm = 0; mm < i; ++mm)
+                    acc[mm & 3] = fmaf(-sL[(16 * R + i) * LDF + 16 * R + mm], x[mm], acc[mm & 3]);
+                x[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) sX[(16 * R + i) * LDF + 16 * R + j] = x[i];
