@@ -39,9 +39,10 @@ def _oracle_module_forward(m, x):
         A = mf.A_log.exp().repeat_interleave(mf.head_k_dim)
         g = -A * F.softplus(mf.f_proj(xf) + mf.dt_bias)
         b, w = mf.b_proj(xf).sigmoid(), mf.w_proj(xf).sigmoid()
-        sp = lambda t, d: t.reshape(*t.shape[:-1], -1, d).double().cpu().numpy()  # noqa: E731
-        o, _ = orc.recurrent_fwd(sp(q, mf.head_k_dim), sp(k, mf.head_k_dim), sp(v, mf.head_v_dim),
-                                 sp(g, mf.head_k_dim), sp(b, mf.head_k_dim), sp(w, mf.head_v_dim))
+        rep = mf.num_v_heads // mf.num_heads  # grouped value heads (gdn2.py:859-863)
+        sp = lambda t, d, r=1: t.reshape(*t.shape[:-1], -1, d).repeat_interleave(r, dim=-2).double().cpu().numpy()  # noqa: E731
+        o, _ = orc.recurrent_fwd(sp(q, mf.head_k_dim, rep), sp(k, mf.head_k_dim, rep), sp(v, mf.head_v_dim),
+                                 sp(g, mf.head_k_dim, rep), sp(b, mf.head_k_dim, rep), sp(w, mf.head_v_dim))
         o = torch.from_numpy(o).float().to(x.device)
         gate = mf.g_proj(xf).reshape(*o.shape)
         o = mf.o_norm(o, gate)
@@ -146,11 +147,15 @@ def test_bf16_forward_finite(gpu_device):
     assert out.dtype == torch.bfloat16 and torch.isfinite(out.float()).all()
 
 
-def test_gva_module(gpu_device):
-    print("[case] GVA module", flush=True)
+@pytest.mark.parametrize("T", [20, 150])
+def test_gva_module(gpu_device, T):
+    """Grouped value heads (num_v_heads = 2 num_heads) in inference, where the decay
+    activation runs in-kernel with each key head's A_log / dt_bias repeated for its value
+    heads (and, at T <= 64, the b / w sigmoids too), against the oracle composition."""
+    print(f"[case] GVA module T={T}", flush=True)
     m = _layer(gpu_device, hidden_size=64, num_heads=2, head_dim=16, num_v_heads=4).eval()
-    x = torch.randn(1, 20, 64, device=gpu_device)
+    x = torch.randn(1, T, 64, device=gpu_device)
     with torch.no_grad():
         out, _, _ = m(x)
-    assert out.shape == (1, 20, 64) and torch.isfinite(out).all()
-    assert np.isfinite(out.cpu().numpy()).all()
+    assert out.shape == (1, T, 64) and torch.isfinite(out).all()
+    assert rel_l2(out, _oracle_module_forward(m, x)) <= 1e-4
