@@ -270,29 +270,37 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
                     for (int u = 0; u < PF; ++u)
                         if (ctid + 256 * u < U16) land_transposed<PK, KP>(sB[buf], src[u], u, ctid);
                 };
+                // Step s lands chunk nch-2-s, requested two steps earlier, and
+                // reuses its register set for chunk nch-4-s, so every request
+                // has two chunk steps of memory latency to hide.  Unrolled by
+                // two so that the register sets A / B swap roles at compile time.
                 if (nch > 1) {
                     issue(pA, gc0 + nch - 2);
                     issue_d(fastc, dA, nch - 2);
                 }
+                if (nch > 2) {
+                    issue(pB, gc0 + nch - 3);
+                    issue_d(fastc, dB, nch - 3);
+                }
                 __syncthreads();
                 for (int s = 0; s < nch; s += 2) {
-                    if (s + 2 < nch) {
-                        issue(pB, gc0 + nch - 3 - s);
-                        issue_d(fastc, dB, nch - 3 - s);
-                    }
                     if (s + 1 < nch) {
                         land_d(fastc, dA, nch - 2 - s, 1);
                         land(pA, 1);
                     }
-                    __syncthreads();
-                    if (s + 1 >= nch) break;
                     if (s + 3 < nch) {
                         issue(pA, gc0 + nch - 4 - s);
                         issue_d(fastc, dA, nch - 4 - s);
                     }
+                    __syncthreads();
+                    if (s + 1 >= nch) break;
                     if (s + 2 < nch) {
                         land_d(fastc, dB, nch - 3 - s, 0);
                         land(pB, 0);
+                    }
+                    if (s + 4 < nch) {
+                        issue(pB, gc0 + nch - 5 - s);
+                        issue_d(fastc, dB, nch - 5 - s);
                     }
                     __syncthreads();
                 }

@@ -819,17 +819,30 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                         if (idx < U16) dst[idx] = src[u];
                     }
                 };
-                // Two chunks in flight: at step jc the blob and rows of chunk
-                // jc+1 (requested two steps earlier) land in the idle buffer
-                // after chunk jc+2 has been requested.  Unrolled by two so the
-                // register sets A / B swap roles at compile time.
+                // Chunk jc+1 lands in the idle buffer at step jc.  Unrolled by
+                // two so that the register sets A / B swap roles at compile time.
+                //  * DEEP (training emission, or value slices narrower than 64
+                //    so that several workgroups share each blob): chunk jc+1 was
+                //    requested two steps earlier and its register set is reused
+                //    for chunk jc+3 right after landing, so every request has two
+                //    chunk steps of memory latency to hide (training forward at
+                //    config 4: 0.69 -> 0.62 ms).
+                //  * otherwise chunk jc+2 is requested before chunk jc+1 lands,
+                //    one step of latency per request, which measured faster for
+                //    64-column slices without emission (0.241 vs 0.251 ms at
+                //    config 1).
+                constexpr bool DEEP = TRAIN || BV < 64;
                 if (nch > 1) {
                     issue(pA, gc0 + 1);
                     issue_z(fastc, zA, 1);
                 }
+                if (DEEP && nch > 2) {
+                    issue(pB, gc0 + 2);
+                    issue_z(fastc, zB, 2);
+                }
                 __syncthreads();
                 for (int jc = 0; jc < nch; jc += 2) {
-                    if (jc + 2 < nch) {
+                    if (!DEEP && jc + 2 < nch) {
                         issue(pB, gc0 + jc + 2);
                         issue_z(fastc, zB, jc + 2);
                     }
@@ -837,15 +850,23 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                         land_z(zA, jc + 1, 1);
                         land(pA, 1);
                     }
+                    if (DEEP && jc + 3 < nch) {
+                        issue(pA, gc0 + jc + 3);
+                        issue_z(fastc, zA, jc + 3);
+                    }
                     __syncthreads();
                     if (jc + 1 >= nch) break;
-                    if (jc + 3 < nch) {
+                    if (!DEEP && jc + 3 < nch) {
                         issue(pA, gc0 + jc + 3);
                         issue_z(fastc, zA, jc + 3);
                     }
                     if (jc + 2 < nch) {
                         land_z(zB, jc + 2, 0);
                         land(pB, 0);
+                    }
+                    if (DEEP && jc + 4 < nch) {
+                        issue(pB, gc0 + jc + 4);
+                        issue_z(fastc, zB, jc + 4);
                     }
                     __syncthreads();
                 }
