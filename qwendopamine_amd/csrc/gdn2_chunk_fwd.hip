@@ -650,6 +650,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     const int VP = p.VP, vt = vs * NCT + wv;
     const bool emit = TRAIN && active && 16 * vt < V;
     const Q ident = identity_q4<PK>(l);
+    // Outputs leave through transposed tiles when the operand precision is the
+    // output dtype (bf16 with bf16 operands, fp32 with fp32 operands).
+    constexpr bool OUT_T = (std::is_same<TI, bf16_t>::value && PK == PrecKind::BF16) ||
+                           (std::is_same<TI, float>::value && PK == PrecKind::F32);
     // An fp32 accumulator tile (rows 4kg+i, column m) stored transposed, in
     // A-order and the MFMA operand precision (an identity product transposes it).
     auto emit_tile = [&](st *base, int64_t off, f32x4 x) __attribute__((always_inline)) {
@@ -662,6 +666,8 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     const TI *vp = static_cast<const TI *>(p.v);
     const TI *wp = static_cast<const TI *>(p.w);
     TI *op = static_cast<TI *>(p.o);
+    // Whole 4-value output pieces when V and the base allow aligned vector stores.
+    const bool o_vec = (V % 4) == 0 && (reinterpret_cast<uintptr_t>(op) % (4 * sizeof(TI))) == 0;
     const st *wsb = static_cast<const st *>(p.ws);
     auto blob = [&](int gci) {
         return reinterpret_cast<const u32x4 *>(wsb + (static_cast<int64_t>(gci) * H + h) * BL::SIZE);
@@ -1021,7 +1027,31 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     }
                 }
             }
-            if (col_ok) {
+            if constexpr (OUT_T) {
+                // Each O tile transposed by an identity product (exact: the
+                // values are rounded to the output dtype once, by the first
+                // pack), so lane (m, kg) holds token 16rt+m, columns 4kg..4kg+3
+                // and stores them with one 8-byte (bf16) or 16-byte (fp32)
+                // access instead of four 2- or 4-byte ones.
+                const int c0 = vs * BV + 16 * wv + 4 * kg;
+                const bool vec = o_vec && c0 + 4 <= V;
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) {
+                    const Q tr = pack4<PK>(mma1<PK>(zero4(), pack4<PK>(oa[rt]), ident));
+                    const int tok = 16 * rt + m;
+                    if (tok >= lc) continue;
+                    TI *dst = op + ((t0 + tok) * H + h) * V + c0;
+                    if (vec) {
+                        st_q4<PK>(reinterpret_cast<st *>(dst), tr);
+                    } else {
+                        float x[4];
+                        unpack4<PK>(tr, x);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (c0 + i < V) io<TI>::st(dst, i, x[i]);
+                    }
+                }
+            } else if (col_ok) {
 #pragma unroll
                 for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
