@@ -459,18 +459,27 @@ def traffic_probe(torch, nat, dev):
     print("traffic probe done", flush=True)
 
 
-def measured_traffic():
-    """HBM bytes per prefill op from the committed counter summary (None if absent)."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "chunk_fwd_C1_traffic.md")
+def _profile_value(name, key):
+    """Integer ``key: value`` line of a committed counter summary under profiles/ (None if absent)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         with open(path) as f:
             for ln in f:
-                if ln.startswith("traffic_bytes_per_op:"):
+                if ln.startswith(key + ":"):
                     return int(ln.split(":", 1)[1].strip())
     except OSError:
         return None
     return None
+
+
+def measured_traffic():
+    """HBM bytes per prefill op from the committed FETCH_SIZE / WRITE_SIZE summary."""
+    return _profile_value("chunk_fwd_C1_traffic.md", "traffic_bytes_per_op")
+
+
+def measured_mfma_flop():
+    """bf16 MFMA FLOP executed per prefill op from the committed SQ counter summary."""
+    return _profile_value("chunk_kernels_mfma_counters.md", "executed_bf16_mfma_flop_per_prefill_op")
 
 
 def cpu_baseline(torch, inputs, max_threads=16, target_s=10.0, max_reps=200):
@@ -545,6 +554,7 @@ def main() -> int:
     flops = prefill_flops(B, T, H, K, V, C)
     t_op_ms = res["t_prep_ms"] + res["t_scan_ms"]
     achieved = nbytes / (t_op_ms * 1e-3) / 1e9
+    mfma_exec = measured_mfma_flop()
     out = {
         "metric": METRIC,
         "value": round(tokens / (ms * 1e-3), 1),
@@ -576,7 +586,10 @@ def main() -> int:
             "mfma": {"algorithmic_flop": flops,
                      "achieved_TFLOPs": round(flops / (t_op_ms * 1e-3) / 1e12, 2),
                      "peak_TFLOPs": BF16_PEAK_TFLOPS,
-                     "frac": round(flops / (t_op_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+                     "frac": round(flops / (t_op_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                     "counter_flop": mfma_exec,
+                     "counter_frac": (None if mfma_exec is None else
+                                      round(mfma_exec / (t_op_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))},
         },
     }
     if not args.no_decode:
