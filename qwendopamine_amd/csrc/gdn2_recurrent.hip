@@ -421,7 +421,7 @@ __global__ __launch_bounds__(256) void recurrent_fwd_kernel(RecurrentParams p)
 // reads of one slab overlap the state writes of the other.  A decode step is
 // one pass over the whole state, so this overlap is what separates it from a
 // plain read-then-write of 2 x 64 KB per workgroup.
-template <typename TI, typename TG>
+template <typename TI, typename TG, bool H0>
 __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int nslabs)
 {
     constexpr int KD = 128, VD = 128, TPR = 32, RG = 8, NR = KD / RG, SLABS = 2;
@@ -446,42 +446,102 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
     const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
     const bool sig_bw = (p.flags & GDN2_FLAG_SIGMOID_BW) != 0;
 
-    float4 st[SLABS][NR];
+    // Every request below reads an always-valid address: the token inputs of
+    // both slabs first, then both slabs' state.  A slab past the end reads the
+    // last slab, and a state row that does not exist (no initial state, or a
+    // padded pool entry) reads slab 0 of the state array and is zeroed where it
+    // is used.  A load whose result were picked against zero here, or a load
+    // inside a per-slab branch, would make the compiler wait for the first
+    // slab's state before the second slab's requests leave.
     const int slab0 = blockIdx.x * SLABS;
-    auto load_state = [&](float4 (&dst)[NR], int slab) {
-        const float *row = initial_row(p, slab / p.HV, slab % p.HV);
+    float qv[SLABS], kv[SLABS], gv[SLABS], bv[SLABS];
+    float4 vv[SLABS], ww[SLABS];
+    const int tk = tid & (KD - 1);
 #pragma unroll
-        for (int i = 0; i < NR; ++i) {
-            dst[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (row) dst[i] = *reinterpret_cast<const float4 *>(row + (rg + i * RG) * VD + col);
+    for (int s = 0; s < SLABS; ++s) {
+        const int slab = slab0 + s < nslabs ? slab0 + s : nslabs - 1;
+        const int n = slab / p.HV, hv = slab % p.HV;
+        const int h = hv / (p.HV / p.H);
+        const int64_t qk_off = (static_cast<int64_t>(n) * p.H + h) * KD;
+        qv[s] = io<TI>::ld(q, qk_off + tk);
+        kv[s] = io<TI>::ld(k, qk_off + tk);
+        gv[s] = io<TG>::ld(g, static_cast<int64_t>(slab) * KD + tk);
+        bv[s] = io<TI>::ld(b, static_cast<int64_t>(slab) * KD + tk);
+        vv[s] = vec4io<TI>::ld(v, static_cast<int64_t>(slab) * VD + col);
+        ww[s] = vec4io<TI>::ld(w, static_cast<int64_t>(slab) * VD + col);
+    }
+    // Store rows (a state pool reads its index entries here) and the in-kernel
+    // gate's parameters, also before any state request.  With an initial
+    // state the gate parameters are read unconditionally (from the state
+    // array when absent, and then unused).
+    float *dst[SLABS];
+    float dtb[SLABS], alg[SLABS];
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+        const int slab = slab0 + s < nslabs ? slab0 + s : nslabs - 1;
+        const int n = slab / p.HV, hv = slab % p.HV;
+        const int h = hv / (p.HV / p.H);
+        dst[s] = store_row(p, n, hv, 0, n);
+        dtb[s] = alg[s] = 0.f;
+        if constexpr (H0) {
+            const float *dsrc = p.dt_bias ? p.dt_bias : p.h0;
+            const float *asrc = p.A_log ? p.A_log : p.h0;
+            dtb[s] = dsrc[h * KD + tk];
+            alg[s] = asrc[h];
+        } else if (gate) {
+            dtb[s] = p.dt_bias ? p.dt_bias[h * KD + tk] : 0.0f;
+            alg[s] = p.A_log[h];
         }
-    };
-    load_state(st[0], slab0);
+    }
+    float4 st[SLABS][NR];
+    bool zst[SLABS];
+    // H0 (a compile-time choice, so that no branch separates the loads from
+    // their use): an initial-state array exists.
+    if constexpr (H0) {
+        // Both rows first (a state pool reads its index entries here), then
+        // both slabs' loads back to back.
+        const float *src[SLABS];
+#pragma unroll
+        for (int s = 0; s < SLABS; ++s) {
+            const int slab = slab0 + s < nslabs ? slab0 + s : nslabs - 1;
+            const float *row = initial_row(p, slab / p.HV, slab % p.HV);
+            zst[s] = row == nullptr;
+            src[s] = row ? row : p.h0;
+        }
+#pragma unroll
+        for (int s = 0; s < SLABS; ++s)
+#pragma unroll
+            for (int i = 0; i < NR; ++i)
+                st[s][i] = *reinterpret_cast<const float4 *>(src[s] + (rg + i * RG) * VD + col);
+    } else {
+#pragma unroll
+        for (int s = 0; s < SLABS; ++s) {
+            zst[s] = true;
+#pragma unroll
+            for (int i = 0; i < NR; ++i) st[s][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
 #pragma unroll
     for (int s = 0; s < SLABS; ++s) {
         const int slab = slab0 + s;
         if (slab >= nslabs) break;
-        if (s + 1 < SLABS && slab + 1 < nslabs) load_state(st[s + 1], slab + 1);
         const int n = slab / p.HV, hv = slab % p.HV;
         const int h = hv / (p.HV / p.H);
-        const int64_t qk_off = (static_cast<int64_t>(n) * p.H + h) * KD;
-        const int64_t gb_off = static_cast<int64_t>(slab) * KD;
         const int64_t vw_off = static_cast<int64_t>(slab) * VD;
 
-        float qv = 0.f, kv = 0.f, gv = 0.f, bv = 0.f;
+        float qv_ = 0.f, kv_ = 0.f, gv_ = 0.f, bv_ = 0.f;
         if (tid < KD) {
-            qv = io<TI>::ld(q, qk_off + tid);
-            kv = io<TI>::ld(k, qk_off + tid);
-            gv = io<TG>::ld(g, gb_off + tid);
-            bv = io<TI>::ld(b, gb_off + tid);
+            qv_ = qv[s];
+            kv_ = kv[s];
+            gv_ = gv[s];
+            bv_ = bv[s];
         }
-        const float4 vv = vec4io<TI>::ld(v, vw_off + col);
-        float4 ww = vec4io<TI>::ld(w, vw_off + col);
+        float4 vv_ = vv[s], ww_ = ww[s];
         if (sig_bw) {
-            bv = sigmoid_f(bv);
-            ww = make_float4(sigmoid_f(ww.x), sigmoid_f(ww.y), sigmoid_f(ww.z), sigmoid_f(ww.w));
+            bv_ = sigmoid_f(bv_);
+            ww_ = make_float4(sigmoid_f(ww_.x), sigmoid_f(ww_.y), sigmoid_f(ww_.z), sigmoid_f(ww_.w));
         }
-        const float rq = wave_sum(qv * qv), rk = wave_sum(kv * kv), rqk = wave_sum(qv * kv);
+        const float rq = wave_sum(qv_ * qv_), rk = wave_sum(kv_ * kv_), rqk = wave_sum(qv_ * kv_);
         if (lane == 0) {
             s_part[wid][0] = rq;
             s_part[wid][1] = rk;
@@ -498,14 +558,14 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
         const float invq = l2 ? 1.0f / fmaxf(sqrtf(qq), 1e-6f) : 1.0f;
         const float invk = l2 ? 1.0f / fmaxf(sqrtf(kk), 1e-6f) : 1.0f;
         if (tid < KD) {
-            const float kn = kv * invk;
-            s_q[tid] = qv * invq * p.scale;
+            const float kn = kv_ * invk;
+            s_q[tid] = qv_ * invq * p.scale;
             s_k[tid] = kn;
-            s_e[tid] = bv * kn;
-            float gk = gv;
+            s_e[tid] = bv_ * kn;
+            float gk = gv_;
             if (gate) {
-                const float db = p.dt_bias ? p.dt_bias[h * KD + tid] : 0.0f;
-                gk = gate_activation(gv, p.A_log[h], db, use_lb, p.lower_bound);
+                const float db = p.dt_bias ? dtb[s] : 0.0f;
+                gk = gate_activation(gv_, alg[s], db, use_lb, p.lower_bound);
             }
             s_a[tid] = expf(gk);
         }
@@ -513,9 +573,14 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
         __syncthreads();
 
         float4 pr = make_float4(0.f, 0.f, 0.f, 0.f), po = pr;
+        // Opaque here, so that the zeroing of a missing row is not hoisted up
+        // to the loads (where overwriting their registers would wait for them).
+        int zs = zst[s] ? 1 : 0;
+        asm volatile("" : "+v"(zs));
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
             const int r = rg + i * RG;
+            if (zs) st[s][i] = make_float4(0.f, 0.f, 0.f, 0.f);
             const float a = s_a[r];
             st[s][i].x *= a;
             st[s][i].y *= a;
@@ -541,10 +606,9 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
             R.x += a.x; R.y += a.y; R.z += a.z; R.w += a.w;
             PO.x += c.x; PO.y += c.y; PO.z += c.z; PO.w += c.w;
         }
-        const float4 u = make_float4(ww.x * vv.x - R.x, ww.y * vv.y - R.y, ww.z * vv.z - R.z,
-                                     ww.w * vv.w - R.w);
+        const float4 u = make_float4(ww_.x * vv_.x - R.x, ww_.y * vv_.y - R.y, ww_.z * vv_.z - R.z,
+                                     ww_.w * vv_.w - R.w);
         // One token per sequence: its state is the final state (packed position n).
-        float *dst = store_row(p, n, hv, 0, n);
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
             const int r = rg + i * RG;
@@ -553,7 +617,7 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
             st[s][i].y = fmaf(kr, u.y, st[s][i].y);
             st[s][i].z = fmaf(kr, u.z, st[s][i].z);
             st[s][i].w = fmaf(kr, u.w, st[s][i].w);
-            if (dst) *reinterpret_cast<float4 *>(dst + r * VD + col) = st[s][i];
+            if (dst[s]) *reinterpret_cast<float4 *>(dst[s] + r * VD + col) = st[s][i];
         }
         if (rg == 0) vec4io<TI>::st(o, vw_off + col, f4_fma(u, kq, PO));
         __syncthreads();
@@ -592,8 +656,12 @@ static hipError_t launch_tpr(const RecurrentParams &p, int N, hipStream_t stream
     const bool trans = (p.flags & GDN2_FLAG_TRANSPOSE_STATE) != 0;
     if (p.T == 1 && !p.cu_seqlens && p.K == 128 && p.V == 128 && !trans) {
         const int nslabs = N * p.HV;
-        hipLaunchKernelGGL((decode_step_kernel<TI, TG>), dim3((nslabs + 1) / 2), dim3(256), 0, stream,
-                           p, nslabs);
+        if (p.h0)
+            hipLaunchKernelGGL((decode_step_kernel<TI, TG, true>), dim3((nslabs + 1) / 2), dim3(256), 0,
+                               stream, p, nslabs);
+        else
+            hipLaunchKernelGGL((decode_step_kernel<TI, TG, false>), dim3((nslabs + 1) / 2), dim3(256), 0,
+                               stream, p, nslabs);
         return hipGetLastError();
     }
     // Narrowest row that still covers V with float4 lanes, capped at 128 columns.
