@@ -151,10 +151,20 @@ struct TransposedSlab {
     static constexpr int TILE_FLOATS = VB * LD;
     static_assert(VB * Q % 256 == 0, "tile must split evenly over 256 threads");
 
+    // Every block's requests leave before the first one is used.  Block b's
+    // PER (= BI) raw float4 wait in raw[b0 .. b0 + BI) -- the register rows
+    // its transposed values end up in when NR >= BI (NR is then a multiple of
+    // BI), a separate BI-entry array otherwise.  Pieces outside the slab read
+    // the slab's first element (always valid) and are zeroed when written to
+    // the tile.
+    static constexpr int RAWN = NR >= BI ? NR : BI;
     static __device__ void load(float4 (&st)[NR], const float *base, int K, int V, int c0,
                                 float *tile)
     {
+        static_assert(PER == BI, "a block's raw pieces fill exactly its register rows");
         const int tid = threadIdx.x, cq = tid % TPR, rg = tid / TPR;
+        float4 rawbuf[NR >= BI ? 1 : RAWN];
+        float4 *raw = NR >= BI ? st : rawbuf;
 #pragma unroll
         for (int b0 = 0; b0 < NR; b0 += BI) {
             const int k0 = b0 * RG;
@@ -162,9 +172,18 @@ struct TransposedSlab {
             for (int j = 0; j < PER; ++j) {
                 const int idx = tid + j * 256, vl = idx / Q, kq = idx % Q;
                 const int vv = c0 + vl, kk = k0 + 4 * kq;
-                float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (vv < V && kk < K)
-                    x = *reinterpret_cast<const float4 *>(base + static_cast<int64_t>(vv) * K + kk);
+                const int64_t off = (vv < V && kk < K) ? static_cast<int64_t>(vv) * K + kk : 0;
+                raw[b0 + j] = *reinterpret_cast<const float4 *>(base + off);
+            }
+        }
+#pragma unroll
+        for (int b0 = 0; b0 < NR; b0 += BI) {
+            const int k0 = b0 * RG;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int idx = tid + j * 256, vl = idx / Q, kq = idx % Q;
+                const int vv = c0 + vl, kk = k0 + 4 * kq;
+                const float4 x = (vv < V && kk < K) ? raw[b0 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
                 float *t = tile + vl * LD + 4 * kq;
                 t[0] = x.x; t[1] = x.y; t[2] = x.z; t[3] = x.w;
             }
