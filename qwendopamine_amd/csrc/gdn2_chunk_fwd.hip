@@ -838,41 +838,47 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 //    64-column slices without emission (0.241 vs 0.251 ms at
                 //    config 1).
                 constexpr bool DEEP = TRAIN || BV < 64;
-                if (nch > 1) {
-                    issue(pA, gc0 + 1);
-                    issue_z(fastc, zA, 1);
-                }
-                if (DEEP && nch > 2) {
-                    issue(pB, gc0 + 2);
-                    issue_z(fastc, zB, 2);
+                // Requests are issued unconditionally, past the last chunk for
+                // the last chunk again (data unused): with a request skipped on
+                // some paths the compiler cannot count the loads issued after
+                // the ones being landed and waits for all of them, which makes
+                // the prefetch synchronous.
+                auto cl = [&](int j) __attribute__((always_inline)) { return j < nch ? j : nch - 1; };
+                if (nch > 0) {
+                    issue(pA, gc0 + cl(1));
+                    issue_z(fastc, zA, cl(1));
+                    if (DEEP) {
+                        issue(pB, gc0 + cl(2));
+                        issue_z(fastc, zB, cl(2));
+                    }
                 }
                 __syncthreads();
                 for (int jc = 0; jc < nch; jc += 2) {
-                    if (!DEEP && jc + 2 < nch) {
-                        issue(pB, gc0 + jc + 2);
-                        issue_z(fastc, zB, jc + 2);
+                    if (!DEEP) {
+                        issue(pB, gc0 + cl(jc + 2));
+                        issue_z(fastc, zB, cl(jc + 2));
                     }
                     if (jc + 1 < nch) {
                         land_z(zA, jc + 1, 1);
                         land(pA, 1);
                     }
-                    if (DEEP && jc + 3 < nch) {
-                        issue(pA, gc0 + jc + 3);
-                        issue_z(fastc, zA, jc + 3);
+                    if (DEEP) {
+                        issue(pA, gc0 + cl(jc + 3));
+                        issue_z(fastc, zA, cl(jc + 3));
                     }
                     __syncthreads();
                     if (jc + 1 >= nch) break;
-                    if (!DEEP && jc + 3 < nch) {
-                        issue(pA, gc0 + jc + 3);
-                        issue_z(fastc, zA, jc + 3);
+                    if (!DEEP) {
+                        issue(pA, gc0 + cl(jc + 3));
+                        issue_z(fastc, zA, cl(jc + 3));
                     }
                     if (jc + 2 < nch) {
                         land_z(zB, jc + 2, 0);
                         land(pB, 0);
                     }
-                    if (DEEP && jc + 4 < nch) {
-                        issue(pB, gc0 + jc + 4);
-                        issue_z(fastc, zB, jc + 4);
+                    if (DEEP) {
+                        issue(pB, gc0 + cl(jc + 4));
+                        issue_z(fastc, zB, cl(jc + 4));
                     }
                     __syncthreads();
                 }
