@@ -58,10 +58,12 @@ enum gdn2_status {
 #define GDN2_FLAG_INPLACE_FINAL_STATE 32u /* gdn2_recurrent_fwd_ex with state  *
                                            * indices: per-token states go to    *
                                            * the indexed slots, not token rows  */
-#define GDN2_FLAG_SIGMOID_BW 64u /* recurrent calls: b and w hold the           *
-                                  * pre-activation logits; the kernel uses      *
-                                  * sigmoid(b), sigmoid(w) in fp32 (the module's *
-                                  * b_proj / w_proj activations, gdn2.py:864-865)*/
+#define GDN2_FLAG_SIGMOID_BW 64u /* recurrent calls and gdn2_chunk_fwd (not    *
+                                  * with SAVE_FOR_BWD, not gdn2_chunk_fwd_prep): *
+                                  * b and w hold the pre-activation logits; the  *
+                                  * kernels use sigmoid(b), sigmoid(w) in fp32   *
+                                  * (the module's b_proj / w_proj activations,   *
+                                  * gdn2.py:864-865)                             */
 
 int gdn2_abi_version(void);
 const char *gdn2_status_string(int status);

@@ -19,11 +19,13 @@ static int check_chunk_args(int io_dtype, int g_dtype, const int64_t *cu_seqlens
     if (!valid_dtype(io_dtype) || !valid_dtype(g_dtype)) return GDN2_ERR_INVALID;
     if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
     if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND |
-                  GDN2_FLAG_SAVE_FOR_BWD | GDN2_FLAG_TRANSPOSE_STATE))
+                  GDN2_FLAG_SAVE_FOR_BWD | GDN2_FLAG_TRANSPOSE_STATE | GDN2_FLAG_SIGMOID_BW))
         return GDN2_ERR_INVALID;
     if ((flags & GDN2_FLAG_LOWER_BOUND) && !(flags & GDN2_FLAG_GATE_IN_KERNEL))
         return GDN2_ERR_INVALID;
     if ((flags & GDN2_FLAG_GATE_IN_KERNEL) && !A_log) return GDN2_ERR_INVALID;
+    // Gate logits are an inference option: the backward reads b and w as given.
+    if ((flags & GDN2_FLAG_SIGMOID_BW) && (flags & GDN2_FLAG_SAVE_FOR_BWD)) return GDN2_ERR_INVALID;
     if ((cu_seqlens == nullptr) != (cu_seqlens_host == nullptr)) return GDN2_ERR_INVALID;
     if (cu_seqlens && (B != 1 || num_seqs < 0)) return GDN2_ERR_INVALID;
     if (cu_seqlens_host) {
@@ -260,6 +262,8 @@ int gdn2_chunk_fwd_prep(const void *q, const void *k, const void *g, const void 
     const int st = check_chunk_args(io_dtype, g_dtype, cu_seqlens, cu_seqlens_host, num_seqs, B,
                                     T, H, K, V, flags, A_log);
     if (st != GDN2_OK) return st;
+    // The separate scan entry point has no flags, so w could not be activated there.
+    if (flags & GDN2_FLAG_SIGMOID_BW) return GDN2_ERR_INVALID;
     if (static_cast<int64_t>(B) * T > 0 && (!q || !k || !g || !b)) return GDN2_ERR_INVALID;
     fill_chunk_args(a, q, k, nullptr, g, b, nullptr, nullptr, nullptr, nullptr, A_log, dt_bias,
                     lower_bound, cu_seqlens, cu_seqlens_host, num_seqs, B, T, H, K, V, scale,

@@ -50,6 +50,18 @@ namespace gdn2 {
 
 namespace {
 
+// x rounded to T (nearest even) and back to fp32.
+template <typename T>
+__device__ __forceinline__ float round_to(float x)
+{
+    if constexpr (std::is_same<T, bf16_t>::value)
+        return bf16_bits_to_f32(f32_to_bf16_bits(x));
+    else if constexpr (std::is_same<T, f16_t>::value)
+        return static_cast<float>(static_cast<_Float16>(x));
+    else
+        return x;
+}
+
 // Four consecutive input values kept as the input dtype's bits (two registers
 // for 16-bit inputs, half of what fp32 values take) and widened to fp32 where
 // they are used.
@@ -94,6 +106,25 @@ struct Raw4 {
             } else {
                 u[i] = reinterpret_cast<const uint32_t *>(base)[off + c0 + i];
             }
+        }
+    }
+    // Four fp32 values into the input dtype's bits (rounded to nearest even).
+    __device__ __forceinline__ void set(const float (&x)[4])
+    {
+        if constexpr (W == 2) {
+            uint16_t h[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (std::is_same<T, bf16_t>::value)
+                    h[i] = f32_to_bf16_bits(x[i]);
+                else
+                    h[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x[i]));
+            }
+            u[0] = h[0] | (static_cast<uint32_t>(h[1]) << 16);
+            u[1] = h[2] | (static_cast<uint32_t>(h[3]) << 16);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) u[i] = __float_as_uint(x[i]);
         }
     }
     __device__ __forceinline__ void unpack(float (&x)[4]) const
@@ -306,6 +337,18 @@ chunk_prep_kernel(ChunkParams p, int items)
                 kr[kt].load_checked(k, roff, c0, K, row_ok, p.vec_ok);
                 br[kt].load_checked(b, roff, c0, K, row_ok, p.vec_ok);
                 load4<TG>(g, roff, c0, K, row_ok, p.vec_ok, gv[kt]);
+            }
+        }
+        // b given as logits: activated once here and rounded to the input
+        // dtype, as the module's torch sigmoid of b_proj(x) is (gdn2.py:864).
+        if (p.flags & GDN2_FLAG_SIGMOID_BW) {
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) {
+                float x[4];
+                br[kt].unpack(x);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[i] = sigmoid_f(x[i]);
+                br[kt].set(x);
             }
         }
 
@@ -612,7 +655,7 @@ chunk_prep_kernel(ChunkParams p, int items)
 // ---------------------------------------------------------------------------
 // Scan: one workgroup per (sequence, head, value slice of BV columns).
 // ---------------------------------------------------------------------------
-template <PrecKind PK, int KP, int BV, typename TI, bool TRAIN>
+template <PrecKind PK, int KP, int BV, typename TI, bool TRAIN, bool SIGW = false>
 __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB, int NP)
 {
     using P = Prec<PK>;
@@ -754,6 +797,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             }
         }
     };
+    // SIGW (GDN2_FLAG_SIGMOID_BW, inference only): w holds the logits.
     auto land_z = [&](const ZRaw &r, int jc, int buf) __attribute__((always_inline)) {
         int64_t t0;
         int lc;
@@ -769,8 +813,11 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             const int kt = tok >> 4, kgz = (tok & 15) >> 2, iz = tok & 3;
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
-                // Zero past the sequence end (and past V, zero-filled by issue_z).
-                const float z = tok < lc ? io<TI>::ld(rv, e) * io<TI>::ld(rw, e) : 0.f;
+                // Zero past the sequence end (and past V, zero-filled by issue_z);
+                // w given as logits is activated here and rounded to the input
+                // dtype, as the module's torch sigmoid of w_proj(x) is (gdn2.py:865).
+                const float wv_ = SIGW ? round_to<TI>(sigmoid_f(io<TI>::ld(rw, e))) : io<TI>::ld(rw, e);
+                const float z = tok < lc ? io<TI>::ld(rv, e) * wv_ : 0.f;
                 const int cl = c + e, ct = cl >> 4, nz = cl & 15;
                 dst[(kt * 4 + ct) * 256 + (nz + 16 * kgz) * 4 + iz] = P::from_f32(z);
             }
@@ -1128,6 +1175,9 @@ hipError_t launch_scan(const ChunkParams &p, int BVsel, hipStream_t stream)
         const int NVB = (p.V + BV - 1) / BV;
         if (p.hs)
             hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI, true>), dim3(groups * 8 * NVB),
+                               dim3(512), 0, stream, p, NVB, NP);
+        else if (p.flags & GDN2_FLAG_SIGMOID_BW)  // never with the training workspace
+            hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI, false, true>), dim3(groups * 8 * NVB),
                                dim3(512), 0, stream, p, NVB, NP);
         else
             hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI, false>), dim3(groups * 8 * NVB),

@@ -495,13 +495,7 @@ class GatedDeltaNet2(nn.Module):
         gate_kw: dict = {}
         if fuse:
             A_log, dt_bias = self._gate_params(rep)
-            gate_kw = dict(use_gate_in_kernel=True, A_log=A_log, dt_bias=dt_bias)
-            if algo == "chunk":
-                # The chunk kernels take activated b and w (one elementwise pass
-                # each, small next to a prefill).
-                b, w = b.sigmoid(), w.sigmoid()
-            else:
-                gate_kw["bw_logits"] = True
+            gate_kw = dict(use_gate_in_kernel=True, A_log=A_log, dt_bias=dt_bias, bw_logits=True)
         b, w, v, k = b.to(dt), w.to(dt), v.to(dt), k.to(dt)
         if algo == "chunk":
             o, recurrent_state = ops.chunk_gdn2(

@@ -353,6 +353,7 @@ def chunk_gdn2_fwd(
     save_for_bwd: bool = False,
     transpose_state_layout: bool = False,
     return_intermediate_states: bool = False,
+    bw_logits: bool = False,
 ):
     """Launch the chunkwise HIP forward (reference ``chunk_gdn2.py:1165-1264``).
 
@@ -362,7 +363,9 @@ def chunk_gdn2_fwd(
     * ``save_for_bwd`` appends ``saved``: the inputs as the kernels read them, plus the training
       workspace that ``chunk_gdn2_bwd`` consumes.
 
-    ``transpose_state_layout`` makes every state ``[.., V, K]``.
+    ``transpose_state_layout`` makes every state ``[.., V, K]``. ``bw_logits`` passes ``b`` and
+    ``w`` as the pre-activation logits, activated in-kernel (forward only: not with the
+    saved training workspace).
     """
     name = "chunk_gdn2"
     _require_gpu(name, q, k, v, g, b, w, initial_state)
@@ -396,6 +399,11 @@ def chunk_gdn2_fwd(
         raise NotImplementedError(f"{name}: apply the gate before the op when gradients are needed")
     if keep:
         flags |= nat.FLAG_SAVE_FOR_BWD
+    if bw_logits:
+        if keep:
+            raise NotImplementedError(f"{name}: bw_logits is a forward-only option; activate b and w "
+                                      "before the op when the training workspace is kept")
+        flags |= nat.FLAG_SIGMOID_BW
     st = lib.gdn2_chunk_fwd(
         nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(g), nat.ptr(b), nat.ptr(w),
         nat.dtype_code(dt), nat.dtype_code(g.dtype), nat.ptr(o),
@@ -536,6 +544,8 @@ def chunk_gdn2(
     if scale is None:
         scale = k.shape[-1] ** -0.5
     _require_gpu("chunk_gdn2", q, k, v, g, b, w, initial_state)
+    if return_intermediate_states and kwargs.get("bw_logits", False):
+        b, w = b.sigmoid(), w.sigmoid()  # the intermediate states use the training workspace
     if return_intermediate_states:
         assert torch.is_inference_mode_enabled(), (
             "return_intermediate_states is only allowed in inference mode"
@@ -549,12 +559,24 @@ def chunk_gdn2(
             transpose_state_layout=transpose_state_layout, return_intermediate_states=True,
         )
         return o.type_as(q), ht, h
-    if use_gate_in_kernel and torch.is_grad_enabled() and any(
+    needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (q, k, v, g, b, w, A_log, dt_bias, initial_state)
-    ):
+    )
+    if use_gate_in_kernel and needs_grad:
         # Differentiable gate in torch, then the kernels on the activated decay.
         g = gate_activation(g, A_log, dt_bias, lower_bound)
         use_gate_in_kernel, A_log, dt_bias, lower_bound = False, None, None, None
+    if kwargs.get("bw_logits", False):
+        # b and w given as logits (an extension of this backend): activated in the
+        # kernels when no gradient is needed, by torch otherwise.
+        if not needs_grad:
+            o, ht = chunk_gdn2_fwd(
+                q, k, v, g, b, w, scale, initial_state, output_final_state, use_qk_l2norm_in_kernel,
+                use_gate_in_kernel, A_log, dt_bias, lower_bound, cu_seqlens,
+                transpose_state_layout=transpose_state_layout, bw_logits=True,
+            )
+            return o.type_as(q), ht
+        b, w = b.sigmoid(), w.sigmoid()
     return ChunkGDN2Function.apply(
         q, k, v, g, b, w, A_log, dt_bias, scale, initial_state, output_final_state,
         use_qk_l2norm_in_kernel, use_gate_in_kernel, cu_seqlens, lower_bound, transpose_state_layout,

@@ -122,3 +122,55 @@ def test_return_intermediate_states_needs_inference_mode(gpu_device):
     t, _ = to_device(inp, gpu_device, torch.float32)
     with pytest.raises(AssertionError):
         chunk_gdn2(*(t[n] for n in NAMES), return_intermediate_states=True)
+
+
+@pytest.mark.parametrize("dtype,K,V,T", [(torch.float32, 64, 48, 150), (torch.bfloat16, 128, 128, 130)])
+def test_chunk_sigmoid_bw_logits(gpu_device, dtype, K, V, T):
+    """b and w passed to the chunk op as logits (GDN2_FLAG_SIGMOID_BW), with the in-kernel
+    gate: the module's fused prefill path. The oracle gets sigmoid(b), sigmoid(w) of the
+    same rounded logits in float64; the kernels activate them in fp32 without rounding."""
+    from qwendopamine_amd.ops import chunk_gdn2
+
+    print(f"[case] chunk sigmoid b/w {dtype} K={K} V={V} T={T}", flush=True)
+    B, H = 2, 2
+    inp = rand_inputs(B, T, H, K, V, seed=111)
+    rng = np.random.default_rng(112)
+    bl, wl = rng.standard_normal((B, T, H, K)) * 2, rng.standard_normal((B, T, H, V)) * 2
+    graw = rng.standard_normal((B, T, H, K))
+    A_log = np.log(rng.uniform(1, 16, H))
+    dt_bias = rng.standard_normal(H * K) * 0.5
+    g = -np.exp(A_log)[:, None] * np.logaddexp(0.0, graw + dt_bias.reshape(H, K))
+    inp.update(b=bl, w=wl, g=graw)
+    t, r = to_device(inp, gpu_device, dtype)
+    t["g"] = torch.from_numpy(graw).to(gpu_device, torch.float32)
+    with torch.no_grad():
+        o, ht = chunk_gdn2(
+            *(t[n] for n in NAMES), initial_state=t["h0"].float(), output_final_state=True,
+            use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+            A_log=torch.tensor(A_log, dtype=torch.float32, device=gpu_device),
+            dt_bias=torch.tensor(dt_bias, dtype=torch.float32, device=gpu_device), bw_logits=True,
+        )
+    torch.cuda.synchronize()
+    sig = lambda x: 1.0 / (1.0 + np.exp(-x))  # noqa: E731
+    o_ref, s_ref = orc.recurrent_fwd(r["q"], r["k"], r["v"], g, sig(r["b"]), sig(r["w"]), r["h0"])
+    assert rel_l2(o, o_ref) <= REL_TOL[dtype]
+    assert rel_l2(ht, s_ref) <= REL_TOL[dtype]
+
+
+def test_chunk_sigmoid_bw_logits_rejected_with_training_workspace(gpu_device):
+    """The logits option is forward-only: the C ABI refuses it together with the saved
+    training workspace, and the separate prep entry point (whose scan has no flags) refuses
+    it outright."""
+    from qwendopamine_amd import _native as nat
+    from qwendopamine_amd.ops import chunk_gdn2_fwd
+
+    inp = rand_inputs(1, 70, 2, 32, 32, seed=113)
+    t, _ = to_device(inp, gpu_device, torch.float32)
+    with pytest.raises(NotImplementedError):
+        chunk_gdn2_fwd(*(t[n] for n in NAMES), 32 ** -0.5, None, False, True,
+                       save_for_bwd=True, bw_logits=True)
+    lib = nat.load()
+    st = lib.gdn2_chunk_fwd_prep(None, None, None, None, nat.DTYPE_F32, nat.DTYPE_F32, None, None,
+                                 0.0, None, None, 1, 1, 0, 2, 32, 32, 1.0, nat.FLAG_SIGMOID_BW,
+                                 None, 0, None)
+    assert st == nat.ERR_INVALID

@@ -149,13 +149,15 @@ def test_transposed_state_pool_decode(gpu_device):
     _check_pool(ht, st_ref, written, 2e-2, untouched_from=pool)
 
 
-def test_gva_gate_in_kernel_by_key_head(gpu_device):
+@pytest.mark.parametrize("B,T,K,V", [(2, 6, 32, 32), (3, 1, 128, 128)])
+def test_gva_gate_in_kernel_by_key_head(gpu_device, B, T, K, V):
     """Grouped value heads with the in-kernel gate: A_log / dt_bias are indexed by key head,
-    as the reference kernel does (fused_recurrent_gdn2.py:259-265)."""
+    as the reference kernel does (fused_recurrent_gdn2.py:259-265).  T = 1 with K = V = 128
+    runs the decode-step kernel with an initial state (12 slabs over 6 workgroups)."""
     from qwendopamine_amd.ops import fused_recurrent_gdn2_fwd
 
-    print("[case] GVA gate in kernel", flush=True)
-    B, T, H, HV, K, V = 2, 6, 2, 4, 32, 32
+    print(f"[case] GVA gate in kernel B={B} T={T} K={K} V={V}", flush=True)
+    H, HV = 2, 4
     inp = rand_inputs(B, T, H, K, V, HV=HV, seed=81)
     rng = np.random.default_rng(82)
     graw = rng.standard_normal((B, T, HV, K))
