@@ -148,6 +148,19 @@ int gdn2_short_conv_fwd(int ntensors, const void *const *x, const void *const *w
                         int B, int T, int W, int silu, void *stream);
 
 /*
+ * gdn2_short_conv_fwd with strided input rows: row (b, t) of x_i starts at
+ * x_i + (b*T + t) * x_row_stride[i] elements (x_row_stride[i] >= D_i; NULL =
+ * contiguous rows).  It lets q, k and v be column ranges of one fused input
+ * projection's output, as the module's inference path produces them, with no
+ * copies.  Same reference function as gdn2_short_conv_fwd (gdn2.py:395-430).
+ */
+int gdn2_short_conv_fwd_ex(int ntensors, const void *const *x, const int64_t *x_row_stride,
+                           const void *const *weight, const void *const *bias,
+                           const void *const *cache_in, void *const *cache_out, void *const *y,
+                           const int *dims, int io_dtype, int B, int T, int W, int silu,
+                           void *stream);
+
+/*
  * Gated RMS norm of the mixer's epilogue.  Replaces RMSNormGated.forward
  * (reference gdn2.py:433-452): for each of `rows` rows of N values,
  *   out = x * rsqrt(mean(x^2) + eps) * weight * silu(z)

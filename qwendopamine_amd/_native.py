@@ -61,6 +61,9 @@ SIGNATURES: dict[str, tuple] = {
     "gdn2_short_conv_fwd": (
         _i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     ),
+    "gdn2_short_conv_fwd_ex": (
+        _i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    ),
     "gdn2_gated_rmsnorm_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i64, _i, _f, _vp]),
     "gdn2_chunk_states": (_i, [_vp, _sz, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "gdn2_chunk_fwd_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _vp, _i]),

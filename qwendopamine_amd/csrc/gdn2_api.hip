@@ -179,6 +179,15 @@ int gdn2_short_conv_fwd(int ntensors, const void *const *x, const void *const *w
                         void *const *cache_out, void *const *y, const int *dims, int io_dtype,
                         int B, int T, int W, int silu, void *stream)
 {
+    return gdn2_short_conv_fwd_ex(ntensors, x, nullptr, weight, bias, cache_in, cache_out, y, dims,
+                                  io_dtype, B, T, W, silu, stream);
+}
+
+int gdn2_short_conv_fwd_ex(int ntensors, const void *const *x, const int64_t *x_row_stride,
+                           const void *const *weight, const void *const *bias,
+                           const void *const *cache_in, void *const *cache_out, void *const *y,
+                           const int *dims, int io_dtype, int B, int T, int W, int silu, void *stream)
+{
     if (!valid_dtype(io_dtype)) return GDN2_ERR_INVALID;
     if (ntensors < 1 || ntensors > 3 || !x || !weight || !y || !dims) return GDN2_ERR_INVALID;
     if (B < 0 || T < 0 || W < 1) return GDN2_ERR_INVALID;
@@ -193,6 +202,8 @@ int gdn2_short_conv_fwd(int ntensors, const void *const *x, const void *const *w
         ConvTensor &c = p.t[i];
         c.D = dims[j];
         if (c.D <= 0) return GDN2_ERR_INVALID;
+        c.ldx = x_row_stride ? x_row_stride[j] : c.D;
+        if (c.ldx < c.D) return GDN2_ERR_INVALID;
         if (B * static_cast<int64_t>(T) > 0 && (!x[j] || !weight[j] || !y[j])) return GDN2_ERR_INVALID;
         c.x = x[j]; c.w = weight[j]; c.y = y[j];
         c.bias = bias ? bias[j] : nullptr;

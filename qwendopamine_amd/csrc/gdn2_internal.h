@@ -87,13 +87,14 @@ hipError_t launch_chunk_states(const void *hs, int io_dtype, void *out, bool tra
 
 // Short convolution (prologue): up to three tensors per launch.
 struct ConvTensor {
-    const void *x;          // [B, T, D]
+    const void *x;          // [B, T, D]: row (b, t) at x + (b * T + t) * ldx
     const void *w;          // [D, W]
     const void *bias;       // [D] or NULL
     const void *cache_in;   // [B, D, W-1] or NULL (read on single-token calls)
     void *cache_out;        // [B, D, ncache] or NULL
     void *y;                // [B, T, D]
     int D;
+    int64_t ldx;            // input row stride in elements (>= D)
 };
 
 struct ConvParams {

@@ -76,14 +76,14 @@ __global__ __launch_bounds__(256) void short_conv_kernel(ConvParams p, int TT)
         const int tt = t0 - (W - 1) + j;
         float v = 0.0f;
         if (tt >= 0)
-            v = io<T>::ld(x, (row0 + tt) * D + d);
+            v = io<T>::ld(x, (row0 + tt) * ct.ldx + d);
         else if (p.T == 1 && ct.cache_in)
             v = io<T>::ld(static_cast<const T *>(ct.cache_in),
                           (static_cast<int64_t>(b) * D + d) * (W - 1) + (W - 1 + tt));
         hist[j] = v;
     }
     for (int t = t0; t < t1; ++t) {
-        hist[W - 1] = io<T>::ld(x, (row0 + t) * D + d);
+        hist[W - 1] = io<T>::ld(x, (row0 + t) * ct.ldx + d);
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < W; ++j) acc = fmaf(wt[j], hist[j], acc);
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(64) void short_conv_vec_kernel(ConvParams p)
     for (int r = 0; r < W - 1 + TT; ++r) {
         const int tt = t0 - (W - 1) + r;
         const int tc = tt < 0 ? 0 : (tt < p.T ? tt : p.T - 1);
-        VT::load(x + (row0 + tc) * D + d0, xin[r]);
+        VT::load(x + (row0 + tc) * ct.ldx + d0, xin[r]);
     }
     // The group's weights [CPT][W] are W contiguous 16-byte pieces.
     float wflat[W][CPT], wt[W][CPT], bias[CPT];
@@ -363,7 +363,7 @@ hipError_t conv_t(const ConvParams &p, int maxD, int ntensors, hipStream_t s)
     bool vec = true;
     for (int i = 0; i < ntensors; ++i) {
         const ConvTensor &c = p.t[i];
-        vec = vec && c.D % CPT == 0 &&
+        vec = vec && c.D % CPT == 0 && c.ldx % CPT == 0 &&
               ((reinterpret_cast<uintptr_t>(c.x) | reinterpret_cast<uintptr_t>(c.y) |
                 reinterpret_cast<uintptr_t>(c.w) | reinterpret_cast<uintptr_t>(c.bias)) & 15) == 0;
     }

@@ -399,6 +399,19 @@ class GatedDeltaNet2(nn.Module):
             self._gate_cache = cached
         return cached[1], cached[2]
 
+    def _fused_input_weight(self) -> tuple[torch.Tensor, list[int]]:
+        """The first-stage input projections stacked as one weight, ``[q; k; v; b; w;
+        f_proj[0]; g_proj[0]]`` (none has a bias), and their output widths.  Used by the
+        inference path for a single GEMM; cached until any of the weights changes."""
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.b_proj.weight,
+              self.w_proj.weight, self.f_proj[0].weight, self.g_proj[0].weight)
+        key = tuple((t.data_ptr(), t._version, t.dtype) for t in ws)
+        cached = getattr(self, "_in_cache", None)
+        if cached is None or cached[0] != key:
+            cached = (key, torch.cat([t.detach() for t in ws], dim=0), [int(t.shape[0]) for t in ws])
+            self._in_cache = cached
+        return cached[1], cached[2]
+
     def _algorithm(self, mode: str, backend: str, needs_grad: bool) -> str:
         if backend in ("torch-chunk", "compiled"):
             algo = "chunk"
@@ -446,8 +459,24 @@ class GatedDeltaNet2(nn.Module):
             hidden_states = _index_first_axis(hidden_states, indices).unsqueeze(0)
 
         x = hidden_states
+        # Inference with the in-kernel activations: g, b and w go to the kernels
+        # as raw projections (see below).
+        fuse = (_inference(x, self.A_log, self.dt_bias, self.f_proj[1].weight, self.b_proj.weight,
+                           self.w_proj.weight)
+                and self.fp32_decay and not self.allow_neg_eigval)
         convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d) if self.use_short_conv else ()
-        if self.use_short_conv and _inference(x, *(c.conv1d.weight for c in convs)):
+        g0 = None
+        if fuse and self.use_short_conv and _inference(x, *(c.conv1d.weight for c in convs)):
+            # The seven first-stage input projections as one GEMM; q, k and v
+            # are convolved in place as column ranges of its output.
+            W_in, sizes = self._fused_input_weight()
+            qr, kr, vr, b, w, f0, g0 = F.linear(x, W_in).split(sizes, dim=-1)
+            (q, k, v), new = ops.short_convolution(
+                [qr, kr, vr], [c.conv1d.weight for c in convs], [c.conv1d.bias for c in convs],
+                None if cq is None else [cq, ck, cv], want_state, self.q_conv1d.activation)
+            cq, ck, cv = new if new is not None else (None, None, None)
+            g = self.f_proj[1](f0)
+        elif self.use_short_conv and _inference(x, *(c.conv1d.weight for c in convs)):
             # q, k and v convolutions in one launch.
             raw = [self.q_proj(x), self.k_proj(x), self.v_proj(x)]
             (q, k, v), new = ops.short_convolution(
@@ -464,12 +493,10 @@ class GatedDeltaNet2(nn.Module):
         # Decay g = -exp(A_log) * softplus(f_proj(x) + dt_bias), always in fp32;
         # b = sigmoid(b_proj(x)), w = sigmoid(w_proj(x)) (gdn2.py:840-866).  In
         # inference these activations run inside the kernels on the raw
-        # projections (same fp32 formula for g; b and w are not rounded to the
-        # input dtype in between).
-        fuse = (_inference(x, self.A_log, self.dt_bias, self.f_proj[1].weight, self.b_proj.weight,
-                           self.w_proj.weight)
-                and self.fp32_decay and not self.allow_neg_eigval)
-        if fuse:
+        # projections (same fp32 formula for g).
+        if g0 is not None:
+            pass  # g, b, w came from the fused projection above
+        elif fuse:
             g, b, w = self.f_proj(x), self.b_proj(x), self.w_proj(x)
         else:
             A = self.A_log.float().exp().repeat_interleave(self.head_k_dim)
@@ -512,7 +539,7 @@ class GatedDeltaNet2(nn.Module):
             self._update_cache(past_key_values, recurrent_state,
                                (cq, ck, cv) if self.use_short_conv else None)
 
-        gate = _split_heads(self.g_proj(x), self.head_v_dim)
+        gate = _split_heads(self.g_proj(x) if g0 is None else self.g_proj[1](g0), self.head_v_dim)
         o = self.o_norm(o, gate)
         out = self.o_proj(o.reshape(*o.shape[:-2], -1))
         if padded:

@@ -131,7 +131,23 @@ class SwiGLU(nn.Module):
         self.w3 = nn.Linear(hidden, n_embd, bias=bias)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.w3(F.silu(self.w1(x)) * self.w2(x))
+        if torch.is_grad_enabled() and any(t.requires_grad for t in (x, self.w1.weight, self.w2.weight)):
+            return self.w3(F.silu(self.w1(x)) * self.w2(x))
+        # Inference: w1 and w2 as one GEMM (the same dot products, one launch).
+        a, b = F.linear(x, *self._fused12()).chunk(2, dim=-1)
+        return self.w3(F.silu(a) * b)
+
+    def _fused12(self) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """[w1; w2] weights (and biases), cached until either changes."""
+        ps = [self.w1.weight, self.w2.weight] + ([self.w1.bias, self.w2.bias] if self.w1.bias is not None else [])
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in ps)
+        cached = getattr(self, "_cache12", None)
+        if cached is None or cached[0] != key:
+            w = torch.cat([self.w1.weight.detach(), self.w2.weight.detach()], dim=0)
+            bias = None if self.w1.bias is None else torch.cat([self.w1.bias.detach(), self.w2.bias.detach()])
+            cached = (key, w, bias)
+            self._cache12 = cached
+        return cached[1], cached[2]
 
 
 class LLaMAMLP(nn.Module):

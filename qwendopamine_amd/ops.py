@@ -608,6 +608,9 @@ def short_convolution(
     * a single-token call convolves the cache ``[B, D, W-1]`` followed by the new token;
     * with ``output_final_state`` the new cache holds the last ``min(T, W-1)`` inputs (``W-1`` when ``T == 1``).
 
+    Inputs may be column ranges of a wider ``[B, T, N]`` tensor (unit channel stride, rows
+    ``stride(1)`` apart): they are read in place, with no copy.
+
     Returns ``(ys, new_caches)``. Inference only: there is no backward.
     """
     name = "short_convolution"
@@ -620,10 +623,23 @@ def short_convolution(
     W = int(weights[0].shape[-1])
     if activation not in (None, "silu"):
         raise NotImplementedError(f"{name}: activation {activation!r}")
-    xs = [x.to(dt).contiguous() for x in xs]
     for x in xs:
         if x.dim() != 3 or tuple(x.shape[:2]) != (B, T):
             raise ValueError(f"{name}: inputs must share [B, T, D]; got {tuple(x.shape)}")
+
+    def row_stride(x: torch.Tensor) -> int | None:
+        """Element distance of consecutive (b, t) rows, or None if rows are not evenly spaced."""
+        if x.dtype != dt or x.stride(2) != 1:
+            return None
+        if T > 1:
+            ok = x.stride(1) >= x.shape[2] and (B <= 1 or x.stride(0) == T * x.stride(1))
+            return x.stride(1) if ok else None
+        if B > 1:
+            return x.stride(0) if x.stride(0) >= x.shape[2] else None
+        return x.shape[2]
+
+    xs = [x if row_stride(x) is not None else x.to(dt).contiguous() for x in xs]
+    ldx = (ctypes.c_int64 * 3)(*([row_stride(x) for x in xs] + [0] * (3 - n)))
     dims = [x.shape[2] for x in xs]
     ws = [w.detach().reshape(d, W).to(dt).contiguous() for w, d in zip(weights, dims)]
     bs = None
@@ -641,8 +657,8 @@ def short_convolution(
     ys = [torch.empty_like(x) for x in xs]
     dims_arr = (ctypes.c_int * 3)(*(dims + [dims[0]] * (3 - n)))
     lib = nat.load()
-    st = lib.gdn2_short_conv_fwd(
-        n, _ptr_array([nat.ptr(x) for x in xs]), _ptr_array([nat.ptr(w) for w in ws]),
+    st = lib.gdn2_short_conv_fwd_ex(
+        n, _ptr_array([nat.ptr(x) for x in xs]), ctypes.addressof(ldx), _ptr_array([nat.ptr(w) for w in ws]),
         None if bs is None else _ptr_array([nat.ptr(b_) for b_ in bs]),
         None if cs is None else _ptr_array([nat.ptr(c) for c in cs]),
         None if new is None else _ptr_array([nat.ptr(c) for c in new]),

@@ -155,3 +155,28 @@ def test_module_inference_prologue_matches_training_path(gpu_device):
     torch.cuda.synchronize()
     assert rel_l2(out_a, out_b.detach()) <= 2e-2
     assert rel_l2(step_a, step_b.detach()) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,T,with_cache", [(3, 130, False), (4, 1, True), (1, 37, False)])
+def test_short_conv_reads_column_ranges_in_place(gpu_device, dtype, B, T, with_cache):
+    """q, k and v as column ranges of one wider [B, T, N] tensor (the module's fused input
+    projection) give bit-identical outputs and caches to contiguous copies of them."""
+    from qwendopamine_amd.ops import short_convolution
+
+    print(f"[case] strided conv {dtype} B={B} T={T} cache={with_cache}", flush=True)
+    W, dims = 4, (64, 64, 96)
+    gen = torch.Generator(device=gpu_device).manual_seed(7)
+    wide = torch.randn(B, T, sum(dims) + 40, generator=gen, device=gpu_device).to(dtype)
+    offs = np.cumsum((0,) + dims[:-1])
+    views = [wide[..., o:o + d] for o, d in zip(offs, dims)]
+    assert not views[1].is_contiguous()
+    ws = [torch.randn(d, 1, W, generator=gen, device=gpu_device).to(dtype) * 0.3 for d in dims]
+    bs = [torch.randn(d, generator=gen, device=gpu_device).to(dtype) * 0.1 for d in dims]
+    caches = [torch.randn(B, d, W - 1, generator=gen, device=gpu_device).to(dtype) for d in dims] \
+        if with_cache else None
+    ys, new = short_convolution(views, ws, bs, caches, True)
+    ys_ref, new_ref = short_convolution([v.contiguous() for v in views], ws, bs, caches, True)
+    torch.cuda.synchronize()
+    for a, b in zip(ys + new, ys_ref + new_ref):
+        assert torch.equal(a, b)
