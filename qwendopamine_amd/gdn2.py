@@ -470,12 +470,15 @@ class GatedDeltaNet2(nn.Module):
             # The seven first-stage input projections as one GEMM; q, k and v
             # are convolved in place as column ranges of its output.
             W_in, sizes = self._fused_input_weight()
-            qr, kr, vr, b, w, f0, g0 = F.linear(x, W_in).split(sizes, dim=-1)
+            y = F.linear(x.reshape(-1, x.shape[-1]), W_in)  # [tokens, sum(sizes)]
+            qr, kr, vr, b, w, f0, g0 = (t.view(*x.shape[:-1], -1) if i < 5 else t
+                                        for i, t in enumerate(y.split(sizes, dim=-1)))
             (q, k, v), new = ops.short_convolution(
                 [qr, kr, vr], [c.conv1d.weight for c in convs], [c.conv1d.bias for c in convs],
                 None if cq is None else [cq, ck, cv], want_state, self.q_conv1d.activation)
             cq, ck, cv = new if new is not None else (None, None, None)
-            g = self.f_proj[1](f0)
+            # The low-rank second stages read their 2-D column ranges in place.
+            g = self.f_proj[1](f0).view(*x.shape[:-1], -1)
         elif self.use_short_conv and _inference(x, *(c.conv1d.weight for c in convs)):
             # q, k and v convolutions in one launch.
             raw = [self.q_proj(x), self.k_proj(x), self.v_proj(x)]
@@ -539,7 +542,8 @@ class GatedDeltaNet2(nn.Module):
             self._update_cache(past_key_values, recurrent_state,
                                (cq, ck, cv) if self.use_short_conv else None)
 
-        gate = _split_heads(self.g_proj(x) if g0 is None else self.g_proj[1](g0), self.head_v_dim)
+        gate = _split_heads(self.g_proj(x) if g0 is None else self.g_proj[1](g0).view(*x.shape[:-1], -1),
+                            self.head_v_dim)
         o = self.o_norm(o, gate)
         out = self.o_proj(o.reshape(*o.shape[:-2], -1))
         if padded:
