@@ -167,6 +167,9 @@ int gdn2_short_conv_fwd_ex(int ntensors, const void *const *x, const int64_t *x_
  * with the reference's rounding to io_dtype after every op.  weight [N] is
  * io_dtype, or float32 (weight_dtype = GDN2_DTYPE_F32), in which case torch's
  * promotion makes the last two products and `out` float32.
+ * z = NULL drops the gate: out = weight * (x * rsqrt(mean(x^2) + eps)), the
+ * plain RMSNorm.forward of the decoder hosts (reference
+ * models/normalization.py:40-51), with the same rounding.  N <= 2048.
  */
 int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int weight_dtype,
                            void *out, int io_dtype, int64_t rows, int N, float eps, void *stream);

@@ -385,6 +385,14 @@ def gated_rmsnorm(x, z, weight, eps=1e-5):
     return x * inv * np.asarray(weight, dtype=np.float64) * (z / (1.0 + np.exp(-z)))
 
 
+def rmsnorm(x, weight, eps=1e-5):
+    r"""``weight * x * rsqrt(mean(x^2) + eps)`` over the last axis, float64
+    (models/normalization.py:40-51): the gated norm without its gate."""
+    x = np.asarray(x, dtype=np.float64)
+    inv = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
+    return x * inv * np.asarray(weight, dtype=np.float64)
+
+
 def _l2norm_vjp(x_raw, dy, eps=L2_EPS):
     """VJP of ``y = x / max(||x||, eps)`` over the last axis."""
     n = np.sqrt((x_raw * x_raw).sum(-1, keepdims=True))

@@ -222,9 +222,9 @@ int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int
     if (!valid_dtype(io_dtype) || !valid_dtype(weight_dtype)) return GDN2_ERR_INVALID;
     if (weight_dtype != io_dtype && weight_dtype != GDN2_DTYPE_F32) return GDN2_ERR_INVALID;
     if (rows < 0 || N <= 0) return GDN2_ERR_INVALID;
-    if (N > 512) return GDN2_ERR_UNSUPPORTED;
+    if (N > 2048) return GDN2_ERR_UNSUPPORTED;
     if (rows == 0) return GDN2_OK;
-    if (!x || !z || !weight || !out) return GDN2_ERR_INVALID;
+    if (!x || !weight || !out) return GDN2_ERR_INVALID;  // z may be NULL: no gate
     if ((rows + 3) / 4 > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
     NormParams p;
     p.x = x; p.z = z; p.weight = weight; p.out = out;

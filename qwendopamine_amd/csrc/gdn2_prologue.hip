@@ -6,7 +6,9 @@
 //    the token axis, plus bias and SiLU, for up to three tensors (q, k, v)
 //    in one launch, with the reference's conv-cache semantics.
 //  * gated_rmsnorm_kernel -- RMSNormGated.forward (gdn2.py:433-452):
-//    x * rsqrt(mean(x^2) + eps) * weight * silu(z) over the last axis.
+//    x * rsqrt(mean(x^2) + eps) * weight * silu(z) over the last axis;
+//    without z (GATE false) the same pass is RMSNorm.forward
+//    (models/normalization.py:40-51), weight * (x * rsqrt(mean(x^2) + eps)).
 //
 // Both follow the reference's rounding: it computes in the input dtype, so
 // every torch op's result is rounded to that dtype (the conv output before
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(256) void short_conv_kernel(ConvParams p, int TT)
 }
 
 // One wave per row of N = 64 * EPL elements at most; four rows per workgroup.
-template <typename T, int EPL>
+template <typename T, int EPL, bool GATE>
 __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(NormParams p)
 {
     const int lane = threadIdx.x & 63;
@@ -116,7 +118,7 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(NormParams p)
     if (row >= p.rows) return;  // whole waves leave; no barriers below
     const int N = p.N;
     const T *x = static_cast<const T *>(p.x) + row * N;
-    const T *z = static_cast<const T *>(p.z) + row * N;
+    const T *z = GATE ? static_cast<const T *>(p.z) + row * N : nullptr;
     float xv[EPL], sq = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
@@ -133,12 +135,14 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(NormParams p)
         const float wgt = p.w_f32 ? static_cast<const float *>(p.weight)[c]
                                   : io<T>::ld(static_cast<const T *>(p.weight), c);
         const float a = round_to<T>(xv[e] * inv);
-        const float gz = round_to<T>(silu_f32(io<T>::ld(z, c)));
         if (p.w_f32) {
             // An fp32 weight promotes the rest of the expression to fp32.
-            static_cast<float *>(p.out)[row * N + c] = a * wgt * gz;
+            static_cast<float *>(p.out)[row * N + c] =
+                GATE ? a * wgt * round_to<T>(silu_f32(io<T>::ld(z, c))) : a * wgt;
         } else {
-            io<T>::st(static_cast<T *>(p.out), row * N + c, round_to<T>(round_to<T>(a * wgt) * gz));
+            const float aw = round_to<T>(a * wgt);
+            io<T>::st(static_cast<T *>(p.out), row * N + c,
+                      GATE ? round_to<T>(aw * round_to<T>(silu_f32(io<T>::ld(z, c)))) : aw);
         }
     }
 }
@@ -279,33 +283,45 @@ __global__ __launch_bounds__(64) void short_conv_vec_kernel(ConvParams p)
     }
 }
 
-// Vectorised gated RMS norm: LPR lanes per row, 16 bytes (EPV values) per
-// lane, so a row of N = LPR * EPV values moves as LPR contiguous 16-byte
-// pieces and is reduced by xor-shuffles inside its lane group.  Each thread
-// takes RPT rows (RPB rows apart) and requests all of them before computing.
-template <typename T, int LPR, int RPT>
+// Vectorised gated RMS norm: LPR lanes per row, VPL 16-byte pieces (EPV
+// values each) per lane, so a row of N = VPL * LPR * EPV values moves as
+// VPL passes of LPR contiguous 16-byte pieces and is reduced by
+// xor-shuffles inside its lane group.  Each thread takes RPT rows (RPB rows
+// apart) and requests all of them before computing.  GATE false: no z, the
+// plain RMSNorm.
+template <typename T, int LPR, int RPT, int VPL, bool GATE>
 __global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(NormParams p)
 {
     using VT = Vec16<T>;
-    constexpr int EPV = VT::N, RPB = 256 / LPR;
-    const int N = LPR * EPV;
+    constexpr int EPV = VT::N, RPB = 256 / LPR, EPL = VPL * EPV, PS = LPR * EPV;
+    const int N = VPL * PS;
     const int sub = threadIdx.x % LPR;
     int64_t off[RPT];
     bool live[RPT];
-    float xv[RPT][EPV], zv[RPT][EPV];
+    float xv[RPT][EPL], zv[RPT][GATE ? EPL : 1];
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
         int64_t row = (static_cast<int64_t>(blockIdx.x) * RPT + r) * RPB + threadIdx.x / LPR;
         live[r] = row < p.rows;
         if (!live[r]) row = p.rows - 1;  // stay in bounds; keep the shuffles uniform
         off[r] = row * N + sub * EPV;
-        VT::load(static_cast<const T *>(p.x) + off[r], xv[r]);
-        VT::load(static_cast<const T *>(p.z) + off[r], zv[r]);
-    }
-    float wgt[EPV];
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-        const int c = sub * EPV + e;
+        for (int v = 0; v < VPL; ++v) {
+            float t[EPV];
+            VT::load(static_cast<const T *>(p.x) + off[r] + v * PS, t);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) xv[r][v * EPV + e] = t[e];
+            if constexpr (GATE) {
+                VT::load(static_cast<const T *>(p.z) + off[r] + v * PS, t);
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) zv[r][v * EPV + e] = t[e];
+            }
+        }
+    }
+    float wgt[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const int c = (e / EPV) * PS + sub * EPV + e % EPV;
         wgt[e] = p.w_f32 ? static_cast<const float *>(p.weight)[c]
                          : io<T>::ld(static_cast<const T *>(p.weight), c);
     }
@@ -313,26 +329,38 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(NormParams p)
     for (int r = 0; r < RPT; ++r) {
         float sq = 0.0f;
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) sq += round_to<T>(xv[r][e] * xv[r][e]);
+        for (int e = 0; e < EPL; ++e) sq += round_to<T>(xv[r][e] * xv[r][e]);
 #pragma unroll
         for (int o = 1; o < LPR; o <<= 1) sq += __shfl_xor(sq, o, 64);
         const float var = round_to<T>(sq / static_cast<float>(N));
         const float inv = round_to<T>(rsqrtf(round_to<T>(var + p.eps)));
-        float out[EPV];
+        float out[EPL];
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) {
+        for (int e = 0; e < EPL; ++e) {
             const float a = round_to<T>(xv[r][e] * inv);
-            const float gz = round_to<T>(silu_f32(zv[r][e]));
-            out[e] = p.w_f32 ? a * wgt[e] * gz : round_to<T>(round_to<T>(a * wgt[e]) * gz);
+            if constexpr (GATE) {
+                const float gz = round_to<T>(silu_f32(zv[r][e]));
+                out[e] = p.w_f32 ? a * wgt[e] * gz : round_to<T>(round_to<T>(a * wgt[e]) * gz);
+            } else {
+                out[e] = p.w_f32 ? a * wgt[e] : round_to<T>(a * wgt[e]);
+            }
         }
         if (!live[r]) continue;
-        if (p.w_f32) {
-            float *o = static_cast<float *>(p.out) + off[r];
 #pragma unroll
-            for (int e = 0; e < EPV; e += 4)
-                *reinterpret_cast<float4 *>(o + e) = make_float4(out[e], out[e + 1], out[e + 2], out[e + 3]);
-        } else {
-            VT::store(static_cast<T *>(p.out) + off[r], out);
+        for (int v = 0; v < VPL; ++v) {
+            if (p.w_f32) {
+                float *o = static_cast<float *>(p.out) + off[r] + v * PS;
+#pragma unroll
+                for (int e = 0; e < EPV; e += 4)
+                    *reinterpret_cast<float4 *>(o + e) =
+                        make_float4(out[v * EPV + e], out[v * EPV + e + 1], out[v * EPV + e + 2],
+                                    out[v * EPV + e + 3]);
+            } else {
+                float t[EPV];
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) t[e] = out[v * EPV + e];
+                VT::store(static_cast<T *>(p.out) + off[r] + v * PS, t);
+            }
         }
     }
 }
@@ -379,38 +407,49 @@ hipError_t conv_t(const ConvParams &p, int maxD, int ntensors, hipStream_t s)
     }
 }
 
-template <typename T, int LPR>
+template <typename T, int LPR, int VPL, bool GATE>
 hipError_t norm_vec(const NormParams &p, hipStream_t s)
 {
     constexpr int RPT = 1, RPB = 256 / LPR;
-    hipLaunchKernelGGL((gated_rmsnorm_vec_kernel<T, LPR, RPT>),
+    hipLaunchKernelGGL((gated_rmsnorm_vec_kernel<T, LPR, RPT, VPL, GATE>),
                        dim3(static_cast<unsigned>((p.rows + RPB * RPT - 1) / (RPB * RPT))), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+template <typename T, bool GATE>
+hipError_t norm_g(const NormParams &p, hipStream_t s)
+{
+    // Rows of N = VPL * LPR * (16 bytes of T), LPR a power of two <= 64,
+    // VPL in {1, 2, 4}, 16-byte aligned.
+    constexpr int EPV = Vec16<T>::N;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.z) |
+                           reinterpret_cast<uintptr_t>(p.out)) & 15) == 0;
+    if (aligned && p.N % EPV == 0) {
+        switch (p.N / EPV) {
+        case 4: return norm_vec<T, 4, 1, GATE>(p, s);
+        case 8: return norm_vec<T, 8, 1, GATE>(p, s);
+        case 16: return norm_vec<T, 16, 1, GATE>(p, s);
+        case 32: return norm_vec<T, 32, 1, GATE>(p, s);
+        case 64: return norm_vec<T, 64, 1, GATE>(p, s);
+        case 128: return norm_vec<T, 64, 2, GATE>(p, s);
+        case 256: return norm_vec<T, 64, 4, GATE>(p, s);
+        default: break;
+        }
+    }
+    const dim3 grid(static_cast<unsigned>((p.rows + 3) / 4));
+    if (p.N <= 64) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 1, GATE>), grid, dim3(256), 0, s, p);
+    else if (p.N <= 128) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 2, GATE>), grid, dim3(256), 0, s, p);
+    else if (p.N <= 256) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 4, GATE>), grid, dim3(256), 0, s, p);
+    else if (p.N <= 512) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 8, GATE>), grid, dim3(256), 0, s, p);
+    else if (p.N <= 1024) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 16, GATE>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 32, GATE>), grid, dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
 template <typename T>
 hipError_t norm_t(const NormParams &p, hipStream_t s)
 {
-    // Rows of N = LPR * (16 bytes of T), LPR a power of two <= 64, 16-byte aligned.
-    constexpr int EPV = Vec16<T>::N;
-    const bool aligned = ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.z) |
-                           reinterpret_cast<uintptr_t>(p.out)) & 15) == 0;
-    if (aligned && p.N % EPV == 0) {
-        switch (p.N / EPV) {
-        case 4: return norm_vec<T, 4>(p, s);
-        case 8: return norm_vec<T, 8>(p, s);
-        case 16: return norm_vec<T, 16>(p, s);
-        case 32: return norm_vec<T, 32>(p, s);
-        case 64: return norm_vec<T, 64>(p, s);
-        default: break;
-        }
-    }
-    const dim3 grid(static_cast<unsigned>((p.rows + 3) / 4));
-    if (p.N <= 64) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 1>), grid, dim3(256), 0, s, p);
-    else if (p.N <= 128) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 2>), grid, dim3(256), 0, s, p);
-    else if (p.N <= 256) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 4>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 8>), grid, dim3(256), 0, s, p);
-    return hipGetLastError();
+    return p.z ? norm_g<T, true>(p, s) : norm_g<T, false>(p, s);
 }
 
 }  // namespace

@@ -35,6 +35,7 @@ __all__ = [
     "gate_activation",
     "short_convolution",
     "gated_rmsnorm",
+    "rms_norm",
 ]
 
 
@@ -696,6 +697,35 @@ def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: f
     lib = nat.load()
     st = lib.gdn2_gated_rmsnorm_fwd(
         nat.ptr(xc), nat.ptr(zc), nat.ptr(wc), nat.dtype_code(wdt), nat.ptr(out), nat.dtype_code(dt),
+        xc.numel() // N, N, float(eps), nat.stream_handle(x.device),
+    )
+    nat.check(st, name)
+    return out
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """``weight * (x * rsqrt(mean(x^2) + eps))`` over the last axis (N <= 2048).
+
+    This is reference ``RMSNorm.forward`` (``models/normalization.py:40-51``), the decoder
+    hosts' norm, rounded to the input dtype after every op as the reference is.  It runs
+    on the gated norm's entry point with the gate left out.
+
+    Output dtype: as for ``gated_rmsnorm``.  Inference only: there is no backward.
+    """
+    name = "rms_norm"
+    _require_gpu(name, x, weight)
+    if weight.numel() != x.shape[-1]:
+        raise ValueError(f"{name}: weight must have {x.shape[-1]} elements")
+    dt = x.dtype
+    N = x.shape[-1]
+    xc = x.contiguous()
+    wd = weight.detach()
+    wdt = torch.float32 if (wd.dtype == torch.float32 and dt != torch.float32) else dt
+    wc = wd.to(wdt).contiguous()
+    out = torch.empty(x.shape, dtype=wdt, device=x.device)
+    lib = nat.load()
+    st = lib.gdn2_gated_rmsnorm_fwd(
+        nat.ptr(xc), None, nat.ptr(wc), nat.dtype_code(wdt), nat.ptr(out), nat.dtype_code(dt),
         xc.numel() // N, N, float(eps), nat.stream_handle(x.device),
     )
     nat.check(st, name)

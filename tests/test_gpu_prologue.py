@@ -2,13 +2,15 @@
 
 Kernels:
 * the fused q/k/v short convolution (``ops.short_convolution``);
-* the gated RMS norm (``ops.gated_rmsnorm``).
+* the gated RMS norm (``ops.gated_rmsnorm``), and the same entry point without the gate
+  (``ops.rms_norm``, the decoder hosts' RMSNorm).
 
 Checks:
-* **Oracle.** Against the float64 oracle (``oracle.short_conv``, ``oracle.gated_rmsnorm``)
+* **Oracle.** Against the float64 oracle (``oracle.short_conv``, ``oracle.gated_rmsnorm``,
+  ``oracle.rmsnorm``)
   at relative L2 <= 1e-4 (float32) / 2e-2 (bf16, fp16).
 * **Reference rounding (norm).** Against the reference's own torch formula evaluated in
-  the input dtype on the GPU (gdn2.py:448-452). The norm kernel rounds after every op as
+  the input dtype on the GPU (gdn2.py:448-452; models/normalization.py:48-50). The norm kernel rounds after every op as
   that code does, so the two agree to within one bf16 unit in the last place.
 * **Conv accuracy.** The conv kernel accumulates in fp32 and rounds once, as the
   reference's cuDNN target does; torch's bf16 depthwise conv on this image rounds
@@ -95,7 +97,8 @@ def test_short_conv_bf16_at_least_as_accurate_as_torch(gpu_device):
 
 
 @pytest.mark.parametrize("dtype,N", [(torch.float32, 128), (torch.bfloat16, 64), (torch.bfloat16, 128),
-                                     (torch.float16, 100), (torch.bfloat16, 256)])
+                                     (torch.float16, 100), (torch.bfloat16, 256), (torch.bfloat16, 1024),
+                                     (torch.float32, 1024), (torch.float16, 1000)])
 def test_gated_rmsnorm_matches_oracle(gpu_device, dtype, N):
     from qwendopamine_amd.ops import gated_rmsnorm
 
@@ -132,6 +135,49 @@ def test_gated_rmsnorm_rounds_like_the_reference(gpu_device):
     _same_rounding(out, ref)
     out32 = gated_rmsnorm(x, z, w.float(), 1e-5)
     ref32 = ref_formula(x, z, w.float())
+    assert out32.dtype == torch.float32 == ref32.dtype
+    assert rel_l2(out32, ref32) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype,N", [(torch.bfloat16, 1024), (torch.bfloat16, 2048), (torch.float32, 1024),
+                                     (torch.float16, 1000), (torch.bfloat16, 64), (torch.float32, 2000)])
+def test_rms_norm_matches_oracle(gpu_device, dtype, N):
+    """The gated norm's entry point without z: the decoder hosts' RMSNorm."""
+    from qwendopamine_amd.ops import rms_norm
+
+    print(f"[case] rms_norm dtype={dtype} N={N}", flush=True)
+    rng = np.random.default_rng(N + 1)
+    x, w = rng.standard_normal((37, 5, N)) * 2, rng.standard_normal(N)
+    xt, wt = (torch.from_numpy(a).to(gpu_device, dtype) for a in (x, w))
+    out = rms_norm(xt, wt, 1e-5)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype
+    ref = orc.rmsnorm(xt.double().cpu().numpy(), wt.double().cpu().numpy(), 1e-5)
+    assert rel_l2(out, ref) <= REL_TOL[dtype]
+
+
+@pytest.mark.parametrize("N", [1024, 1000])
+def test_rms_norm_rounds_like_the_reference(gpu_device, N):
+    """Reference RMSNorm.forward (models/normalization.py:40-51) evaluated in bf16 by torch
+    against the kernel, vectorised (N = 1024) and element-wise (N = 1000); an fp32 weight
+    promotes the result to fp32 in both."""
+    from qwendopamine_amd.ops import rms_norm
+
+    print(f"[case] rms_norm reference rounding N={N}", flush=True)
+    torch.manual_seed(2)
+    x = torch.randn(2048, N, device=gpu_device, dtype=torch.bfloat16) * 3
+    w = torch.randn(N, device=gpu_device, dtype=torch.bfloat16)
+
+    def ref_formula(x, w):
+        variance = x.pow(2).mean(-1, keepdim=True)
+        return w * (x * torch.rsqrt(variance + 1e-5))
+
+    out = rms_norm(x, w, 1e-5)
+    ref = ref_formula(x, w)
+    torch.cuda.synchronize()
+    _same_rounding(out, ref)
+    out32 = rms_norm(x, w.float(), 1e-5)
+    ref32 = ref_formula(x, w.float())
     assert out32.dtype == torch.float32 == ref32.dtype
     assert rel_l2(out32, ref32) <= 1e-5
 

@@ -287,6 +287,19 @@ def test_gated_rmsnorm_equals_torch_rms_norm():
     np.testing.assert_allclose(orc.gated_rmsnorm(x, z, w, 1e-5), ref.numpy(), rtol=1e-12, atol=1e-12)
 
 
+def test_rmsnorm_equals_torch_rms_norm():
+    """The plain norm against torch's library rms_norm in float64, and its defining
+    property: with unit weight and eps = 0 every row has unit root mean square."""
+    import torch
+
+    rng = np.random.default_rng(34)
+    x, w = rng.standard_normal((9, 1024)) * 3, rng.standard_normal(1024)
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(x), (1024,), torch.from_numpy(w), eps=1e-5)
+    np.testing.assert_allclose(orc.rmsnorm(x, w, 1e-5), ref.numpy(), rtol=1e-12, atol=1e-12)
+    y = orc.rmsnorm(x, np.ones(1024), 0.0)
+    np.testing.assert_allclose(np.sqrt((y * y).mean(-1)), 1.0, rtol=1e-12)
+
+
 def test_vjp_matches_finite_differences():
     q, k, v, g, b, w, s0 = _rand(1, 11, 2, 6, 5, seed=9, decay="paper")
     rng = np.random.default_rng(10)
