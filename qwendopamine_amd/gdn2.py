@@ -434,6 +434,13 @@ class GatedDeltaNet2(nn.Module):
         output_attentions: bool | None = False,
         **kwargs: Any,
     ):
+        """Reference ``GatedDeltaNet2.forward`` (``gdn2.py:780-1004``).
+
+        Extension keyword (no counterpart in the reference): ``update_cache_in_place=True``
+        makes a single-token inference call with an existing cache write the new recurrent
+        and conv states into the cache's own tensors instead of fresh ones, so their
+        addresses stay fixed (hosts that replay a captured decode step use it).
+        """
         batch, seq_len, _ = hidden_states.shape
         if not hidden_states.is_cuda:
             raise RuntimeError(
@@ -445,6 +452,9 @@ class GatedDeltaNet2(nn.Module):
         recurrent_state, conv_states = self._get_cache(past_key_values)
         cq, ck, cv = conv_states if conv_states is not None else (None, None, None)
         cu_seqlens = kwargs.get("cu_seqlens")
+        in_place = bool(kwargs.get("update_cache_in_place")) and want_state and seq_len == 1 \
+            and cu_seqlens is None and recurrent_state is not None \
+            and recurrent_state.dtype == torch.float32 and recurrent_state.is_contiguous()
 
         # Padding: drop masked tokens, run packed, scatter back (gdn2.py:799-813).
         padded = (
@@ -473,9 +483,12 @@ class GatedDeltaNet2(nn.Module):
             y = F.linear(x.reshape(-1, x.shape[-1]), W_in)  # [tokens, sum(sizes)]
             qr, kr, vr, b, w, f0, g0 = (t.view(*x.shape[:-1], -1) if i < 5 else t
                                         for i, t in enumerate(y.split(sizes, dim=-1)))
+            conv_in = None if cq is None else [cq, ck, cv]
+            conv_out = conv_in if in_place and conv_in is not None and all(
+                c.dtype == qr.dtype and c.is_contiguous() for c in conv_in) else None
             (q, k, v), new = ops.short_convolution(
                 [qr, kr, vr], [c.conv1d.weight for c in convs], [c.conv1d.bias for c in convs],
-                None if cq is None else [cq, ck, cv], want_state, self.q_conv1d.activation)
+                conv_in, want_state, self.q_conv1d.activation, out_caches=conv_out)
             cq, ck, cv = new if new is not None else (None, None, None)
             # The low-rank second stages read their 2-D column ranges in place.
             g = self.f_proj[1](f0).view(*x.shape[:-1], -1)
@@ -531,6 +544,12 @@ class GatedDeltaNet2(nn.Module):
             o, recurrent_state = ops.chunk_gdn2(
                 q, k, v, g, b, w, initial_state=h0, output_final_state=want_state,
                 use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens, **gate_kw,
+            )
+        elif in_place:
+            # The decode kernel updates the cached state where it lies.
+            o, recurrent_state = ops.fused_recurrent_gdn2_fwd(
+                q=q, k=k, v=v, g=g, b=b, w=w, initial_state=recurrent_state, output_final_state=True,
+                inplace_final_state=True, use_qk_l2norm_in_kernel=True, **gate_kw,
             )
         else:
             o, recurrent_state = ops.fused_recurrent_gdn2(

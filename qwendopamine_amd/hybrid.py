@@ -101,11 +101,18 @@ def apply_rotary_emb(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> t
     ``x [B, T, heads, D]``, in fp32, result in ``x``'s dtype (reference ``model.py:40-61``)."""
     rot = 2 * cos.shape[-1]
     xf = x.float()
+    if rot == x.shape[-1] and x.shape[1] == 1:
+        # Single-token (decode) calls are bound by launches: the pair rotation
+        # (x1 c - x2 s, x1 s + x2 c) is the complex product of x1 + i x2 with
+        # c + i s, three launches instead of about ten.  Long prefills keep the
+        # real form (torch's broadcast complex product measured slower there).
+        xc = torch.view_as_complex(xf.contiguous().view(*x.shape[:-1], rot // 2, 2))
+        rc = torch.complex(cos.float(), sin.float())[None, :, None, :]
+        return torch.view_as_real(xc * rc).flatten(-2).to(x.dtype)
     x1, x2 = xf[..., :rot:2], xf[..., 1:rot:2]
     c, s = cos[None, :, None, :], sin[None, :, None, :]
     y = torch.stack((x1 * c - x2 * s, x1 * s + x2 * c), dim=-1).flatten(-2)
-    if rot < x.shape[-1]:
-        y = torch.cat((y, xf[..., rot:]), dim=-1)
+    y = torch.cat((y, xf[..., rot:]), dim=-1)
     return y.to(x.dtype)
 
 
@@ -272,10 +279,13 @@ class Block(nn.Module):
             self.gdn2_cache = cache
             return h
         step = dict(self.gdn2_cache)
-        h, _, step = self.attn(x, past_key_values=step, use_cache=True)
-        self.gdn2_cache["recurrent_state"].copy_(step["recurrent_state"])
+        h, _, step = self.attn(x, past_key_values=step, use_cache=True, update_cache_in_place=True)
+        # Decode steps update the cache where it lies; other calls return fresh tensors.
+        if step["recurrent_state"] is not self.gdn2_cache["recurrent_state"]:
+            self.gdn2_cache["recurrent_state"].copy_(step["recurrent_state"])
         for dst, src in zip(self.gdn2_cache["conv_state"], step["conv_state"]):
-            dst.copy_(src)
+            if src is not dst:
+                dst.copy_(src)
         return h
 
 

@@ -601,6 +601,7 @@ def short_convolution(
     caches: list[torch.Tensor | None] | None = None,
     output_final_state: bool = False,
     activation: str | None = "silu",
+    out_caches: list[torch.Tensor] | None = None,
 ) -> tuple[list[torch.Tensor], list[torch.Tensor] | None]:
     """Causal depthwise conv1d (+ SiLU) of up to three ``[B, T, D]`` tensors in one launch.
 
@@ -611,6 +612,10 @@ def short_convolution(
 
     Inputs may be column ranges of a wider ``[B, T, N]`` tensor (unit channel stride, rows
     ``stride(1)`` apart): they are read in place, with no copy.
+
+    ``out_caches`` (an extension of this backend; single-token calls only): contiguous
+    ``[B, D, W-1]`` tensors that receive the new caches, possibly the input caches
+    themselves (each cache entry is read before it is overwritten, by the same lane).
 
     Returns ``(ys, new_caches)``. Inference only: there is no backward.
     """
@@ -653,8 +658,16 @@ def short_convolution(
             if c is not None and tuple(c.shape) != (B, d, W - 1):
                 raise ValueError(f"{name}: cache must be {(B, d, W - 1)}; got {tuple(c.shape)}")
     keep = W - 1 if T == 1 else min(T, W - 1)
-    new = [torch.empty(B, d, keep, dtype=dt, device=x.device) for x, d in zip(xs, dims)] \
-        if output_final_state else None
+    if out_caches is not None:
+        if T != 1 or not output_final_state or len(out_caches) != n:
+            raise ValueError(f"{name}: out_caches needs a single-token call with output_final_state")
+        for c, d in zip(out_caches, dims):
+            if tuple(c.shape) != (B, d, W - 1) or c.dtype != dt or not c.is_contiguous():
+                raise ValueError(f"{name}: out_caches must be contiguous {(B, d, W - 1)} {dt} tensors")
+        new = list(out_caches)
+    else:
+        new = [torch.empty(B, d, keep, dtype=dt, device=x.device) for x, d in zip(xs, dims)] \
+            if output_final_state else None
     ys = [torch.empty_like(x) for x in xs]
     dims_arr = (ctypes.c_int * 3)(*(dims + [dims[0]] * (3 - n)))
     lib = nat.load()

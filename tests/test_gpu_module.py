@@ -107,6 +107,30 @@ def test_dict_cache_decode_continues_prefill(gpu_device):
     assert rel_l2(torch.cat(steps, 1), full[:, 37:]) <= 1e-4
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_updates_cache_in_place(gpu_device, dtype):
+    """update_cache_in_place (an extension keyword): decode steps write the new recurrent
+    and conv states into the cache's own tensors, with results identical to the default
+    (fresh tensors) path."""
+    print(f"[case] in-place cache update {dtype}", flush=True)
+    m = _layer(gpu_device, layer_idx=0).to(dtype).eval()
+    x = torch.randn(2, 24, 64, device=gpu_device, dtype=dtype)
+    with torch.no_grad():
+        c_ref: dict = {}
+        c_inp: dict = {}
+        m(x[:, :20], past_key_values=c_ref, use_cache=True)
+        m(x[:, :20], past_key_values=c_inp, use_cache=True)
+        state, convs = c_inp["recurrent_state"], c_inp["conv_state"]
+        for t in range(20, 24):
+            o_ref, _, _ = m(x[:, t:t + 1], past_key_values=c_ref, use_cache=True)
+            o_inp, _, _ = m(x[:, t:t + 1], past_key_values=c_inp, use_cache=True, update_cache_in_place=True)
+            assert c_inp["recurrent_state"] is state
+            assert all(a is b for a, b in zip(c_inp["conv_state"], convs))
+            assert torch.equal(o_inp, o_ref)
+            assert torch.equal(state, c_ref["recurrent_state"])
+            assert all(torch.equal(a, b) for a, b in zip(convs, c_ref["conv_state"]))
+
+
 def test_incremental_decoding_updates_state(gpu_device):
     m = _layer(gpu_device, layer_idx=0)
     cache: dict = {}

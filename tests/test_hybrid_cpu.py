@@ -75,6 +75,22 @@ def test_rope_rotation_properties():
     assert torch.allclose(scores[:9], shifted[3:12])
 
 
+def test_rope_complex_product_equals_pair_formula():
+    """The single-token full-width rotation (a complex product) against the interleaved-pair formula of
+    reference model.py:40-61, written out here with separate real products, in fp32."""
+    D, L = 64, 1
+    cos, sin = build_rope_cache(9, D, "cpu")
+    cos, sin = cos[5:6], sin[5:6]  # one decode position
+    x = torch.randn(7, L, 3, D, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    xf = x.float()
+    x1, x2 = xf[..., 0::2], xf[..., 1::2]
+    c, s = cos[None, :, None, :], sin[None, :, None, :]
+    ref = torch.stack((x1 * c - x2 * s, x1 * s + x2 * c), dim=-1).flatten(-2)
+    out = apply_rotary_emb(x, cos, sin)
+    assert out.dtype == torch.bfloat16
+    torch.testing.assert_close(out.float(), ref.to(torch.bfloat16).float(), rtol=2 ** -7, atol=1e-6)
+
+
 def test_streaming_attention_matches_uncached_forward():
     torch.manual_seed(0)
     cfg = HybridConfig(n_layer=3, n_embd=128, n_head=4, head_size=32, n_query_groups=2, intermediate_size=256,
