@@ -666,7 +666,6 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     constexpr int NBUF = DB ? 2 : 1;
     constexpr int NKT = KP / 16, NKS = KP / 32, NCT = BV / 16;
     constexpr int U16 = static_cast<int>(BL::BYTES / 16);
-    constexpr int PF = (U16 + 255) / 256;
     __shared__ __align__(16) st sB[NBUF][BL::SIZE];
     // z = w * v of the chunk as K16 B operands: block (token tile kt, column tile c).
     __shared__ __align__(16) st sZ[NBUF][16 * 256];
@@ -855,21 +854,37 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 land_z(zA, 0, 0);
             }
             if constexpr (DB) {
-                u32x4 pA[PF], pB[PF];
-                auto issue = [&](u32x4 (&dst)[PF], int gci) __attribute__((always_inline)) {
+                // Blocks (0, 2), (0, 3), (1, 2), (1, 3) of X and of Aqk lie above the
+                // causal diagonal and are never read here (the products use blocks
+                // (R, J) with J < 2 or J <= R, see pair_off), so the per-chunk copies
+                // skip them: compact unit c maps to blob unit cmap(c), which steps over
+                // the four skipped runs of 2 * BU units.  With c = ctid + 256 u and
+                // ctid < 256, each threshold test folds to a constant except in the
+                // one step u it falls in.
+                constexpr int BU = 256 * static_cast<int>(sizeof(st)) / 16;  // units per 16x16 block
+                constexpr int AQU = static_cast<int>(BL::AQ * static_cast<int64_t>(sizeof(st)) / 16);
+                constexpr int NC = U16 - 8 * BU, PFC = (NC + 255) / 256;
+                auto cmap = [&](int c, int u) __attribute__((always_inline)) {
+                    auto ge = [&](int t) __attribute__((always_inline)) {
+                        return t <= 256 * u ? 1 : (t >= 256 * u + 256 ? 0 : (c >= t ? 1 : 0));
+                    };
+                    return c + 2 * BU * (ge(2 * BU) + ge(4 * BU) + ge(AQU - 2 * BU) + ge(AQU));
+                };
+                u32x4 pA[PFC], pB[PFC];
+                auto issue = [&](u32x4 (&dst)[PFC], int gci) __attribute__((always_inline)) {
                     const u32x4 *src = blob(gci);
 #pragma unroll
-                    for (int u = 0; u < PF; ++u) {
-                        const int idx = ctid + 256 * u;
-                        dst[u] = src[idx < U16 ? idx : U16 - 1];
+                    for (int u = 0; u < PFC; ++u) {
+                        const int c = ctid + 256 * u;
+                        dst[u] = src[cmap(c < NC ? c : NC - 1, u)];
                     }
                 };
-                auto land = [&](const u32x4 (&src)[PF], int buf) __attribute__((always_inline)) {
+                auto land = [&](const u32x4 (&src)[PFC], int buf) __attribute__((always_inline)) {
                     u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf]);
 #pragma unroll
-                    for (int u = 0; u < PF; ++u) {
-                        const int idx = ctid + 256 * u;
-                        if (idx < U16) dst[idx] = src[u];
+                    for (int u = 0; u < PFC; ++u) {
+                        const int c = ctid + 256 * u;
+                        if (c < NC) dst[cmap(c, u)] = src[u];
                     }
                 };
                 // Chunk jc+1 lands in the idle buffer at step jc.  Unrolled by
