@@ -482,38 +482,98 @@ def measured_mfma_flop():
     return _profile_value("chunk_kernels_mfma_counters.md", "executed_bf16_mfma_flop_per_prefill_op")
 
 
-def cpu_baseline(torch, inputs, max_threads=16, target_s=10.0, max_reps=200):
-    """Time the C port of the reference recurrence on this host's cores, same prefill inputs:
-    repeated passes over the full config-1 batch for about `target_s` seconds of CPU work."""
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import cpu_lib
+def _cpu_model():
+    """``lscpu`` model name of this host (``/proc/cpuinfo`` as a fallback)."""
+    import subprocess
 
-    q, k, v, g, b, w = (x.float().cpu().numpy() for x in inputs)
-    B, T, H, K = q.shape
-    threads = max(1, min(max_threads, len(os.sched_getaffinity(0))))
-    cpu_lib.recurrent_fwd_f32(q[:, :64], k[:, :64], v[:, :64], g[:, :64], b[:, :64], w[:, :64],
-                              nthreads=threads)
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < target_s and len(times) < max_reps):
-        t0 = time.perf_counter()
-        cpu_lib.recurrent_fwd_f32(q, k, v, g, b, w, nthreads=threads)
-        times.append(time.perf_counter() - t0)
-    reps = len(times)
-    t = statistics.median(times)
-    model = ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for ln in out.splitlines():
+            if ln.strip().startswith("Model name:"):
+                return ln.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
                 if ln.startswith("model name"):
-                    model = ln.split(":", 1)[1].strip()
-                    break
+                    return ln.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(B * T / t, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"full config-1 prefill batch (B{B} T{T} H{H} K{K}), fp32 token recurrence "
-                      f"(oracle/gdn2_cpu.c, OpenMP over sequence-heads), median of {reps} runs "
-                      f"of {t:.2f} s; cpu: {model}"}
+    return "unknown"
+
+
+def _median_time(fn, runs=5):
+    """One warm-up call, then the median of ``runs`` timed calls (seconds)."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_baseline(torch, inputs):
+    """The CPU baselines of BASELINE's plan, on this host's cores (a reported baseline only).
+
+    * Config 0 (fp32 B1 T512 H4 K=V=64, seed 0), the whole workload: the PyTorch CPU
+      restatement of the reference recurrence (``oracle/gdn2_torch.recurrent_fwd``), its
+      safe chunkwise form (``chunk_fwd``) and the C port (``oracle/gdn2_cpu.c``), each on
+      every core of the affinity mask and on one thread; median of 5 runs after a warm-up.
+    * Config 1 (the GPU workload, fp32 recurrence on the same bf16-rounded inputs): the C
+      port on every core over the full batch, and on one thread over a sample (sequence 0,
+      all 16 heads, its first 1024 tokens); median of 5 runs after a warm-up.
+    ``value`` is the config-1 figure on every core, in tokens (all heads) per second.
+    """
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import cpu_lib
+    from oracle import gdn2_oracle as orc
+    from oracle import gdn2_torch
+
+    cores = len(os.sched_getaffinity(0))
+    prev_threads = torch.get_num_threads()
+    names = ("q", "k", "v", "g", "b", "w")
+
+    # ---- config 0
+    c0 = orc.make_inputs(0, 1, 512, 4, 64, 64)
+    c0_np = [c0[n].astype("float32") for n in names]
+    c0_t = [torch.from_numpy(a) for a in c0_np]
+    B0, T0, H0 = 1, 512, 4
+    c0_res = {}
+    for label, nth in (("all_cores", cores), ("one_thread", 1)):
+        torch.set_num_threads(nth)
+        r = {}
+        r["torch_recurrent"] = B0 * T0 / _median_time(lambda: gdn2_torch.recurrent_fwd(*c0_t))
+        r["torch_chunk"] = B0 * T0 / _median_time(lambda: gdn2_torch.chunk_fwd(*c0_t))
+        r["c_port"] = B0 * T0 / _median_time(lambda: cpu_lib.recurrent_fwd_f32(*c0_np, nthreads=nth))
+        c0_res[label] = {k: round(v, 1) for k, v in r.items()}
+    torch.set_num_threads(prev_threads)
+
+    # ---- config 1
+    q, k, v, g, b, w = (x.float().cpu().numpy() for x in inputs)
+    B, T, H, K = q.shape
+    full = (q, k, v, g, b, w)
+    t_all = _median_time(lambda: cpu_lib.recurrent_fwd_f32(*full, nthreads=cores))
+    Ts = min(T, 1024)
+    sample = tuple(x[:1, :Ts] for x in full)
+    t_one = _median_time(lambda: cpu_lib.recurrent_fwd_f32(*sample, nthreads=1))
+    model = _cpu_model()
+    used = min(cores, B * H)
+    return {
+        "value": round(B * T / t_all, 1), "unit": "tokens/s", "cores": used, "kind": "port",
+        "sample": (f"config 1 full batch (B{B} T{T} H{H} K{K}), fp32 token recurrence of the C port "
+                   f"(oracle/gdn2_cpu.c, OpenMP over the {B * H} sequence-heads, {cores} threads "
+                   f"requested), median of 5 runs of {t_all:.3f} s after a warm-up; cpu: {model}"),
+        "cpu_model": model,
+        "affinity_cores": cores,
+        "one_thread": {"value": round(Ts / t_one, 1), "unit": "tokens/s",
+                       "sample": f"sequence 0, all {H} heads, first {Ts} tokens; median of 5 "
+                                 f"runs of {t_one:.3f} s"},
+        "config0": {"unit": "tokens/s", "workload": "fp32 B1 T512 H4 K=V=64, seed 0 (whole workload)",
+                    "all_cores_threads": cores, **c0_res,
+                    "note": "config 0 has 4 sequence-heads, so the C port keeps at most 4 threads busy"},
+    }
 
 
 def main() -> int:

@@ -544,8 +544,6 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
     for (int s = 0; s < SLABS; ++s) {
         const int slab = slab0 + s;
         if (slab >= nslabs) break;
-        const int n = slab / p.HV, hv = slab % p.HV;
-        const int h = hv / (p.HV / p.H);
         const int64_t vw_off = static_cast<int64_t>(slab) * VD;
 
         float qv_ = 0.f, kv_ = 0.f, gv_ = 0.f, bv_ = 0.f;

@@ -41,6 +41,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from ._stacked import drop, stacked_rows
 from . import ops
 
 try:  # transformers is optional: only needed for HF Cache objects
@@ -228,7 +229,7 @@ class GatedDeltaNet2(nn.Module):
             hidden_size = int(cfg)
 
         if backend not in GDN2_BACKENDS:
-            raise ValueError(f"Invalid GDN-2 backend '{backend}'. Valid backends: {list(GDN2_BACKENDS)}")
+            raise ValueError(f"GatedDeltaNet2: unknown backend {backend!r}; choose one of {sorted(GDN2_BACKENDS)}")
 
         self.hidden_size = hidden_size
         self.num_heads = 16 if num_heads is None else num_heads
@@ -236,7 +237,8 @@ class GatedDeltaNet2(nn.Module):
         self.num_v_heads = self.num_heads if num_v_heads is None else num_v_heads
         if self.num_v_heads > self.num_heads and self.num_v_heads % self.num_heads != 0:
             raise ValueError(
-                f"num_v_heads={self.num_v_heads} must be divisible by num_heads={self.num_heads}."
+                f"GatedDeltaNet2: {self.num_v_heads} value heads cannot be grouped over "
+                f"{self.num_heads} key heads (need a whole multiple)"
             )
         self.layer_idx = layer_idx
         self.mode = mode
@@ -402,15 +404,16 @@ class GatedDeltaNet2(nn.Module):
     def _fused_input_weight(self) -> tuple[torch.Tensor, list[int]]:
         """The first-stage input projections stacked as one weight, ``[q; k; v; b; w;
         f_proj[0]; g_proj[0]]`` (none has a bias), and their output widths.  Used by the
-        inference path for a single GEMM; cached until any of the weights changes."""
-        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.b_proj.weight,
-              self.w_proj.weight, self.f_proj[0].weight, self.g_proj[0].weight)
-        key = tuple((t.data_ptr(), t._version, t.dtype) for t in ws)
-        cached = getattr(self, "_in_cache", None)
-        if cached is None or cached[0] != key:
-            cached = (key, torch.cat([t.detach() for t in ws], dim=0), [int(t.shape[0]) for t in ws])
-            self._in_cache = cached
-        return cached[1], cached[2]
+        inference path for a single GEMM.  The seven parameters are row views of the
+        stacked tensor, so the module holds one copy of these weights."""
+        ws = [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.b_proj.weight,
+              self.w_proj.weight, self.f_proj[0].weight, self.g_proj[0].weight]
+        return stacked_rows(self, "_in_cache", ws), [int(t.shape[0]) for t in ws]
+
+    def _apply(self, fn, *args, **kwargs):
+        # Parameters are about to be converted or moved: the caches would hold the old copies.
+        drop(self, "_in_cache", "_gate_cache")
+        return super()._apply(fn, *args, **kwargs)
 
     def _algorithm(self, mode: str, backend: str, needs_grad: bool) -> str:
         if backend in ("torch-chunk", "compiled"):

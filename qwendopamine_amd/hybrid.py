@@ -33,6 +33,7 @@ from torch.nn import functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import ops
+from ._stacked import drop, stacked_rows
 from .gdn2 import GatedDeltaNet2, _inference
 
 
@@ -149,16 +150,14 @@ class SwiGLU(nn.Module):
         return self.w3(F.silu(a) * b)
 
     def _fused12(self) -> tuple[torch.Tensor, torch.Tensor | None]:
-        """[w1; w2] weights (and biases), cached until either changes."""
-        ps = [self.w1.weight, self.w2.weight] + ([self.w1.bias, self.w2.bias] if self.w1.bias is not None else [])
-        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in ps)
-        cached = getattr(self, "_cache12", None)
-        if cached is None or cached[0] != key:
-            w = torch.cat([self.w1.weight.detach(), self.w2.weight.detach()], dim=0)
-            bias = None if self.w1.bias is None else torch.cat([self.w1.bias.detach(), self.w2.bias.detach()])
-            cached = (key, w, bias)
-            self._cache12 = cached
-        return cached[1], cached[2]
+        """[w1; w2] weights (and biases) as one tensor each; w1 and w2 are row views of it."""
+        w = stacked_rows(self, "_cache12", [self.w1.weight, self.w2.weight])
+        bias = None if self.w1.bias is None else stacked_rows(self, "_cache12b", [self.w1.bias, self.w2.bias])
+        return w, bias
+
+    def _apply(self, fn, *args, **kwargs):
+        drop(self, "_cache12", "_cache12b")
+        return super()._apply(fn, *args, **kwargs)
 
 
 class LLaMAMLP(nn.Module):

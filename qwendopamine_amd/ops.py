@@ -64,6 +64,19 @@ def _check_shapes(name, q, k, v, g, b, w, same_heads: bool) -> None:
         raise ValueError(f"{name}: value heads {HV} incompatible with key heads {H}")
 
 
+def _check_packed(q: torch.Tensor, initial_state: torch.Tensor | None, cu_seqlens) -> None:
+    """Packed (``cu_seqlens``) calls take one row of tokens and one state per sequence."""
+    if cu_seqlens is None:
+        return
+    if q.shape[0] != 1:
+        raise ValueError(f"packed sequences (cu_seqlens) go in a single row: got batch {q.shape[0]}, "
+                         "concatenate the sequences along the token axis")
+    n = len(cu_seqlens) - 1
+    if initial_state is not None and initial_state.shape[0] != n:
+        raise ValueError(f"cu_seqlens lists {n} sequences but initial_state holds "
+                         f"{initial_state.shape[0]} states")
+
+
 def _flags(use_qk_l2norm_in_kernel: bool, use_gate_in_kernel: bool, lower_bound) -> int:
     f = 0
     if use_qk_l2norm_in_kernel:
@@ -86,7 +99,7 @@ def _gate_tensors(use_gate_in_kernel, A_log, dt_bias, heads: int, K: int):
     if not use_gate_in_kernel:
         return None, None
     if A_log is None:
-        raise AssertionError("A_log must be provided when use_gate_in_kernel=True.")
+        raise AssertionError("use_gate_in_kernel needs the A_log keyword argument")
     a = A_log.detach().float().contiguous()
     if a.numel() != heads:
         raise ValueError(f"A_log must have {heads} elements, got {a.numel()}")
@@ -290,22 +303,11 @@ def fused_recurrent_gdn2(
     Shapes: ``q, k [B,T,H,K]``, ``v, w [B,T,HV,V]``, ``g, b [B,T,HV,K]``,
     ``initial_state [N,HV,K,V]`` float32.  Returns ``(o [B,T,HV,V], final_state)``.
     """
-    if cu_seqlens is not None:
-        if q.shape[0] != 1:
-            raise ValueError(
-                f"The batch size is expected to be 1 rather than {q.shape[0]} when using "
-                "`cu_seqlens`. Please flatten variable-length inputs before processing."
-            )
-        if initial_state is not None and initial_state.shape[0] != len(cu_seqlens) - 1:
-            raise ValueError(
-                "The number of initial states is expected to be equal to the number of "
-                f"input sequences, i.e., {len(cu_seqlens) - 1} rather than "
-                f"{initial_state.shape[0]}."
-            )
+    _check_packed(q, initial_state, cu_seqlens)
     assert b.shape == (*q.shape[:2], v.shape[2], k.shape[-1]) or b.shape == (*q.shape[:3], k.shape[-1]), (
-        f"b must have shape [B, T, HV, K]; got {tuple(b.shape)}"
+        f"erase gate b: expected [B, T, HV, K], got {tuple(b.shape)}"
     )
-    assert w.shape == v.shape, f"w must have shape [B, T, HV, V] matching v; got {tuple(w.shape)}"
+    assert w.shape == v.shape, f"write gate w: expected the shape of v {tuple(v.shape)}, got {tuple(w.shape)}"
     return fused_recurrent_gdn2_fwd(
         q=q, k=k, v=v, g=g, b=b, w=w, A_log=A_log, dt_bias=dt_bias, scale=scale,
         initial_state=initial_state, inplace_final_state=False,
@@ -504,43 +506,28 @@ def chunk_gdn2(
     ``return_intermediate_states``, it returns ``(o, final_state, h)`` instead, with ``h`` the
     per-chunk start states (``chunk_gdn2.py:1415-1421``).
     """
-    if cu_seqlens is not None:
-        if q.shape[0] != 1:
-            raise ValueError(
-                f"The batch size is expected to be 1 rather than {q.shape[0]} when using "
-                "`cu_seqlens`. Please flatten variable-length inputs before processing."
-            )
-        if initial_state is not None and initial_state.shape[0] != len(cu_seqlens) - 1:
-            raise ValueError(
-                "The number of initial states is expected to be equal to the number of "
-                f"input sequences, i.e., {len(cu_seqlens) - 1} rather than "
-                f"{initial_state.shape[0]}."
-            )
+    _check_packed(q, initial_state, cu_seqlens)
     if initial_state is not None:
-        assert initial_state.dtype == torch.float32, "initial_state must be in float32."
+        assert initial_state.dtype == torch.float32, f"initial_state: float32 expected, got {initial_state.dtype}"
     A_log, dt_bias = None, None
     if use_gate_in_kernel:
-        assert "A_log" in kwargs, "A_log must be provided when use_gate_in_kernel=True."
+        assert "A_log" in kwargs, "use_gate_in_kernel needs the A_log keyword argument"
         A_log, dt_bias = kwargs["A_log"], kwargs.get("dt_bias")
     if safe_gate and use_gate_in_kernel:
         if lower_bound is None:
-            raise ValueError("`lower_bound` must be specified when `safe_gate=True` and `use_gate_in_kernel=True`.")
+            raise ValueError("safe_gate with the in-kernel gate needs a lower_bound value")
         if not (-5 <= lower_bound < 0):
-            raise ValueError(f"`lower_bound` must be in the safe range [-5, 0), got {lower_bound}.")
+            raise ValueError(f"lower_bound {lower_bound} lies outside [-5, 0), where the bounded gate is defined")
     if not (safe_gate and use_gate_in_kernel):
         lower_bound = None
-    assert q.shape == k.shape == g.shape, "q, k, g must have the same shape."
-    assert k.shape[-1] <= 256, "Currently we only support key headdim <=256 for GDN-2 :-("
-    assert b.shape == q.shape, (
-        "b (channel-wise erase gate) must have shape [B, T, H, K] matching q; "
-        f"got {tuple(b.shape)} vs q {tuple(q.shape)}."
+    assert q.shape == k.shape == g.shape, (
+        f"q, k and g share one [B, T, H, K] shape; got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(g.shape)}"
     )
-    assert w.shape == v.shape, (
-        "w (channel-wise write gate) must have shape [B, T, H, V] matching v; "
-        f"got {tuple(w.shape)} vs v {tuple(v.shape)}."
-    )
+    assert k.shape[-1] <= 256, f"key head dim {k.shape[-1]} exceeds the chunk op's limit of 256"
+    assert b.shape == q.shape, f"erase gate b: expected the shape of q {tuple(q.shape)}, got {tuple(b.shape)}"
+    assert w.shape == v.shape, f"write gate w: expected the shape of v {tuple(v.shape)}, got {tuple(w.shape)}"
     assert v.shape == (*q.shape[:3], v.shape[-1]), (
-        "v must be of shape (batch size, seq len, num of head, head dim)."
+        f"v: expected [B, T, H, V] with the B, T, H of q {tuple(q.shape[:3])}, got {tuple(v.shape)}"
     )
     if scale is None:
         scale = k.shape[-1] ** -0.5
@@ -549,10 +536,10 @@ def chunk_gdn2(
         b, w = b.sigmoid(), w.sigmoid()  # the intermediate states use the training workspace
     if return_intermediate_states:
         assert torch.is_inference_mode_enabled(), (
-            "return_intermediate_states is only allowed in inference mode"
+            "return_intermediate_states: run the call under torch.inference_mode()"
         )
         assert disable_recompute is False, (
-            "return_intermediate_states must be used with disable_recompute=False"
+            "return_intermediate_states cannot be combined with disable_recompute=True"
         )
         o, ht, h = chunk_gdn2_fwd(
             q, k, v, g, b, w, scale, initial_state, output_final_state, use_qk_l2norm_in_kernel,

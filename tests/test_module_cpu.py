@@ -229,3 +229,29 @@ def test_product_package_never_touches_the_oracle():
         for needle in ("from oracle", "import oracle", "libgdn2_cpu", "gdn2_oracle", "cpu_lib"):
             assert needle not in text, f"{p.name} references {needle}"
     assert np is not None
+
+
+def test_stacked_input_weight_is_the_only_copy():
+    """The inference path's stacked projection weight holds the parameters' storage (one
+    copy), survives an inference-mode build for later training, follows optimiser steps
+    and load_state_dict in place, and is rebuilt after a dtype conversion."""
+    torch.manual_seed(0)
+    m = GatedDeltaNet2(hidden_size=64, num_heads=2, head_dim=32)
+    sd = {k: v.clone() for k, v in m.state_dict().items()}
+    with torch.inference_mode():
+        W, sizes = m._fused_input_weight()
+    assert not W.is_inference() and sum(sizes) == W.shape[0]
+    assert m.q_proj.weight.data_ptr() == W.data_ptr()
+    assert m.g_proj[0].weight.data_ptr() == W[-sizes[-1]:].data_ptr()
+    assert all(torch.equal(sd[k], v) for k, v in m.state_dict().items())
+    x = torch.randn(3, 64)
+    (m.q_proj(x).sum() + m.w_proj(x).sum()).backward()
+    torch.optim.SGD(m.parameters(), lr=0.1).step()
+    W2, _ = m._fused_input_weight()
+    assert W2 is W and torch.equal(W2[:64], m.q_proj.weight.detach())
+    assert not torch.equal(W2[:64], sd["q_proj.weight"])
+    m.load_state_dict(sd)
+    assert torch.equal(m._fused_input_weight()[0][:64], sd["q_proj.weight"])
+    m.double()
+    W3, _ = m._fused_input_weight()
+    assert W3.dtype == torch.float64 and m.q_proj.weight.data_ptr() == W3.data_ptr()

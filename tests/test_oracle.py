@@ -405,6 +405,37 @@ def test_c_port_matches_oracle():
     assert orc.rel_l2(o2, o1) < 1e-5 and orc.rel_l2(s2, s1) < 1e-5
 
 
+@pytest.mark.parametrize("fn", ["recurrent_fwd", "chunk_fwd"])
+def test_torch_restatement_matches_oracle(fn):
+    """The float32 PyTorch CPU restatement (the timed CPU baseline) equals the float64
+    oracle, with a state, ragged chunk tails and the BASELINE decay distribution."""
+    import torch
+
+    from oracle import gdn2_torch
+
+    args = _rand(2, 150, 3, 24, 20, seed=15, decay="paper")
+    o1, s1 = orc.recurrent_fwd(*args)
+    t = [torch.from_numpy(np.ascontiguousarray(a)).float() for a in args]
+    o2, s2 = getattr(gdn2_torch, fn)(*t[:6], initial_state=t[6])
+    assert o2.dtype == torch.float32 and s2.shape == (2, 3, 24, 20)
+    assert orc.rel_l2(o2.double().numpy(), o1) < 1e-5 and orc.rel_l2(s2.double().numpy(), s1) < 1e-5
+
+
+def test_torch_restatement_config0():
+    """Both torch restatements on the config-0 workload against the committed fixture."""
+    import torch
+
+    from oracle import gdn2_torch
+
+    inp = orc.make_inputs(0, 1, 512, 4, 64, 64)
+    f = np.load(GOLDEN / "gdn2_config0_fingerprint.npz")
+    t = [torch.from_numpy(inp[n]).float() for n in ("q", "k", "v", "g", "b", "w")]
+    for fn in (gdn2_torch.recurrent_fwd, gdn2_torch.chunk_fwd):
+        o, ht = fn(*t)
+        assert orc.rel_l2(ht.double().numpy(), f["ht"]) < 1e-5
+        assert orc.rel_l2(o[0, :64, 0].double().numpy(), f["o_head0_first64"]) < 1e-5
+
+
 # ---------------------------------------------------------------- planted bugs
 def _mutant(kind, q, k, v, g, b, w, s0):
     """The recurrence with one plausible mistake (used only to show the pins bite)."""
