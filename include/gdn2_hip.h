@@ -45,6 +45,8 @@ enum gdn2_status {
     GDN2_ERR_UNSUPPORTED = -2, /* valid request this build does not handle */
     GDN2_ERR_LAUNCH = -3,      /* the HIP runtime rejected a launch        */
     GDN2_ERR_WORKSPACE = -4,   /* workspace missing or too small           */
+    GDN2_ERR_SCRATCH = -5,     /* gdn2_chunk_fwd_static: the shape needs    *
+                                * more than GDN2_STATIC_SCRATCH_BYTES       */
 };
 
 /* Flags (bitwise or). */
@@ -279,6 +281,29 @@ int gdn2_chunk_bwd(const void *q, const void *k, const void *v, const void *g, c
                    int num_seqs, int B, int T, int H, int K, int V, float scale,
                    unsigned flags, const void *saved, size_t saved_bytes, void *workspace,
                    size_t workspace_bytes, void *stream);
+
+/*
+ * gdn2_chunk_fwd without a workspace argument: allocates nothing.
+ * This entry point has no counterpart in the reference.  It is for callers that
+ * cannot allocate device memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  Arguments and results are those of
+ * gdn2_chunk_fwd (inference only: GDN2_FLAG_SAVE_FOR_BWD is rejected); the
+ * per-chunk blobs live in a static device array of GDN2_STATIC_SCRATCH_BYTES
+ * (72 MiB) on each GPU the library runs on, held until the process ends.
+ * A shape whose gdn2_chunk_fwd_workspace_size() exceeds that returns
+ * GDN2_ERR_SCRATCH before anything is launched (72 MiB holds 1143 (chunk, head)
+ * blobs at d_k = 128 in bf16 / fp16, e.g. 4096 tokens x 16 heads).
+ * `stream` must belong to the current device.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams or two host
+ * threads) race.
+ */
+#define GDN2_STATIC_SCRATCH_BYTES 75497472
+int gdn2_chunk_fwd_static(const void *q, const void *k, const void *v, const void *g,
+                          const void *b, const void *w, int io_dtype, int g_dtype, void *o,
+                          const float *initial_state, float *final_state, const float *A_log,
+                          const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
+                          const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H,
+                          int K, int V, float scale, unsigned flags, void *stream);
 
 #ifdef __cplusplus
 }

@@ -36,6 +36,8 @@ ERR_INVALID = -1
 ERR_UNSUPPORTED = -2
 ERR_LAUNCH = -3
 ERR_WORKSPACE = -4
+ERR_SCRATCH = -5
+STATIC_SCRATCH_BYTES = 75497472  # GDN2_STATIC_SCRATCH_BYTES
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -71,6 +73,11 @@ SIGNATURES: dict[str, tuple] = {
         _i,
         [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp,
          _i, _i, _i, _i, _i, _i, _f, _u, _vp, _sz, _vp],
+    ),
+    "gdn2_chunk_fwd_static": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp,
+         _i, _i, _i, _i, _i, _i, _f, _u, _vp],
     ),
     "gdn2_chunk_fwd_prep": (
         _i,
@@ -125,7 +132,7 @@ def check(status: int, what: str) -> None:
     if status == OK:
         return
     msg = load().gdn2_status_string(status).decode()
-    if status == ERR_INVALID:
+    if status in (ERR_INVALID, ERR_SCRATCH):
         raise ValueError(f"{what}: {msg}")
     if status == ERR_UNSUPPORTED:
         raise NotImplementedError(f"{what}: {msg}")

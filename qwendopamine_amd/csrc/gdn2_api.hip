@@ -72,6 +72,9 @@ const char *gdn2_status_string(int status)
     case GDN2_ERR_UNSUPPORTED: return "unsupported shape, dtype or option";
     case GDN2_ERR_LAUNCH: return "kernel launch failed";
     case GDN2_ERR_WORKSPACE: return "workspace missing or too small";
+    case GDN2_ERR_SCRATCH:
+        return "the shape needs more than the static scratch array of gdn2_chunk_fwd_static "
+               "holds (GDN2_STATIC_SCRATCH_BYTES = 72 MiB); use gdn2_chunk_fwd with a workspace";
     default: return "unknown status";
     }
 }

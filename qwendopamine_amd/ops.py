@@ -31,6 +31,7 @@ __all__ = [
     "fused_recurrent_gdn2_fwd",
     "chunk_gdn2",
     "chunk_gdn2_fwd",
+    "chunk_gdn2_static",
     "ChunkGDN2Function",
     "gate_activation",
     "short_convolution",
@@ -433,6 +434,96 @@ def chunk_gdn2_fwd(
                  scale=float(scale), flags=flags & ~nat.FLAG_SAVE_FOR_BWD,
                  transpose=transpose_state_layout)
     return res + (saved,)
+
+
+def chunk_gdn2_static(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    b: torch.Tensor,
+    w: torch.Tensor,
+    out: torch.Tensor,
+    final_state: torch.Tensor | None = None,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    lower_bound: float | None = None,
+    cu_seqlens: torch.Tensor | None = None,
+    cu_seqlens_cpu: torch.Tensor | None = None,
+    transpose_state_layout: bool = False,
+    bw_logits: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Chunkwise forward (inference) that allocates nothing: C entry ``gdn2_chunk_fwd_static``.
+
+    For callers that cannot allocate device memory (graph capture, serving loops).  The
+    results equal ``chunk_gdn2_fwd``'s; the per-chunk workspace is a static device array
+    of ``_native.STATIC_SCRATCH_BYTES`` (72 MiB) per GPU, so larger shapes raise
+    ``ValueError``.  Nothing is copied or allocated here either: ``q, k, v, b, w`` must be
+    contiguous, 16-byte aligned and of one dtype, ``g`` contiguous in float32 or that dtype,
+    ``out`` a contiguous tensor shaped like ``v``, the states contiguous float32
+    ``[N, H, K, V]`` (``[N, H, V, K]`` transposed), ``A_log`` / ``dt_bias`` contiguous float32,
+    and packed sequences need both ``cu_seqlens`` (device) and ``cu_seqlens_cpu`` (host),
+    int64.  Calls that overlap on one GPU share its array and race.
+    Returns ``(out, final_state)``.
+    """
+    name = "chunk_gdn2_static"
+    _require_gpu(name, q, k, v, g, b, w, out, initial_state, final_state, A_log, dt_bias, cu_seqlens)
+    _check_shapes(name, q, k, v, g, b, w, same_heads=True)
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    dt = q.dtype
+    for nm, x in (("q", q), ("k", k), ("v", v), ("b", b), ("w", w), ("out", out)):
+        if x.dtype != dt or not x.is_contiguous() or x.data_ptr() % 16:
+            raise ValueError(f"{name}: {nm} must be a contiguous, 16-byte aligned {dt} tensor")
+    if g.dtype not in (torch.float32, dt) or not g.is_contiguous():
+        raise ValueError(f"{name}: g must be contiguous float32 or {dt}")
+    if out.shape != v.shape:
+        raise ValueError(f"{name}: out must have the shape of v {tuple(v.shape)}")
+    if (cu_seqlens is None) != (cu_seqlens_cpu is None):
+        raise ValueError(f"{name}: packed sequences need both cu_seqlens and cu_seqlens_cpu")
+    N = B
+    if cu_seqlens is not None:
+        _check_packed(q, initial_state, cu_seqlens_cpu)
+        if (cu_seqlens.dtype != torch.int64 or cu_seqlens_cpu.dtype != torch.int64
+                or cu_seqlens_cpu.is_cuda or not cu_seqlens.is_contiguous()
+                or not cu_seqlens_cpu.is_contiguous() or cu_seqlens.numel() != cu_seqlens_cpu.numel()):
+            raise ValueError(f"{name}: cu_seqlens / cu_seqlens_cpu must be contiguous int64 on the "
+                             "device / host, of equal length")
+        N = cu_seqlens_cpu.numel() - 1
+    sk = (V, K) if transpose_state_layout else (K, V)
+    for nm, x in (("initial_state", initial_state), ("final_state", final_state)):
+        if x is not None and (x.dtype != torch.float32 or not x.is_contiguous()
+                              or tuple(x.shape) != (N, H, *sk)):
+            raise ValueError(f"{name}: {nm} must be a contiguous float32 {(N, H, *sk)} tensor")
+    for nm, x in (("A_log", A_log), ("dt_bias", dt_bias)):
+        if x is not None and (x.dtype != torch.float32 or not x.is_contiguous()):
+            raise ValueError(f"{name}: {nm} must be contiguous float32")
+    if use_gate_in_kernel and A_log is None:
+        raise AssertionError("use_gate_in_kernel needs the A_log keyword argument")
+    flags = _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound)
+    if transpose_state_layout:
+        flags |= nat.FLAG_TRANSPOSE_STATE
+    if bw_logits:
+        flags |= nat.FLAG_SIGMOID_BW
+    if scale is None:
+        scale = K**-0.5
+    lib = nat.load()
+    with torch.cuda.device(q.device):
+        st = lib.gdn2_chunk_fwd_static(
+            nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(g), nat.ptr(b), nat.ptr(w),
+            nat.dtype_code(dt), nat.dtype_code(g.dtype), nat.ptr(out),
+            nat.ptr(initial_state), nat.ptr(final_state),
+            nat.ptr(A_log if use_gate_in_kernel else None), nat.ptr(dt_bias if use_gate_in_kernel else None),
+            float(lower_bound) if lower_bound is not None else 0.0,
+            nat.ptr(cu_seqlens), None if cu_seqlens_cpu is None else cu_seqlens_cpu.data_ptr(), N,
+            B, T, H, K, V, float(scale), flags, nat.stream_handle(q.device),
+        )
+    nat.check(st, name)
+    return out, final_state
 
 
 class ChunkGDN2Function(torch.autograd.Function):
