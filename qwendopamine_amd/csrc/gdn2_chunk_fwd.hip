@@ -527,31 +527,43 @@ chunk_prep_kernel(ChunkParams p, int items)
         // A = scaled keys of block I (LDS), B = this block's Qb / Eb (registers).
         // Lane (n, kg) of the result holds Aqk[16R+n][16I+4kg+i], which is the
         // K16 A-operand order of Aqk, so it is stored as is.
+        // Instantiated per wave index (a compile-time RR), so that the causal
+        // block conditions fold and the block's LDS reads are one straight-line
+        // batch instead of a read-wait-use chain behind a branch per block.
         f32x4 aq[4], al[4];
+        auto products = [&](auto Rc) __attribute__((always_inline)) {
+            constexpr int RR = decltype(Rc)::value;
 #pragma unroll
-        for (int I = 0; I < 4; ++I) {
-            aq[I] = zero4();
-            al[I] = zero4();
-            if (I <= R) {
+            for (int I = 0; I < 4; ++I) {
+                aq[I] = zero4();
+                al[I] = zero4();
+                if (I <= RR) {
 #pragma unroll
-                for (int s = 0; s < NKS; ++s) {
-                    Q a[2];
+                    for (int s = 0; s < NKS; ++s) {
+                        Q a[2];
 #pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const int c0 = 32 * s + 16 * hh + 4 * kg;
-                        Q raw = ld_q4<PK>(sKend + (16 * I + m) * LDK + c0);
-                        if (I != R - 1) {
-                            float x[4];
-                            unpack4<PK>(raw, x);
-                            const float4 sc = *reinterpret_cast<const float4 *>(&sPf[R][I][c0]);
-                            raw = pack4<PK>(x[0] * sc.x, x[1] * sc.y, x[2] * sc.z, x[3] * sc.w);
+                        for (int hh = 0; hh < 2; ++hh) {
+                            const int c0 = 32 * s + 16 * hh + 4 * kg;
+                            Q raw = ld_q4<PK>(sKend + (16 * I + m) * LDK + c0);
+                            if (I != RR - 1) {
+                                float x[4];
+                                unpack4<PK>(raw, x);
+                                const float4 sc = *reinterpret_cast<const float4 *>(&sPf[RR][I][c0]);
+                                raw = pack4<PK>(x[0] * sc.x, x[1] * sc.y, x[2] * sc.z, x[3] * sc.w);
+                            }
+                            a[hh] = raw;
                         }
-                        a[hh] = raw;
+                        aq[I] = mma2<PK>(aq[I], a[0], a[1], fqb[2 * s], fqb[2 * s + 1]);
+                        al[I] = mma2<PK>(al[I], a[0], a[1], feb[2 * s], feb[2 * s + 1]);
                     }
-                    aq[I] = mma2<PK>(aq[I], a[0], a[1], fqb[2 * s], fqb[2 * s + 1]);
-                    al[I] = mma2<PK>(al[I], a[0], a[1], feb[2 * s], feb[2 * s + 1]);
                 }
             }
+        };
+        switch (R) {
+        case 0: products(std::integral_constant<int, 0>{}); break;
+        case 1: products(std::integral_constant<int, 1>{}); break;
+        case 2: products(std::integral_constant<int, 2>{}); break;
+        default: products(std::integral_constant<int, 3>{}); break;
         }
         if (wave_slow) {
 #pragma unroll
@@ -667,8 +679,11 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     constexpr int NKT = KP / 16, NKS = KP / 32, NCT = BV / 16;
     constexpr int U16 = static_cast<int>(BL::BYTES / 16);
     __shared__ __align__(16) st sB[NBUF][BL::SIZE];
-    // z = w * v of the chunk as K16 B operands: block (token tile kt, column tile c).
-    __shared__ __align__(16) st sZ[NBUF][16 * 256];
+    // z = w * v of the chunk, row-major [token][column of the slice] with a
+    // 16-byte skew per row; the compute waves turn each 16-token tile into
+    // their K16 B operand with one identity product.
+    constexpr int LDZ = BV + 16 / static_cast<int>(sizeof(st));
+    __shared__ __align__(16) st sZ[NBUF][64 * LDZ];
 
     // XCD-aware order: all value slices of a (sequence, head) pair share
     // blockIdx % 8, hence one XCD and one L2.
@@ -734,10 +749,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             }
         }
     };
-    // Copy waves: z = w * v of chunk jc for this value slice, in the K16
-    // B-operand order the compute waves read (zero past the sequence end and
-    // past V).  issue_z requests the raw rows (16-byte loads); land_z forms z
-    // and scatters it into LDS, so the two can sit a chunk apart.
+    // Copy waves: z = w * v of chunk jc for this value slice, row-major in LDS
+    // (zero past the sequence end and past V).  issue_z requests the raw rows
+    // (16-byte loads); land_z forms z and stores it with one 16-byte LDS write
+    // per row piece, so the two can sit a chunk apart.
     const int v0 = vs * BV;
     constexpr int EPV = 16 / static_cast<int>(sizeof(TI));  // values per 16-byte load
     constexpr int ZT = kChunk * BV / EPV;                    // loads per tensor per chunk
@@ -802,6 +817,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         int lc;
         chunk_rows(jc, t0, lc);
         st *dst = sZ[buf];
+        static_assert(EPV * sizeof(st) == 16, "one z row piece is one 16-byte LDS store");
 #pragma unroll
         for (int a = 0; a < NZT; ++a) {
             const int task = ctid + 256 * a;
@@ -809,7 +825,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
             const TI *rv = reinterpret_cast<const TI *>(&r.v[a]);
             const TI *rw = reinterpret_cast<const TI *>(&r.w[a]);
-            const int kt = tok >> 4, kgz = (tok & 15) >> 2, iz = tok & 3;
+            st zr[EPV];
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
                 // Zero past the sequence end (and past V, zero-filled by issue_z);
@@ -817,9 +833,9 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // dtype, as the module's torch sigmoid of w_proj(x) is (gdn2.py:865).
                 const float wv_ = SIGW ? round_to<TI>(sigmoid_f(io<TI>::ld(rw, e))) : io<TI>::ld(rw, e);
                 const float z = tok < lc ? io<TI>::ld(rv, e) * wv_ : 0.f;
-                const int cl = c + e, ct = cl >> 4, nz = cl & 15;
-                dst[(kt * 4 + ct) * 256 + (nz + 16 * kgz) * 4 + iz] = P::from_f32(z);
+                zr[e] = P::from_f32(z);
             }
+            *reinterpret_cast<u32x4 *>(dst + tok * LDZ + c) = __builtin_bit_cast(u32x4, zr);
         }
     };
 
@@ -978,10 +994,15 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 for (int kt = 0; kt < NKT; ++kt) emit_tile(hsb, k16_block(kt, vt, VP) + 4 * l, S[kt]);
             }
 
-            // z = w * v as B operand (contraction over tokens), staged in LDS.
+            // z = w * v as B operand (contraction over tokens): token tile kt
+            // read row-major (lane (m, kg): token 16kt+m, columns 4kg..4kg+3 of
+            // this wave's 16) and transposed by the identity product, whose
+            // accumulator holds tokens 4kg+i of column m -- the B-operand order.
             Q zf[4];
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) zf[kt] = ld_q4<PK>(sZ[buf] + (kt * 4 + wv) * 256 + 4 * l);
+            for (int kt = 0; kt < 4; ++kt)
+                zf[kt] = pack4<PK>(mma1<PK>(zero4(), ld_q4<PK>(sZ[buf] + (16 * kt + m) * LDZ + 16 * wv + 4 * kg),
+                                            ident));
             Q sf[NKT];
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) sf[kt] = pack4<PK>(S[kt]);
