@@ -177,6 +177,45 @@ int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int
                            void *out, int io_dtype, int64_t rows, int N, float eps, void *stream);
 
 /*
+ * Fused module decode step: one token per sequence through the whole mixer
+ * core, with no HBM round trip of q, k, v or o in between.  Replaces, for the
+ * decode call of GatedDeltaNet2.forward, the chain
+ *   ShortConvolution of q, k, v with the conv caches   (reference gdn2.py:395-430)
+ *   -> gate and b / w activations                      (gdn2.py:840-866)
+ *   -> fused_recurrent_gdn2 (T = 1, in-place state)    (gdn2_ops/fused_recurrent_gdn2.py:461-555)
+ *   -> RMSNormGated of the output with its gate        (gdn2.py:433-452)
+ * for num_v_heads == num_heads and K == V in {64, 128}.
+ *
+ *   raw_qkv[t] + n * ld_qkv[t]     row n of the raw q / k / v projections (before
+ *                                  the convolution), channel h * K + c of head h
+ *   g, b, w (+ n * ld)             decay (raw with GDN2_FLAG_GATE_IN_KERNEL), erase and
+ *                                  write gates (logits with GDN2_FLAG_SIGMOID_BW),
+ *                                  rows [H * K]
+ *   conv_weight[t] [H*K, W], conv_bias[t] [H*K] or NULL, W = conv_width = 4
+ *   conv_cache_in[t]  [N, H*K, W-1] or NULL (zero history); conv_cache_out[t]
+ *                     receives the last W-1 inputs, may equal conv_cache_in[t]
+ *   initial_state / final_state    [N, H, K, V] float32 rows at the given row
+ *                     strides (elements), may be the same array (in place); the
+ *                     initial state may be NULL (zero)
+ *   gate + n * ld_gate  the output gate g_proj(x) [H * V] (NULL: no gate)
+ *   norm_weight [V] in io_dtype or float32 (NULL: o is returned un-normalised)
+ *   o  [N, H, V] in io_dtype, float32 when norm_weight is float32 and io_dtype
+ *      is not (torch's promotion)
+ * Flags: GDN2_FLAG_L2NORM_QK, GATE_IN_KERNEL, LOWER_BOUND, SIGMOID_BW.
+ */
+int gdn2_decode_fused(const void *const raw_qkv[3], const int64_t ld_qkv[3], const void *g,
+                      int64_t ldg, int g_dtype, const void *b, int64_t ldb, const void *w,
+                      int64_t ldw, const void *const conv_weight[3], const void *const conv_bias[3],
+                      int conv_width, const void *const conv_cache_in[3],
+                      void *const conv_cache_out[3], const float *initial_state,
+                      int64_t initial_state_row_stride, float *final_state,
+                      int64_t final_state_row_stride, const float *A_log, const float *dt_bias,
+                      float lower_bound, const void *gate, int64_t ld_gate,
+                      const void *norm_weight, int norm_weight_dtype, float eps, void *o,
+                      int io_dtype, int N, int H, int K, int V, float scale, unsigned flags,
+                      void *stream);
+
+/*
  * Bytes of device workspace gdn2_chunk_fwd needs for this shape.
  */
 size_t gdn2_chunk_fwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,

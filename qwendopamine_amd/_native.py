@@ -67,6 +67,11 @@ SIGNATURES: dict[str, tuple] = {
         _i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     ),
     "gdn2_gated_rmsnorm_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i64, _i, _f, _vp]),
+    "gdn2_decode_fused": (
+        _i,
+        [_vp, _vp, _vp, _i64, _i, _vp, _i64, _vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _i64, _vp, _i64,
+         _vp, _vp, _f, _vp, _i64, _vp, _i, _f, _vp, _i, _i, _i, _i, _i, _f, _u, _vp],
+    ),
     "gdn2_chunk_states": (_i, [_vp, _sz, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "gdn2_chunk_fwd_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _vp, _i]),
     "gdn2_chunk_fwd": (

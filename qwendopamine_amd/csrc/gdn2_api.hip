@@ -237,6 +237,74 @@ int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+int gdn2_decode_fused(const void *const raw_qkv[3], const int64_t ld_qkv[3], const void *g,
+                      int64_t ldg, int g_dtype, const void *b, int64_t ldb, const void *w,
+                      int64_t ldw, const void *const conv_weight[3], const void *const conv_bias[3],
+                      int conv_width, const void *const conv_cache_in[3],
+                      void *const conv_cache_out[3], const float *initial_state,
+                      int64_t initial_state_row_stride, float *final_state,
+                      int64_t final_state_row_stride, const float *A_log, const float *dt_bias,
+                      float lower_bound, const void *gate, int64_t ld_gate,
+                      const void *norm_weight, int norm_weight_dtype, float eps, void *o,
+                      int io_dtype, int N, int H, int K, int V, float scale, unsigned flags,
+                      void *stream)
+{
+    if (!valid_dtype(io_dtype) || !valid_dtype(g_dtype)) return GDN2_ERR_INVALID;
+    if (g_dtype != GDN2_DTYPE_F32 && g_dtype != io_dtype) return GDN2_ERR_UNSUPPORTED;
+    if (N < 0 || H <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
+    if (K != V || (K != 64 && K != 128) || conv_width != 4) return GDN2_ERR_UNSUPPORTED;
+    if (flags & ~(GDN2_FLAG_L2NORM_QK | GDN2_FLAG_GATE_IN_KERNEL | GDN2_FLAG_LOWER_BOUND |
+                  GDN2_FLAG_SIGMOID_BW))
+        return GDN2_ERR_INVALID;
+    if ((flags & GDN2_FLAG_LOWER_BOUND) && !(flags & GDN2_FLAG_GATE_IN_KERNEL)) return GDN2_ERR_INVALID;
+    if ((flags & GDN2_FLAG_GATE_IN_KERNEL) && !A_log) return GDN2_ERR_INVALID;
+    if (static_cast<int64_t>(N) * H > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
+    if (N == 0) return GDN2_OK;
+    if (!raw_qkv || !ld_qkv || !conv_weight || !g || !b || !w || !o) return GDN2_ERR_INVALID;
+    const int64_t HD = static_cast<int64_t>(H) * K;
+    DecodeFusedParams p;
+    for (int t = 0; t < 3; ++t) {
+        if (!raw_qkv[t] || !conv_weight[t] || ld_qkv[t] < HD) return GDN2_ERR_INVALID;
+        p.x[t] = raw_qkv[t];
+        p.ldx[t] = ld_qkv[t];
+        p.cw[t] = conv_weight[t];
+        p.cb[t] = conv_bias ? conv_bias[t] : nullptr;
+        p.cin[t] = conv_cache_in ? conv_cache_in[t] : nullptr;
+        p.cout[t] = conv_cache_out ? conv_cache_out[t] : nullptr;
+    }
+    if (ldg < HD || ldb < HD || ldw < HD) return GDN2_ERR_INVALID;
+    if (gate && (ld_gate < HD || !norm_weight)) return GDN2_ERR_INVALID;
+    if (norm_weight && norm_weight_dtype != GDN2_DTYPE_F32 && norm_weight_dtype != io_dtype)
+        return GDN2_ERR_INVALID;
+    const int64_t slab = HD * V;
+    for (const void *st : {static_cast<const void *>(initial_state), static_cast<const void *>(final_state)})
+        if (st && (reinterpret_cast<uintptr_t>(st) % 16)) return GDN2_ERR_INVALID;
+    if (initial_state && (initial_state_row_stride < slab || initial_state_row_stride % 4))
+        return GDN2_ERR_INVALID;
+    if (final_state && (final_state_row_stride < slab || final_state_row_stride % 4))
+        return GDN2_ERR_INVALID;
+    p.g = g; p.b = b; p.w = w;
+    p.ldg = ldg; p.ldb = ldb; p.ldw = ldw;
+    p.h0 = initial_state;
+    p.ht = final_state;
+    p.h0_stride = initial_state_row_stride;
+    p.ht_stride = final_state_row_stride;
+    p.A_log = A_log;
+    p.dt_bias = dt_bias;
+    p.lower_bound = lower_bound;
+    p.z = gate;
+    p.ldz = ld_gate;
+    p.nw = norm_weight;
+    p.nw_f32 = norm_weight && norm_weight_dtype == GDN2_DTYPE_F32 && io_dtype != GDN2_DTYPE_F32;
+    p.eps = eps;
+    p.o = o;
+    p.N = N; p.H = H; p.D = K;
+    p.scale = scale;
+    p.flags = flags;
+    const hipError_t err = launch_decode_fused(p, io_dtype, g_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
 size_t gdn2_chunk_fwd_workspace_size(int B, int T, int H, int K, int V, int io_dtype,
                                      const int64_t *cu_seqlens_host, int num_seqs)
 {

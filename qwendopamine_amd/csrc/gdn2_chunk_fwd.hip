@@ -50,18 +50,6 @@ namespace gdn2 {
 
 namespace {
 
-// x rounded to T (nearest even) and back to fp32.
-template <typename T>
-__device__ __forceinline__ float round_to(float x)
-{
-    if constexpr (std::is_same<T, bf16_t>::value)
-        return bf16_bits_to_f32(f32_to_bf16_bits(x));
-    else if constexpr (std::is_same<T, f16_t>::value)
-        return static_cast<float>(static_cast<_Float16>(x));
-    else
-        return x;
-}
-
 // Four consecutive input values kept as the input dtype's bits (two registers
 // for 16-bit inputs, half of what fp32 values take) and widened to fp32 where
 // they are used.

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/gdn2_hip.h"
 
 namespace gdn2 {
@@ -86,6 +88,24 @@ __device__ __forceinline__ float softplus_f(float x)
 
 // torch.sigmoid in fp32 (GDN2_FLAG_SIGMOID_BW): 1 / (1 + e^-x), 0 for x -> -inf.
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// x * sigmoid(x) with the hardware reciprocal (1 ulp in fp32) instead of an
+// IEEE divide, for the module's SiLUs whose results are rounded to the input
+// dtype right after (the short convolution, the output gate).
+__device__ __forceinline__ float silu_f32(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// x rounded to T (nearest even) and back to fp32: the rounding of a torch op
+// computed in T.
+template <typename T>
+__device__ __forceinline__ float round_to(float x)
+{
+    if constexpr (std::is_same<T, bf16_t>::value)
+        return bf16_bits_to_f32(f32_to_bf16_bits(x));
+    else if constexpr (std::is_same<T, f16_t>::value)
+        return static_cast<float>(static_cast<_Float16>(x));
+    else
+        return x;
+}
 
 // Decay activation applied in-kernel when GDN2_FLAG_GATE_IN_KERNEL is set:
 //   g = -exp(A_log[h]) * softplus(g_raw + dt_bias[h, d])         (default)

@@ -34,6 +34,38 @@ struct RecurrentParams {
 hipError_t launch_recurrent_fwd(const RecurrentParams &p, int io_dtype, int g_dtype, int N,
                                 hipStream_t stream);
 
+// Fused module decode step (one token per sequence, HV == H, K == V == D):
+// short convolution of the raw q / k / v projections with the conv caches,
+// gate and b / w activations, the recurrence, and the gated RMS norm of the
+// output.  Row n of a [N, C] input is at base + n * ld (unit channel stride).
+struct DecodeFusedParams {
+    const void *x[3];     // raw q, k, v projection rows: channel h * D + c of head h
+    int64_t ldx[3];
+    const void *cw[3];    // conv weights [H * D, W]
+    const void *cb[3];    // conv biases [H * D] or NULL
+    const void *cin[3];   // conv caches [N, H * D, W - 1] or NULL (zero history)
+    void *cout[3];        // new conv caches (may equal cin) or NULL
+    const void *g, *b, *w;
+    int64_t ldg, ldb, ldw;
+    const float *h0;      // [N, H, D, D] rows h0_stride apart, or NULL
+    float *ht;            // may equal h0 (in place), or NULL
+    int64_t h0_stride, ht_stride;
+    const float *A_log, *dt_bias;
+    float lower_bound;
+    const void *z;        // output gate rows [N, H * D] (NULL: no gate)
+    int64_t ldz;
+    const void *nw;       // norm weight [D] (NULL: no norm, o as computed)
+    int nw_f32;           // norm weight (and output) float32 while the io dtype is 16-bit
+    float eps;
+    void *o;              // [N, H, D]
+    int N, H, D;
+    float scale;
+    unsigned flags;
+};
+
+hipError_t launch_decode_fused(const DecodeFusedParams &p, int io_dtype, int g_dtype,
+                               hipStream_t stream);
+
 struct ChunkFwdArgs {
     const void *q, *k, *v, *g, *b, *w;
     void *o;

@@ -24,29 +24,6 @@ namespace gdn2 {
 
 namespace {
 
-template <typename T>
-__device__ __forceinline__ float round_to(float x);
-template <>
-__device__ __forceinline__ float round_to<float>(float x)
-{
-    return x;
-}
-template <>
-__device__ __forceinline__ float round_to<bf16_t>(float x)
-{
-    return bf16_bits_to_f32(f32_to_bf16_bits(x));
-}
-template <>
-__device__ __forceinline__ float round_to<f16_t>(float x)
-{
-    return static_cast<float>(static_cast<_Float16>(x));
-}
-
-// x * sigmoid(x) with the hardware reciprocal (1 ulp in fp32) instead of an
-// IEEE divide: the divide dominated these passes' VALU time, and the result is
-// rounded to bf16 / fp16 right after for 16-bit inputs.
-__device__ __forceinline__ float silu_f32(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
-
 // One thread per (tensor, batch row, channel d, tile of TT tokens).  The
 // thread keeps the last W inputs of its channel in registers, so each input
 // is read once (plus W-1 tokens of history at the tile start); a wave covers

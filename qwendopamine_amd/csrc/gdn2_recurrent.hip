@@ -641,6 +641,244 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
     }
 }
 
+// Fused module decode step (one token per sequence, HV == H, K == V == D).
+// Replaces, for the module's decode call, the chain ShortConvolution x 3
+// (reference gdn2.py:395-430) -> gate and b / w activations (gdn2.py:840-866)
+// -> fused_recurrent_gdn2 (fused_recurrent_gdn2.py:461-555) -> RMSNormGated
+// (gdn2.py:433-452), so that q, k, v and o make no HBM round trip between
+// them.  Each step keeps the arithmetic of the separate HIP passes:
+//  * the convolution in the op order and roundings of short_conv_vec_kernel
+//    (fp32 accumulation, the output rounded to the io dtype before and after
+//    the SiLU), the new cache = the last W-1 inputs;
+//  * the recurrence as decode_step_kernel computes it (at D = 128 the same
+//    thread mapping and summation order);
+//  * the output rounded to the io dtype, then the gated norm in the lane
+//    layout and op order of gated_rmsnorm_kernel.
+// Mapping: D * D / 64 threads per (sequence, head) -- one wave at D = 64, so
+// the step needs no block barrier there -- each holding 16 float4 of the
+// state; thread c < D owns channel c of the per-channel inputs.
+template <typename TI, typename TG, int D, bool H0>
+__global__ __launch_bounds__(D * D / 64) void decode_fused_kernel(DecodeFusedParams p)
+{
+    constexpr int NT = D * D / 64, NW = NT / kWave;
+    constexpr int TPR = D / 4, RG = NT / TPR, NR = D / RG, W = 4, EPL = D / kWave;
+    static_assert(NR * RG == D && TPR <= kWave && EPL * kWave == D, "decode mapping");
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    const int cq = tid % TPR, rg = tid / TPR, col = 4 * cq;
+    const int n = blockIdx.x / p.H, h = blockIdx.x % p.H;
+    const int64_t HD = static_cast<int64_t>(p.H) * D;
+
+    __shared__ __align__(16) float s_q[D], s_k[D], s_e[D], s_a[D], s_v[D], s_w[D], s_o[D];
+    __shared__ float s_part[NW][3];
+    __shared__ float4 s_red[NW][2][TPR];
+
+    const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
+    const bool gate = (p.flags & GDN2_FLAG_GATE_IN_KERNEL) != 0;
+    const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
+    const bool sig_bw = (p.flags & GDN2_FLAG_SIGMOID_BW) != 0;
+
+    // Every request first: the channel inputs (thread c < D; the others read
+    // channel D-1 and discard it), wave 0's output gate and norm weight, then
+    // the state.
+    const bool chan = tid < D;
+    const int c = chan ? tid : D - 1;
+    const int64_t ch = static_cast<int64_t>(h) * D + c;
+    float xh[3][W], wt[3][W], bias[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        const TI *x = static_cast<const TI *>(p.x[t]);
+        const TI *cw = static_cast<const TI *>(p.cw[t]);
+        const TI *ci = static_cast<const TI *>(p.cin[t]);
+        xh[t][W - 1] = io<TI>::ld(x, n * p.ldx[t] + ch);
+#pragma unroll
+        for (int j = 0; j < W - 1; ++j)
+            xh[t][j] = ci ? io<TI>::ld(ci, (n * HD + ch) * (W - 1) + j) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < W; ++j) wt[t][j] = io<TI>::ld(cw, ch * W + j);
+        bias[t] = p.cb[t] ? io<TI>::ld(static_cast<const TI *>(p.cb[t]), ch) : 0.0f;
+    }
+    float gv = io<TG>::ld(static_cast<const TG *>(p.g), n * p.ldg + ch);
+    float bv = io<TI>::ld(static_cast<const TI *>(p.b), n * p.ldb + ch);
+    float wv = io<TI>::ld(static_cast<const TI *>(p.w), n * p.ldw + ch);
+    const float a_log = gate ? p.A_log[h] : 0.0f;
+    const float dtb = gate && p.dt_bias ? p.dt_bias[ch] : 0.0f;
+    float zr[EPL], nwr[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const int cz = lane + kWave * e;
+        zr[e] = p.z ? io<TI>::ld(static_cast<const TI *>(p.z), n * p.ldz + static_cast<int64_t>(h) * D + cz) : 0.0f;
+        nwr[e] = !p.nw ? 0.0f
+                       : (p.nw_f32 ? static_cast<const float *>(p.nw)[cz]
+                                   : io<TI>::ld(static_cast<const TI *>(p.nw), cz));
+    }
+    float4 st[NR];
+    if constexpr (H0) {
+        const float *src = p.h0 + n * p.h0_stride + static_cast<int64_t>(h) * D * D;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) st[i] = *reinterpret_cast<const float4 *>(src + (rg + i * RG) * D + col);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    // Short convolution + SiLU; the new cache holds the last W-1 inputs (read
+    // above by this thread, so an in-place cache update is safe).
+    float xc[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < W; ++j) acc = fmaf(wt[t][j], xh[t][j], acc);
+        xc[t] = round_to<TI>(silu_f32(round_to<TI>(acc + bias[t])));
+        if (chan && p.cout[t]) {
+            TI *co = static_cast<TI *>(p.cout[t]);
+#pragma unroll
+            for (int j = 0; j < W - 1; ++j) io<TI>::st(co, (n * HD + ch) * (W - 1) + j, xh[t][j + 1]);
+        }
+    }
+    if (sig_bw) {
+        bv = sigmoid_f(bv);
+        wv = sigmoid_f(wv);
+    }
+    const float gk = gate ? gate_activation(gv, a_log, dtb, use_lb, p.lower_bound) : gv;
+    const float qx = chan ? xc[0] : 0.0f, kx = chan ? xc[1] : 0.0f;
+    float qq = wave_sum(qx * qx), kk = wave_sum(kx * kx), qk = wave_sum(qx * kx);
+    if constexpr (NW > 1) {
+        if (lane == 0) {
+            s_part[wid][0] = qq;
+            s_part[wid][1] = kk;
+            s_part[wid][2] = qk;
+        }
+        __syncthreads();
+        qq = kk = qk = 0.f;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            qq += s_part[i][0];
+            kk += s_part[i][1];
+            qk += s_part[i][2];
+        }
+    }
+    const float invq = l2 ? 1.0f / fmaxf(sqrtf(qq), 1e-6f) : 1.0f;
+    const float invk = l2 ? 1.0f / fmaxf(sqrtf(kk), 1e-6f) : 1.0f;
+    if (chan) {
+        const float kn = kx * invk;
+        s_q[c] = qx * invq * p.scale;
+        s_k[c] = kn;
+        s_e[c] = bv * kn;
+        s_a[c] = expf(gk);
+        s_v[c] = xc[2];
+        s_w[c] = wv;
+    }
+    const float kq = qk * invq * invk * p.scale;
+    __syncthreads();
+
+    float4 pr = make_float4(0.f, 0.f, 0.f, 0.f), po = pr;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int r = rg + i * RG;
+        const float a = s_a[r];
+        st[i].x *= a;
+        st[i].y *= a;
+        st[i].z *= a;
+        st[i].w *= a;
+        pr = f4_fma(st[i], s_e[r], pr);
+        po = f4_fma(st[i], s_q[r], po);
+    }
+#pragma unroll
+    for (int off = TPR; off < kWave; off <<= 1) {
+        const float4 a = shfl_xor4(pr, off), cc = shfl_xor4(po, off);
+        pr.x += a.x; pr.y += a.y; pr.z += a.z; pr.w += a.w;
+        po.x += cc.x; po.y += cc.y; po.z += cc.z; po.w += cc.w;
+    }
+    float4 R = pr, PO = po;
+    if constexpr (NW > 1) {
+        if (lane < TPR) {
+            s_red[wid][0][cq] = pr;
+            s_red[wid][1][cq] = po;
+        }
+        __syncthreads();
+        R = s_red[0][0][cq];
+        PO = s_red[0][1][cq];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) {
+            const float4 a = s_red[i][0][cq], cc = s_red[i][1][cq];
+            R.x += a.x; R.y += a.y; R.z += a.z; R.w += a.w;
+            PO.x += cc.x; PO.y += cc.y; PO.z += cc.z; PO.w += cc.w;
+        }
+    }
+    const float4 vv = *reinterpret_cast<const float4 *>(&s_v[col]);
+    const float4 ww = *reinterpret_cast<const float4 *>(&s_w[col]);
+    const float4 u = make_float4(ww.x * vv.x - R.x, ww.y * vv.y - R.y, ww.z * vv.z - R.z,
+                                 ww.w * vv.w - R.w);
+    float *dst = p.ht ? p.ht + n * p.ht_stride + static_cast<int64_t>(h) * D * D : nullptr;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int r = rg + i * RG;
+        const float kr = s_k[r];
+        st[i].x = fmaf(kr, u.x, st[i].x);
+        st[i].y = fmaf(kr, u.y, st[i].y);
+        st[i].z = fmaf(kr, u.z, st[i].z);
+        st[i].w = fmaf(kr, u.w, st[i].w);
+        if (dst) *reinterpret_cast<float4 *>(dst + r * D + col) = st[i];
+    }
+    if (rg == 0) {
+        const float4 o4 = f4_fma(u, kq, PO);
+        s_o[col] = round_to<TI>(o4.x);
+        s_o[col + 1] = round_to<TI>(o4.y);
+        s_o[col + 2] = round_to<TI>(o4.z);
+        s_o[col + 3] = round_to<TI>(o4.w);
+    }
+    __syncthreads();
+    if (wid != 0) return;  // no barriers below
+
+    // Output: RMSNormGated (gdn2.py:433-452) over the head's D values.
+    const int64_t obase = (static_cast<int64_t>(n) * p.H + h) * D;
+    float xo[EPL], sq = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        xo[e] = s_o[lane + kWave * e];
+        sq += round_to<TI>(xo[e] * xo[e]);
+    }
+    if (!p.nw) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) io<TI>::st(static_cast<TI *>(p.o), obase + lane + kWave * e, xo[e]);
+        return;
+    }
+    const float var = round_to<TI>(wave_sum(sq) / static_cast<float>(D));
+    const float inv = round_to<TI>(rsqrtf(round_to<TI>(var + p.eps)));
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const int cz = lane + kWave * e;
+        const float a = round_to<TI>(xo[e] * inv);
+        if (p.nw_f32) {
+            // An fp32 weight promotes the rest of the expression to fp32.
+            static_cast<float *>(p.o)[obase + cz] = p.z ? a * nwr[e] * round_to<TI>(silu_f32(zr[e])) : a * nwr[e];
+        } else {
+            const float aw = round_to<TI>(a * nwr[e]);
+            io<TI>::st(static_cast<TI *>(p.o), obase + cz,
+                       p.z ? round_to<TI>(aw * round_to<TI>(silu_f32(zr[e]))) : aw);
+        }
+    }
+}
+
+template <typename TI, typename TG>
+static hipError_t launch_decode_fused_t(const DecodeFusedParams &p, hipStream_t stream)
+{
+    const dim3 grid(p.N * p.H);
+    if (p.D == 64) {
+        if (p.h0)
+            hipLaunchKernelGGL((decode_fused_kernel<TI, TG, 64, true>), grid, dim3(64), 0, stream, p);
+        else
+            hipLaunchKernelGGL((decode_fused_kernel<TI, TG, 64, false>), grid, dim3(64), 0, stream, p);
+    } else {
+        if (p.h0)
+            hipLaunchKernelGGL((decode_fused_kernel<TI, TG, 128, true>), grid, dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL((decode_fused_kernel<TI, TG, 128, false>), grid, dim3(256), 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
 template <typename TI, typename TG, int TPR>
 static hipError_t launch_nr(const RecurrentParams &p, int N, hipStream_t stream)
 {
@@ -695,6 +933,21 @@ static hipError_t launch_g(const RecurrentParams &p, int g_dtype, int N, hipStre
     case GDN2_DTYPE_F32: return launch_tpr<TI, float>(p, N, stream);
     case GDN2_DTYPE_BF16: return launch_tpr<TI, bf16_t>(p, N, stream);
     default: return launch_tpr<TI, f16_t>(p, N, stream);
+    }
+}
+
+hipError_t launch_decode_fused(const DecodeFusedParams &p, int io_dtype, int g_dtype,
+                               hipStream_t stream)
+{
+    if (p.N == 0) return hipSuccess;
+    switch (io_dtype) {
+    case GDN2_DTYPE_F32: return launch_decode_fused_t<float, float>(p, stream);
+    case GDN2_DTYPE_BF16:
+        return g_dtype == GDN2_DTYPE_F32 ? launch_decode_fused_t<bf16_t, float>(p, stream)
+                                         : launch_decode_fused_t<bf16_t, bf16_t>(p, stream);
+    default:
+        return g_dtype == GDN2_DTYPE_F32 ? launch_decode_fused_t<f16_t, float>(p, stream)
+                                         : launch_decode_fused_t<f16_t, f16_t>(p, stream);
     }
 }
 

@@ -252,6 +252,10 @@ class GatedDeltaNet2(nn.Module):
         self.backend = backend
         self.compile_backend = compile_backend
         self.fp32_decay = fp32_decay
+        # Single-token inference calls run the fused decode kernel (conv, gates,
+        # recurrence and output norm in one launch) when its conditions hold;
+        # False runs the same steps as separate passes.
+        self.fused_decode = True
 
         self.head_k_dim = self.head_dim
         self.head_v_dim = int(self.head_dim * self.expand_v)
@@ -415,6 +419,39 @@ class GatedDeltaNet2(nn.Module):
         drop(self, "_in_cache", "_gate_cache")
         return super()._apply(fn, *args, **kwargs)
 
+    def _decode_fused(self, x, past_key_values, recurrent_state, conv_states, want_state, in_place,
+                      use_cache):
+        """Single-token inference step on the fused decode kernel (``ops.decode_step_fused``):
+        the short convolutions, the gate and b / w activations, the recurrence and the gated
+        output norm in one launch, between the input projections and ``o_proj``.  Same
+        result and cache updates as the separate passes of ``forward``."""
+        batch = x.shape[0]
+        W_in, sizes = self._fused_input_weight()
+        y = F.linear(x.reshape(batch, x.shape[-1]), W_in)  # [B, sum(sizes)]
+        qr, kr, vr, b, w, f0, g0 = y.split(sizes, dim=-1)
+        g = self.f_proj[1](f0)
+        z = self.g_proj[1](g0)
+        dt = x.dtype
+        caches = list(conv_states) if all(c is not None for c in conv_states) else None
+        if caches is not None and not all(c.dtype == dt and c.is_contiguous() for c in caches):
+            caches, in_place = [c.to(dt).contiguous() for c in caches], False
+        h0 = recurrent_state
+        if h0 is not None and (h0.dtype != torch.float32 or not h0.is_contiguous()):
+            h0, in_place = h0.float().contiguous(), False
+        if in_place and caches is None:
+            in_place = False
+        A_log, dt_bias = self._gate_params(1)
+        convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d)
+        o, state, new_caches = ops.decode_step_fused(
+            [qr, kr, vr], [c.conv1d.weight for c in convs], [c.conv1d.bias for c in convs], caches,
+            g, b, w, h0, z, self.o_norm.weight, self.o_norm.eps,
+            num_heads=self.num_heads, head_dim=self.head_k_dim, A_log=A_log, dt_bias=dt_bias,
+            update_cache_in_place=in_place, output_final_state=want_state)
+        if use_cache or past_key_values is not None:
+            self._update_cache(past_key_values, state, tuple(new_caches))
+        out = self.o_proj(o.reshape(batch, 1, -1))
+        return out, None, past_key_values
+
     def _algorithm(self, mode: str, backend: str, needs_grad: bool) -> str:
         if backend in ("torch-chunk", "compiled"):
             algo = "chunk"
@@ -478,6 +515,16 @@ class GatedDeltaNet2(nn.Module):
                            self.w_proj.weight)
                 and self.fp32_decay and not self.allow_neg_eigval)
         convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d) if self.use_short_conv else ()
+        if (fuse and self.fused_decode and seq_len == 1 and not padded and cu_seqlens is None and self.use_short_conv
+                and self.num_v_heads == self.num_heads and self.head_k_dim == self.head_v_dim
+                and self.head_k_dim in (64, 128) and self.conv_size == 4
+                and all(c.activation == "silu" for c in convs)
+                and self._algorithm(mode, resolve_gdn2_backend(self.backend, training=self.training,
+                                                               seq_len=seq_len), False) == "recurrent"
+                and _inference(x, *(c.conv1d.weight for c in convs), self.o_norm.weight,
+                               self.f_proj[1].weight, self.g_proj[1].weight)):
+            return self._decode_fused(x, past_key_values, recurrent_state, (cq, ck, cv), want_state,
+                                      in_place, use_cache)
         g0 = None
         if fuse and self.use_short_conv and _inference(x, *(c.conv1d.weight for c in convs)):
             # The seven first-stage input projections as one GEMM; q, k and v

@@ -37,6 +37,7 @@ __all__ = [
     "short_convolution",
     "gated_rmsnorm",
     "rms_norm",
+    "decode_step_fused",
 ]
 
 
@@ -821,3 +822,125 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.
     )
     nat.check(st, name)
     return out
+
+
+def _rows2d(name: str, x: torch.Tensor, dt: torch.dtype, width: int) -> int:
+    """Row stride of a [N, >= width] tensor read in place (unit channel stride)."""
+    if x.dim() != 2 or x.dtype != dt or x.stride(1) != 1 or x.shape[1] < width:
+        raise ValueError(f"decode_step_fused: {name} must be [N, {width}] {dt} rows with unit channel "
+                         f"stride; got {tuple(x.shape)} {x.dtype} strides {x.stride()}")
+    return x.stride(0) if x.shape[0] > 1 else max(x.stride(0), width)
+
+
+def decode_step_fused(
+    x_qkv: list[torch.Tensor],
+    conv_weights: list[torch.Tensor],
+    conv_biases: list[torch.Tensor | None] | None,
+    conv_caches: list[torch.Tensor] | None,
+    g: torch.Tensor,
+    b: torch.Tensor,
+    w: torch.Tensor,
+    initial_state: torch.Tensor | None,
+    gate: torch.Tensor | None,
+    norm_weight: torch.Tensor | None,
+    eps: float = 1e-5,
+    *,
+    num_heads: int,
+    head_dim: int,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    lower_bound: float | None = None,
+    scale: float | None = None,
+    use_qk_l2norm_in_kernel: bool = True,
+    bw_logits: bool = True,
+    update_cache_in_place: bool = False,
+    output_final_state: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor | None, list[torch.Tensor] | None]:
+    """One decode token per sequence through the whole mixer core (C entry ``gdn2_decode_fused``).
+
+    Fuses, for ``num_v_heads == num_heads`` and ``K == V == head_dim`` in {64, 128}, the
+    module's decode chain: ``ShortConvolution`` of q, k, v with the conv caches
+    (reference ``gdn2.py:395-430``), the gate and b / w activations (``:840-866``), the
+    recurrence (``fused_recurrent_gdn2.py:461-555``) and ``RMSNormGated`` of the output
+    (``:433-452``).  Each stage keeps the arithmetic of its separate HIP pass.
+
+    ``x_qkv``: the raw q, k, v projections, ``[N, H * D]`` each (column ranges of a wider
+    projection output are read in place); ``g`` the decay pre-activation when ``A_log`` is
+    given (else the activated decay), ``b`` / ``w`` the erase / write gates (logits when
+    ``bw_logits``), ``gate`` the output gate ``g_proj(x)``, all ``[N, H * D]``.
+    ``conv_weights[t]`` is the Conv1d weight ``[H * D, 1, 4]``; ``conv_caches[t]``
+    ``[N, H * D, 3]`` or ``None`` (zero history).  ``initial_state`` ``[N, H, D, D]`` float32.
+
+    Returns ``(o [N, H, D], final_state, new_conv_caches)``.  With ``update_cache_in_place``
+    the conv caches and ``initial_state`` are updated where they lie and returned.
+    Inference only.
+    """
+    name = "decode_step_fused"
+    H, D = num_heads, head_dim
+    HD = H * D
+    _require_gpu(name, *x_qkv, g, b, w, initial_state, gate, norm_weight)
+    dt = x_qkv[0].dtype
+    N = x_qkv[0].shape[0]
+    if len(x_qkv) != 3 or len(conv_weights) != 3:
+        raise ValueError(f"{name}: q, k and v with one conv weight each")
+    ld = [_rows2d(nm, x, dt, HD) for nm, x in zip(("q", "k", "v"), x_qkv)]
+    g_dt = g.dtype if g.dtype in (torch.float32, dt) else None
+    if g_dt is None:
+        raise ValueError(f"{name}: g must be float32 or {dt}")
+    ldg, ldb, ldw = _rows2d("g", g, g_dt, HD), _rows2d("b", b, dt, HD), _rows2d("w", w, dt, HD)
+    ldz = 0 if gate is None else _rows2d("gate", gate, dt, HD)
+    if any(x.shape[0] != N for x in (*x_qkv, g, b, w)) or (gate is not None and gate.shape[0] != N):
+        raise ValueError(f"{name}: every input needs {N} rows")
+    W = int(conv_weights[0].shape[-1])
+    cw = [wt.detach().reshape(HD, W).to(dt).contiguous() for wt in conv_weights]
+    cb = None
+    if conv_biases is not None and any(x is not None for x in conv_biases):
+        cb = [None if x is None else x.detach().to(dt).contiguous() for x in conv_biases]
+    cin = None
+    if conv_caches is not None:
+        cin = list(conv_caches)
+        for c in cin:
+            if tuple(c.shape) != (N, HD, W - 1) or c.dtype != dt or not c.is_contiguous():
+                raise ValueError(f"{name}: conv caches must be contiguous {(N, HD, W - 1)} {dt} tensors")
+    if update_cache_in_place:
+        if cin is None or initial_state is None:
+            raise ValueError(f"{name}: update_cache_in_place needs conv caches and an initial state")
+        cout, ht = cin, initial_state
+    else:
+        cout = [torch.empty(N, HD, W - 1, dtype=dt, device=g.device) for _ in range(3)]
+        ht = torch.empty(N, H, D, D, dtype=torch.float32, device=g.device) if output_final_state else None
+    for nm, st in (("initial_state", initial_state), ("final state", ht)):
+        if st is not None and (st.dtype != torch.float32 or tuple(st.shape) != (N, H, D, D)
+                               or st.stride()[1:] != (D * D, D, 1)):
+            raise ValueError(f"{name}: {nm} must be float32 [N, H, D, D] with contiguous rows")
+    nwt = None
+    nw_code = nat.DTYPE_F32
+    if norm_weight is not None:
+        nwt = norm_weight.detach()
+        nwt = nwt if nwt.dtype in (torch.float32, dt) else nwt.to(dt)
+        nwt = nwt.contiguous()
+        nw_code = nat.dtype_code(nwt.dtype)
+    out_dt = torch.float32 if (nwt is not None and nwt.dtype == torch.float32 and dt != torch.float32) else dt
+    o = torch.empty(N, H, D, dtype=out_dt, device=g.device)
+    a_log, dtb = _gate_tensors(A_log is not None, A_log, dt_bias, H, D)
+    flags = _flags(use_qk_l2norm_in_kernel, A_log is not None, lower_bound)
+    if bw_logits:
+        flags |= nat.FLAG_SIGMOID_BW
+    if scale is None:
+        scale = D**-0.5
+    i64x3 = (ctypes.c_int64 * 3)(*ld)
+    lib = nat.load()
+    st = lib.gdn2_decode_fused(
+        _ptr_array([nat.ptr(x) for x in x_qkv]), ctypes.addressof(i64x3),
+        nat.ptr(g), ldg, nat.dtype_code(g_dt), nat.ptr(b), ldb, nat.ptr(w), ldw,
+        _ptr_array([nat.ptr(x) for x in cw]), None if cb is None else _ptr_array([nat.ptr(x) for x in cb]), W,
+        None if cin is None else _ptr_array([nat.ptr(x) for x in cin]), _ptr_array([nat.ptr(x) for x in cout]),
+        nat.ptr(initial_state), 0 if initial_state is None else initial_state.stride(0),
+        nat.ptr(ht), 0 if ht is None else ht.stride(0),
+        nat.ptr(a_log), nat.ptr(dtb), float(lower_bound) if lower_bound is not None else 0.0,
+        nat.ptr(gate), ldz, nat.ptr(nwt), nw_code, float(eps), nat.ptr(o),
+        nat.dtype_code(dt), N, H, D, D, float(scale), flags, nat.stream_handle(g.device),
+    )
+    _ptr_array.keep.clear()
+    nat.check(st, name)
+    return o, ht, cout
