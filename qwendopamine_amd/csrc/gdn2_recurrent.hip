@@ -677,39 +677,53 @@ __global__ __launch_bounds__(D * D / 64) void decode_fused_kernel(DecodeFusedPar
     const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
     const bool sig_bw = (p.flags & GDN2_FLAG_SIGMOID_BW) != 0;
 
-    // Every request first: the channel inputs (thread c < D; the others read
-    // channel D-1 and discard it), wave 0's output gate and norm weight, then
-    // the state.
+    // Every request first, straight-line: the channel inputs (thread c < D; the
+    // others read channel D-1 and discard it), wave 0's output gate and norm
+    // weight, then the state.  An absent optional input (conv cache, bias,
+    // gate, norm weight, gate parameters) is read from an always-valid address
+    // -- the conv weights, HD * W elements -- and zeroed by a uniform factor
+    // where it is used: a load behind a branch on the pointer would wait for
+    // its data right there, before the next request leaves.
     const bool chan = tid < D;
     const int c = chan ? tid : D - 1;
     const int64_t ch = static_cast<int64_t>(h) * D + c;
-    float xh[3][W], wt[3][W], bias[3];
+    const TI *safe = static_cast<const TI *>(p.cw[0]);
+    float xh[3][W], wt[3][W], bias[3], mcache[3], mbias[3];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
         const TI *x = static_cast<const TI *>(p.x[t]);
         const TI *cw = static_cast<const TI *>(p.cw[t]);
-        const TI *ci = static_cast<const TI *>(p.cin[t]);
+        const bool hc = p.cin[t] != nullptr, hb = p.cb[t] != nullptr;
+        const TI *ci = hc ? static_cast<const TI *>(p.cin[t]) : safe;
+        const TI *cb = hb ? static_cast<const TI *>(p.cb[t]) : safe;
+        const int64_t coff = hc ? (n * HD + ch) * (W - 1) : ch;
+        mcache[t] = hc ? 1.0f : 0.0f;
+        mbias[t] = hb ? 1.0f : 0.0f;
         xh[t][W - 1] = io<TI>::ld(x, n * p.ldx[t] + ch);
 #pragma unroll
-        for (int j = 0; j < W - 1; ++j)
-            xh[t][j] = ci ? io<TI>::ld(ci, (n * HD + ch) * (W - 1) + j) : 0.0f;
+        for (int j = 0; j < W - 1; ++j) xh[t][j] = io<TI>::ld(ci, coff + (hc ? j : 0));
 #pragma unroll
         for (int j = 0; j < W; ++j) wt[t][j] = io<TI>::ld(cw, ch * W + j);
-        bias[t] = p.cb[t] ? io<TI>::ld(static_cast<const TI *>(p.cb[t]), ch) : 0.0f;
+        bias[t] = io<TI>::ld(cb, ch);
     }
     float gv = io<TG>::ld(static_cast<const TG *>(p.g), n * p.ldg + ch);
     float bv = io<TI>::ld(static_cast<const TI *>(p.b), n * p.ldb + ch);
     float wv = io<TI>::ld(static_cast<const TI *>(p.w), n * p.ldw + ch);
-    const float a_log = gate ? p.A_log[h] : 0.0f;
-    const float dtb = gate && p.dt_bias ? p.dt_bias[ch] : 0.0f;
+    const float *fsafe = reinterpret_cast<const float *>(safe);  // HD * W * sizeof(TI) >= 4 * HD bytes
+    const float a_log = (gate ? p.A_log : fsafe)[gate ? h : 0];
+    const float dtb = (gate && p.dt_bias ? p.dt_bias : fsafe)[gate && p.dt_bias ? ch : 0];
+    const float mdtb = gate && p.dt_bias ? 1.0f : 0.0f;
+    const bool hz = p.z != nullptr, hn = p.nw != nullptr;
+    const TI *zp = hz ? static_cast<const TI *>(p.z) : safe;
+    const TI *nwp = hn && !p.nw_f32 ? static_cast<const TI *>(p.nw) : safe;
+    const float *nwf = hn && p.nw_f32 ? static_cast<const float *>(p.nw) : fsafe;
     float zr[EPL], nwr[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
         const int cz = lane + kWave * e;
-        zr[e] = p.z ? io<TI>::ld(static_cast<const TI *>(p.z), n * p.ldz + static_cast<int64_t>(h) * D + cz) : 0.0f;
-        nwr[e] = !p.nw ? 0.0f
-                       : (p.nw_f32 ? static_cast<const float *>(p.nw)[cz]
-                                   : io<TI>::ld(static_cast<const TI *>(p.nw), cz));
+        zr[e] = io<TI>::ld(zp, hz ? n * p.ldz + static_cast<int64_t>(h) * D + cz : cz);
+        const float nf = nwf[cz], nt = io<TI>::ld(nwp, cz);
+        nwr[e] = p.nw_f32 ? nf : nt;
     }
     float4 st[NR];
     if constexpr (H0) {
@@ -726,10 +740,12 @@ __global__ __launch_bounds__(D * D / 64) void decode_fused_kernel(DecodeFusedPar
     float xc[3];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
+#pragma unroll
+        for (int j = 0; j < W - 1; ++j) xh[t][j] *= mcache[t];
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < W; ++j) acc = fmaf(wt[t][j], xh[t][j], acc);
-        xc[t] = round_to<TI>(silu_f32(round_to<TI>(acc + bias[t])));
+        xc[t] = round_to<TI>(silu_f32(round_to<TI>(acc + bias[t] * mbias[t])));
         if (chan && p.cout[t]) {
             TI *co = static_cast<TI *>(p.cout[t]);
 #pragma unroll
@@ -740,7 +756,7 @@ __global__ __launch_bounds__(D * D / 64) void decode_fused_kernel(DecodeFusedPar
         bv = sigmoid_f(bv);
         wv = sigmoid_f(wv);
     }
-    const float gk = gate ? gate_activation(gv, a_log, dtb, use_lb, p.lower_bound) : gv;
+    const float gk = gate ? gate_activation(gv, a_log, dtb * mdtb, use_lb, p.lower_bound) : gv;
     const float qx = chan ? xc[0] : 0.0f, kx = chan ? xc[1] : 0.0f;
     float qq = wave_sum(qx * qx), kk = wave_sum(kx * kx), qk = wave_sum(qx * kx);
     if constexpr (NW > 1) {
