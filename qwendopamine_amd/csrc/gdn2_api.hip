@@ -385,7 +385,7 @@ int gdn2_chunk_states(const void *saved, size_t saved_bytes, int io_dtype, void 
 {
     if (!valid_dtype(io_dtype) || B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
     if (cu_seqlens_host && (B != 1 || num_seqs < 0)) return GDN2_ERR_INVALID;
-    if (K > 128) return GDN2_ERR_UNSUPPORTED;
+    if (!chunk_k_supported(K, io_dtype)) return GDN2_ERR_UNSUPPORTED;
     const int64_t nc = count_chunks(B, T, cu_seqlens_host, num_seqs);
     if (nc == 0) return GDN2_OK;
     if (!saved || !out) return GDN2_ERR_INVALID;

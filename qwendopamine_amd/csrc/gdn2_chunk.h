@@ -186,7 +186,10 @@ __device__ __forceinline__ float row16_scan(float x)
     return x;
 }
 
-inline int kp_for(int K) { return K <= 32 ? 32 : (K <= 64 ? 64 : 128); }
+// Padded key width of the chunk kernels (d_k <= 256; 256 only for 16-bit io,
+// whose blob still fits the scans' LDS once).
+inline int kp_for(int K) { return K <= 32 ? 32 : (K <= 64 ? 64 : (K <= 128 ? 128 : 256)); }
+inline bool chunk_k_supported(int K, int io_dtype) { return K <= 128 || (K <= 256 && io_dtype != GDN2_DTYPE_F32); }
 inline int bv_for(int V) { return V <= 16 ? 16 : (V <= 32 ? 32 : 64); }
 
 // Value-slice width of the sequential scans: the widest of 64/32/16 columns
@@ -213,7 +216,8 @@ inline int64_t blob_bytes(int io_dtype, int KP)
     switch (KP) {
     case 32: return f32 ? Blob<PrecKind::F32, 32>::BYTES : Blob<PrecKind::BF16, 32>::BYTES;
     case 64: return f32 ? Blob<PrecKind::F32, 64>::BYTES : Blob<PrecKind::BF16, 64>::BYTES;
-    default: return f32 ? Blob<PrecKind::F32, 128>::BYTES : Blob<PrecKind::BF16, 128>::BYTES;
+    case 128: return f32 ? Blob<PrecKind::F32, 128>::BYTES : Blob<PrecKind::BF16, 128>::BYTES;
+    default: return Blob<PrecKind::BF16, 256>::BYTES;
     }
 }
 

@@ -124,7 +124,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
     using st = typename P::st;
     using BL = Blob<PK, KP>;
     using Q = Q4<PK>;
-    constexpr bool DB = PK != PrecKind::F32;  // double-buffered blobs (16-bit only)
+    constexpr bool DB = PK != PrecKind::F32 && KP <= 128;  // double-buffered blobs where two fit
     constexpr int NBUF = DB ? 2 : 1;
     constexpr int NKT = KP / 16, NKS = KP / 32, NCT = BV / 16;
     constexpr int U16 = static_cast<int>(BL::BYTES / 16);
@@ -487,8 +487,11 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     // in exact arithmetic; to keep that cancellation accurate, the factor
     // tiles of the pair products carry fp32 precision: for 16-bit MFMA
     // operands as two planes, x = hi + lo.
-    constexpr int NPL = PK == PrecKind::F32 ? 1 : 2;
-    constexpr int NVS = PK == PrecKind::F32 ? 1 : 2;  // value tiles per staged slice
+    // At KP = 256 one plane and one value tile per slice: two planes of the three
+    // factor tiles alone would take 192 KB of LDS.
+    constexpr int NPL = PK == PrecKind::F32 || KP > 128 ? 1 : 2;
+    constexpr int NVS = PK == PrecKind::F32 || KP > 128 ? 1 : 2;  // value tiles per staged slice
+    constexpr int NLT = (NKT + 7) / 8;  // channel tiles per wave for the G_last rowsum
     constexpr int EPU = 16 / static_cast<int>(sizeof(st));
     constexpr int BLK = 256;
     // Transposed (B-order) factor tiles of every token block, for the pair products.
@@ -789,7 +792,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     for (int J = 0; J < 4; ++J) aT[J] = lT[J] = aN[J] = lN[J] = zero4();
 #pragma unroll
     for (int j = 0; j < NKH; ++j) cq[j] = ce[j] = ck[j] = zero4();
-    float last_acc = 0.f;  // this lane's part of rowsum(dS1 * S0) for channel tile wv
+    float last_acc[NLT];  // this lane's part of rowsum(dS1 * S0) for channel tiles wv + 8t
+#pragma unroll
+    for (int t = 0; t < NLT; ++t) last_acc[t] = 0.f;
     for (int vt0 = 0; vt0 < NVT; vt0 += NVS) {
         __syncthreads();  // previous slice fully consumed
         land_slice(pre);
@@ -819,14 +824,18 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
             store4<TI>(dvp, off, c, V, xv);
             store4<TI>(dwp, off, c, V, xw);
         }
-        if (wv < NKT) {
 #pragma unroll
-            for (int vl = 0; vl < NVS; ++vl) {
-                float a4[4], c4[4];
-                unpack4<PK>(ld_q4<PK>(blkD(wv, vl)), a4);
-                unpack4<PK>(ld_q4<PK>(blkH(wv, vl)), c4);
+        for (int t = 0; t < NLT; ++t) {
+            const int dt = wv + 8 * t;
+            if (dt < NKT) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) last_acc = fmaf(a4[i], c4[i], last_acc);
+                for (int vl = 0; vl < NVS; ++vl) {
+                    float a4[4], c4[4];
+                    unpack4<PK>(ld_q4<PK>(blkD(dt, vl)), a4);
+                    unpack4<PK>(ld_q4<PK>(blkH(dt, vl)), c4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) last_acc[t] = fmaf(a4[i], c4[i], last_acc[t]);
+                }
             }
         }
 #pragma unroll
@@ -856,13 +865,16 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     // ---- G_last term: part 1 exp(G_last) rowsum(dS1 * S0) (channel tile wv),
     // part 2 this block's sum of dKt * Kt (ck = dKt here).  Together they are
     // rowsum(dS1 * S1) written through the saved S0 and U only. ----
-    if (wv < NKT) {
-        const int dt = wv;
-        float acc = last_acc;
-        acc += __shfl_xor(acc, 16, 64);
-        acc += __shfl_xor(acc, 32, 64);
-        const int c = 16 * dt + m;
-        if (kg == 0) sLast[c] = acc * fexp2(sT[0][c] + sT[1][c] + sT[2][c] + sT[3][c]);
+#pragma unroll
+    for (int t = 0; t < NLT; ++t) {
+        const int dt = wv + 8 * t;
+        if (dt < NKT) {
+            float acc = last_acc[t];
+            acc += __shfl_xor(acc, 16, 64);
+            acc += __shfl_xor(acc, 32, 64);
+            const int c = 16 * dt + m;
+            if (kg == 0) sLast[c] = acc * fexp2(sT[0][c] + sT[1][c] + sT[2][c] + sT[3][c]);
+        }
     }
 #pragma unroll
     for (int j = 0; j < NKH; ++j) {
@@ -1097,7 +1109,10 @@ hipError_t launch_bwd_kp(const BwdParams &p, int total_chunks, hipStream_t strea
     switch (kp_for(p.K)) {
     case 32: return launch_bwd<PK, 32, TI, TG>(p, total_chunks, stream);
     case 64: return launch_bwd<PK, 64, TI, TG>(p, total_chunks, stream);
-    default: return launch_bwd<PK, 128, TI, TG>(p, total_chunks, stream);
+    case 128: return launch_bwd<PK, 128, TI, TG>(p, total_chunks, stream);
+    default:
+        if constexpr (PK != PrecKind::F32) return launch_bwd<PK, 256, TI, TG>(p, total_chunks, stream);
+        return hipErrorInvalidValue;  // not reached: fp32 beyond d_k = 128 is rejected before
     }
 }
 
@@ -1106,7 +1121,7 @@ hipError_t launch_bwd_kp(const BwdParams &p, int total_chunks, hipStream_t strea
 size_t chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype,
                                  const int64_t *cu_host, int num_seqs)
 {
-    if (K > 128) return 0;
+    if (!chunk_k_supported(K, io_dtype)) return 0;
     const int64_t nc = count_chunks(B, T, cu_host, num_seqs);
     return static_cast<size_t>(bwd_layout(nc, H, K, V, io_dtype).total);
 }
@@ -1114,14 +1129,14 @@ size_t chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
 size_t chunk_train_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype,
                                    const int64_t *cu_host, int num_seqs)
 {
-    if (K > 128) return 0;
+    if (!chunk_k_supported(K, io_dtype)) return 0;
     const int64_t nc = count_chunks(B, T, cu_host, num_seqs);
     return static_cast<size_t>(train_layout(nc, H, K, V, io_dtype).total);
 }
 
 int launch_chunk_bwd(const ChunkBwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream)
 {
-    if (a.K > 128) return GDN2_ERR_UNSUPPORTED;
+    if (!chunk_k_supported(a.K, io_dtype)) return GDN2_ERR_UNSUPPORTED;
     if (g_dtype != GDN2_DTYPE_F32 && g_dtype != io_dtype) return GDN2_ERR_UNSUPPORTED;
     const int64_t nc = count_chunks(a.B, a.T, a.cu_host, a.num_seqs);
     if (nc * a.H > 2147483647LL / 2) return GDN2_ERR_UNSUPPORTED;

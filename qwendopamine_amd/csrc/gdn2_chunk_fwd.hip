@@ -245,7 +245,7 @@ __device__ __forceinline__ PrepItem prep_item(const ChunkParams &p, int item)
 // ---------------------------------------------------------------------------
 template <PrecKind PK, int KP, typename TI, typename TG>
 __global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(PK == PrecKind::F32 && KP == 128 ? 1 : 3))) void
+__attribute__((amdgpu_waves_per_eu((PK == PrecKind::F32 && KP == 128) || KP > 128 ? 1 : 3))) void
 chunk_prep_kernel(ChunkParams p, int items)
 {
     using P = Prec<PK>;
@@ -260,7 +260,10 @@ chunk_prep_kernel(ChunkParams p, int items)
     constexpr int SZ1 = SZK > 64 * LDF * 4 ? SZK : 64 * LDF * 4;
     __shared__ __align__(16) unsigned char smem1[SZ1];  // Kend, then L (fp32)
     __shared__ __align__(16) st sEt[NKT * 4 * 256];     // Ebar^T, K16 blocks (channel, token)
-    __shared__ __align__(16) float sX[64 * LDF];        // row staging, block vectors, then X
+    // sX holds, in turn: waves 0-1's row staging, the block vectors, then X.
+    constexpr int SZX0 = 64 * LDF > 24 * KP ? 64 * LDF : 24 * KP;
+    constexpr int SZX = SZX0 > 8 * (KP * 4 + 16) ? SZX0 : 8 * (KP * 4 + 16);
+    __shared__ __align__(16) float sX[SZX];
     __shared__ __align__(16) float sT[4][KP];           // in-block decay totals (log2)
     st *sKend = reinterpret_cast<st *>(smem1);
     float *sL = reinterpret_cast<float *>(smem1);
@@ -268,7 +271,7 @@ chunk_prep_kernel(ChunkParams p, int items)
     float(*sEr)[KP] = reinterpret_cast<float(*)[KP]>(sX);              // 2^(decay before block)
     float(*sEa)[KP] = reinterpret_cast<float(*)[KP]>(sX + 4 * KP);     // 2^(decay after block)
     float(*sPf)[4][KP] = reinterpret_cast<float(*)[4][KP]>(sX + 8 * KP);  // key scale of block pair (R, I)
-    static_assert(24 * KP <= 64 * LDF, "block vectors must fit in sX");
+    static_assert(24 * KP <= SZX, "block vectors must fit in sX");
     static_assert(sizeof(sX) >= 2 * 16 * (KP * 4 + 16) && sizeof(smem1) >= 2 * 16 * (KP * 4 + 16),
                   "row staging must fit in sX and smem1");
 
@@ -662,7 +665,8 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     using st = typename P::st;
     using BL = Blob<PK, KP>;
     using Q = Q4<PK>;
-    constexpr bool DB = PK != PrecKind::F32;  // double-buffer the blob (fits only for 16-bit)
+    // Double-buffer the blob where two fit in LDS (16-bit storage, KP <= 128).
+    constexpr bool DB = PK != PrecKind::F32 && KP <= 128;
     constexpr int NBUF = DB ? 2 : 1;
     constexpr int NKT = KP / 16, NKS = KP / 32, NCT = BV / 16;
     constexpr int U16 = static_cast<int>(BL::BYTES / 16);
@@ -1230,7 +1234,10 @@ hipError_t launch_kp(const ChunkParams &p, int total_chunks, int stages, hipStre
     switch (kp_for(p.K)) {
     case 32: return launch_all<PK, 32, TI, TG>(p, total_chunks, stages, stream);
     case 64: return launch_all<PK, 64, TI, TG>(p, total_chunks, stages, stream);
-    default: return launch_all<PK, 128, TI, TG>(p, total_chunks, stages, stream);
+    case 128: return launch_all<PK, 128, TI, TG>(p, total_chunks, stages, stream);
+    default:
+        if constexpr (PK != PrecKind::F32) return launch_all<PK, 256, TI, TG>(p, total_chunks, stages, stream);
+        return hipErrorInvalidValue;  // not reached: the callers reject fp32 beyond d_k = 128
     }
 }
 
@@ -1240,14 +1247,14 @@ size_t chunk_fwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
                                  const int64_t *cu_host, int num_seqs)
 {
     (void)V;
-    if (K > 128) return 0;
+    if (!chunk_k_supported(K, io_dtype)) return 0;
     const int64_t nc = count_chunks(B, T, cu_host, num_seqs);
     return static_cast<size_t>(nc) * H * static_cast<size_t>(blob_bytes(io_dtype, kp_for(K)));
 }
 
 int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream)
 {
-    if (a.K > 128) return GDN2_ERR_UNSUPPORTED;
+    if (!chunk_k_supported(a.K, io_dtype)) return GDN2_ERR_UNSUPPORTED;
     if (g_dtype != GDN2_DTYPE_F32 && g_dtype != io_dtype) return GDN2_ERR_UNSUPPORTED;
     const int64_t nc = count_chunks(a.B, a.T, a.cu_host, a.num_seqs);
     if (nc * a.H > 2147483647LL / 2) return GDN2_ERR_UNSUPPORTED;

@@ -116,4 +116,8 @@ def test_chunk_workspace_size(lib):
     cu = (ctypes.c_int64 * 4)(0, 10, 10, 75)
     n2 = lib.gdn2_chunk_fwd_workspace_size(1, 75, 2, 64, 64, 0, ctypes.cast(cu, ctypes.c_void_p), 3)
     assert n2 == (1 + 0 + 2) * 2 * ((192 * 64 + 8192) * 4 + 64 * 4)
-    assert lib.gdn2_chunk_fwd_workspace_size(1, 64, 1, 200, 64, 1, None, 1) == 0
+    # d_k in (128, 256]: KP = 256 blobs (X, Aqk 64x64; -W, Qbar 64x256; Ktilde^T 256x64; 256
+    # decay floats) for 16-bit inputs; float32 inputs are not supported there, nor d_k > 256.
+    assert lib.gdn2_chunk_fwd_workspace_size(1, 64, 1, 200, 64, 1, None, 1) == (2 * 4096 + 3 * 16384) * 2 + 256 * 4
+    assert lib.gdn2_chunk_fwd_workspace_size(1, 64, 1, 200, 64, 0, None, 1) == 0
+    assert lib.gdn2_chunk_fwd_workspace_size(1, 64, 1, 257, 64, 1, None, 1) == 0
