@@ -10,7 +10,10 @@ Mirrors the reference op interfaces so callers can swap them in unchanged:
   (chunkwise prefill and training forward/backward).
 
 Both run the hand-written kernels of ``libgdn2_hip.so`` on the current HIP
-stream of the inputs' device.  Inputs must be ROCm GPU tensors: there is no
+stream of the inputs' device.  Like the reference ops (``chunk_gdn2.py:1267``,
+``fused_recurrent_gdn2.py:344``), the public ops are excluded from
+``torch.compile`` tracing (``torch.compiler.disable``): a compiled caller breaks
+its graph around them and runs them eagerly.  Inputs must be ROCm GPU tensors: there is no
 CPU path, and a missing library raises.  Semantics follow the reference
 oracle ``torch_recurrent_gdn2`` (``gdn2.py:100-184``); the final state is
 float32 (as the reference's accelerated ops return it).
@@ -131,6 +134,7 @@ def _cu(cu_seqlens, device, total_tokens: int):
     return cu_dev, cu_host
 
 
+@torch.compiler.disable
 def fused_recurrent_gdn2_fwd(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -280,6 +284,7 @@ def fused_recurrent_gdn2_fwd(
     return out, ht
 
 
+@torch.compiler.disable
 def fused_recurrent_gdn2(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -439,6 +444,7 @@ def chunk_gdn2_fwd(
     return res + (saved,)
 
 
+@torch.compiler.disable
 def chunk_gdn2_static(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -569,6 +575,7 @@ class ChunkGDN2Function(torch.autograd.Function):
         return (dq, dk, dv, dg, db, dw, None, None, None, dh0, None, None, None, None, None, None)
 
 
+@torch.compiler.disable
 def chunk_gdn2(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -675,6 +682,7 @@ def _ptr_array(ptrs) -> int:
 _ptr_array.keep = []
 
 
+@torch.compiler.disable
 def short_convolution(
     xs: list[torch.Tensor],
     weights: list[torch.Tensor],
@@ -765,6 +773,7 @@ def short_convolution(
     return ys, new
 
 
+@torch.compiler.disable
 def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
     """``x * rsqrt(mean(x^2) + eps) * weight * silu(z)`` over the last axis.
 
@@ -797,6 +806,7 @@ def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: f
     return out
 
 
+@torch.compiler.disable
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
     """``weight * (x * rsqrt(mean(x^2) + eps))`` over the last axis (N <= 2048).
 
@@ -834,6 +844,7 @@ def _rows2d(name: str, x: torch.Tensor, dt: torch.dtype, width: int) -> int:
     return x.stride(0) if x.shape[0] > 1 else max(x.stride(0), width)
 
 
+@torch.compiler.disable
 def decode_step_fused(
     x_qkv: list[torch.Tensor],
     conv_weights: list[torch.Tensor],

@@ -255,3 +255,21 @@ def test_stacked_input_weight_is_the_only_copy():
     m.double()
     W3, _ = m._fused_input_weight()
     assert W3.dtype == torch.float64 and m.q_proj.weight.data_ptr() == W3.data_ptr()
+
+
+def test_ops_are_not_traced_by_torch_compile():
+    """As the reference's ops (chunk_gdn2.py:1267, fused_recurrent_gdn2.py:344), the public
+    ops carry torch.compiler.disable: a compiled caller runs them eagerly, so the op's own
+    error for CPU tensors comes through instead of a tracing failure in the ctypes shim."""
+    from qwendopamine_amd import ops
+
+    x = torch.randn(1, 8, 2, 16)
+
+    def f(q):
+        o, _ = ops.chunk_gdn2(q, q, q, -q.abs(), q.sigmoid(), q.sigmoid())
+        return o * 2
+
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        torch.compile(f, backend="eager")(x)
+    for name in ("chunk_gdn2", "fused_recurrent_gdn2", "fused_recurrent_gdn2_fwd", "decode_step_fused"):
+        assert getattr(getattr(ops, name), "_torchdynamo_disable", False), name
