@@ -309,6 +309,8 @@ def bench_prologue(torch, dev, reps=20):
 
     * Prologue: the q/k/v short convolution + SiLU in one launch.
     * Epilogue: the gated RMS norm.
+    * Decode step: the fused kernel (conv, gates, recurrence and gated norm in one
+      launch) against the separate HIP passes, one token per sequence.
 
     Both are set against the torch ops of the reference module that they replace
     (gdn2.py:395-452). Each is timed as a HIP-graph replay of `reps` calls. The HBM
@@ -367,10 +369,38 @@ def bench_prologue(torch, dev, reps=20):
             torch.cuda.synchronize(dev)
         return e0.elapsed_time(e1) * 1e3 / reps
 
+    # Decode step at the same module shape (one token for each of the B sequences): the
+    # fused kernel (conv + gates + recurrence + gated norm, caches and state updated in
+    # place) against the three separate HIP passes it replaces.
+    yd = torch.randn(B, 7 * D, generator=gen, device=dev).to(bf)
+    qr, kr, vr, bl, wl, gr, zd = yd.split(D, dim=-1)
+    caches = [torch.randn(B, D, W - 1, generator=gen, device=dev).to(bf) for _ in range(3)]
+    state = torch.randn(B, H, Dh, Dh, generator=gen, device=dev) * 0.05
+    A_log = torch.log(torch.rand(H, generator=gen, device=dev) * 15 + 1)
+    dt_bias = torch.randn(H * Dh, generator=gen, device=dev) * 0.5
+    sp = lambda t: t.view(B, 1, H, Dh)  # noqa: E731
+
+    def dec_fused():
+        ops.decode_step_fused([qr, kr, vr], ws, None, caches, gr, bl, wl, state, zd, nw, 1e-5, num_heads=H,
+                              head_dim=Dh, A_log=A_log, dt_bias=dt_bias, update_cache_in_place=True)
+
+    def dec_separate():
+        (q, k, v), _ = ops.short_convolution([qr.unsqueeze(1), kr.unsqueeze(1), vr.unsqueeze(1)], ws, None,
+                                             caches, True, out_caches=caches)
+        od, _ = ops.fused_recurrent_gdn2_fwd(sp(q), sp(k), sp(v), sp(gr), sp(bl), sp(wl), A_log=A_log,
+                                             dt_bias=dt_bias, initial_state=state, inplace_final_state=True,
+                                             use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+                                             bw_logits=True)
+        ops.gated_rmsnorm(od, sp(zd), nw, 1e-5)
+
     conv_bytes = 6 * B * T * D * 2
     norm_bytes = 3 * B * T * H * Dh * 2
+    # fused decode: state read + write, raw q/k/v/g/b/w/z rows, conv caches read + write,
+    # conv weights, normalised output
+    dec_bytes = 2 * B * H * Dh * Dh * 4 + 7 * B * D * 2 + 2 * 3 * B * D * (W - 1) * 2 + 3 * D * W * 2 + B * D * 2
     t = {k: timed(f) for k, f in (("conv", conv_hip), ("conv_torch", conv_torch),
-                                  ("norm", norm_hip), ("norm_torch", norm_torch))}
+                                  ("norm", norm_hip), ("norm_torch", norm_torch),
+                                  ("dec_fused", dec_fused), ("dec_separate", dec_separate))}
     return {
         "config": {"workload": "C3 module shape: B4 T2048, q/k/v 1024 channels, conv width 4; "
                                "norm over 16 heads x 64", "dtype": "bf16"},
@@ -382,6 +412,10 @@ def bench_prologue(torch, dev, reps=20):
                           "algorithmic_bytes": norm_bytes,
                           "achieved_GBps": round(norm_bytes / (t["norm"] * 1e-6) / 1e9, 1),
                           "frac_hbm_peak": round(norm_bytes / (t["norm"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+        "decode_step": {"workload": f"B{B} one token, {H} heads x {Dh}, conv caches and state in place",
+                        "fused_us": round(t["dec_fused"], 2), "separate_hip_us": round(t["dec_separate"], 2),
+                        "algorithmic_bytes": dec_bytes,
+                        "achieved_GBps": round(dec_bytes / (t["dec_fused"] * 1e-6) / 1e9, 1)},
     }
 
 
