@@ -480,15 +480,21 @@ def bench_e2e(torch, dev, n_prompt=2048, n_new=256, batch=4):
 
 
 def traffic_probe(torch, nat, dev):
-    """Short run for the rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE): first a
-    256 MiB device-to-device copy whose bytes are known, which calibrates the
-    counters, then two prefill ops, eight eager decode steps and two training
-    forward + backward steps."""
+    """Short run for the rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE): first three
+    kernels whose bytes are known, which calibrate the counters -- a 256 MiB
+    device-to-device copy (256 MiB read + written), a 1 GiB fill (written only) and a
+    sum over the same 1 GiB (read only) -- then two prefill ops, eight eager decode
+    steps and two training forward + backward steps."""
     a = torch.empty(64 << 20, dtype=torch.float32, device=dev).uniform_()
     c = torch.empty_like(a)
     c.copy_(a)
     torch.cuda.synchronize(dev)
     del a, c
+    big = torch.empty(256 << 20, dtype=torch.float32, device=dev)
+    big.fill_(1.0)
+    total = big.sum()
+    torch.cuda.synchronize(dev)
+    del big, total
     bench_prefill(torch, nat, dev, steps=2, warmup=0)
     bench_decode(torch, nat, dev, eager_steps=8)
     bench_train(torch, nat, dev, steps=2, warmup=0)
