@@ -304,6 +304,39 @@ def bench_decode(torch, nat, dev, reps=3, eager_steps=0, variant="plain"):
                         "state": variant})
 
 
+def copy_ceiling(torch, dev, reps=3, copies=256):
+    """Device-to-device copy of a tensor the size of the C2 state (67.1 MB read + 67.1 MB
+    written), `copies` back to back in one HIP graph: the practical read+write bandwidth
+    the decode step is compared with."""
+    N, H, K, V = (DECODE[x] for x in ("N", "H", "K", "V"))
+    src = torch.randn(N, H, K, V, device=dev)
+    dst = torch.empty_like(src)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            dst.copy_(src)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(copies):
+            dst.copy_(src)
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        times.append(e0.elapsed_time(e1))
+    us = statistics.median(times) * 1e3 / copies
+    nbytes = 2 * src.numel() * 4
+    return {"bytes": nbytes, "us_per_copy": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+
+
 def bench_prologue(torch, dev, reps=20):
     """The mixer's prologue and epilogue kernels at config 3's module shape.
 
@@ -700,6 +733,9 @@ def main() -> int:
             r = bench_decode(torch, nat, dev, variant=variant)
             out["decode"][variant] = {x: r[x] for x in ("us_per_step", "achieved_GBps",
                                                         "frac_hbm_peak")}
+        cc = copy_ceiling(torch, dev)
+        out["decode"]["copy_ceiling"] = cc
+        out["decode"]["frac_copy_ceiling"] = round(out["decode"]["achieved_GBps"] / cc["GBps"], 4)
     if not args.no_train:
         out["train"] = bench_train(torch, nat, dev, max(2, args.steps // 2), 1)
     if not args.no_prologue:
