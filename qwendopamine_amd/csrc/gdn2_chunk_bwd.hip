@@ -130,8 +130,11 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
     constexpr int U16 = static_cast<int>(BL::BYTES / 16);
     constexpr int PF = (U16 + 255) / 256;
     __shared__ __align__(16) st sB[NBUF][BL::SIZE];
-    // dO of the chunk as K16 B operands: block (token tile kt, column tile c).
-    __shared__ __align__(16) st sD[NBUF][16 * 256];
+    // dO of the chunk, row-major [token][column of the slice] with a 16-byte
+    // skew per row; the compute waves turn each 16-token tile into their K16
+    // B operand with one identity product.
+    constexpr int LDD = BV + 16 / static_cast<int>(sizeof(st));
+    __shared__ __align__(16) st sD[NBUF][64 * LDD];
 
     // XCD-aware order, as in the forward scan.
     const int Lid = blockIdx.x;
@@ -165,8 +168,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
         lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
     };
 
-    // Copy waves: dO rows of chunk jc for this value slice in the K16
-    // B-operand order (zero past the sequence end and past V).
+    // Copy waves: dO rows of chunk jc for this value slice, row-major in LDS
+    // (zero past the sequence end and past V), one 16-byte LDS store per row
+    // piece.
     const int v0 = vs * BV;
     constexpr int EPV = 16 / static_cast<int>(sizeof(TI));
     constexpr int ZT = kChunk * BV / EPV;
@@ -202,13 +206,14 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
         int lc;
         chunk_rows(jc, t0, lc);
         st *dst = sD[buf];
+        static_assert(EPV * sizeof(st) == 16, "one dO row piece is one 16-byte LDS store");
 #pragma unroll
         for (int a = 0; a < NZT; ++a) {
             const int task = ctid + 256 * a;
             if (task >= ZT) continue;
             const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
             const TI *rd = reinterpret_cast<const TI *>(&r.d[a]);
-            const int kt = tok >> 4, kgz = (tok & 15) >> 2, iz = tok & 3;
+            st zr[EPV];
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
                 float x = 0.f;
@@ -217,9 +222,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
                 } else {
                     if (tok < lc && v0 + c + e < V) x = io<TI>::ld(dop, ((t0 + tok) * H + h) * V + v0 + c + e);
                 }
-                const int cl = c + e, ct = cl >> 4, nz = cl & 15;
-                dst[(kt * 4 + ct) * 256 + (nz + 16 * kgz) * 4 + iz] = P::from_f32(x);
+                zr[e] = P::from_f32(x);
             }
+            *reinterpret_cast<u32x4 *>(dst + tok * LDD + c) = __builtin_bit_cast(u32x4, zr);
         }
     };
 
@@ -344,9 +349,13 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
                                   pack4<PK>(mma1<PK>(zero4(), pack4<PK>(dS[kt]), ident)));
                 }
 
+                // dO read row-major (lane (m, kg): token 16kt+m, columns 4kg..4kg+3
+                // of this wave's 16) and transposed by the identity product.
                 Q df[4];
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt) df[kt] = ld_q4<PK>(sD[buf] + (kt * 4 + wv) * 256 + 4 * l);
+                for (int kt = 0; kt < 4; ++kt)
+                    df[kt] = pack4<PK>(mma1<PK>(zero4(), ld_q4<PK>(sD[buf] + (16 * kt + m) * LDD + 16 * wv + 4 * kg),
+                                                ident));
                 Q sf[NKT];
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt) sf[kt] = pack4<PK>(dS[kt]);
