@@ -55,13 +55,31 @@ struct BwdParams {
     void *dhs, *dys;                    // backward scratch
 };
 
+// LDS layout of the backward scan's transposed blob.  Block b of 256 elements
+// (blob offset 256 b) starts at PB * b; with 16-bit storage each 16-lane group
+// of a block is followed by 4 elements of padding (PB = 272), so that the 64
+// lanes of one landing store (below) reach 64 distinct banks instead of 8.
+// Lane l's 4 values of a block are at lane(l).
+template <PrecKind PK>
+struct TLay {
+    static constexpr int GP = sizeof(typename Prec<PK>::st) == 2 ? 4 : 0;  // padding per 16-lane group
+    static constexpr int PB = 256 + 4 * GP;
+    static __device__ __forceinline__ constexpr int64_t blk(int64_t off) { return (off >> 8) * PB; }
+    static __device__ __forceinline__ int lane(int l) { return 4 * l + GP * (l >> 4); }
+    template <int KP>
+    static constexpr int64_t size()
+    {
+        return blk(Blob<PK, KP>::GL) + (Blob<PK, KP>::SIZE - Blob<PK, KP>::GL);
+    }
+};
+
 // Unit j*256 + ct (ct < 256 the copy thread) of a forward blob, 16 bytes,
 // landed in LDS with each matrix region transposed: element M[a][b] of a K16
 // fragment-native [Mr][Kc] region goes to element M^T[b][a] of the
-// fragment-native [Kc][Mr] region at the same base; the exp(G_last) vector
-// is copied as is.  Every region boundary is a multiple of 256 units' worth
-// of elements, so the region of unit group j is a compile-time constant once
-// the caller's loop over j is unrolled.
+// fragment-native [Kc][Mr] region at the same base, in the TLay layout; the
+// exp(G_last) vector is copied as is.  Every region boundary is a multiple of
+// 256 units' worth of elements, so the region of unit group j is a
+// compile-time constant once the caller's loop over j is unrolled.
 template <PrecKind PK, int KP>
 __device__ __forceinline__ void land_transposed(typename Prec<PK>::st *dst, u32x4 val, int j, int ct)
 {
@@ -86,14 +104,15 @@ __device__ __forceinline__ void land_transposed(typename Prec<PK>::st *dst, u32x
     } else if (e0 < BL::GL) {
         base = BL::KT; Mr = KP; Kc = 64;
     } else {
-        *reinterpret_cast<u32x4 *>(dst + e) = val;
+        *reinterpret_cast<u32x4 *>(dst + TLay<PK>::blk(BL::GL) + (e - BL::GL)) = val;
         return;
     }
     const int loc = e - base, blk = loc >> 8, wi = loc & 255;
     const int nkc = Kc >> 4, nm = Mr >> 4;
     const int mt = blk / nkc, kt = blk - mt * nkc;
     const int L0 = wi >> 2, a0 = L0 & 15, b0 = (L0 >> 4) * 4;
-    st *d = dst + base + ((kt * nm + mt) << 8) + 4 * b0 + 64 * (a0 >> 2) + (a0 & 3);
+    // Transposed lane b0 + c + 16 (a0 >> 2), slot a0 & 3.
+    st *d = dst + TLay<PK>::blk(base + ((kt * nm + mt) << 8)) + 4 * b0 + (64 + TLay<PK>::GP) * (a0 >> 2) + (a0 & 3);
     if constexpr (EPU == 8) {
         // Lanes L0 (row a0) and L0 + 1 (row a0 + 1): the pair (M[a0][b], M[a0+1][b])
         // is contiguous in the transposed block.
@@ -129,7 +148,8 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
     constexpr int NKT = KP / 16, NKS = KP / 32, NCT = BV / 16;
     constexpr int U16 = static_cast<int>(BL::BYTES / 16);
     constexpr int PF = (U16 + 255) / 256;
-    __shared__ __align__(16) st sB[NBUF][BL::SIZE];
+    using TL = TLay<PK>;
+    __shared__ __align__(16) st sB[NBUF][TL::template size<KP>()];
     // dO of the chunk, row-major [token][column of the slice] with a 16-byte
     // skew per row; the compute waves turn each 16-token tile into their K16
     // B operand with one identity product.
@@ -329,6 +349,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
             copy_loop(std::false_type{});
     } else {
         const Q ident = identity_q4<PK>(l);
+        const int ll = TL::lane(l);  // this lane's 4 values in a transposed block
         __syncthreads();
         for (int s = 0; s < nch; ++s) {
             const int buf = DB ? (s & 1) : 0;
@@ -368,13 +389,13 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
 #pragma unroll
                     for (int s2 = 0; s2 < 2; ++s2)
                         if (2 * s2 + 1 >= rt)
-                            acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::AQ + k16_block(rt, 2 * s2, 64) + 4 * l),
-                                           ld_q4<PK>(Bk + BL::AQ + k16_block(rt, 2 * s2 + 1, 64) + 4 * l),
+                            acc = mma2<PK>(acc, ld_q4<PK>(Bk + TL::blk(BL::AQ + k16_block(rt, 2 * s2, 64)) + ll),
+                                           ld_q4<PK>(Bk + TL::blk(BL::AQ + k16_block(rt, 2 * s2 + 1, 64)) + ll),
                                            df[2 * s2], df[2 * s2 + 1]);
 #pragma unroll
                     for (int s2 = 0; s2 < NKS; ++s2)
-                        acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::KT + k16_block(rt, 2 * s2, KP) + 4 * l),
-                                       ld_q4<PK>(Bk + BL::KT + k16_block(rt, 2 * s2 + 1, KP) + 4 * l),
+                        acc = mma2<PK>(acc, ld_q4<PK>(Bk + TL::blk(BL::KT + k16_block(rt, 2 * s2, KP)) + ll),
+                                       ld_q4<PK>(Bk + TL::blk(BL::KT + k16_block(rt, 2 * s2 + 1, KP)) + ll),
                                        sf[2 * s2], sf[2 * s2 + 1]);
                     duf[rt] = pack4<PK>(acc);
                 }
@@ -386,15 +407,15 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
 #pragma unroll
                     for (int s2 = 0; s2 < 2; ++s2)
                         if (2 * s2 + 1 >= rt)
-                            acc = mma2<PK>(acc, ld_q4<PK>(Bk + BL::X + k16_block(rt, 2 * s2, 64) + 4 * l),
-                                           ld_q4<PK>(Bk + BL::X + k16_block(rt, 2 * s2 + 1, 64) + 4 * l),
+                            acc = mma2<PK>(acc, ld_q4<PK>(Bk + TL::blk(BL::X + k16_block(rt, 2 * s2, 64)) + ll),
+                                           ld_q4<PK>(Bk + TL::blk(BL::X + k16_block(rt, 2 * s2 + 1, 64)) + ll),
                                            duf[2 * s2], duf[2 * s2 + 1]);
                     if (emit)
                         st_q4<PK>(dyb + k16_block(rt, vt, VP) + 4 * l,
                                   pack4<PK>(mma1<PK>(zero4(), pack4<PK>(acc), ident)));
                 }
                 // dS0 = Diag(exp(G_last)) dS1 + Qbar^T dO + (-W)^T dU.
-                const float *gl = reinterpret_cast<const float *>(Bk + BL::GL);
+                const float *gl = reinterpret_cast<const float *>(Bk + TL::blk(BL::GL));
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt) {
                     const float4 gv = *reinterpret_cast<const float4 *>(gl + 16 * kt + 4 * kg);
@@ -404,11 +425,11 @@ __global__ __launch_bounds__(512) void chunk_bwd_scan_kernel(BwdParams p, int NV
                     dS[kt][3] *= gv.w;
 #pragma unroll
                     for (int s2 = 0; s2 < 2; ++s2) {
-                        dS[kt] = mma2<PK>(dS[kt], ld_q4<PK>(Bk + BL::QB + k16_block(kt, 2 * s2, 64) + 4 * l),
-                                          ld_q4<PK>(Bk + BL::QB + k16_block(kt, 2 * s2 + 1, 64) + 4 * l),
+                        dS[kt] = mma2<PK>(dS[kt], ld_q4<PK>(Bk + TL::blk(BL::QB + k16_block(kt, 2 * s2, 64)) + ll),
+                                          ld_q4<PK>(Bk + TL::blk(BL::QB + k16_block(kt, 2 * s2 + 1, 64)) + ll),
                                           df[2 * s2], df[2 * s2 + 1]);
-                        dS[kt] = mma2<PK>(dS[kt], ld_q4<PK>(Bk + BL::WN + k16_block(kt, 2 * s2, 64) + 4 * l),
-                                          ld_q4<PK>(Bk + BL::WN + k16_block(kt, 2 * s2 + 1, 64) + 4 * l),
+                        dS[kt] = mma2<PK>(dS[kt], ld_q4<PK>(Bk + TL::blk(BL::WN + k16_block(kt, 2 * s2, 64)) + ll),
+                                          ld_q4<PK>(Bk + TL::blk(BL::WN + k16_block(kt, 2 * s2 + 1, 64)) + ll),
                                           duf[2 * s2], duf[2 * s2 + 1]);
                     }
                 }
