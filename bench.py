@@ -344,6 +344,8 @@ def bench_prologue(torch, dev, reps=20):
     * Epilogue: the gated RMS norm.
     * Decode step: the fused kernel (conv, gates, recurrence and gated norm in one
       launch) against the separate HIP passes, one token per sequence.
+    * Prefill: the chunk op with the gated norm in its scan's output stage against the
+      chunk op followed by the norm pass.
 
     Both are set against the torch ops of the reference module that they replace
     (gdn2.py:395-452). Each is timed as a HIP-graph replay of `reps` calls. The HBM
@@ -426,6 +428,19 @@ def bench_prologue(torch, dev, reps=20):
                                              bw_logits=True)
         ops.gated_rmsnorm(od, sp(zd), nw, 1e-5)
 
+    # Prefill at the same shape: the chunk op (in-kernel gate, b / w logits) followed by the
+    # gated norm, against the chunk op with the norm in its scan's output stage.
+    pq, pk, pv, pf, pb, pw = (torch.randn(B, T, H, Dh, generator=gen, device=dev).to(bf) for _ in range(6))
+    pkw = dict(use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, A_log=A_log, dt_bias=dt_bias,
+               bw_logits=True)
+
+    def pre_separate():
+        op_, _ = ops.chunk_gdn2(pq, pk, pv, pf, pb, pw, output_final_state=True, **pkw)
+        ops.gated_rmsnorm(op_, z, nw, 1e-5)
+
+    def pre_fused():
+        ops.chunk_gdn2_gated_norm(pq, pk, pv, pf, pb, pw, z, nw, 1e-5, output_final_state=True, **pkw)
+
     conv_bytes = 6 * B * T * D * 2
     norm_bytes = 3 * B * T * H * Dh * 2
     # fused decode: state read + write, raw q/k/v/g/b/w/z rows, conv caches read + write,
@@ -433,7 +448,8 @@ def bench_prologue(torch, dev, reps=20):
     dec_bytes = 2 * B * H * Dh * Dh * 4 + 7 * B * D * 2 + 2 * 3 * B * D * (W - 1) * 2 + 3 * D * W * 2 + B * D * 2
     t = {k: timed(f) for k, f in (("conv", conv_hip), ("conv_torch", conv_torch),
                                   ("norm", norm_hip), ("norm_torch", norm_torch),
-                                  ("dec_fused", dec_fused), ("dec_separate", dec_separate))}
+                                  ("dec_fused", dec_fused), ("dec_separate", dec_separate),
+                                  ("pre_fused", pre_fused), ("pre_separate", pre_separate))}
     return {
         "config": {"workload": "C3 module shape: B4 T2048, q/k/v 1024 channels, conv width 4; "
                                "norm over 16 heads x 64", "dtype": "bf16"},
@@ -449,6 +465,8 @@ def bench_prologue(torch, dev, reps=20):
                         "fused_us": round(t["dec_fused"], 2), "separate_hip_us": round(t["dec_separate"], 2),
                         "algorithmic_bytes": dec_bytes,
                         "achieved_GBps": round(dec_bytes / (t["dec_fused"] * 1e-6) / 1e9, 1)},
+        "prefill_norm": {"workload": f"B{B} T{T}, {H} heads x {Dh}: chunk op + gated norm",
+                         "fused_us": round(t["pre_fused"], 2), "separate_hip_us": round(t["pre_separate"], 2)},
     }
 
 

@@ -239,6 +239,30 @@ int gdn2_chunk_fwd(const void *q, const void *k, const void *v, const void *g, c
                    size_t workspace_bytes, void *stream);
 
 /*
+ * gdn2_chunk_fwd with the module's gated output norm applied in the scan's
+ * output stage: o = RMSNormGated(chunk output, gate) in io_dtype, the output
+ * never leaving the chip unnormalised.  Replaces chunk_gdn2 followed by
+ * RMSNormGated.forward (reference gdn2_ops/chunk_gdn2.py:1268-1434 and
+ * src/qwendopamine/models/gdn2/gdn2.py:433-452, as GatedDeltaNet2.forward calls
+ * them at gdn2.py:875-927), with the norm's roundings of gdn2_gated_rmsnorm_fwd:
+ * the result equals gdn2_chunk_fwd followed by gdn2_gated_rmsnorm_fwd bit for bit.
+ *   gate         [total tokens, ld_gate] rows in io_dtype; head h reads columns
+ *                h*V .. h*V+V-1 (a column range of a wider tensor is allowed)
+ *   norm_weight  [V] in io_dtype
+ * Inference only (GDN2_FLAG_SAVE_FOR_BWD is rejected); bf16 io and V in
+ * {16, 32, 64} (one workgroup owns a whole value row), otherwise
+ * GDN2_ERR_UNSUPPORTED.  ld_gate a multiple of 4, gate and o 8-byte aligned.
+ */
+int gdn2_chunk_fwd_gated_norm(const void *q, const void *k, const void *v, const void *g,
+                              const void *b, const void *w, int io_dtype, int g_dtype, void *o,
+                              const void *gate, int64_t ld_gate, const void *norm_weight, float eps,
+                              const float *initial_state, float *final_state, const float *A_log,
+                              const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
+                              const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H,
+                              int K, int V, float scale, unsigned flags, void *workspace,
+                              size_t workspace_bytes, void *stream);
+
+/*
  * The two stages of gdn2_chunk_fwd, for callers that schedule or time them
  * separately.  Calling prep then scan on the same workspace equals
  * gdn2_chunk_fwd.

@@ -333,6 +333,39 @@ int gdn2_chunk_fwd(const void *q, const void *k, const void *v, const void *g, c
     return launch_chunk_fwd(a, io_dtype, g_dtype, static_cast<hipStream_t>(stream));
 }
 
+int gdn2_chunk_fwd_gated_norm(const void *q, const void *k, const void *v, const void *g,
+                              const void *b, const void *w, int io_dtype, int g_dtype, void *o,
+                              const void *gate, int64_t ld_gate, const void *norm_weight, float eps,
+                              const float *initial_state, float *final_state, const float *A_log,
+                              const float *dt_bias, float lower_bound, const int64_t *cu_seqlens,
+                              const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H,
+                              int K, int V, float scale, unsigned flags, void *workspace,
+                              size_t workspace_bytes, void *stream)
+{
+    ChunkFwdArgs a;
+    const int st = check_chunk_args(io_dtype, g_dtype, cu_seqlens, cu_seqlens_host, num_seqs, B,
+                                    T, H, K, V, flags, A_log);
+    if (st != GDN2_OK) return st;
+    if (flags & GDN2_FLAG_SAVE_FOR_BWD) return GDN2_ERR_INVALID;  // an inference epilogue
+    if (io_dtype != GDN2_DTYPE_BF16 || (V != 16 && V != 32 && V != 64)) return GDN2_ERR_UNSUPPORTED;
+    if (static_cast<int64_t>(B) * T > 0 &&
+        (!q || !k || !v || !g || !b || !w || !o || !gate || !norm_weight))
+        return GDN2_ERR_INVALID;
+    // 8-byte gate and output accesses: 4-value groups of every row.
+    if (ld_gate < static_cast<int64_t>(H) * V || (ld_gate % 4) != 0 ||
+        (reinterpret_cast<uintptr_t>(gate) % 8) != 0 || (reinterpret_cast<uintptr_t>(o) % 8) != 0)
+        return GDN2_ERR_INVALID;
+    fill_chunk_args(a, q, k, v, g, b, w, o, initial_state, final_state, A_log, dt_bias,
+                    lower_bound, cu_seqlens, cu_seqlens_host, num_seqs, B, T, H, K, V, scale,
+                    flags, workspace, workspace_bytes);
+    a.stages = 3;
+    a.z = gate;
+    a.ldz = ld_gate;
+    a.nw = norm_weight;
+    a.eps = eps;
+    return launch_chunk_fwd(a, io_dtype, g_dtype, static_cast<hipStream_t>(stream));
+}
+
 int gdn2_chunk_fwd_prep(const void *q, const void *k, const void *g, const void *b,
                         int io_dtype, int g_dtype, const float *A_log, const float *dt_bias,
                         float lower_bound, const int64_t *cu_seqlens,

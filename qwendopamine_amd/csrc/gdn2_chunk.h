@@ -43,6 +43,13 @@ struct ChunkParams {
     // VP = V rounded up to 16.
     void *hs, *us;
     int VP;
+    // Gated output norm in the scan (inference, BV == V): gate rows z (token
+    // row stride ldz, head h at column h * V), weight nw [V], eps.  z == null
+    // leaves the outputs unnormalised.
+    const void *z;
+    int64_t ldz;
+    const void *nw;
+    float eps;
 };
 
 // Per (chunk, head) blob, in storage elements.

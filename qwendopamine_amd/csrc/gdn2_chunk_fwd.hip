@@ -380,15 +380,39 @@ chunk_prep_kernel(ChunkParams p, int items)
         if (p.flags & GDN2_FLAG_GATE_IN_KERNEL) {
             const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
             const float a_log = p.A_log[h];
+            // dt_bias of this lane's channels, all requested before any is used
+            // (a load inside a per-element branch would wait for each one in
+            // turn): 4-channel groups when K % 4 == 0, else clamped elements.
+            float dbv[NKT][4];
+            if (p.dt_bias) {
+                const float *db = p.dt_bias + static_cast<int64_t>(h) * K;
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) {
+                    const int c0 = 16 * kt + 4 * kg;
+                    if (p.vec_ok) {
+                        const float4 d4 = *reinterpret_cast<const float4 *>(db + (c0 < K ? c0 : K - 4));
+                        dbv[kt][0] = d4.x;
+                        dbv[kt][1] = d4.y;
+                        dbv[kt][2] = d4.z;
+                        dbv[kt][3] = d4.w;
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) dbv[kt][i] = db[c0 + i < K ? c0 + i : K - 1];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dbv[kt][i] = 0.0f;
+            }
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int c = 16 * kt + 4 * kg + i;
-                    if (row_ok && c < K) {
-                        const float db = p.dt_bias ? p.dt_bias[h * K + c] : 0.0f;
-                        gv[kt][i] = gate_activation(gv[kt][i], a_log, db, use_lb, p.lower_bound);
-                    }
+                    const float act = gate_activation(gv[kt][i], a_log, dbv[kt][i], use_lb, p.lower_bound);
+                    gv[kt][i] = (row_ok && c < K) ? act : gv[kt][i];
                 }
         }
 #pragma unroll
@@ -658,7 +682,7 @@ chunk_prep_kernel(ChunkParams p, int items)
 // ---------------------------------------------------------------------------
 // Scan: one workgroup per (sequence, head, value slice of BV columns).
 // ---------------------------------------------------------------------------
-template <PrecKind PK, int KP, int BV, typename TI, bool TRAIN, bool SIGW = false>
+template <PrecKind PK, int KP, int BV, typename TI, bool TRAIN, bool SIGW = false, bool NORM = false>
 __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB, int NP)
 {
     using P = Prec<PK>;
@@ -676,6 +700,9 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     // their K16 B operand with one identity product.
     constexpr int LDZ = BV + 16 / static_cast<int>(sizeof(st));
     __shared__ __align__(16) st sZ[NBUF][64 * LDZ];
+    // NORM: per-token sums of squares of each compute wave's 16 output columns,
+    // by chunk parity.
+    __shared__ float sNP[NORM ? 2 : 1][NORM ? 4 : 1][NORM ? 64 : 1];
 
     // XCD-aware order: all value slices of a (sequence, head) pair share
     // blockIdx % 8, hence one XCD and one L2.
@@ -703,6 +730,8 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     // output dtype (bf16 with bf16 operands, fp32 with fp32 operands).
     constexpr bool OUT_T = (std::is_same<TI, bf16_t>::value && PK == PrecKind::BF16) ||
                            (std::is_same<TI, float>::value && PK == PrecKind::F32);
+    static_assert(!NORM || (OUT_T && !TRAIN && !std::is_same<TI, float>::value),
+                  "the fused gated norm is a 16-bit inference epilogue");
     // An fp32 accumulator tile (rows 4kg+i, column m) stored transposed, in
     // A-order and the MFMA operand precision (an identity product transposes it).
     auto emit_tile = [&](st *base, int64_t off, f32x4 x) __attribute__((always_inline)) {
@@ -970,6 +999,60 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         else
             copy_loop(std::false_type{});
     } else {
+        // NORM (gated output norm, BV == V): chunk jc's rounded, transposed
+        // outputs and its gate rows stay in registers until the barrier that
+        // ends step jc.  Each compute wave has then written its per-token sums
+        // of squares to sNP[jc & 1], and the chunk is normalised and stored at
+        // the start of step jc + 1 (the last chunk after the loop).  The sums
+        // follow gated_rmsnorm_vec_kernel's order (8 consecutive columns per
+        // partial, then a pairwise tree), so the result equals the separate
+        // norm pass bit for bit.
+        Q otr[4], zq[4];
+        float nwv[4] = {0.f, 0.f, 0.f, 0.f};
+        const int c0n = 16 * wv + 4 * kg;  // this lane's 4 output columns (BV == V)
+        if constexpr (NORM) {
+            if (active) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) nwv[i] = io<TI>::ld(static_cast<const TI *>(p.nw), c0n + i);
+            }
+        }
+        auto issue_gate = [&](int64_t t0n, int lcn) __attribute__((always_inline)) {
+            const TI *zp = static_cast<const TI *>(p.z);
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const int tok = 16 * rt + m;  // rows past the chunk read its first row (unused)
+                const int64_t row = t0n + (tok < lcn ? tok : 0);
+                zq[rt] = ld_q4<PK>(reinterpret_cast<const st *>(zp + row * p.ldz + static_cast<int64_t>(h) * V + c0n));
+            }
+        };
+        auto finish_norm = [&](int jn, int64_t t0n, int lcn) __attribute__((always_inline)) {
+            const float *P = &sNP[jn & 1][0][0];
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const int tok = 16 * rt + m;
+                float tot;
+                if constexpr (NCT >= 4)
+                    tot = (P[tok] + P[64 + tok]) + (P[128 + tok] + P[192 + tok]);
+                else if constexpr (NCT == 2)
+                    tot = P[tok] + P[64 + tok];
+                else
+                    tot = P[tok];
+                const float var = round_to<TI>(tot / static_cast<float>(V));
+                const float inv = round_to<TI>(rsqrtf(round_to<TI>(var + p.eps)));
+                float x[4], zz[4], out[4];
+                unpack4<PK>(otr[rt], x);
+                unpack4<PK>(zq[rt], zz);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float a = round_to<TI>(x[i] * inv);
+                    const float gz = round_to<TI>(silu_f32(zz[i]));
+                    out[i] = round_to<TI>(round_to<TI>(a * nwv[i]) * gz);
+                }
+                if (tok < lcn)
+                    st_q4<PK>(reinterpret_cast<st *>(op + ((t0n + tok) * H + h) * V + c0n),
+                              pack4<PK>(out[0], out[1], out[2], out[3]));
+            }
+        };
         __syncthreads();
         for (int jc = 0; jc < nch; ++jc) {
             const int buf = DB ? (jc & 1) : 0;
@@ -978,6 +1061,13 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
             const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
             const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
+            if constexpr (NORM) {
+                if (jc > 0) {
+                    const int64_t rp = len - static_cast<int64_t>(jc - 1) * kChunk;
+                    finish_norm(jc - 1, t0 - kChunk, rp < kChunk ? static_cast<int>(rp) : kChunk);
+                }
+                issue_gate(t0, lc);
+            }
 
             // Training mode: this chunk's start state, A-order tiles (kt, vt).
             if constexpr (TRAIN) if (emit) {
@@ -1119,6 +1209,23 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
 #pragma unroll
                 for (int rt = 0; rt < 4; ++rt) {
                     const Q tr = pack4<PK>(mma1<PK>(zero4(), pack4<PK>(oa[rt]), ident));
+                    if constexpr (NORM) {
+                        // Rounded squares summed in order over this lane's 4
+                        // columns, continuing the left neighbour's 4 (lanes kg
+                        // and kg ^ 1 hold 8 consecutive columns), then the two
+                        // 8-column partials of the wave's 16 columns added.
+                        otr[rt] = tr;
+                        float x[4], r[4];
+                        unpack4<PK>(tr, x);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) r[i] = round_to<TI>(x[i] * x[i]);
+                        const float left = __shfl(((r[0] + r[1]) + r[2]) + r[3], (l + 48) & 63, 64);
+                        const float s8 = (kg & 1) ? ((((left + r[0]) + r[1]) + r[2]) + r[3])
+                                                  : ((r[0] + r[1]) + r[2]) + r[3];
+                        const float pa = __shfl(s8, m + 16, 64), pb = __shfl(s8, m + 48, 64);
+                        if (kg == 0) sNP[jc & 1][wv][16 * rt + m] = pa + pb;
+                        continue;
+                    }
                     const int tok = 16 * rt + m;
                     if (tok >= lc) continue;
                     TI *dst = op + ((t0 + tok) * H + h) * V + c0;
@@ -1150,6 +1257,13 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             __syncthreads();
             if constexpr (!DB) {
                 if (jc + 1 < nch) __syncthreads();
+            }
+        }
+        if constexpr (NORM) {
+            if (active && nch > 0) {
+                const int64_t rp = len - static_cast<int64_t>(nch - 1) * kChunk;
+                finish_norm(nch - 1, bos + static_cast<int64_t>(nch - 1) * kChunk,
+                            rp < kChunk ? static_cast<int>(rp) : kChunk);
             }
         }
     }
@@ -1201,7 +1315,17 @@ hipError_t launch_scan(const ChunkParams &p, int BVsel, hipStream_t stream)
     auto go = [&](auto bvtag) {
         constexpr int BV = decltype(bvtag)::value;
         const int NVB = (p.V + BV - 1) / BV;
-        if (p.hs)
+        if (p.z) {
+            // Gated output norm (bf16 inference; the caller checked BV == V).
+            if constexpr (std::is_same<TI, bf16_t>::value && PK == PrecKind::BF16) {
+                if (p.flags & GDN2_FLAG_SIGMOID_BW)
+                    hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI, false, true, true>),
+                                       dim3(groups * 8 * NVB), dim3(512), 0, stream, p, NVB, NP);
+                else
+                    hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI, false, false, true>),
+                                       dim3(groups * 8 * NVB), dim3(512), 0, stream, p, NVB, NP);
+            }
+        } else if (p.hs)
             hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI, true>), dim3(groups * 8 * NVB),
                                dim3(512), 0, stream, p, NVB, NP);
         else if (p.flags & GDN2_FLAG_SIGMOID_BW)  // never with the training workspace
@@ -1225,7 +1349,8 @@ hipError_t launch_all(const ChunkParams &p, int total_chunks, int stages, hipStr
         if (e != hipSuccess) return e;
     }
     if (!(stages & 2) || p.num_seqs == 0) return hipSuccess;
-    return launch_scan<PK, KP, TI>(p, scan_bv(p.num_seqs * p.H, p.V), stream);
+    // The fused norm needs whole value rows in one workgroup: BV = V.
+    return launch_scan<PK, KP, TI>(p, p.z ? bv_for(p.V) : scan_bv(p.num_seqs * p.H, p.V), stream);
 }
 
 template <PrecKind PK, typename TI, typename TG>
@@ -1255,6 +1380,9 @@ size_t chunk_fwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
 int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream)
 {
     if (!chunk_k_supported(a.K, io_dtype)) return GDN2_ERR_UNSUPPORTED;
+    if (a.z && (io_dtype != GDN2_DTYPE_BF16 || a.V != bv_for(a.V) || (a.V % 16) != 0 ||
+                (a.flags & GDN2_FLAG_SAVE_FOR_BWD)))
+        return GDN2_ERR_UNSUPPORTED;
     if (g_dtype != GDN2_DTYPE_F32 && g_dtype != io_dtype) return GDN2_ERR_UNSUPPORTED;
     const int64_t nc = count_chunks(a.B, a.T, a.cu_host, a.num_seqs);
     if (nc * a.H > 2147483647LL / 2) return GDN2_ERR_UNSUPPORTED;
@@ -1282,6 +1410,10 @@ int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream
     p.ws = a.workspace;
     p.VP = static_cast<int>(round_up(a.V, 16));
     p.hs = p.us = nullptr;
+    p.z = a.z;
+    p.ldz = a.ldz;
+    p.nw = a.nw;
+    p.eps = a.eps;
     if (train) {
         unsigned char *base = static_cast<unsigned char *>(a.workspace);
         p.hs = base + tl.hs;

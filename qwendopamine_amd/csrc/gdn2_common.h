@@ -80,14 +80,24 @@ __device__ __forceinline__ float wave_sum(float x)
     return x;
 }
 
-// torch.nn.functional.softplus with its default threshold of 20.
+// torch.nn.functional.softplus with its default threshold of 20, from the
+// hardware exp2 / log2 instead of the library expf / log1pf (which cost about
+// as much as the rest of the prologue):  max(x, 0) + log1p(e^-|x|), with
+// log1p(u) = u ln(w) / (w - 1) for w = 1 + u (Kahan's correction of the
+// rounding of w; u itself when w rounds to 1): a few ulp in fp32.
 __device__ __forceinline__ float softplus_f(float x)
 {
-    return x > 20.0f ? x : log1pf(expf(x));
+    constexpr float kLog2eF = 1.4426950408889634f, kLn2F = 0.6931471805599453f;
+    const float u = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2eF);  // e^-|x| in (0, 1]
+    const float w = 1.0f + u;
+    const float l1p = w == 1.0f ? u : u * (__builtin_amdgcn_logf(w) * kLn2F) * __builtin_amdgcn_rcpf(w - 1.0f);
+    const float r = fmaxf(x, 0.0f) + l1p;
+    return x > 20.0f ? x : r;
 }
 
-// torch.sigmoid in fp32 (GDN2_FLAG_SIGMOID_BW): 1 / (1 + e^-x), 0 for x -> -inf.
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+// torch.sigmoid in fp32 (GDN2_FLAG_SIGMOID_BW): 1 / (1 + e^-x) with the
+// hardware reciprocal (1 ulp), 0 for x -> -inf.
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // x * sigmoid(x) with the hardware reciprocal (1 ulp in fp32) instead of an
 // IEEE divide, for the module's SiLUs whose results are rounded to the input
@@ -115,7 +125,7 @@ __device__ __forceinline__ float gate_activation(float graw, float a_log, float 
 {
     const float x = graw + dt_bias;
     const float a = expf(a_log);
-    if (use_lower_bound) return lower_bound / (1.0f + expf(-a * x));
+    if (use_lower_bound) return lower_bound * sigmoid_f(a * x);
     return -a * softplus_f(x);
 }
 

@@ -83,6 +83,11 @@ struct ChunkFwdArgs {
     void *workspace;
     size_t workspace_bytes;
     int stages;  // bit 0: prep, bit 1: scan
+    // Gated output norm fused into the scan (null z: none).
+    const void *z = nullptr;
+    int64_t ldz = 0;
+    const void *nw = nullptr;
+    float eps = 0.f;
 };
 
 size_t chunk_fwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype,

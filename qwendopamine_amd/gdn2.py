@@ -256,6 +256,13 @@ class GatedDeltaNet2(nn.Module):
         # recurrence and output norm in one launch) when its conditions hold;
         # False runs the same steps as separate passes.
         self.fused_decode = True
+        # Chunked inference applies the gated output norm in the scan's output
+        # stage when one scan workgroup owns a whole value row anyway (bf16,
+        # head_v_dim in {16, 32, 64}, at least 256 sequence-heads or 16-wide
+        # heads); False always runs the norm as its own pass.  With fewer
+        # sequence-heads the scan splits value rows over more workgroups and the
+        # norm pass is faster.
+        self.fused_norm = True
 
         self.head_k_dim = self.head_dim
         self.head_v_dim = int(self.head_dim * self.expand_v)
@@ -590,7 +597,21 @@ class GatedDeltaNet2(nn.Module):
             A_log, dt_bias = self._gate_params(rep)
             gate_kw = dict(use_gate_in_kernel=True, A_log=A_log, dt_bias=dt_bias, bw_logits=True)
         b, w, v, k = b.to(dt), w.to(dt), v.to(dt), k.to(dt)
-        if algo == "chunk":
+        normed = None
+        n_seq = batch if cu_seqlens is None else cu_seqlens.numel() - 1
+        if (algo == "chunk" and fuse and self.fused_norm and dt == torch.bfloat16
+                and self.head_v_dim in (16, 32, 64) and self.o_norm.weight.dtype == dt
+                and (n_seq * self.num_v_heads >= 256 or self.head_v_dim == 16)
+                and _inference(self.o_norm.weight, *(p for p in self.g_proj.parameters()))):
+            # The gated output norm in the scan's output stage (bit-identical to
+            # the separate pass).
+            gate = self.g_proj(x) if g0 is None else self.g_proj[1](g0).view(*x.shape[:-1], -1)
+            normed, recurrent_state = ops.chunk_gdn2_gated_norm(
+                q, k, v, g, b, w, gate, self.o_norm.weight, self.o_norm.eps, initial_state=h0,
+                output_final_state=want_state, use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens,
+                **gate_kw,
+            )
+        elif algo == "chunk":
             o, recurrent_state = ops.chunk_gdn2(
                 q, k, v, g, b, w, initial_state=h0, output_final_state=want_state,
                 use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens, **gate_kw,
@@ -611,9 +632,12 @@ class GatedDeltaNet2(nn.Module):
             self._update_cache(past_key_values, recurrent_state,
                                (cq, ck, cv) if self.use_short_conv else None)
 
-        gate = _split_heads(self.g_proj(x) if g0 is None else self.g_proj[1](g0).view(*x.shape[:-1], -1),
-                            self.head_v_dim)
-        o = self.o_norm(o, gate)
+        if normed is not None:
+            o = normed
+        else:
+            gate = _split_heads(self.g_proj(x) if g0 is None else self.g_proj[1](g0).view(*x.shape[:-1], -1),
+                                self.head_v_dim)
+            o = self.o_norm(o, gate)
         out = self.o_proj(o.reshape(*o.shape[:-2], -1))
         if padded:
             out = _pad_input(out.squeeze(0), indices, batch, seq_len)

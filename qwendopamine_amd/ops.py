@@ -774,6 +774,93 @@ def short_convolution(
 
 
 @torch.compiler.disable
+def chunk_gdn2_gated_norm(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    b: torch.Tensor,
+    w: torch.Tensor,
+    gate: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float = 1e-5,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    lower_bound: float | None = None,
+    cu_seqlens: torch.LongTensor | None = None,
+    bw_logits: bool = False,
+):
+    """``chunk_gdn2`` followed by the module's gated output norm, in one pass over the output.
+
+    The norm (``RMSNormGated``, reference ``gdn2.py:433-452``) runs in the scan's output stage,
+    with the roundings of :func:`gated_rmsnorm`: the result equals
+    ``gated_rmsnorm(chunk_gdn2(...)[0], gate, norm_weight, eps)`` bit for bit.
+
+    * ``gate``: ``[B, T, H, V]`` or ``[B, T, H * V]`` in the inputs' dtype; the token rows may be
+      a column range of a wider tensor (unit channel stride, one row stride).
+    * ``norm_weight``: ``[V]`` in the inputs' dtype.
+
+    Inference only (no autograd); bfloat16 inputs with ``V`` in {16, 32, 64}, where one scan
+    workgroup owns a whole value row. Returns ``(o, final_state)``.
+    """
+    name = "chunk_gdn2_gated_norm"
+    _require_gpu(name, q, k, v, g, b, w, gate, norm_weight, initial_state)
+    _check_shapes(name, q, k, v, g, b, w, same_heads=True)
+    _check_packed(q, initial_state, cu_seqlens)
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    dt = q.dtype
+    if dt != torch.bfloat16 or V not in (16, 32, 64):
+        raise NotImplementedError(f"{name}: bfloat16 inputs with a value head dim of 16, 32 or 64 "
+                                  f"(got {dt}, {V})")
+    if norm_weight.numel() != V or norm_weight.dtype != dt:
+        raise ValueError(f"{name}: norm_weight must hold {V} {dt} values")
+    gt = gate.reshape(B, T, H * V) if gate.dim() == 4 and gate.stride(-2) == V else gate
+    if (gt.dim() != 3 or gt.dtype != dt or tuple(gt.shape) != (B, T, H * V) or gt.stride(-1) != 1
+            or (B > 1 and gt.stride(0) != T * gt.stride(1))):
+        raise ValueError(f"{name}: gate must be [B, T, H * V] {dt} token rows with unit channel stride; "
+                         f"got {tuple(gate.shape)} {gate.dtype} strides {gate.stride()}")
+    ld_gate = gt.stride(1) if T > 1 else max(gt.stride(1), H * V)
+    if scale is None:
+        scale = K ** -0.5
+    q, k, v, b, w = (_io(x, dt) for x in (q, k, v, b, w))
+    g = _io(g, g.dtype if g.dtype in (torch.float32, dt) else torch.float32)
+    cu_dev, cu_host = _cu(cu_seqlens, q.device, T)
+    N = B if cu_seqlens is None else cu_host.numel() - 1
+    h0 = None if initial_state is None else initial_state.float().contiguous()
+    if h0 is not None and tuple(h0.shape) != (N, H, K, V):
+        raise ValueError(f"{name}: initial_state must be {(N, H, K, V)}, got {tuple(h0.shape)}")
+    ht = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) if output_final_state else None
+    o = torch.empty_like(v)
+    lib = nat.load()
+    cu_host_p = None if cu_host is None else cu_host.data_ptr()
+    ws_bytes = lib.gdn2_chunk_fwd_workspace_size(B, T, H, K, V, nat.dtype_code(dt), cu_host_p, N)
+    if ws_bytes == 0 and B * T > 0 and K > 128:
+        raise NotImplementedError(f"{name}: key head dim {K} beyond the chunk kernels' 256")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    a_log, dtb = _gate_tensors(use_gate_in_kernel, A_log, dt_bias, H, K)
+    flags = _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound)
+    if bw_logits:
+        flags |= nat.FLAG_SIGMOID_BW
+    wn = norm_weight.detach().contiguous()
+    st = lib.gdn2_chunk_fwd_gated_norm(
+        nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(g), nat.ptr(b), nat.ptr(w),
+        nat.dtype_code(dt), nat.dtype_code(g.dtype), nat.ptr(o), nat.ptr(gt), ld_gate, nat.ptr(wn),
+        float(eps), nat.ptr(h0), nat.ptr(ht), nat.ptr(a_log), nat.ptr(dtb),
+        float(lower_bound) if lower_bound is not None else 0.0,
+        nat.ptr(cu_dev), cu_host_p, N, B, T, H, K, V, float(scale), flags,
+        ws.data_ptr(), ws.numel(), nat.stream_handle(q.device),
+    )
+    nat.check(st, name)
+    return o, ht
+
+
+@torch.compiler.disable
 def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
     """``x * rsqrt(mean(x^2) + eps) * weight * silu(z)`` over the last axis.
 

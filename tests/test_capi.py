@@ -78,6 +78,29 @@ def test_invalid_arguments_rejected_before_launch(lib):
     assert st == nat.ERR_INVALID
 
 
+def test_gated_norm_chunk_arguments_rejected_before_launch(lib):
+    """The fused-norm chunk forward: bf16 only, V in {16, 32, 64}, inference only, and the
+    gate / output alignment it reads with 8-byte accesses."""
+    from qwendopamine_amd import _native as nat
+
+    def call(io=1, V=64, flags=0, ld=64, gate=0x1000, o=0x2000, tensors=True):
+        t = 0x3000 if tensors else None
+        return lib.gdn2_chunk_fwd_gated_norm(t, t, t, t, t, t, io, 0, o, gate, ld, t, 1e-5, None, None,
+                                             None, None, 0.0, None, None, 1, 1, 8, 1, 16, V, 1.0,
+                                             flags, None, 0, None)
+
+    assert call(io=0) == nat.ERR_UNSUPPORTED                  # float32
+    assert call(io=2) == nat.ERR_UNSUPPORTED                  # float16
+    assert call(V=128, ld=128) == nat.ERR_UNSUPPORTED         # a row spans several workgroups
+    assert call(V=48, ld=48) == nat.ERR_UNSUPPORTED
+    assert call(flags=nat.FLAG_SAVE_FOR_BWD) == nat.ERR_INVALID  # inference only
+    assert call(ld=62) == nat.ERR_INVALID                     # row stride below H * V
+    assert call(ld=66) == nat.ERR_INVALID                     # not a multiple of 4
+    assert call(gate=0x1002) == nat.ERR_INVALID               # misaligned gate
+    assert call(o=0x2004) == nat.ERR_INVALID                  # misaligned output
+    assert call(tensors=False) == nat.ERR_INVALID             # null tensors with tokens
+
+
 def test_serving_arguments_rejected_before_launch(lib):
     from qwendopamine_amd import _native as nat
 
