@@ -641,6 +641,207 @@ __global__ __launch_bounds__(256) void decode_step_kernel(RecurrentParams p, int
     }
 }
 
+// One step of the half-wave butterfly transpose-reduction over N values per
+// lane: lanes with bit N/2 of their half-wave index keep the upper half and
+// send the lower one to their partner (lane ^ N/2), the others the opposite;
+// after the steps N = 32 .. 2, lane j holds x[j] summed over the 32 lanes.
+// Compile-time N keeps every index constant (register arrays indexed at run
+// time would be lowered to compare / select chains).
+template <int N>
+__device__ __forceinline__ void half_wave_butterfly(float (&x)[32], int hl)
+{
+    constexpr int H2 = N / 2;
+    const bool up = (hl & H2) != 0;
+#pragma unroll
+    for (int t = 0; t < H2; ++t) {
+        const float send = up ? x[t] : x[t + H2];
+        const float keep = up ? x[t + H2] : x[t];
+        x[t] = keep + __shfl_xor(send, H2, kWave);
+    }
+    if constexpr (N > 2) half_wave_butterfly<H2>(x, hl);
+}
+
+// Decode step with [V, K] (transposed) states, K = V = 128: two (sequence,
+// value head) slabs per workgroup of 256 threads, requests ordered as in
+// decode_step_kernel.  Thread (ck, rv) = (tid % 32, tid / 32) holds key
+// columns 4ck..4ck+3 of state rows v = rv + 8i, i < 16, so each half-wave
+// reads and writes whole 512-byte rows.  The contractions over K (S^T e and
+// S^T q for every v) stay inside the half-wave: a butterfly
+// transpose-reduction (exchange half of the remaining values with lane
+// ^ 16, 8, 4, 2, 1) leaves lane j of half-wave rv with the complete sum for
+// value rv + 8 (j / 2): the e-contraction on even j, the q-contraction on odd j.
+template <typename TI, typename TG, bool H0>
+__global__ __launch_bounds__(256) void decode_step_t_kernel(RecurrentParams p, int nslabs)
+{
+    constexpr int KD = 128, VD = 128, NI = 16, SLABS = 2;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1), wid = tid / kWave;
+    const int ck = tid & 31, rv = tid >> 5;
+    const int kc = 4 * ck;
+    const int vsel = rv + 8 * (ck >> 1);  // the value this lane completes
+
+    __shared__ float s_q[KD], s_k[KD], s_e[KD], s_a[KD];
+    __shared__ float s_part[4][4];
+    __shared__ float s_u[VD];
+
+    const TI *q = static_cast<const TI *>(p.q);
+    const TI *k = static_cast<const TI *>(p.k);
+    const TI *v = static_cast<const TI *>(p.v);
+    const TI *b = static_cast<const TI *>(p.b);
+    const TI *w = static_cast<const TI *>(p.w);
+    const TG *g = static_cast<const TG *>(p.g);
+    TI *o = static_cast<TI *>(p.o);
+    const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
+    const bool gate = (p.flags & GDN2_FLAG_GATE_IN_KERNEL) != 0;
+    const int use_lb = (p.flags & GDN2_FLAG_LOWER_BOUND) != 0;
+    const bool sig_bw = (p.flags & GDN2_FLAG_SIGMOID_BW) != 0;
+
+    // Token inputs, store rows and gate parameters of both slabs, then both
+    // slabs' state, all from always-valid addresses (as in decode_step_kernel).
+    const int slab0 = blockIdx.x * SLABS;
+    float qv[SLABS], kv[SLABS], gv[SLABS], bv[SLABS], vv[SLABS], ww[SLABS];
+    const int tk = tid & (KD - 1);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+        const int slab = slab0 + s < nslabs ? slab0 + s : nslabs - 1;
+        const int n = slab / p.HV, hv = slab % p.HV;
+        const int h = hv / (p.HV / p.H);
+        const int64_t qk_off = (static_cast<int64_t>(n) * p.H + h) * KD;
+        qv[s] = io<TI>::ld(q, qk_off + tk);
+        kv[s] = io<TI>::ld(k, qk_off + tk);
+        gv[s] = io<TG>::ld(g, static_cast<int64_t>(slab) * KD + tk);
+        bv[s] = io<TI>::ld(b, static_cast<int64_t>(slab) * KD + tk);
+        vv[s] = io<TI>::ld(v, static_cast<int64_t>(slab) * VD + vsel);
+        ww[s] = io<TI>::ld(w, static_cast<int64_t>(slab) * VD + vsel);
+    }
+    float *dst[SLABS];
+    float dtb[SLABS], alg[SLABS];
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+        const int slab = slab0 + s < nslabs ? slab0 + s : nslabs - 1;
+        const int n = slab / p.HV, hv = slab % p.HV;
+        const int h = hv / (p.HV / p.H);
+        dst[s] = store_row(p, n, hv, 0, n);
+        dtb[s] = alg[s] = 0.f;
+        if constexpr (H0) {
+            const float *dsrc = p.dt_bias ? p.dt_bias : p.h0;
+            const float *asrc = p.A_log ? p.A_log : p.h0;
+            dtb[s] = dsrc[h * KD + tk];
+            alg[s] = asrc[h];
+        } else if (gate) {
+            dtb[s] = p.dt_bias ? p.dt_bias[h * KD + tk] : 0.0f;
+            alg[s] = p.A_log[h];
+        }
+    }
+    float4 st[SLABS][NI];
+    bool zst[SLABS];
+    if constexpr (H0) {
+        const float *src[SLABS];
+#pragma unroll
+        for (int s = 0; s < SLABS; ++s) {
+            const int slab = slab0 + s < nslabs ? slab0 + s : nslabs - 1;
+            const float *row = initial_row(p, slab / p.HV, slab % p.HV);
+            zst[s] = row == nullptr;
+            src[s] = row ? row : p.h0;
+        }
+#pragma unroll
+        for (int s = 0; s < SLABS; ++s)
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+                st[s][i] = *reinterpret_cast<const float4 *>(src[s] + (rv + 8 * i) * KD + kc);
+    } else {
+#pragma unroll
+        for (int s = 0; s < SLABS; ++s) {
+            zst[s] = true;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) st[s][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+        const int slab = slab0 + s;
+        if (slab >= nslabs) break;
+
+        float qv_ = 0.f, kv_ = 0.f, gv_ = 0.f, bv_ = 0.f;
+        if (tid < KD) {
+            qv_ = qv[s];
+            kv_ = kv[s];
+            gv_ = gv[s];
+            bv_ = bv[s];
+        }
+        float vv_ = vv[s], ww_ = ww[s];
+        if (sig_bw) {
+            bv_ = sigmoid_f(bv_);
+            ww_ = sigmoid_f(ww_);
+        }
+        const float rq = wave_sum(qv_ * qv_), rk = wave_sum(kv_ * kv_), rqk = wave_sum(qv_ * kv_);
+        if (lane == 0) {
+            s_part[wid][0] = rq;
+            s_part[wid][1] = rk;
+            s_part[wid][2] = rqk;
+        }
+        __syncthreads();
+        float qq = 0.f, kk = 0.f, qk = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qq += s_part[i][0];
+            kk += s_part[i][1];
+            qk += s_part[i][2];
+        }
+        const float invq = l2 ? 1.0f / fmaxf(sqrtf(qq), 1e-6f) : 1.0f;
+        const float invk = l2 ? 1.0f / fmaxf(sqrtf(kk), 1e-6f) : 1.0f;
+        if (tid < KD) {
+            const float kn = kv_ * invk;
+            s_q[tid] = qv_ * invq * p.scale;
+            s_k[tid] = kn;
+            s_e[tid] = bv_ * kn;
+            float gk = gv_;
+            if (gate) {
+                const float db = p.dt_bias ? dtb[s] : 0.0f;
+                gk = gate_activation(gv_, alg[s], db, use_lb, p.lower_bound);
+            }
+            s_a[tid] = expf(gk);
+        }
+        const float kq = qk * invq * invk * p.scale;
+        __syncthreads();
+
+        const float4 a4 = *reinterpret_cast<const float4 *>(&s_a[kc]);
+        const float4 e4 = *reinterpret_cast<const float4 *>(&s_e[kc]);
+        const float4 q4 = *reinterpret_cast<const float4 *>(&s_q[kc]);
+        const float4 k4 = *reinterpret_cast<const float4 *>(&s_k[kc]);
+        int zs = zst[s] ? 1 : 0;
+        asm volatile("" : "+v"(zs));
+        // x[2i] = this lane's part of (S^T e)[rv + 8i], x[2i + 1] of (S^T q)[rv + 8i].
+        float x[2 * NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if (zs) st[s][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            st[s][i].x *= a4.x;
+            st[s][i].y *= a4.y;
+            st[s][i].z *= a4.z;
+            st[s][i].w *= a4.w;
+            x[2 * i] = fmaf(st[s][i].w, e4.w, fmaf(st[s][i].z, e4.z, fmaf(st[s][i].y, e4.y, st[s][i].x * e4.x)));
+            x[2 * i + 1] =
+                fmaf(st[s][i].w, q4.w, fmaf(st[s][i].z, q4.z, fmaf(st[s][i].y, q4.y, st[s][i].x * q4.x)));
+        }
+        static_assert(2 * NI == 32, "one value per lane of a half-wave");
+        half_wave_butterfly<32>(x, ck);
+        // Even lanes: u = w v - S^T e for their value; odd lanes: o = S^T q + (k.q) u.
+        const float u = ww_ * vv_ - x[0];
+        const float u_pair = __shfl_xor(u, 1, kWave);
+        if ((ck & 1) == 0) s_u[vsel] = u;
+        else io<TI>::st(o, static_cast<int64_t>(slab) * VD + vsel, fmaf(u_pair, kq, x[0]));
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const float uv = s_u[rv + 8 * i];
+            st[s][i] = f4_fma(k4, uv, st[s][i]);
+            if (dst[s]) *reinterpret_cast<float4 *>(dst[s] + (rv + 8 * i) * KD + kc) = st[s][i];
+        }
+        __syncthreads();
+    }
+}
+
 // Fused module decode step (one token per sequence, HV == H, K == V == D).
 // Replaces, for the module's decode call, the chain ShortConvolution x 3
 // (reference gdn2.py:395-430) -> gate and b / w activations (gdn2.py:840-866)
@@ -925,14 +1126,17 @@ template <typename TI, typename TG>
 static hipError_t launch_tpr(const RecurrentParams &p, int N, hipStream_t stream)
 {
     const bool trans = (p.flags & GDN2_FLAG_TRANSPOSE_STATE) != 0;
-    if (p.T == 1 && !p.cu_seqlens && p.K == 128 && p.V == 128 && !trans) {
+    if (p.T == 1 && !p.cu_seqlens && p.K == 128 && p.V == 128) {
         const int nslabs = N * p.HV;
-        if (p.h0)
-            hipLaunchKernelGGL((decode_step_kernel<TI, TG, true>), dim3((nslabs + 1) / 2), dim3(256), 0,
-                               stream, p, nslabs);
+        const dim3 grid((nslabs + 1) / 2);
+        if (trans && p.h0)
+            hipLaunchKernelGGL((decode_step_t_kernel<TI, TG, true>), grid, dim3(256), 0, stream, p, nslabs);
+        else if (trans)
+            hipLaunchKernelGGL((decode_step_t_kernel<TI, TG, false>), grid, dim3(256), 0, stream, p, nslabs);
+        else if (p.h0)
+            hipLaunchKernelGGL((decode_step_kernel<TI, TG, true>), grid, dim3(256), 0, stream, p, nslabs);
         else
-            hipLaunchKernelGGL((decode_step_kernel<TI, TG, false>), dim3((nslabs + 1) / 2), dim3(256), 0,
-                               stream, p, nslabs);
+            hipLaunchKernelGGL((decode_step_kernel<TI, TG, false>), grid, dim3(256), 0, stream, p, nslabs);
         return hipGetLastError();
     }
     // Narrowest row that still covers V with float4 lanes, capped at 128 columns.

@@ -135,6 +135,38 @@ def test_transposed_state_layout(gpu_device, dtype, K, V, T):
     assert rel_l2(ht, np.swapaxes(s_ref, -1, -2)) <= REL_TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_transposed_decode_step_no_state_gate_logits(gpu_device, dtype):
+    """The [V, K] decode-step kernel without an initial state, with the in-kernel gate and b / w
+    logits, an odd number of slabs (the last workgroup holds one)."""
+    from qwendopamine_amd.ops import fused_recurrent_gdn2
+
+    print(f"[case] transposed decode step, no state, gate logits {dtype}", flush=True)
+    B, H, K, V = 3, 3, 128, 128
+    inp = rand_inputs(B, 1, H, K, V, seed=63, h0_std=0.0)
+    rng = np.random.default_rng(64)
+    bl, wl = rng.standard_normal((B, 1, H, K)) * 2, rng.standard_normal((B, 1, H, V)) * 2
+    graw = rng.standard_normal((B, 1, H, K))
+    A_log = np.log(rng.uniform(1, 16, H))
+    dt_bias = rng.standard_normal(H * K) * 0.5
+    g = -np.exp(A_log)[:, None] * np.logaddexp(0.0, graw + dt_bias.reshape(H, K))
+    inp.update(b=bl, w=wl, g=graw)
+    t, r = to_device(inp, gpu_device, dtype)
+    t["g"] = torch.from_numpy(graw).to(gpu_device, torch.float32)
+    with torch.no_grad():
+        o, ht = fused_recurrent_gdn2(
+            *(t[n] for n in NAMES), output_final_state=True, use_qk_l2norm_in_kernel=True,
+            use_gate_in_kernel=True, A_log=torch.tensor(A_log, dtype=torch.float32, device=gpu_device),
+            dt_bias=torch.tensor(dt_bias, dtype=torch.float32, device=gpu_device), bw_logits=True,
+            transpose_state_layout=True)
+    torch.cuda.synchronize()
+    sig = lambda x: 1.0 / (1.0 + np.exp(-x))  # noqa: E731
+    o_ref, s_ref = orc.recurrent_fwd(r["q"], r["k"], r["v"], g, sig(r["b"]), sig(r["w"]), None)
+    assert tuple(ht.shape) == (B, H, V, K)
+    assert rel_l2(o, o_ref) <= REL_TOL[dtype]
+    assert rel_l2(ht, np.swapaxes(s_ref, -1, -2)) <= REL_TOL[dtype]
+
+
 def test_transposed_state_pool_decode(gpu_device):
     print("[case] transposed pooled decode", flush=True)
     N, H, K, V = 5, 4, 128, 128
