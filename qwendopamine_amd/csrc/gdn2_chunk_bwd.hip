@@ -726,11 +726,48 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
             for (int i = 0; i < 4; ++i) gv[j][i] = row16_scan(gv[j][i] * kLog2e);
         }
     };
+    // The rows again after the V-contractions, without the gates: their
+    // in-block prefix sums G stay in registers from the first load.
+    auto reload_qkb = [&](Raw4<TI> (&qv)[NKH], Raw4<TI> (&kv)[NKH], Raw4<TI> (&bv)[NKH]) __attribute__((always_inline)) {
+        const TI *q = static_cast<const TI *>(p.q);
+        const TI *k = static_cast<const TI *>(p.k);
+        const TI *b = static_cast<const TI *>(p.b);
+        if (K == KP) {
+            const int64_t off = row_ok ? roff : (t0 * H + h) * static_cast<int64_t>(K);
+#pragma unroll
+            for (int j = 0; j < NKH; ++j) {
+                const int c0 = 16 * (hh * NKH + j) + 4 * kg;
+                qv[j].load(q + off + c0);
+                kv[j].load(k + off + c0);
+                bv[j].load(b + off + c0);
+            }
+#pragma unroll
+            for (int j = 0; j < NKH; ++j) {
+                if (!row_ok) {
+                    qv[j].zero();
+                    kv[j].zero();
+                    bv[j].zero();
+                }
+            }
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < NKH; ++j) {
+            const int c0 = 16 * (hh * NKH + j) + 4 * kg;
+            float x[4];
+            load4<TI>(q, roff, c0, K, row_ok, p.vec_ok, x);
+            qv[j].set(x);
+            load4<TI>(k, roff, c0, K, row_ok, p.vec_ok, x);
+            kv[j].set(x);
+            load4<TI>(b, roff, c0, K, row_ok, p.vec_ok, x);
+            bv[j].set(x);
+        }
+    };
     float invq, invk, qmul;
     bool bigq, bigk, wave_slow;
+    float gv[NKH][4];  // in-block log2 decay prefix G of this wave's rows and channels
     {
     Raw4<TI> qv[NKH], kv[NKH], bv[NKH];
-    float gv[NKH][4];
     load_rows(qv, kv, bv, gv, [&]() __attribute__((always_inline)) { issue_slice(pre, 0); });
     {
         float sq = 0.f, sk = 0.f;
@@ -889,8 +926,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     }
 
     Raw4<TI> qv[NKH], kv[NKH], bv[NKH];
-    float gv[NKH][4];
-    load_rows(qv, kv, bv, gv, []() {});
+    reload_qkb(qv, kv, bv);
 
     // ---- G_last term: part 1 exp(G_last) rowsum(dS1 * S0) (channel tile wv),
     // part 2 this block's sum of dKt * Kt (ck = dKt here).  Together they are
