@@ -177,6 +177,40 @@ int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int
                            void *out, int io_dtype, int64_t rows, int N, float eps, void *stream);
 
 /*
+ * Backward of the short convolution on a prefill call (no cache), for training
+ * without torch's conv: the gradient of ShortConvolution.forward (reference
+ * gdn2.py:395-430, whose backward torch's autograd runs through F.conv1d and
+ * F.silu), y = silu(round(bias + conv(x))).  Recomputes the rounded
+ * pre-activation, then dpre = round(dy * silu'(pre)) (torch's SiLU backward),
+ *   dx[t] = sum_j w[j] dpre[t + W-1-j],
+ *   dweight[d, j] = sum_{b,t} dpre[t] x[t-W+1+j],  dbias[d] = sum_{b,t} dpre[t]
+ * with fp32 accumulation, deterministic (per-tile partials summed in a fixed
+ * order).  x rows [B*T, x_row_stride >= D]; dy, dx contiguous [B, T, D];
+ * weight / dweight [D, W]; bias / dbias [D] or NULL; silu: apply the SiLU.
+ * workspace: at least gdn2_short_conv_bwd_workspace_size() bytes.
+ */
+size_t gdn2_short_conv_bwd_workspace_size(int B, int T, int D, int conv_width);
+int gdn2_short_conv_bwd(const void *x, int64_t x_row_stride, const void *weight, const void *bias,
+                        const void *dy, void *dx, void *dweight, void *dbias, int io_dtype, int B,
+                        int T, int D, int conv_width, int silu, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/*
+ * Backward of the gated RMS norm (reference RMSNormGated.forward, gdn2.py:433-452,
+ * whose backward torch's autograd runs through its five ops): for `rows` rows of
+ * N <= 256 values, with r = rsqrt(mean(x^2) + eps), xn = x r, s = silu(z),
+ *   dx = r (g - xn mean(g xn)),  g = dy weight s;   dz = dy xn weight silu'(z);
+ *   dweight = sum over rows of dy xn s
+ * in fp32 (deterministic partial sums).  weight / dweight in io_dtype or float32.
+ * workspace: at least gdn2_gated_rmsnorm_bwd_workspace_size() bytes.
+ */
+size_t gdn2_gated_rmsnorm_bwd_workspace_size(int64_t rows, int N);
+int gdn2_gated_rmsnorm_bwd(const void *x, const void *z, const void *weight, int weight_dtype,
+                           const void *dy, void *dx, void *dz, void *dweight, int io_dtype,
+                           int64_t rows, int N, float eps, void *workspace, size_t workspace_bytes,
+                           void *stream);
+
+/*
  * Fused module decode step: one token per sequence through the whole mixer
  * core, with no HBM round trip of q, k, v or o in between.  Replaces, for the
  * decode call of GatedDeltaNet2.forward, the chain

@@ -79,6 +79,16 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp,
          _i, _i, _i, _i, _i, _i, _f, _u, _vp, _sz, _vp],
     ),
+    "gdn2_short_conv_bwd_workspace_size": (_sz, [_i, _i, _i, _i]),
+    "gdn2_short_conv_bwd": (
+        _i,
+        [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp],
+    ),
+    "gdn2_gated_rmsnorm_bwd_workspace_size": (_sz, [_i64, _i]),
+    "gdn2_gated_rmsnorm_bwd": (
+        _i,
+        [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i64, _i, _f, _vp, _sz, _vp],
+    ),
     "gdn2_chunk_fwd_gated_norm": (
         _i,
         [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _i64, _vp, _f, _vp, _vp, _vp, _vp, _f,

@@ -237,6 +237,61 @@ int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+size_t gdn2_short_conv_bwd_workspace_size(int B, int T, int D, int conv_width)
+{
+    if (B < 0 || T < 0 || D < 0 || conv_width < 1 || conv_width > 8) return 0;
+    return static_cast<size_t>(conv_bwd_partial_floats(B, T, D, conv_width)) * sizeof(float);
+}
+
+int gdn2_short_conv_bwd(const void *x, int64_t x_row_stride, const void *weight, const void *bias,
+                        const void *dy, void *dx, void *dweight, void *dbias, int io_dtype, int B,
+                        int T, int D, int conv_width, int silu, void *workspace,
+                        size_t workspace_bytes, void *stream)
+{
+    if (!valid_dtype(io_dtype) || B < 0 || T < 0 || D < 0) return GDN2_ERR_INVALID;
+    if (conv_width < 1 || conv_width > 8) return GDN2_ERR_UNSUPPORTED;
+    if (static_cast<int64_t>(B) * T * D == 0) return GDN2_OK;
+    if (!x || !weight || !dy || !dx || !dweight || (dbias && !bias) || x_row_stride < D)
+        return GDN2_ERR_INVALID;
+    if (static_cast<int64_t>(B) * ((T + 31) / 32) > 65535) return GDN2_ERR_UNSUPPORTED;  // grid.y
+    if (!workspace || workspace_bytes < gdn2_short_conv_bwd_workspace_size(B, T, D, conv_width))
+        return GDN2_ERR_WORKSPACE;
+    ConvBwdParams p;
+    p.x = x; p.w = weight; p.bias = bias; p.dy = dy; p.dx = dx; p.dw = dweight; p.dbias = dbias;
+    p.part = static_cast<float *>(workspace);
+    p.B = B; p.T = T; p.D = D; p.W = conv_width; p.ldx = x_row_stride; p.silu = silu != 0;
+    const hipError_t err = launch_short_conv_bwd(p, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+size_t gdn2_gated_rmsnorm_bwd_workspace_size(int64_t rows, int N)
+{
+    if (rows < 0 || N <= 0 || N > 256) return 0;
+    return static_cast<size_t>(norm_bwd_blocks(rows) * 4 * N) * sizeof(float);
+}
+
+int gdn2_gated_rmsnorm_bwd(const void *x, const void *z, const void *weight, int weight_dtype,
+                           const void *dy, void *dx, void *dz, void *dweight, int io_dtype,
+                           int64_t rows, int N, float eps, void *workspace, size_t workspace_bytes,
+                           void *stream)
+{
+    if (!valid_dtype(io_dtype) || !valid_dtype(weight_dtype)) return GDN2_ERR_INVALID;
+    if (weight_dtype != io_dtype && weight_dtype != GDN2_DTYPE_F32) return GDN2_ERR_INVALID;
+    if (rows < 0 || N <= 0) return GDN2_ERR_INVALID;
+    if (N > 256) return GDN2_ERR_UNSUPPORTED;
+    if (rows == 0) return GDN2_OK;
+    if (!x || !z || !weight || !dy || !dx || !dz || !dweight) return GDN2_ERR_INVALID;
+    if (!workspace || workspace_bytes < gdn2_gated_rmsnorm_bwd_workspace_size(rows, N))
+        return GDN2_ERR_WORKSPACE;
+    NormBwdParams p;
+    p.x = x; p.z = z; p.weight = weight; p.dy = dy; p.dx = dx; p.dz = dz; p.dweight = dweight;
+    p.part = static_cast<float *>(workspace);
+    p.rows = rows; p.N = N; p.eps = eps;
+    p.w_f32 = weight_dtype == GDN2_DTYPE_F32;
+    const hipError_t err = launch_gated_rmsnorm_bwd(p, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
 int gdn2_decode_fused(const void *const raw_qkv[3], const int64_t ld_qkv[3], const void *g,
                       int64_t ldg, int g_dtype, const void *b, int64_t ldb, const void *w,
                       int64_t ldw, const void *const conv_weight[3], const void *const conv_bias[3],

@@ -155,4 +155,34 @@ struct NormParams {
 
 hipError_t launch_gated_rmsnorm(const NormParams &p, int io_dtype, hipStream_t stream);
 
+// Backward of the short convolution on a prefill call (no cache).
+struct ConvBwdParams {
+    const void *x;      // [B, T, D] input rows: row (b, t) at x + (b * T + t) * ldx
+    const void *w;      // [D, W]
+    const void *bias;   // [D] or NULL
+    const void *dy;     // [B, T, D] gradient of the output, contiguous
+    void *dx;           // [B, T, D], contiguous
+    void *dw;           // [D, W]
+    void *dbias;        // [D] or NULL
+    float *part;        // conv_bwd_partial_floats(B, T, D, W) floats of scratch
+    int B, T, D, W;
+    int64_t ldx;
+    int silu;
+};
+int64_t conv_bwd_partial_floats(int B, int T, int D, int W);
+hipError_t launch_short_conv_bwd(const ConvBwdParams &p, int io_dtype, hipStream_t stream);
+
+// Backward of the gated RMS norm (rows of N <= 256 values).
+struct NormBwdParams {
+    const void *x, *z, *weight, *dy;
+    void *dx, *dz, *dweight;
+    float *part;        // norm_bwd_blocks(rows) * 4 * N floats of scratch
+    int64_t rows;
+    int N;
+    int w_f32;          // weight (and its gradient) in float32
+    float eps;
+};
+int64_t norm_bwd_blocks(int64_t rows);
+hipError_t launch_gated_rmsnorm_bwd(const NormBwdParams &p, int io_dtype, hipStream_t stream);
+
 }  // namespace gdn2

@@ -114,6 +114,9 @@ class ShortConvolution(nn.Module):
         self.activation = activation
         self.conv1d = nn.Conv1d(hidden_size, hidden_size, kernel_size, groups=hidden_size,
                                 bias=bias, padding=kernel_size - 1)
+        # Training prefill (no cache) runs the HIP forward and backward kernels;
+        # False uses torch's conv1d and SiLU.
+        self.hip_backward = True
 
     def forward(self, x: torch.Tensor, cache: torch.Tensor | None = None,
                 output_final_state: bool = False, cu_seqlens: torch.Tensor | None = None):
@@ -122,11 +125,17 @@ class ShortConvolution(nn.Module):
                                             None if cache is None else [cache], output_final_state,
                                             self.activation)
             return ys[0], None if new is None else new[0]
-        # Differentiable path (training): torch's depthwise conv.
         bsz, seq, dim = x.shape
+        keep = self.kernel_size - 1
+        if (self.hip_backward and x.is_cuda and cache is None and self.kernel_size <= 8
+                and self.activation in (None, "silu") and (seq > 1 or not output_final_state)):
+            # Differentiable path (training) on the HIP kernels.
+            y = ops.short_conv_autograd(x, self.conv1d.weight, self.conv1d.bias, self.activation)
+            new_cache = x.transpose(1, 2)[:, :, -keep:] if output_final_state else None
+            return y, new_cache
+        # Differentiable path (training): torch's depthwise conv.
         xt = x.transpose(1, 2)
         wgt, bias = self.conv1d.weight, self.conv1d.bias
-        keep = self.kernel_size - 1
         if cache is None and output_final_state and seq == 1:
             cache = x.new_zeros(bsz, dim, keep)
         if cache is not None and seq == 1:
@@ -153,10 +162,15 @@ class RMSNormGated(nn.Module):
         self.hidden_size = hidden_size
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(hidden_size))
+        # Training runs the HIP forward and backward kernels (rows of up to 256
+        # values); False uses torch ops.
+        self.hip_backward = True
 
     def forward(self, x: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
         if _inference(x, z, self.weight):
             return ops.gated_rmsnorm(x, z, self.weight, self.eps)
+        if self.hip_backward and x.is_cuda and x.shape[-1] <= 256 and z.shape == x.shape:
+            return ops.gated_rmsnorm_autograd(x, z, self.weight, self.eps)
         # Differentiable path (training): torch ops, same rounding.
         inv = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
         return x * inv * self.weight * F.silu(z)

@@ -893,6 +893,104 @@ def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: f
     return out
 
 
+class ShortConvFunction(torch.autograd.Function):
+    """Prefill ``ShortConvolution`` (no cache) with the HIP forward and backward.
+
+    Forward: :func:`short_convolution` (``gdn2.py:395-430`` with the reference's rounding).
+    Backward: ``gdn2_short_conv_bwd`` -- the gradients torch's autograd gives through
+    ``F.conv1d`` and ``F.silu``, in fp32 with deterministic sums.
+    """
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, silu: bool):
+        (y,), _ = short_convolution([x], [weight], [bias], None, False, "silu" if silu else None)
+        ctx.save_for_backward(x, weight, bias)
+        ctx.silu = silu
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight, bias = ctx.saved_tensors
+        name = "short_convolution backward"
+        B, T, D = x.shape
+        W = int(weight.shape[-1])
+        dt = x.dtype
+        xc = x if (x.stride(2) == 1 and (B <= 1 or x.stride(0) == T * x.stride(1)) and x.stride(1) >= D) \
+            else x.contiguous()
+        ld = xc.stride(1) if T > 1 else (xc.stride(0) if B > 1 else D)
+        dyc = dy.to(dt).contiguous()
+        wc = weight.detach().reshape(D, W).to(dt).contiguous()
+        bc = None if bias is None else bias.detach().to(dt).contiguous()
+        dx = torch.empty(B, T, D, dtype=dt, device=x.device)
+        dw = torch.empty(D, W, dtype=dt, device=x.device)
+        db = None if bias is None else torch.empty(D, dtype=dt, device=x.device)
+        lib = nat.load()
+        wsb = lib.gdn2_short_conv_bwd_workspace_size(B, T, D, W)
+        ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=x.device)
+        st = lib.gdn2_short_conv_bwd(nat.ptr(xc), ld, nat.ptr(wc), nat.ptr(bc), nat.ptr(dyc), nat.ptr(dx),
+                                     nat.ptr(dw), nat.ptr(db), nat.dtype_code(dt), B, T, D, W, int(ctx.silu),
+                                     ws.data_ptr(), ws.numel(), nat.stream_handle(x.device))
+        nat.check(st, name)
+        dwo = dw.reshape(weight.shape).to(weight.dtype)
+        dbo = None if db is None else db.to(bias.dtype)
+        return dx, dwo, dbo, None
+
+
+@torch.compiler.disable
+def short_conv_autograd(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                        activation: str | None = "silu") -> torch.Tensor:
+    """Differentiable prefill short convolution (no cache) on the HIP kernels; ``[B, T, D]`` in
+    and out, ``weight`` the Conv1d weight ``[D, 1, W]`` (W <= 8)."""
+    _require_gpu("short_conv_autograd", x)
+    if activation not in (None, "silu"):
+        raise NotImplementedError(f"short_conv_autograd: activation {activation!r}")
+    return ShortConvFunction.apply(x, weight, bias, activation == "silu")
+
+
+class GatedRMSNormFunction(torch.autograd.Function):
+    """``RMSNormGated`` with the HIP forward (:func:`gated_rmsnorm`, the reference's rounding)
+    and backward (``gdn2_gated_rmsnorm_bwd``: dx, dz, dweight in fp32, deterministic)."""
+
+    @staticmethod
+    def forward(ctx, x, z, weight, eps: float):
+        out = gated_rmsnorm(x, z, weight, eps)
+        ctx.save_for_backward(x, z, weight)
+        ctx.eps = eps
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, z, weight = ctx.saved_tensors
+        name = "gated_rmsnorm backward"
+        dt = x.dtype
+        N = x.shape[-1]
+        xc, zc = x.contiguous(), z.to(dt).contiguous()
+        wdt = torch.float32 if weight.dtype == torch.float32 else dt
+        wc = weight.detach().to(wdt).contiguous()
+        dyc = dout.to(dt).contiguous()
+        rows = xc.numel() // N
+        dx, dz = torch.empty_like(xc), torch.empty_like(zc)
+        dw = torch.empty(N, dtype=wdt, device=x.device)
+        lib = nat.load()
+        wsb = lib.gdn2_gated_rmsnorm_bwd_workspace_size(rows, N)
+        ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=x.device)
+        st = lib.gdn2_gated_rmsnorm_bwd(nat.ptr(xc), nat.ptr(zc), nat.ptr(wc), nat.dtype_code(wdt), nat.ptr(dyc),
+                                        nat.ptr(dx), nat.ptr(dz), nat.ptr(dw), nat.dtype_code(dt), rows, N,
+                                        float(ctx.eps), ws.data_ptr(), ws.numel(), nat.stream_handle(x.device))
+        nat.check(st, name)
+        return dx, dz.to(z.dtype), dw.to(weight.dtype), None
+
+
+@torch.compiler.disable
+def gated_rmsnorm_autograd(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor,
+                           eps: float = 1e-5) -> torch.Tensor:
+    """Differentiable gated RMS norm on the HIP kernels (rows of up to 256 values)."""
+    _require_gpu("gated_rmsnorm_autograd", x, z, weight)
+    if x.shape[-1] > 256:
+        raise NotImplementedError("gated_rmsnorm_autograd: rows of up to 256 values")
+    return GatedRMSNormFunction.apply(x, z, weight, eps)
+
+
 @torch.compiler.disable
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
     """``weight * (x * rsqrt(mean(x^2) + eps))`` over the last axis (N <= 2048).
