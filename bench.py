@@ -441,6 +441,45 @@ def bench_prologue(torch, dev, reps=20):
     def pre_fused():
         ops.chunk_gdn2_gated_norm(pq, pk, pv, pf, pb, pw, z, nw, 1e-5, output_final_state=True, **pkw)
 
+    # Training: forward + backward of the q / k / v convolutions and of the gated norm, on the
+    # HIP kernels (autograd functions) against torch's autograd through the reference's ops.
+    xg = [x.detach().clone().requires_grad_(True) for x in xs]
+    wg = [w.detach().clone().requires_grad_(True) for w in ws]
+    dyc = torch.randn(B, T, D, generator=gen, device=dev).to(bf)
+    og, zg = o.detach().clone().requires_grad_(True), z.detach().clone().requires_grad_(True)
+    nwg = nw.detach().clone().requires_grad_(True)
+    dyn = torch.randn(B, T, H, Dh, generator=gen, device=dev).to(bf)
+
+    def conv_train_hip():
+        for x, w in zip(xg, wg):
+            ops.short_conv_autograd(x, w, None, "silu").backward(dyc)
+
+    def conv_train_torch():
+        for x, w in zip(xg, wg):
+            F.silu(F.conv1d(x.transpose(1, 2), w, None, padding=W - 1, groups=D)[..., :T]).transpose(1, 2) \
+                .backward(dyc)
+
+    def norm_train_hip():
+        ops.gated_rmsnorm_autograd(og, zg, nwg, 1e-5).backward(dyn)
+
+    def norm_train_torch():
+        (og * torch.rsqrt(og.pow(2).mean(-1, keepdim=True) + 1e-5) * nwg * F.silu(zg)).backward(dyn)
+
+    def eager(fn, reps_=10):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps_):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) * 1e3 / reps_
+
+    train_t = {k: eager(f) for k, f in (("conv_hip", conv_train_hip), ("conv_torch", conv_train_torch),
+                                         ("norm_hip", norm_train_hip), ("norm_torch", norm_train_torch))}
+
     conv_bytes = 6 * B * T * D * 2
     norm_bytes = 3 * B * T * H * Dh * 2
     # fused decode: state read + write, raw q/k/v/g/b/w/z rows, conv caches read + write,
@@ -465,6 +504,11 @@ def bench_prologue(torch, dev, reps=20):
                         "fused_us": round(t["dec_fused"], 2), "separate_hip_us": round(t["dec_separate"], 2),
                         "algorithmic_bytes": dec_bytes,
                         "achieved_GBps": round(dec_bytes / (t["dec_fused"] * 1e-6) / 1e9, 1)},
+        "training_fwd_bwd": {"workload": "forward + backward, eager (autograd), same shapes",
+                             "short_conv_qkv_us": round(train_t["conv_hip"], 1),
+                             "short_conv_qkv_torch_us": round(train_t["conv_torch"], 1),
+                             "gated_rmsnorm_us": round(train_t["norm_hip"], 1),
+                             "gated_rmsnorm_torch_us": round(train_t["norm_torch"], 1)},
         "prefill_norm": {"workload": f"B{B} T{T}, {H} heads x {Dh}: chunk op + gated norm",
                          "fused_us": round(t["pre_fused"], 2), "separate_hip_us": round(t["pre_separate"], 2)},
     }

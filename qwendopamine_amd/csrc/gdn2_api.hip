@@ -267,7 +267,7 @@ int gdn2_short_conv_bwd(const void *x, int64_t x_row_stride, const void *weight,
 size_t gdn2_gated_rmsnorm_bwd_workspace_size(int64_t rows, int N)
 {
     if (rows < 0 || N <= 0 || N > 256) return 0;
-    return static_cast<size_t>(norm_bwd_blocks(rows) * 4 * N) * sizeof(float);
+    return static_cast<size_t>(norm_bwd_blocks(rows) * N) * sizeof(float);
 }
 
 int gdn2_gated_rmsnorm_bwd(const void *x, const void *z, const void *weight, int weight_dtype,

@@ -176,7 +176,7 @@ hipError_t launch_short_conv_bwd(const ConvBwdParams &p, int io_dtype, hipStream
 struct NormBwdParams {
     const void *x, *z, *weight, *dy;
     void *dx, *dz, *dweight;
-    float *part;        // norm_bwd_blocks(rows) * 4 * N floats of scratch
+    float *part;        // norm_bwd_blocks(rows) * N floats of scratch
     int64_t rows;
     int N;
     int w_f32;          // weight (and its gradient) in float32

@@ -10,7 +10,7 @@
 //    (gdn2.py:433-452): with r = rsqrt(mean(x^2) + eps), xn = x r, s = silu(z),
 //      dx = r (g - xn mean(g xn)),  g = dy w s
 //      dz = dy xn w silu'(z),       dw = sum over rows of dy xn s
-//    in fp32, with per-wave partial sums of dw.
+//    in fp32, with per-workgroup partial sums of dw.
 //  * partial_reduce_kernel -- sums the partials over tiles / waves in a fixed
 //    order (deterministic) and writes the weight-shaped gradients.
 //
@@ -107,87 +107,112 @@ __global__ __launch_bounds__(256) void short_conv_bwd_kernel(ConvBwdParams p)
     part[static_cast<int64_t>(W) * p.D + d] = db;
 }
 
-// One wave per row at a time (a persistent grid of waves walking the rows);
-// lane l holds columns l, l + 64, ... (up to 4).  Per-wave partial sums of dw
-// go to part[wave][N].
-template <typename T, typename TW>
+// A grid of workgroups walking the rows: wave w of workgroup b handles rows
+// (4 (4 b + w) + j) + k * 16 * gridDim.x, j < 4 (four rows' requests in
+// flight per iteration); lane l holds columns l, l + 64, ... (up to 4).  The
+// four waves' partial sums of dw are combined in LDS in a fixed order and
+// written as the workgroup's partial row part[b][N].
+template <typename T, typename TW, int MAXC>
 __global__ __launch_bounds__(256) void gated_rmsnorm_bwd_kernel(NormBwdParams p)
 {
-    constexpr int MAXC = 4;
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
+    constexpr int RPI = 4;
+    __shared__ float s_acc[4][256];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int N = p.N;
     const T *x = static_cast<const T *>(p.x);
     const T *z = static_cast<const T *>(p.z);
     const T *dy = static_cast<const T *>(p.dy);
     T *dx = static_cast<T *>(p.dx);
     T *dz = static_cast<T *>(p.dz);
-    float wv[MAXC], acc[MAXC];
+    float wv_[MAXC], acc[MAXC];
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
         const int c = lane + 64 * i;
-        wv[i] = c < N ? io<TW>::ld(static_cast<const TW *>(p.weight), c) : 0.0f;
+        wv_[i] = c < N ? io<TW>::ld(static_cast<const TW *>(p.weight), c) : 0.0f;
         acc[i] = 0.0f;
     }
-    for (int64_t row = wave; row < p.rows; row += nwaves) {
-        const int64_t off = row * N;
-        float xv[MAXC], zv[MAXC], gv[MAXC];
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 16;
+    for (int64_t base = (static_cast<int64_t>(blockIdx.x) * 4 + wv) * RPI; base < p.rows; base += stride) {
+        float xv[RPI][MAXC], zv[RPI][MAXC], gv[RPI][MAXC];
 #pragma unroll
-        for (int i = 0; i < MAXC; ++i) {
-            const int c = lane + 64 * i;
-            const int cc = c < N ? c : N - 1;  // valid address; zeroed below
-            xv[i] = io<T>::ld(x, off + cc);
-            zv[i] = io<T>::ld(z, off + cc);
-            gv[i] = io<T>::ld(dy, off + cc);
+        for (int j = 0; j < RPI; ++j) {
+            const int64_t row = base + j < p.rows ? base + j : p.rows - 1;  // valid address
+#pragma unroll
+            for (int i = 0; i < MAXC; ++i) {
+                const int c = lane + 64 * i;
+                const int64_t off = row * N + (c < N ? c : N - 1);
+                xv[j][i] = io<T>::ld(x, off);
+                zv[j][i] = io<T>::ld(z, off);
+                gv[j][i] = io<T>::ld(dy, off);
+            }
         }
-        float sq = 0.0f;
 #pragma unroll
-        for (int i = 0; i < MAXC; ++i) {
-            if (lane + 64 * i >= N) xv[i] = zv[i] = gv[i] = 0.0f;
-            sq = fmaf(xv[i], xv[i], sq);
-        }
-        sq = wave_sum(sq);
-        const float r = rsqrtf(sq / static_cast<float>(N) + p.eps);
-        float xn[MAXC], sz[MAXC], g[MAXC], dot = 0.0f;
+        for (int j = 0; j < RPI; ++j) {
+            const int64_t row = base + j;
+            const bool live = row < p.rows;
+            float sq = 0.0f;
 #pragma unroll
-        for (int i = 0; i < MAXC; ++i) {
-            xn[i] = xv[i] * r;
-            const float sg = 1.0f / (1.0f + expf(-zv[i]));
-            sz[i] = zv[i] * sg;
-            g[i] = gv[i] * wv[i] * sz[i];
-            dot = fmaf(g[i], xn[i], dot);
-            // dz = dy xn w silu'(z); dw += dy xn s
-            const float dzv = gv[i] * xn[i] * wv[i] * (sg * (1.0f + zv[i] * (1.0f - sg)));
-            const int c = lane + 64 * i;
-            if (c < N) io<T>::st(dz, off + c, dzv);
-            acc[i] = fmaf(gv[i], xn[i] * sz[i], acc[i]);
-        }
-        dot = wave_sum(dot) / static_cast<float>(N);
+            for (int i = 0; i < MAXC; ++i) {
+                if (lane + 64 * i >= N || !live) xv[j][i] = zv[j][i] = gv[j][i] = 0.0f;
+                sq = fmaf(xv[j][i], xv[j][i], sq);
+            }
+            sq = wave_sum(sq);
+            const float r = rsqrtf(sq / static_cast<float>(N) + p.eps);
+            float xn[MAXC], g[MAXC], dot = 0.0f;
 #pragma unroll
-        for (int i = 0; i < MAXC; ++i) {
-            const int c = lane + 64 * i;
-            if (c < N) io<T>::st(dx, off + c, r * (g[i] - xn[i] * dot));
+            for (int i = 0; i < MAXC; ++i) {
+                xn[i] = xv[j][i] * r;
+                const float sg = 1.0f / (1.0f + expf(-zv[j][i]));
+                const float sz = zv[j][i] * sg;
+                g[i] = gv[j][i] * wv_[i] * sz;
+                dot = fmaf(g[i], xn[i], dot);
+                // dz = dy xn w silu'(z); dw += dy xn s
+                const float dzv = gv[j][i] * xn[i] * wv_[i] * (sg * (1.0f + zv[j][i] * (1.0f - sg)));
+                const int c = lane + 64 * i;
+                if (live && c < N) io<T>::st(dz, row * N + c, dzv);
+                acc[i] = fmaf(gv[j][i], xn[i] * sz, acc[i]);
+            }
+            dot = wave_sum(dot) / static_cast<float>(N);
+#pragma unroll
+            for (int i = 0; i < MAXC; ++i) {
+                const int c = lane + 64 * i;
+                if (live && c < N) io<T>::st(dx, row * N + c, r * (g[i] - xn[i] * dot));
+            }
         }
     }
 #pragma unroll
-    for (int i = 0; i < MAXC; ++i) {
-        const int c = lane + 64 * i;
-        if (c < N) p.part[wave * N + c] = acc[i];
-    }
+    for (int i = 0; i < MAXC; ++i) s_acc[wv][lane + 64 * i] = acc[i];
+#pragma unroll
+    for (int i = MAXC; i < 4; ++i) s_acc[wv][lane + 64 * i] = 0.0f;
+    __syncthreads();
+    for (int c = threadIdx.x; c < N; c += 256)
+        p.part[static_cast<int64_t>(blockIdx.x) * N + c] = (s_acc[0][c] + s_acc[1][c]) + (s_acc[2][c] + s_acc[3][c]);
 }
 
-// out[e] = sum over k < nparts of part[k * E + e], e < E, summed in order k;
-// written in TO.  With a `split`, elements e = j * D + d of [W + 1][D]
-// partials go to a [D][W] weight (j < W) and a [D] bias (j == W).
+// out[e] = sum over k < nparts of part[k * E + e], e < E, in a fixed order
+// (deterministic): workgroup b takes 64 consecutive e, its four waves the
+// parts k = w mod 4 with four accumulators each, combined in LDS.  Written in
+// TO.  With W > 0, elements e = j * D + d of [W + 1][D] partials go to a
+// [D][W] weight (j < W) and a [D] bias (j == W).
 template <typename TO>
 __global__ __launch_bounds__(256) void partial_reduce_kernel(const float *part, int64_t nparts, int64_t E,
                                                              void *out, void *out_bias, int D, int W)
 {
-    const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (e >= E) return;
-    float s = 0.0f;
-    for (int64_t k = 0; k < nparts; ++k) s += part[k * E + e];
+    __shared__ float s_sum[4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+    const int64_t ec = e < E ? e : E - 1;
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t k = wv;
+    for (; k + 12 < nparts; k += 16) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] += part[(k + 4 * u) * E + ec];
+    }
+    for (; k < nparts; k += 4) a[0] += part[k * E + ec];
+    s_sum[wv][lane] = (a[0] + a[1]) + (a[2] + a[3]);
+    __syncthreads();
+    if (wv != 0 || e >= E) return;
+    const float s = (s_sum[0][lane] + s_sum[1][lane]) + (s_sum[2][lane] + s_sum[3][lane]);
     if (W == 0) {
         io<TO>::st(static_cast<TO *>(out), e, s);
         return;
@@ -209,7 +234,7 @@ hipError_t conv_bwd_w(const ConvBwdParams &p, hipStream_t s)
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t E = static_cast<int64_t>(W + 1) * p.D;
-    hipLaunchKernelGGL((partial_reduce_kernel<T>), dim3(static_cast<unsigned>((E + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL((partial_reduce_kernel<T>), dim3(static_cast<unsigned>((E + 63) / 64)), dim3(256), 0, s,
                        p.part, static_cast<int64_t>(p.B) * tiles, E, p.dw, p.dbias, p.D, W);
     return hipGetLastError();
 }
@@ -233,11 +258,17 @@ template <typename T, typename TW>
 hipError_t norm_bwd_t(const NormBwdParams &p, hipStream_t s)
 {
     const int blocks = static_cast<int>(norm_bwd_blocks(p.rows));
-    hipLaunchKernelGGL((gated_rmsnorm_bwd_kernel<T, TW>), dim3(blocks), dim3(256), 0, s, p);
+    // Columns per lane: N <= 64, 128 or 256.
+    if (p.N <= 64)
+        hipLaunchKernelGGL((gated_rmsnorm_bwd_kernel<T, TW, 1>), dim3(blocks), dim3(256), 0, s, p);
+    else if (p.N <= 128)
+        hipLaunchKernelGGL((gated_rmsnorm_bwd_kernel<T, TW, 2>), dim3(blocks), dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((gated_rmsnorm_bwd_kernel<T, TW, 4>), dim3(blocks), dim3(256), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((partial_reduce_kernel<TW>), dim3((p.N + 255) / 256), dim3(256), 0, s, p.part,
-                       static_cast<int64_t>(blocks) * 4, static_cast<int64_t>(p.N), p.dweight, nullptr, p.N, 0);
+    hipLaunchKernelGGL((partial_reduce_kernel<TW>), dim3((p.N + 63) / 64), dim3(256), 0, s, p.part,
+                       static_cast<int64_t>(blocks), static_cast<int64_t>(p.N), p.dweight, nullptr, p.N, 0);
     return hipGetLastError();
 }
 
@@ -250,10 +281,10 @@ int64_t conv_bwd_partial_floats(int B, int T, int D, int W)
 
 int64_t norm_bwd_blocks(int64_t rows)
 {
-    // Up to 4 rows per wave: enough waves to fill the chip, few partial rows.
-    const int64_t waves = (rows + 3) / 4;
-    const int64_t b = (waves + 3) / 4;
-    return b < 1 ? 1 : (b > 4096 ? 4096 : b);
+    // At least 16 rows (four per wave) per workgroup, at most 1024 workgroups
+    // (four per CU): one partial row per workgroup.
+    const int64_t b = (rows + 15) / 16;
+    return b < 1 ? 1 : (b > 1024 ? 1024 : b);
 }
 
 hipError_t launch_short_conv_bwd(const ConvBwdParams &p, int io_dtype, hipStream_t stream)
