@@ -297,6 +297,40 @@ int gdn2_chunk_fwd_gated_norm(const void *q, const void *k, const void *v, const
                               size_t workspace_bytes, void *stream);
 
 /*
+ * gdn2_chunk_fwd on the raw q, k, v projections, with the module's three
+ * short convolutions (causal depthwise conv1d of width 4, no bias, optional
+ * SiLU) applied inside the chunk kernels: prep convolves q and k as it lands
+ * their rows, the scan's copy waves convolve v as they form w * v.  Replaces
+ * ShortConvolution.forward for q, k, v followed by chunk_gdn2 (reference
+ * src/qwendopamine/models/gdn2/gdn2.py:395-430 and
+ * gdn2_ops/chunk_gdn2.py:1268-1434, as GatedDeltaNet2.forward calls them at
+ * gdn2.py:815-833 and 875-927), prefill without a conv cache: rows before a
+ * sequence's first token read as zero (per cu_seqlens sequence).  Every
+ * convolution output is rounded to io_dtype before and after the SiLU, as in
+ * gdn2_short_conv_fwd, so without cu_seqlens the result equals
+ * gdn2_short_conv_fwd followed by gdn2_chunk_fwd bit for bit.
+ *   q, k, v        raw rows with token strides ld_q, ld_k, ld_v (elements,
+ *                  multiples of 8); head h reads columns h*K.. (h*V.. for v)
+ *   conv_q/k/v     [H*K or H*V][4] taps in io_dtype (the conv1d weights)
+ *   gate           optional: non-NULL applies the gated output norm as
+ *                  gdn2_chunk_fwd_gated_norm does (then V in {16, 32, 64})
+ * The new conv caches (the last three raw rows) are not written: they are
+ * slices of q, k, v.  Inference only; bf16 io, K in {32, 64, 128}, V a
+ * multiple of 16 split into whole value slices, conv_width 4, otherwise
+ * GDN2_ERR_UNSUPPORTED.  q, k, v, g, b, w and the taps 16-byte aligned.
+ */
+int gdn2_chunk_fwd_conv(const void *q, int64_t ld_q, const void *k, int64_t ld_k, const void *v,
+                        int64_t ld_v, const void *conv_q, const void *conv_k, const void *conv_v,
+                        int conv_width, int conv_silu, const void *g, const void *b, const void *w,
+                        int io_dtype, int g_dtype, void *o, const void *gate, int64_t ld_gate,
+                        const void *norm_weight, float eps, const float *initial_state,
+                        float *final_state, const float *A_log, const float *dt_bias,
+                        float lower_bound, const int64_t *cu_seqlens,
+                        const int64_t *cu_seqlens_host, int num_seqs, int B, int T, int H, int K,
+                        int V, float scale, unsigned flags, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/*
  * The two stages of gdn2_chunk_fwd, for callers that schedule or time them
  * separately.  Calling prep then scan on the same workspace equals
  * gdn2_chunk_fwd.

@@ -94,6 +94,11 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _i64, _vp, _f, _vp, _vp, _vp, _vp, _f,
          _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _u, _vp, _sz, _vp],
     ),
+    "gdn2_chunk_fwd_conv": (
+        _i,
+        [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, _i64,
+         _vp, _f, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _u, _vp, _sz, _vp],
+    ),
     "gdn2_chunk_fwd_static": (
         _i,
         [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp,

@@ -421,6 +421,57 @@ int gdn2_chunk_fwd_gated_norm(const void *q, const void *k, const void *v, const
     return launch_chunk_fwd(a, io_dtype, g_dtype, static_cast<hipStream_t>(stream));
 }
 
+int gdn2_chunk_fwd_conv(const void *q, int64_t ld_q, const void *k, int64_t ld_k, const void *v, int64_t ld_v,
+                        const void *conv_q, const void *conv_k, const void *conv_v, int conv_width,
+                        int conv_silu, const void *g, const void *b, const void *w, int io_dtype,
+                        int g_dtype, void *o, const void *gate, int64_t ld_gate,
+                        const void *norm_weight, float eps, const float *initial_state,
+                        float *final_state, const float *A_log, const float *dt_bias, float lower_bound,
+                        const int64_t *cu_seqlens, const int64_t *cu_seqlens_host, int num_seqs, int B,
+                        int T, int H, int K, int V, float scale, unsigned flags, void *workspace,
+                        size_t workspace_bytes, void *stream)
+{
+    ChunkFwdArgs a;
+    const int st = check_chunk_args(io_dtype, g_dtype, cu_seqlens, cu_seqlens_host, num_seqs, B,
+                                    T, H, K, V, flags, A_log);
+    if (st != GDN2_OK) return st;
+    if (flags & GDN2_FLAG_SAVE_FOR_BWD) return GDN2_ERR_INVALID;  // an inference prologue
+    if (conv_width != 4 || (conv_silu != 0 && conv_silu != 1)) return GDN2_ERR_UNSUPPORTED;
+    if (io_dtype != GDN2_DTYPE_BF16 || (K != 32 && K != 64 && K != 128) || V % 16 != 0)
+        return GDN2_ERR_UNSUPPORTED;
+    if (gate && V != 16 && V != 32 && V != 64) return GDN2_ERR_UNSUPPORTED;
+    if (static_cast<int64_t>(B) * T > 0 &&
+        (!q || !k || !v || !g || !b || !w || !o || !conv_q || !conv_k || !conv_v || (gate && !norm_weight)))
+        return GDN2_ERR_INVALID;
+    // 16-byte row pieces of q, k, v, w and the taps.
+    auto a16 = [](const void *x) { return (reinterpret_cast<uintptr_t>(x) % 16) == 0; };
+    if (ld_q < static_cast<int64_t>(H) * K || ld_k < static_cast<int64_t>(H) * K ||
+        ld_v < static_cast<int64_t>(H) * V || ld_q % 8 || ld_k % 8 || ld_v % 8 || !a16(q) || !a16(k) ||
+        !a16(v) || !a16(w) || !a16(b) || !a16(g) || !a16(conv_q) || !a16(conv_k) || !a16(conv_v))
+        return GDN2_ERR_INVALID;
+    if (gate && (ld_gate < static_cast<int64_t>(H) * V || (ld_gate % 4) != 0 ||
+                 (reinterpret_cast<uintptr_t>(gate) % 8) != 0 || (reinterpret_cast<uintptr_t>(o) % 8) != 0))
+        return GDN2_ERR_INVALID;
+    fill_chunk_args(a, q, k, v, g, b, w, o, initial_state, final_state, A_log, dt_bias,
+                    lower_bound, cu_seqlens, cu_seqlens_host, num_seqs, B, T, H, K, V, scale,
+                    flags, workspace, workspace_bytes);
+    a.stages = 3;
+    a.conv_w[0] = conv_q;
+    a.conv_w[1] = conv_k;
+    a.conv_w[2] = conv_v;
+    a.ldq = ld_q;
+    a.ldk = ld_k;
+    a.ldv = ld_v;
+    a.conv_silu = conv_silu;
+    if (gate) {
+        a.z = gate;
+        a.ldz = ld_gate;
+        a.nw = norm_weight;
+        a.eps = eps;
+    }
+    return launch_chunk_fwd(a, io_dtype, g_dtype, static_cast<hipStream_t>(stream));
+}
+
 int gdn2_chunk_fwd_prep(const void *q, const void *k, const void *g, const void *b,
                         int io_dtype, int g_dtype, const float *A_log, const float *dt_bias,
                         float lower_bound, const int64_t *cu_seqlens,

@@ -50,6 +50,14 @@ struct ChunkParams {
     int64_t ldz;
     const void *nw;
     float eps;
+    // Short convolutions in the kernels (inference, conv_w[0] != null): q, k
+    // and v are the raw projections (token row strides ldq, ldk, ldv; head h
+    // at column h * K or h * V), conv_w[i] the [H * K or H * V][4] taps of
+    // q, k, v in the input dtype, conv_silu the SiLU after each; rows before
+    // a sequence's first token read as zero.
+    const void *conv_w[3];
+    int64_t ldq, ldk, ldv;
+    int conv_silu;
 };
 
 // Per (chunk, head) blob, in storage elements.

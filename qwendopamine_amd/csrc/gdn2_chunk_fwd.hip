@@ -209,11 +209,92 @@ struct RowLoad {
     }
 };
 
+// Rows first..first+15 as RowLoad, plus the three rows before them (one more
+// load instruction, rows first-RPI..first-1 of which the last three are
+// used): the window of the causal width-4 convolution.  Rows before lo (the
+// sequence start, relative to the chunk) or at / beyond lc read as zero.
+template <typename T, int KP>
+struct RowLoadConv : RowLoad<T, KP> {
+    using Base = RowLoad<T, KP>;
+    using Base::LPR;
+    using Base::NI;
+    using Base::RPI;
+    using Base::RS;
+    u32x4 hv;
+    bool hok;
+    __device__ __forceinline__ void issue(const T *base, int64_t chunk0, int64_t stride, int first, int lo, int lc,
+                                          int l)
+    {
+        const int hr = first - RPI + l / LPR;
+        hok = hr >= first - 3 && hr >= lo && hr < lc;
+        const int rc = hok ? hr : 0;
+        hv = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const char *>(base + chunk0 + rc * stride) +
+                                              16 * (l % LPR));
+        Base::issue(base, chunk0, stride, first, lc, l);
+    }
+    // Staged as rows first-4..first+15 (LDS rows 0..19); lane (m, kg) then
+    // convolves rows m-3..m of channels 16kt + 4kg + i with the taps at
+    // `taps` ([KP][4] 16-bit values, this wave's LDS copy):
+    //   y = round(sum_j tap[c][j] * x[t-3+j]),  silu: y = round(y * rcp(1 + e^-y))
+    // -- the order and roundings of the separate convolution pass.  Rows
+    // m >= nvalid are zero.
+    __device__ __forceinline__ void land(unsigned char *stg, int l, int m, int kg, int nvalid,
+                                         const unsigned char *taps, bool silu, Raw4<T> (&out)[KP / 16])
+    {
+        static_assert(sizeof(T) == 2, "the fused convolution takes 16-bit inputs");
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int rr = j * RPI + l / LPR;
+            *reinterpret_cast<u32x4 *>(stg + (4 + rr) * RS + 16 * (l % LPR)) =
+                rr < nvalid ? Base::v[j] : u32x4{0, 0, 0, 0};
+        }
+        const int hs = l / LPR - (RPI - 4);
+        if (hs >= 0) *reinterpret_cast<u32x4 *>(stg + hs * RS + 16 * (l % LPR)) = hok ? hv : u32x4{0, 0, 0, 0};
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        auto h2f = [](uint32_t bits) __attribute__((always_inline)) {
+            if constexpr (std::is_same<T, bf16_t>::value)
+                return __uint_as_float(bits << 16);
+            else
+                return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+        };
+#pragma unroll
+        for (int kt = 0; kt < KP / 16; ++kt) {
+            const int c0 = 16 * kt + 4 * kg;
+            float x[4][4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                load4<T>(reinterpret_cast<const T *>(stg + (m + 1 + jj) * RS), 0, c0, KP, true, 1, x[jj]);
+            const u32x4 ta = *reinterpret_cast<const u32x4 *>(taps + 8 * c0);
+            const u32x4 tb = *reinterpret_cast<const u32x4 *>(taps + 8 * c0 + 16);
+            const uint32_t tw[8] = {ta[0], ta[1], ta[2], ta[3], tb[0], tb[1], tb[2], tb[3]};
+            float y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int e = 4 * i + jj;
+                    acc = fmaf(h2f(tw[e >> 1] >> (16 * (e & 1)) & 0xffffu), x[jj][i], acc);
+                }
+                float yi = round_to<T>(acc + 0.0f);
+                if (silu) yi = round_to<T>(silu_f32(yi));
+                y[i] = m < nvalid ? yi : 0.0f;
+            }
+            out[kt].set(y);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    }
+};
+
 // One prep work item: chunk gc (global index over all sequences) of head h;
 // item = gc * H + h, so neighbouring items read neighbouring rows of the
 // [tokens, H, K] inputs and write neighbouring blobs.
 struct PrepItem {
     int gc, h, lc;   // lc = tokens in the chunk (<= kChunk)
+    int jc;          // chunk index within its sequence
+    int64_t t0;      // first token of the chunk
     int64_t chunk0;  // element offset of (token t0, head h, channel 0)
 };
 
@@ -228,6 +309,8 @@ __device__ __forceinline__ PrepItem prep_item(const ChunkParams &p, int item)
     const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
     const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
     it.lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
+    it.jc = jc;
+    it.t0 = t0;
     it.chunk0 = (t0 * p.H + it.h) * static_cast<int64_t>(p.K);
     return it;
 }
@@ -243,11 +326,12 @@ __device__ __forceinline__ PrepItem prep_item(const ChunkParams &p, int item)
 // most 168 registers (q, k, b stay in their 16-bit input form until the
 // factors).  fp32 storage at KP = 128 fits one workgroup per CU.
 // ---------------------------------------------------------------------------
-template <PrecKind PK, int KP, typename TI, typename TG>
+template <PrecKind PK, int KP, typename TI, typename TG, bool CONV = false>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu((PK == PrecKind::F32 && KP == 128) || KP > 128 ? 1 : 3))) void
 chunk_prep_kernel(ChunkParams p, int items)
 {
+    static_assert(!CONV || (sizeof(TI) == 2 && KP <= 128), "the fused convolution takes 16-bit rows, d_k <= 128");
     using P = Prec<PK>;
     using st = typename P::st;
     using BL = Blob<PK, KP>;
@@ -308,7 +392,39 @@ chunk_prep_kernel(ChunkParams p, int items)
 
         Raw4<TI> qr[NKT], kr[NKT], br[NKT];
         float gv[NKT][4];
-        if (rows_whole) {
+        if constexpr (CONV) {
+            // q and k are the raw projections (K == KP): each wave stages its
+            // copy of the head's taps in sEt (unused until the factors) and
+            // convolves its rows while landing them.  The taps are requested
+            // first, so the wait for them does not cover the rows.
+            constexpr int TBY = KP * 8;  // bytes of one tensor's taps [KP][4]
+            static_assert(8 * TBY <= static_cast<int>(sizeof(sEt)), "four waves' taps must fit in sEt");
+            static_assert(20 * RowLoad<TI, KP>::RS <= 16 * (KP * 4 + 16), "20 staged rows must fit the scratch");
+            unsigned char *tq = reinterpret_cast<unsigned char *>(sEt) + R * (2 * TBY);
+            unsigned char *tk = tq + TBY;
+            const bool tl = 16 * l < TBY;
+            const int64_t toff = static_cast<int64_t>(h) * TBY + 16 * (tl ? l : 0);
+            const u32x4 wq4 = *reinterpret_cast<const u32x4 *>(static_cast<const unsigned char *>(p.conv_w[0]) + toff);
+            const u32x4 wk4 = *reinterpret_cast<const u32x4 *>(static_cast<const unsigned char *>(p.conv_w[1]) + toff);
+            RowLoadConv<TI, KP> lq, lk;
+            RowLoad<TI, KP> lb;
+            RowLoad<TG, KP> lg;
+            const int lo = -kChunk * it.jc;
+            lq.issue(q, it.t0 * p.ldq + static_cast<int64_t>(h) * KP, p.ldq, 16 * R, lo, lc, l);
+            lk.issue(k, it.t0 * p.ldk + static_cast<int64_t>(h) * KP, p.ldk, 16 * R, lo, lc, l);
+            lb.issue(b, it.chunk0, stride, 16 * R, lc, l);
+            lg.issue(g, it.chunk0, stride, 16 * R, lc, l);
+            if (tl) {
+                *reinterpret_cast<u32x4 *>(tq + 16 * l) = wq4;
+                *reinterpret_cast<u32x4 *>(tk + 16 * l) = wk4;
+            }
+            const int nvalid = lc - 16 * R;
+            const bool silu = p.conv_silu != 0;
+            lq.land(stg, l, m, kg, nvalid, tq, silu, qr);
+            lk.land(stg, l, m, kg, nvalid, tk, silu, kr);
+            lb.land_raw(stg, l, m, kg, nvalid, br);
+            lg.land(stg, l, m, kg, nvalid, gv);
+        } else if (rows_whole) {
             RowLoad<TI, KP> lq, lk, lb;
             RowLoad<TG, KP> lg;
             lq.issue(q, it.chunk0, stride, 16 * R, lc, l);
@@ -682,9 +798,11 @@ chunk_prep_kernel(ChunkParams p, int items)
 // ---------------------------------------------------------------------------
 // Scan: one workgroup per (sequence, head, value slice of BV columns).
 // ---------------------------------------------------------------------------
-template <PrecKind PK, int KP, int BV, typename TI, bool TRAIN, bool SIGW = false, bool NORM = false>
+template <PrecKind PK, int KP, int BV, typename TI, bool TRAIN, bool SIGW = false, bool NORM = false,
+          bool CONV = false>
 __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB, int NP)
 {
+    static_assert(!CONV || (!TRAIN && sizeof(TI) == 2), "the fused convolution is a 16-bit inference prologue");
     using P = Prec<PK>;
     using st = typename P::st;
     using BL = Blob<PK, KP>;
@@ -780,8 +898,13 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     constexpr int NZT = (ZT + 255) / 256;
     // Whole 16-byte row pieces for every row of this slice (uniform per workgroup).
     const bool zfast = (V % EPV) == 0 && v0 + BV <= V;
+    // CONV: lane ctid takes row piece ctid % PPR of NZT consecutive tokens
+    // (plus the three rows before them, the convolution window) instead of
+    // tokens 256a / PPR apart, so the window rows are shared by its tokens.
+    constexpr int PPR = BV / EPV;        // row pieces per token
+    constexpr int NH = CONV ? 3 : 0;     // window rows before a lane's first token
     struct ZRaw {
-        u32x4 v[NZT], w[NZT];
+        u32x4 v[NZT + NH], w[NZT];
     };
     auto chunk_rows = [&](int jc, int64_t &t0, int &lc) __attribute__((always_inline)) {
         t0 = bos + static_cast<int64_t>(jc) * kChunk;
@@ -796,11 +919,46 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     struct RawRow {
         Raw e[EPV];
     };
+    // CONV taps of the slice's columns, [column][4] 16-bit values, in LDS:
+    // each copy lane stores the taps of its own EPV columns (lanes sharing
+    // columns store the same values) and reads back only those, so no
+    // barrier is needed.
+    const int cz = EPV * (ctid % PPR), tz0 = NZT * (ctid / PPR);
+    const bool zlane = copier && tz0 < kChunk;
+    __shared__ __align__(16) TI sZT[CONV ? BV * 4 : 8];
+    if constexpr (CONV) {
+        if (copier) {
+            const u32x4 *tp = reinterpret_cast<const u32x4 *>(static_cast<const TI *>(p.conv_w[2]) +
+                                                              (static_cast<int64_t>(h) * V + v0 + cz) * 4);
+            u32x4 t4[EPV / 2];
+#pragma unroll
+            for (int i = 0; i < EPV / 2; ++i) t4[i] = tp[i];
+#pragma unroll
+            for (int i = 0; i < EPV / 2; ++i) reinterpret_cast<u32x4 *>(sZT + 4 * cz)[i] = t4[i];
+        }
+    }
     auto issue_z = [&](auto fastc, ZRaw &r, int jc) __attribute__((always_inline)) {
         int64_t t0;
         int lc;
         chunk_rows(jc, t0, lc);
-        if constexpr (decltype(fastc)::value) {
+        if constexpr (CONV) {
+            // Raw v rows (token row stride ldv); window rows before the
+            // sequence start and rows of dead lanes load the chunk's first
+            // row and are zeroed when landed.
+            const int64_t colv = static_cast<int64_t>(h) * V + v0 + cz;
+#pragma unroll
+            for (int j = 0; j < NZT + NH; ++j) {
+                const int tok = tz0 - NH + j;
+                const bool ok = zlane && tok < lc && kChunk * jc + tok >= 0;
+                r.v[j] = *reinterpret_cast<const u32x4 *>(vp + (t0 + (ok ? tok : 0)) * p.ldv + colv);
+            }
+#pragma unroll
+            for (int a = 0; a < NZT; ++a) {
+                const int tok = tz0 + a;
+                const bool live = zlane && tok < lc;
+                r.w[a] = *reinterpret_cast<const u32x4 *>(wp + ((t0 + (live ? tok : 0)) * H + h) * V + v0 + cz);
+            }
+        } else if constexpr (decltype(fastc)::value) {
             // Dead lanes load the chunk's first row piece (always valid) and
             // are zeroed when landed: a select on the loaded value here would
             // make the request wait for its own data.
@@ -839,6 +997,44 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         chunk_rows(jc, t0, lc);
         st *dst = sZ[buf];
         static_assert(EPV * sizeof(st) == 16, "one z row piece is one 16-byte LDS store");
+        if constexpr (CONV) {
+            // v = act(round(sum_j tap[c][j] * v_raw[t-3+j])) in the separate
+            // convolution pass's order and roundings, then z = v * w as below.
+            if (!zlane) return;
+            bool hok[NH];
+#pragma unroll
+            for (int j = 0; j < NH; ++j) hok[j] = kChunk * jc + tz0 - NH + j >= 0;
+            const bool silu = p.conv_silu != 0;
+            st zr[NZT][EPV];
+            // Channel by channel, so that only one column's window is unpacked
+            // at a time.
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const uint2 t2 = reinterpret_cast<const uint2 *>(sZT + 4 * cz)[e];
+                const TI *tw = reinterpret_cast<const TI *>(&t2);
+                float x[NZT + NH];
+#pragma unroll
+                for (int j = 0; j < NZT + NH; ++j) {
+                    const float xv = io<TI>::ld(reinterpret_cast<const TI *>(&r.v[j]), e);
+                    x[j] = (j >= NH || hok[j < NH ? j : 0]) ? xv : 0.f;
+                }
+#pragma unroll
+                for (int a = 0; a < NZT; ++a) {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) acc = fmaf(io<TI>::ld(tw, jj), x[a + jj], acc);
+                    float vc = round_to<TI>(acc + 0.0f);
+                    if (silu) vc = round_to<TI>(silu_f32(vc));
+                    const TI *rw = reinterpret_cast<const TI *>(&r.w[a]);
+                    const float wv_ = SIGW ? round_to<TI>(sigmoid_f(io<TI>::ld(rw, e))) : io<TI>::ld(rw, e);
+                    zr[a][e] = P::from_f32(tz0 + a < lc ? vc * wv_ : 0.f);
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < NZT; ++a)
+                *reinterpret_cast<u32x4 *>(dst + (tz0 + a) * LDZ + cz) = __builtin_bit_cast(u32x4, zr[a]);
+            return;
+        }
 #pragma unroll
         for (int a = 0; a < NZT; ++a) {
             const int task = ctid + 256 * a;
@@ -936,13 +1132,17 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 //    one step of latency per request, which measured faster for
                 //    64-column slices without emission (0.241 vs 0.251 ms at
                 //    config 1).
-                constexpr bool DEEP = TRAIN || BV < 64;
+                //  * CONV (the v rows' convolution window takes more registers):
+                //    one step, with a single z register set, refilled with
+                //    chunk jc+2 right after chunk jc+1 lands from it.
+                constexpr bool DEEP = !CONV && (TRAIN || BV < 64);
                 // Requests are issued unconditionally, past the last chunk for
                 // the last chunk again (data unused): with a request skipped on
                 // some paths the compiler cannot count the loads issued after
                 // the ones being landed and waits for all of them, which makes
                 // the prefetch synchronous.
                 auto cl = [&](int j) __attribute__((always_inline)) { return j < nch ? j : nch - 1; };
+                ZRaw &zC = CONV ? zA : zB;  // the set holding chunk jc+2 at the second half
                 if (nch > 0) {
                     issue(pA, gc0 + cl(1));
                     issue_z(fastc, zA, cl(1));
@@ -955,12 +1155,11 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 for (int jc = 0; jc < nch; jc += 2) {
                     if (!DEEP) {
                         issue(pB, gc0 + cl(jc + 2));
-                        issue_z(fastc, zB, cl(jc + 2));
+                        if (!CONV) issue_z(fastc, zB, cl(jc + 2));
                     }
-                    if (jc + 1 < nch) {
-                        land_z(zA, jc + 1, 1);
-                        land(pA, 1);
-                    }
+                    if (jc + 1 < nch) land_z(zA, jc + 1, 1);
+                    if (CONV) issue_z(fastc, zA, cl(jc + 2));
+                    if (jc + 1 < nch) land(pA, 1);
                     if (DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
                         issue_z(fastc, zA, cl(jc + 3));
@@ -969,12 +1168,11 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     if (jc + 1 >= nch) break;
                     if (!DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
-                        issue_z(fastc, zA, cl(jc + 3));
+                        if (!CONV) issue_z(fastc, zA, cl(jc + 3));
                     }
-                    if (jc + 2 < nch) {
-                        land_z(zB, jc + 2, 0);
-                        land(pB, 0);
-                    }
+                    if (jc + 2 < nch) land_z(zC, jc + 2, 0);
+                    if (CONV) issue_z(fastc, zA, cl(jc + 3));
+                    if (jc + 2 < nch) land(pB, 0);
                     if (DEEP) {
                         issue(pB, gc0 + cl(jc + 4));
                         issue_z(fastc, zB, cl(jc + 4));
@@ -994,7 +1192,9 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 }
             }
         };
-        if (zfast)
+        if constexpr (CONV)
+            copy_loop(std::true_type{});  // whole 16-byte row pieces (checked by the host)
+        else if (zfast)
             copy_loop(std::true_type{});
         else
             copy_loop(std::false_type{});
@@ -1279,14 +1479,14 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     }
 }
 
-template <PrecKind PK, int KP, typename TI, typename TG>
+template <PrecKind PK, int KP, typename TI, typename TG, bool CONV = false>
 hipError_t launch_prep(const ChunkParams &p, int total_chunks, hipStream_t stream)
 {
     if (total_chunks == 0) return hipSuccess;
-    const auto kern = chunk_prep_kernel<PK, KP, TI, TG>;
+    const auto kern = chunk_prep_kernel<PK, KP, TI, TG, CONV>;
     // One resident wave of workgroups (occupancy x CUs of the current device,
     // looked up once per device), each walking items with a stride of the grid.
-    static int resident[64] = {};
+    static int resident[64] = {};  // per instantiation
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -1315,7 +1515,25 @@ hipError_t launch_scan(const ChunkParams &p, int BVsel, hipStream_t stream)
     auto go = [&](auto bvtag) {
         constexpr int BV = decltype(bvtag)::value;
         const int NVB = (p.V + BV - 1) / BV;
-        if (p.z) {
+        if (p.conv_w[0]) {
+            // Fused short convolutions (16-bit inference; the caller checked
+            // the shapes), with or without the gated output norm.
+            if constexpr (std::is_same<TI, bf16_t>::value && PK == PrecKind::BF16 && KP <= 128) {
+                auto conv = [&](auto sigw, auto norm) {
+                    hipLaunchKernelGGL((chunk_scan_kernel<PK, KP, BV, TI, false, decltype(sigw)::value,
+                                                          decltype(norm)::value, true>),
+                                       dim3(groups * 8 * NVB), dim3(512), 0, stream, p, NVB, NP);
+                };
+                const bool sigw = (p.flags & GDN2_FLAG_SIGMOID_BW) != 0;
+                if (p.z) {
+                    if (sigw) conv(std::true_type{}, std::true_type{});
+                    else conv(std::false_type{}, std::true_type{});
+                } else {
+                    if (sigw) conv(std::true_type{}, std::false_type{});
+                    else conv(std::false_type{}, std::false_type{});
+                }
+            }
+        } else if (p.z) {
             // Gated output norm (bf16 inference; the caller checked BV == V).
             if constexpr (std::is_same<TI, bf16_t>::value && PK == PrecKind::BF16) {
                 if (p.flags & GDN2_FLAG_SIGMOID_BW)
@@ -1345,7 +1563,11 @@ template <PrecKind PK, int KP, typename TI, typename TG>
 hipError_t launch_all(const ChunkParams &p, int total_chunks, int stages, hipStream_t stream)
 {
     if (stages & 1) {
-        const hipError_t e = launch_prep<PK, KP, TI, TG>(p, total_chunks, stream);
+        hipError_t e = hipErrorInvalidValue;
+        if (!p.conv_w[0])
+            e = launch_prep<PK, KP, TI, TG>(p, total_chunks, stream);
+        else if constexpr (std::is_same<TI, bf16_t>::value && PK == PrecKind::BF16 && KP <= 128)
+            e = launch_prep<PK, KP, TI, TG, true>(p, total_chunks, stream);
         if (e != hipSuccess) return e;
     }
     if (!(stages & 2) || p.num_seqs == 0) return hipSuccess;
@@ -1383,6 +1605,15 @@ int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream
     if (a.z && (io_dtype != GDN2_DTYPE_BF16 || a.V != bv_for(a.V) || (a.V % 16) != 0 ||
                 (a.flags & GDN2_FLAG_SAVE_FOR_BWD)))
         return GDN2_ERR_UNSUPPORTED;
+    if (a.conv_w[0]) {
+        // Fused convolutions: bf16 rows, K a whole key width (32, 64, 128), V
+        // split into whole 16-byte row pieces of whole value slices, forward
+        // only.
+        const int bv = a.z ? bv_for(a.V) : scan_bv(a.num_seqs * a.H, a.V);
+        if (io_dtype != GDN2_DTYPE_BF16 || (a.flags & GDN2_FLAG_SAVE_FOR_BWD) || kp_for(a.K) != a.K ||
+            a.K > 128 || a.V % bv != 0 || !a.conv_w[1] || !a.conv_w[2])
+            return GDN2_ERR_UNSUPPORTED;
+    }
     if (g_dtype != GDN2_DTYPE_F32 && g_dtype != io_dtype) return GDN2_ERR_UNSUPPORTED;
     const int64_t nc = count_chunks(a.B, a.T, a.cu_host, a.num_seqs);
     if (nc * a.H > 2147483647LL / 2) return GDN2_ERR_UNSUPPORTED;
@@ -1414,6 +1645,11 @@ int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream
     p.ldz = a.ldz;
     p.nw = a.nw;
     p.eps = a.eps;
+    for (int i = 0; i < 3; ++i) p.conv_w[i] = a.conv_w[i];
+    p.ldq = a.ldq;
+    p.ldk = a.ldk;
+    p.ldv = a.ldv;
+    p.conv_silu = a.conv_silu;
     if (train) {
         unsigned char *base = static_cast<unsigned char *>(a.workspace);
         p.hs = base + tl.hs;

@@ -88,6 +88,11 @@ struct ChunkFwdArgs {
     int64_t ldz = 0;
     const void *nw = nullptr;
     float eps = 0.f;
+    // Short convolutions of q, k, v fused into the kernels (null taps: none);
+    // q, k, v are then the raw projections with these token row strides.
+    const void *conv_w[3] = {nullptr, nullptr, nullptr};
+    int64_t ldq = 0, ldk = 0, ldv = 0;
+    int conv_silu = 0;
 };
 
 size_t chunk_fwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype,

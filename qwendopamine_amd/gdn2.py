@@ -277,6 +277,10 @@ class GatedDeltaNet2(nn.Module):
         # sequence-heads the scan splits value rows over more workgroups and the
         # norm pass is faster.
         self.fused_norm = True
+        # Chunked inference prefill convolves q, k and v inside the chunk
+        # kernels (bf16, width-4 convolutions without bias, whole key widths of
+        # 32 / 64 / 128, no packed sequences); False runs the convolution pass.
+        self.fused_conv = True
 
         self.head_k_dim = self.head_dim
         self.head_v_dim = int(self.head_dim * self.expand_v)
@@ -547,6 +551,7 @@ class GatedDeltaNet2(nn.Module):
             return self._decode_fused(x, past_key_values, recurrent_state, (cq, ck, cv), want_state,
                                       in_place, use_cache)
         g0 = None
+        conv_raw = None  # raw q, k, v rows when the chunk kernels convolve them
         if fuse and self.use_short_conv and _inference(x, *(c.conv1d.weight for c in convs)):
             # The seven first-stage input projections as one GEMM; q, k and v
             # are convolved in place as column ranges of its output.
@@ -554,13 +559,30 @@ class GatedDeltaNet2(nn.Module):
             y = F.linear(x.reshape(-1, x.shape[-1]), W_in)  # [tokens, sum(sizes)]
             qr, kr, vr, b, w, f0, g0 = (t.view(*x.shape[:-1], -1) if i < 5 else t
                                         for i, t in enumerate(y.split(sizes, dim=-1)))
-            conv_in = None if cq is None else [cq, ck, cv]
-            conv_out = conv_in if in_place and conv_in is not None and all(
-                c.dtype == qr.dtype and c.is_contiguous() for c in conv_in) else None
-            (q, k, v), new = ops.short_convolution(
-                [qr, kr, vr], [c.conv1d.weight for c in convs], [c.conv1d.bias for c in convs],
-                conv_in, want_state, self.q_conv1d.activation, out_caches=conv_out)
-            cq, ck, cv = new if new is not None else (None, None, None)
+            backend0 = resolve_gdn2_backend(self.backend, training=self.training, seq_len=seq_len)
+            if (self.fused_conv and x.dtype == torch.bfloat16 and cu_seqlens is None and seq_len >= 4
+                    and self._algorithm(mode, backend0, False) == "chunk"
+                    and self.num_v_heads == self.num_heads and self.head_k_dim in (32, 64, 128)
+                    and self.head_v_dim % 16 == 0 and self.conv_size == 4
+                    and all(c.conv1d.bias is None and c.activation == self.q_conv1d.activation
+                            and c.conv1d.weight.dtype == x.dtype for c in convs)
+                    and self.q_conv1d.activation in (None, "silu")):
+                # Prefill: the chunk kernels convolve the raw rows (below); the
+                # new conv caches are the last three raw rows.
+                conv_raw = (qr, kr, vr)
+                q, k, v = qr, kr, vr
+                if want_state:
+                    cq, ck, cv = (t[:, -3:, :].transpose(1, 2).contiguous() for t in conv_raw)
+                else:
+                    cq = ck = cv = None
+            else:
+                conv_in = None if cq is None else [cq, ck, cv]
+                conv_out = conv_in if in_place and conv_in is not None and all(
+                    c.dtype == qr.dtype and c.is_contiguous() for c in conv_in) else None
+                (q, k, v), new = ops.short_convolution(
+                    [qr, kr, vr], [c.conv1d.weight for c in convs], [c.conv1d.bias for c in convs],
+                    conv_in, want_state, self.q_conv1d.activation, out_caches=conv_out)
+                cq, ck, cv = new if new is not None else (None, None, None)
             # The low-rank second stages read their 2-D column ranges in place.
             g = self.f_proj[1](f0).view(*x.shape[:-1], -1)
         elif self.use_short_conv and _inference(x, *(c.conv1d.weight for c in convs)):
@@ -613,10 +635,25 @@ class GatedDeltaNet2(nn.Module):
         b, w, v, k = b.to(dt), w.to(dt), v.to(dt), k.to(dt)
         normed = None
         n_seq = batch if cu_seqlens is None else cu_seqlens.numel() - 1
-        if (algo == "chunk" and fuse and self.fused_norm and dt == torch.bfloat16
-                and self.head_v_dim in (16, 32, 64) and self.o_norm.weight.dtype == dt
-                and (n_seq * self.num_v_heads >= 256 or self.head_v_dim == 16)
-                and _inference(self.o_norm.weight, *(p for p in self.g_proj.parameters()))):
+        norm_in_scan = (algo == "chunk" and fuse and self.fused_norm and dt == torch.bfloat16
+                        and self.head_v_dim in (16, 32, 64) and self.o_norm.weight.dtype == dt
+                        and (n_seq * self.num_v_heads >= 256 or self.head_v_dim == 16)
+                        and _inference(self.o_norm.weight, *(p for p in self.g_proj.parameters())))
+        if conv_raw is not None:
+            # Convolutions in the chunk kernels (and the gated output norm in
+            # the scan where it applies); bit-identical to the separate passes.
+            gate = None
+            if norm_in_scan:
+                gate = self.g_proj(x) if g0 is None else self.g_proj[1](g0).view(*x.shape[:-1], -1)
+            o, recurrent_state = ops.chunk_gdn2_conv(
+                *conv_raw, [c.conv1d.weight for c in convs], g, b, w, num_heads=self.num_heads,
+                activation=self.q_conv1d.activation, gate=gate,
+                norm_weight=self.o_norm.weight if norm_in_scan else None, eps=self.o_norm.eps,
+                initial_state=h0, output_final_state=want_state, use_qk_l2norm_in_kernel=True, **gate_kw,
+            )
+            if norm_in_scan:
+                normed = o
+        elif norm_in_scan:
             # The gated output norm in the scan's output stage (bit-identical to
             # the separate pass).
             gate = self.g_proj(x) if g0 is None else self.g_proj[1](g0).view(*x.shape[:-1], -1)

@@ -860,6 +860,144 @@ def chunk_gdn2_gated_norm(
     return o, ht
 
 
+def _raw_rows(name: str, nm: str, x: torch.Tensor, B: int, T: int, width: int, dt: torch.dtype) -> int:
+    """Token row stride of a ``[B, T, width]`` (or ``[B, T, H, D]``) tensor read in place: unit
+    channel stride, one row stride, 16-byte aligned rows."""
+    if x.dim() == 4:
+        if x.stride(-1) != 1 or x.stride(-2) != x.shape[-1]:
+            raise ValueError(f"{name}: {nm} heads must be contiguous within a token row")
+        x = x.flatten(-2)
+    if (x.dim() != 3 or x.dtype != dt or tuple(x.shape) != (B, T, width) or x.stride(-1) != 1
+            or (B > 1 and x.stride(0) != T * x.stride(1))):
+        raise ValueError(f"{name}: {nm} must be [B, T, {width}] {dt} token rows with unit channel stride; "
+                         f"got {tuple(x.shape)} {x.dtype} strides {x.stride()}")
+    ld = x.stride(1) if T > 1 else max(x.stride(1), width)
+    if ld % 8 or x.data_ptr() % 16:
+        raise ValueError(f"{name}: {nm} rows must start on 16-byte boundaries (row stride {ld})")
+    return ld
+
+
+@torch.compiler.disable
+def chunk_gdn2_conv(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    conv_weights: list[torch.Tensor],
+    g: torch.Tensor,
+    b: torch.Tensor,
+    w: torch.Tensor,
+    *,
+    num_heads: int,
+    activation: str | None = "silu",
+    gate: torch.Tensor | None = None,
+    norm_weight: torch.Tensor | None = None,
+    eps: float = 1e-5,
+    scale: float | None = None,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    lower_bound: float | None = None,
+    cu_seqlens: torch.LongTensor | None = None,
+    bw_logits: bool = False,
+):
+    """``chunk_gdn2`` on the raw q / k / v projections, with the module's short convolutions
+    (reference ``ShortConvolution``, ``gdn2.py:395-430``: causal depthwise conv1d of width 4, no
+    bias, then ``activation``) applied inside the chunk kernels.
+
+    * ``q``, ``k``: ``[B, T, H * K]`` raw projections, ``v``: ``[B, T, H * V]``; the token rows may
+      be column ranges of a wider tensor (one row stride, unit channel stride, 16-byte aligned).
+    * ``conv_weights``: the three Conv1d weights ``[D, 1, 4]`` of q, k, v.
+    * ``g``, ``b``, ``w``: as for :func:`chunk_gdn2` (``[B, T, H, K]`` / ``[B, T, H, V]``).
+    * ``gate`` / ``norm_weight``: optional; applies the gated output norm as
+      :func:`chunk_gdn2_gated_norm` does.
+
+    Rows before a sequence's first token are zero (the prefill padding of the reference, per
+    ``cu_seqlens`` sequence). Each convolution output is rounded to the input dtype before and
+    after the SiLU, as in :func:`short_convolution`, so without ``cu_seqlens`` the result equals
+    ``short_convolution`` followed by ``chunk_gdn2`` (or ``chunk_gdn2_gated_norm``) bit for bit.
+    The new conv caches are the last three raw rows, which the caller slices itself.
+
+    Inference only; bfloat16 inputs, ``K`` in {32, 64, 128}, ``V`` a multiple of 16 (with a gate:
+    16, 32 or 64). Returns ``(o, final_state)`` with ``o`` ``[B, T, H, V]``.
+    """
+    name = "chunk_gdn2_conv"
+    _require_gpu(name, q, k, v, g, b, w, gate, norm_weight, initial_state)
+    if activation not in (None, "silu"):
+        raise NotImplementedError(f"{name}: activation {activation!r}; the kernels apply SiLU or nothing")
+    B, T = q.shape[0], q.shape[1]
+    H = int(num_heads)
+    if g.dim() != 4 or tuple(g.shape[:3]) != (B, T, H):
+        raise ValueError(f"{name}: g must be [B, T, {H}, K]; got {tuple(g.shape)}")
+    K = g.shape[-1]
+    if w.dim() != 4 or tuple(w.shape[:3]) != (B, T, H):
+        raise ValueError(f"{name}: w must be [B, T, {H}, V]; got {tuple(w.shape)}")
+    V = w.shape[-1]
+    if tuple(b.shape) != (B, T, H, K):
+        raise ValueError(f"{name}: b must be {(B, T, H, K)}; got {tuple(b.shape)}")
+    _check_packed(q, initial_state, cu_seqlens)
+    dt = q.dtype
+    if dt != torch.bfloat16 or K not in (32, 64, 128) or V % 16:
+        raise NotImplementedError(f"{name}: bfloat16 inputs with K in (32, 64, 128) and V a multiple of 16 "
+                                  f"(got {dt}, K={K}, V={V})")
+    if gate is not None and V not in (16, 32, 64):
+        raise NotImplementedError(f"{name}: the fused output norm needs V in (16, 32, 64), got {V}")
+    ldq = _raw_rows(name, "q", q, B, T, H * K, dt)
+    ldk = _raw_rows(name, "k", k, B, T, H * K, dt)
+    ldv = _raw_rows(name, "v", v, B, T, H * V, dt)
+    if len(conv_weights) != 3:
+        raise ValueError(f"{name}: conv_weights must hold the q, k and v weights")
+    taps = []
+    for nm, wt, d in zip("qkv", conv_weights, (H * K, H * K, H * V)):
+        if wt.numel() != d * 4:
+            raise NotImplementedError(f"{name}: {nm} convolution must be [{d}, 1, 4] (width 4); "
+                                      f"got {tuple(wt.shape)}")
+        taps.append(_io(wt.detach().reshape(d, 4), dt))
+    ld_gate, gt, wn = 0, None, None
+    if gate is not None:
+        if norm_weight is None or norm_weight.numel() != V or norm_weight.dtype != dt:
+            raise ValueError(f"{name}: norm_weight must hold {V} {dt} values")
+        gt = gate.reshape(B, T, H * V) if gate.dim() == 4 and gate.stride(-2) == V else gate
+        if (gt.dim() != 3 or gt.dtype != dt or tuple(gt.shape) != (B, T, H * V) or gt.stride(-1) != 1
+                or (B > 1 and gt.stride(0) != T * gt.stride(1))):
+            raise ValueError(f"{name}: gate must be [B, T, H * V] {dt} token rows with unit channel "
+                             f"stride; got {tuple(gate.shape)} {gate.dtype} strides {gate.stride()}")
+        ld_gate = gt.stride(1) if T > 1 else max(gt.stride(1), H * V)
+        wn = norm_weight.detach().contiguous()
+    if scale is None:
+        scale = K ** -0.5
+    b, w = (_io(x, dt) for x in (b, w))
+    g = _io(g, g.dtype if g.dtype in (torch.float32, dt) else torch.float32)
+    cu_dev, cu_host = _cu(cu_seqlens, q.device, T)
+    N = B if cu_seqlens is None else cu_host.numel() - 1
+    h0 = None if initial_state is None else initial_state.float().contiguous()
+    if h0 is not None and tuple(h0.shape) != (N, H, K, V):
+        raise ValueError(f"{name}: initial_state must be {(N, H, K, V)}, got {tuple(h0.shape)}")
+    ht = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) if output_final_state else None
+    o = torch.empty(B, T, H, V, dtype=dt, device=q.device)
+    lib = nat.load()
+    cu_host_p = None if cu_host is None else cu_host.data_ptr()
+    ws_bytes = lib.gdn2_chunk_fwd_workspace_size(B, T, H, K, V, nat.dtype_code(dt), cu_host_p, N)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    a_log, dtb = _gate_tensors(use_gate_in_kernel, A_log, dt_bias, H, K)
+    flags = _flags(use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound)
+    if bw_logits:
+        flags |= nat.FLAG_SIGMOID_BW
+    st = lib.gdn2_chunk_fwd_conv(
+        nat.ptr(q), ldq, nat.ptr(k), ldk, nat.ptr(v), ldv, nat.ptr(taps[0]), nat.ptr(taps[1]),
+        nat.ptr(taps[2]), 4, int(activation == "silu"), nat.ptr(g), nat.ptr(b), nat.ptr(w),
+        nat.dtype_code(dt), nat.dtype_code(g.dtype), nat.ptr(o), nat.ptr(gt), ld_gate, nat.ptr(wn),
+        float(eps), nat.ptr(h0), nat.ptr(ht), nat.ptr(a_log), nat.ptr(dtb),
+        float(lower_bound) if lower_bound is not None else 0.0,
+        nat.ptr(cu_dev), cu_host_p, N, B, T, H, K, V, float(scale), flags,
+        ws.data_ptr(), ws.numel(), nat.stream_handle(q.device),
+    )
+    nat.check(st, name)
+    return o, ht
+
+
 @torch.compiler.disable
 def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
     """``x * rsqrt(mean(x^2) + eps) * weight * silu(z)`` over the last axis.

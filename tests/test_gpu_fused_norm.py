@@ -9,8 +9,9 @@
 * **Oracle.** Against the float64 composition ``oracle.recurrent_fwd`` -> ``oracle.gated_rmsnorm``
   on the same bf16-rounded inputs, at the bf16 bar (rel. L2 <= 2e-2).
 * **Module.** ``GatedDeltaNet2`` bf16 prefill takes the fused norm exactly when a scan workgroup
-  owns whole value rows anyway (16-wide heads, or >= 256 sequence-heads); with ``fused_norm``
-  on and off, outputs and caches are then bit-identical.
+  owns whole value rows anyway (16-wide heads, or >= 256 sequence-heads), through
+  ``chunk_gdn2_gated_norm`` or, with the convolutions also in the kernels, ``chunk_gdn2_conv``;
+  with ``fused_norm`` on and off, outputs and caches are then bit-identical.
 """
 
 from __future__ import annotations
@@ -158,13 +159,19 @@ def test_module_prefill_fused_norm_equals_separate(gpu_device, monkeypatch, B, h
     print(f"[case] module prefill fused norm B={B} heads={heads} head_dim={head_dim} padded={padded}",
           flush=True)
     calls = []
-    real = ops.chunk_gdn2_gated_norm
+    real, real_conv = ops.chunk_gdn2_gated_norm, ops.chunk_gdn2_conv
 
     def counting(*a, **kw):
         calls.append(1)
         return real(*a, **kw)
 
+    def counting_conv(*a, **kw):  # the norm in the scan of the conv-fused prefill
+        if kw.get("gate") is not None:
+            calls.append(1)
+        return real_conv(*a, **kw)
+
     monkeypatch.setattr(ops, "chunk_gdn2_gated_norm", counting)
+    monkeypatch.setattr(ops, "chunk_gdn2_conv", counting_conv)
     torch.manual_seed(0)
     m = GatedDeltaNet2(hidden_size=256, num_heads=heads, head_dim=head_dim).to(gpu_device).to(torch.bfloat16).eval()
     x = torch.randn(B, 150, 256, device=gpu_device).to(torch.bfloat16)
