@@ -441,6 +441,23 @@ def bench_prologue(torch, dev, reps=20):
     def pre_fused():
         ops.chunk_gdn2_gated_norm(pq, pk, pv, pf, pb, pw, z, nw, 1e-5, output_final_state=True, **pkw)
 
+    # Prefill from the raw projections (q / k / v as column ranges of one projection output,
+    # as the module holds them): the convolution pass then the chunk op, against the chunk op
+    # that convolves q / k / v itself.  Both follow with the gated norm pass (B4 x 16 heads is
+    # below the sequence-head count where the module fuses the norm).
+    yr = torch.randn(B, T, 3 * D, generator=gen, device=dev).to(bf)
+    rq, rk, rv = yr[..., :D], yr[..., D:2 * D], yr[..., 2 * D:]
+
+    def pconv_separate():
+        (q, k, v), _ = ops.short_convolution([rq, rk, rv], ws, None, None, True)
+        op_, _ = ops.chunk_gdn2(q.view(B, T, H, Dh), k.view(B, T, H, Dh), v.view(B, T, H, Dh), pf, pb, pw,
+                                output_final_state=True, **pkw)
+        ops.gated_rmsnorm(op_, z, nw, 1e-5)
+
+    def pconv_fused():
+        op_, _ = ops.chunk_gdn2_conv(rq, rk, rv, ws, pf, pb, pw, num_heads=H, output_final_state=True, **pkw)
+        ops.gated_rmsnorm(op_, z, nw, 1e-5)
+
     # Training: forward + backward of the q / k / v convolutions and of the gated norm, on the
     # HIP kernels (autograd functions) against torch's autograd through the reference's ops.
     xg = [x.detach().clone().requires_grad_(True) for x in xs]
@@ -488,7 +505,8 @@ def bench_prologue(torch, dev, reps=20):
     t = {k: timed(f) for k, f in (("conv", conv_hip), ("conv_torch", conv_torch),
                                   ("norm", norm_hip), ("norm_torch", norm_torch),
                                   ("dec_fused", dec_fused), ("dec_separate", dec_separate),
-                                  ("pre_fused", pre_fused), ("pre_separate", pre_separate))}
+                                  ("pre_fused", pre_fused), ("pre_separate", pre_separate),
+                                  ("pconv_fused", pconv_fused), ("pconv_separate", pconv_separate))}
     return {
         "config": {"workload": "C3 module shape: B4 T2048, q/k/v 1024 channels, conv width 4; "
                                "norm over 16 heads x 64", "dtype": "bf16"},
@@ -511,6 +529,10 @@ def bench_prologue(torch, dev, reps=20):
                              "gated_rmsnorm_torch_us": round(train_t["norm_torch"], 1)},
         "prefill_norm": {"workload": f"B{B} T{T}, {H} heads x {Dh}: chunk op + gated norm",
                          "fused_us": round(t["pre_fused"], 2), "separate_hip_us": round(t["pre_separate"], 2)},
+        "prefill_conv": {"workload": f"B{B} T{T}, {H} heads x {Dh}: q/k/v convolutions + chunk op + gated norm, "
+                                     "from the raw projections",
+                         "fused_us": round(t["pconv_fused"], 2), "separate_hip_us": round(t["pconv_separate"], 2),
+                         "hbm_bytes_removed": conv_bytes},
     }
 
 

@@ -795,6 +795,13 @@ chunk_prep_kernel(ChunkParams p, int items)
     }
 }
 
+// Registers of the copy waves' value-row requests for one chunk: NV row
+// pieces of v (CONV: the convolution window first) and NW of w.
+template <typename Piece, int NV, int NW>
+struct ZRows {
+    Piece v[NV], w[NW];
+};
+
 // ---------------------------------------------------------------------------
 // Scan: one workgroup per (sequence, head, value slice of BV columns).
 // ---------------------------------------------------------------------------
@@ -898,14 +905,17 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     constexpr int NZT = (ZT + 255) / 256;
     // Whole 16-byte row pieces for every row of this slice (uniform per workgroup).
     const bool zfast = (V % EPV) == 0 && v0 + BV <= V;
-    // CONV: lane ctid takes row piece ctid % PPR of NZT consecutive tokens
+    // CONV: lane ctid takes row piece ctid % PPR of NZC consecutive tokens
     // (plus the three rows before them, the convolution window) instead of
     // tokens 256a / PPR apart, so the window rows are shared by its tokens.
-    constexpr int PPR = BV / EPV;        // row pieces per token
-    constexpr int NH = CONV ? 3 : 0;     // window rows before a lane's first token
-    struct ZRaw {
-        u32x4 v[NZT + NH], w[NZT];
-    };
+    // Slices narrower than 64 use 8-byte pieces (CW = 4 channels), so that
+    // all four copy waves share the convolution arithmetic.
+    constexpr int CW = BV >= 64 ? EPV : EPV / 2;  // channels per CONV piece
+    constexpr int PPR = BV / CW;                  // CONV pieces per token
+    constexpr int NZC = (kChunk * PPR + 255) / 256;
+    constexpr int NH = 3;                         // window rows before a lane's first token
+    using CPiece = std::conditional_t<CW == EPV, u32x4, uint2>;
+    using ZRaw = std::conditional_t<CONV, ZRows<CPiece, NZC + NH, NZC>, ZRows<u32x4, NZT, NZT>>;
     auto chunk_rows = [&](int jc, int64_t &t0, int &lc) __attribute__((always_inline)) {
         t0 = bos + static_cast<int64_t>(jc) * kChunk;
         const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
@@ -923,18 +933,18 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     // each copy lane stores the taps of its own EPV columns (lanes sharing
     // columns store the same values) and reads back only those, so no
     // barrier is needed.
-    const int cz = EPV * (ctid % PPR), tz0 = NZT * (ctid / PPR);
+    const int cz = CW * (ctid % PPR), tz0 = NZC * (ctid / PPR);
     const bool zlane = copier && tz0 < kChunk;
     __shared__ __align__(16) TI sZT[CONV ? BV * 4 : 8];
     if constexpr (CONV) {
         if (copier) {
             const u32x4 *tp = reinterpret_cast<const u32x4 *>(static_cast<const TI *>(p.conv_w[2]) +
                                                               (static_cast<int64_t>(h) * V + v0 + cz) * 4);
-            u32x4 t4[EPV / 2];
+            u32x4 t4[CW / 2];
 #pragma unroll
-            for (int i = 0; i < EPV / 2; ++i) t4[i] = tp[i];
+            for (int i = 0; i < CW / 2; ++i) t4[i] = tp[i];
 #pragma unroll
-            for (int i = 0; i < EPV / 2; ++i) reinterpret_cast<u32x4 *>(sZT + 4 * cz)[i] = t4[i];
+            for (int i = 0; i < CW / 2; ++i) reinterpret_cast<u32x4 *>(sZT + 4 * cz)[i] = t4[i];
         }
     }
     auto issue_z = [&](auto fastc, ZRaw &r, int jc) __attribute__((always_inline)) {
@@ -947,16 +957,16 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             // row and are zeroed when landed.
             const int64_t colv = static_cast<int64_t>(h) * V + v0 + cz;
 #pragma unroll
-            for (int j = 0; j < NZT + NH; ++j) {
+            for (int j = 0; j < NZC + NH; ++j) {
                 const int tok = tz0 - NH + j;
                 const bool ok = zlane && tok < lc && kChunk * jc + tok >= 0;
-                r.v[j] = *reinterpret_cast<const u32x4 *>(vp + (t0 + (ok ? tok : 0)) * p.ldv + colv);
+                r.v[j] = *reinterpret_cast<const CPiece *>(vp + (t0 + (ok ? tok : 0)) * p.ldv + colv);
             }
 #pragma unroll
-            for (int a = 0; a < NZT; ++a) {
+            for (int a = 0; a < NZC; ++a) {
                 const int tok = tz0 + a;
                 const bool live = zlane && tok < lc;
-                r.w[a] = *reinterpret_cast<const u32x4 *>(wp + ((t0 + (live ? tok : 0)) * H + h) * V + v0 + cz);
+                r.w[a] = *reinterpret_cast<const CPiece *>(wp + ((t0 + (live ? tok : 0)) * H + h) * V + v0 + cz);
             }
         } else if constexpr (decltype(fastc)::value) {
             // Dead lanes load the chunk's first row piece (always valid) and
@@ -1005,21 +1015,21 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
 #pragma unroll
             for (int j = 0; j < NH; ++j) hok[j] = kChunk * jc + tz0 - NH + j >= 0;
             const bool silu = p.conv_silu != 0;
-            st zr[NZT][EPV];
+            st zr[NZC][CW];
             // Channel by channel, so that only one column's window is unpacked
             // at a time.
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) {
+            for (int e = 0; e < CW; ++e) {
                 const uint2 t2 = reinterpret_cast<const uint2 *>(sZT + 4 * cz)[e];
                 const TI *tw = reinterpret_cast<const TI *>(&t2);
-                float x[NZT + NH];
+                float x[NZC + NH];
 #pragma unroll
-                for (int j = 0; j < NZT + NH; ++j) {
+                for (int j = 0; j < NZC + NH; ++j) {
                     const float xv = io<TI>::ld(reinterpret_cast<const TI *>(&r.v[j]), e);
                     x[j] = (j >= NH || hok[j < NH ? j : 0]) ? xv : 0.f;
                 }
 #pragma unroll
-                for (int a = 0; a < NZT; ++a) {
+                for (int a = 0; a < NZC; ++a) {
                     float acc = 0.f;
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj) acc = fmaf(io<TI>::ld(tw, jj), x[a + jj], acc);
@@ -1031,8 +1041,8 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 }
             }
 #pragma unroll
-            for (int a = 0; a < NZT; ++a)
-                *reinterpret_cast<u32x4 *>(dst + (tz0 + a) * LDZ + cz) = __builtin_bit_cast(u32x4, zr[a]);
+            for (int a = 0; a < NZC; ++a)
+                *reinterpret_cast<CPiece *>(dst + (tz0 + a) * LDZ + cz) = __builtin_bit_cast(CPiece, zr[a]);
             return;
         }
 #pragma unroll
@@ -1132,17 +1142,19 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 //    one step of latency per request, which measured faster for
                 //    64-column slices without emission (0.241 vs 0.251 ms at
                 //    config 1).
-                //  * CONV (the v rows' convolution window takes more registers):
-                //    one step, with a single z register set, refilled with
-                //    chunk jc+2 right after chunk jc+1 lands from it.
-                constexpr bool DEEP = !CONV && (TRAIN || BV < 64);
+                //  * CONV at KP = 128 (the v rows' convolution window takes more
+                //    registers than the copy waves have left there): one step,
+                //    with a single z register set, refilled with chunk jc+2 right
+                //    after chunk jc+1 lands from it.
+                constexpr bool ONEZ = CONV && KP > 64;
+                constexpr bool DEEP = !ONEZ && (TRAIN || BV < 64);
                 // Requests are issued unconditionally, past the last chunk for
                 // the last chunk again (data unused): with a request skipped on
                 // some paths the compiler cannot count the loads issued after
                 // the ones being landed and waits for all of them, which makes
                 // the prefetch synchronous.
                 auto cl = [&](int j) __attribute__((always_inline)) { return j < nch ? j : nch - 1; };
-                ZRaw &zC = CONV ? zA : zB;  // the set holding chunk jc+2 at the second half
+                ZRaw &zC = ONEZ ? zA : zB;  // the set holding chunk jc+2 at the second half
                 if (nch > 0) {
                     issue(pA, gc0 + cl(1));
                     issue_z(fastc, zA, cl(1));
@@ -1155,10 +1167,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 for (int jc = 0; jc < nch; jc += 2) {
                     if (!DEEP) {
                         issue(pB, gc0 + cl(jc + 2));
-                        if (!CONV) issue_z(fastc, zB, cl(jc + 2));
+                        if (!ONEZ) issue_z(fastc, zB, cl(jc + 2));
                     }
                     if (jc + 1 < nch) land_z(zA, jc + 1, 1);
-                    if (CONV) issue_z(fastc, zA, cl(jc + 2));
+                    if (ONEZ) issue_z(fastc, zA, cl(jc + 2));
                     if (jc + 1 < nch) land(pA, 1);
                     if (DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
@@ -1168,10 +1180,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     if (jc + 1 >= nch) break;
                     if (!DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
-                        if (!CONV) issue_z(fastc, zA, cl(jc + 3));
+                        if (!ONEZ) issue_z(fastc, zA, cl(jc + 3));
                     }
                     if (jc + 2 < nch) land_z(zC, jc + 2, 0);
-                    if (CONV) issue_z(fastc, zA, cl(jc + 3));
+                    if (ONEZ) issue_z(fastc, zA, cl(jc + 3));
                     if (jc + 2 < nch) land(pB, 0);
                     if (DEEP) {
                         issue(pB, gc0 + cl(jc + 4));
