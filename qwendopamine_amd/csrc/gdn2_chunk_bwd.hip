@@ -25,8 +25,9 @@
 //    (the backward contracts over the dimension the forward kept), so the
 //    compute waves issue the same K16 products as the forward scan.  Writes
 //    dh0 and, per chunk, dS1 and dY for the second kernel.
-//  * chunk_bwd_kside_kernel -- one workgroup (8 waves, two per 16-token block)
-//    per (chunk, head), all chunks in parallel: dv, dw from dY, the
+//  * chunk_bwd_kside_kernel -- a persistent grid of 8-wave workgroups (two
+//    waves per 16-token block), one (chunk, head) item at a time, all chunks
+//    in parallel: dv, dw from dY, the
 //    V-contractions above on MFMA over LDS-staged value slices, the in-chunk
 //    pair terms with the forward's factored decays (exact VALU sums on
 //    diagonal blocks whose decay span is too wide), the reverse cumsum, and
@@ -498,7 +499,8 @@ struct Raw4<float> {
 };
 
 // ---------------------------------------------------------------------------
-// K-side gradients: one workgroup of 8 waves per (chunk, head).  Wave
+// K-side gradients: a persistent grid of workgroups of 8 waves, each walking
+// (chunk, head) items blockIdx.x, blockIdx.x + gridDim.x, ...  Wave
 // w = 2R + hh owns token rows 16R..16R+15 (lane (m, kg): row 16R+m) and the
 // channel tiles hh*NKH .. hh*NKH+NKH-1 (channels 16dt + 4kg + i, "A-order",
 // as in the forward prep kernel).  Both waves of a token block compute the
@@ -506,7 +508,7 @@ struct Raw4<float> {
 // waits on another for them.
 // ---------------------------------------------------------------------------
 template <PrecKind PK, int KP, typename TI, typename TG>
-__global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
+__global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p, int items)
 {
     using P = Prec<PK>;
     using st = typename P::st;
@@ -544,10 +546,19 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     __shared__ float sRow[2][2][64];                // per-half row sums (norms, then L2 dots)
     __shared__ int sWide[4][2];
 
-    const int tid = threadIdx.x, wv = tid >> 6, R = wv >> 1, hh = wv & 1;
-    const int l = tid & 63, m = l & 15, kg = l >> 4;
-    const int gc = blockIdx.x, h = blockIdx.y;
+    const int tid0 = threadIdx.x, wv0 = __builtin_amdgcn_readfirstlane(tid0 >> 6);
     const int H = p.H, K = p.K, V = p.V, VP = p.VP;
+
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    // The thread and wave indices are made opaque per item so that the
+    // compiler does not hoist the many per-lane LDS and global addresses out of
+    // the item loop, where they would hold registers through every phase.
+    int tid = tid0, wv = wv0;
+    asm volatile("" : "+v"(tid));
+    asm volatile("" : "+s"(wv));
+    const int R = wv >> 1, hh = wv & 1;
+    const int l = tid & 63, m = l & 15, kg = l >> 4;
+    const int gc = item / H, h = item - (item / H) * H;
 
     int n, jc;
     int64_t bos, len;
@@ -1118,7 +1129,7 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
     __syncthreads();
     pq = sRow[0][0][r] + sRow[0][1][r];
     pk = sRow[1][0][r] + sRow[1][1][r];
-    if (!row_ok) return;
+    if (row_ok) {
 #pragma unroll
     for (int j = 0; j < NKH; ++j) {
         const int c0 = 16 * (hh * NKH + j) + 4 * kg;
@@ -1144,6 +1155,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p)
         store4<TI>(static_cast<TI *>(p.dq), roff, c0, K, dq4);
         store4<TI>(static_cast<TI *>(p.dk), roff, c0, K, dk4);
     }
+    }
+    __syncthreads();  // sRow, sT and the block tables are rewritten by the next item
+    }
 }
 
 template <PrecKind PK, int KP, typename TI, typename TG>
@@ -1164,8 +1178,28 @@ hipError_t launch_bwd(const BwdParams &p, int total_chunks, hipStream_t stream)
     else go(std::integral_constant<int, 64>{});
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || total_chunks == 0) return e;
-    hipLaunchKernelGGL((chunk_bwd_kside_kernel<PK, KP, TI, TG>), dim3(total_chunks, p.H), dim3(512), 0,
-                       stream, p);
+    // One resident wave of workgroups (occupancy x CUs of the current device,
+    // looked up once per device), each walking items (chunk, head) =
+    // item / H, item % H with a stride of the grid.
+    const auto kern = chunk_bwd_kside_kernel<PK, KP, TI, TG>;
+    static int resident[64] = {};  // per instantiation
+    int dev = 0;
+    e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    int slots = dev < 64 ? resident[dev] : 0;
+    if (slots == 0) {
+        int cus = 0, per_cu = 0;
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 512, 0);
+        if (e != hipSuccess) return e;
+        slots = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+        if (dev < 64) resident[dev] = slots;
+    }
+    const int64_t items = static_cast<int64_t>(total_chunks) * p.H;
+    if (items > (int64_t{1} << 30)) return hipErrorInvalidValue;  // item indices stay in int
+    const int grid = static_cast<int>(items < slots ? items : slots);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), 0, stream, p, static_cast<int>(items));
     return hipGetLastError();
 }
 
