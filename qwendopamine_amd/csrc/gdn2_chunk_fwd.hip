@@ -713,7 +713,11 @@ chunk_prep_kernel(ChunkParams p, int items)
                 if (!(col <= row)) aq[I][i] = 0.f;
                 if (!(col < row)) al[I][i] = 0.f;
             }
-            st_q4<PK>(ws + BL::AQ + k16_block(R, I, 64) + 4 * l, pack4<PK>(aq[I]));
+            // Blocks (0, 2), (0, 3), (1, 2), (1, 3) lie above the causal diagonal
+            // and the inference scan never copies them; the training workspace
+            // (p.hs) keeps them, zero, for the backward's transposed landing.
+            if (p.hs || !(R < 2 && I >= 2))
+                st_q4<PK>(ws + BL::AQ + k16_block(R, I, 64) + 4 * l, pack4<PK>(aq[I]));
         }
         __syncthreads();  // all reads of sKend done; its space becomes L
         // Blocks I <= R only: the upper blocks are never read as L and serve as
@@ -772,7 +776,8 @@ chunk_prep_kernel(ChunkParams p, int items)
         for (int J = 0; J < 4; ++J) {
             const float4 xv = *reinterpret_cast<const float4 *>(&sX[(16 * R + m) * LDF + 16 * J + 4 * kg]);
             xt[J] = pack4<PK>(xv.x, xv.y, xv.z, xv.w);
-            st_q4<PK>(ws + BL::X + k16_block(R, J, 64) + 4 * l, xt[J]);
+            if (p.hs || !(R < 2 && J >= 2))  // as for Aqk above
+                st_q4<PK>(ws + BL::X + k16_block(R, J, 64) + 4 * l, xt[J]);
         }
         // W^T(ct, R) = Ebar^T(ct, :) X^T(:, R): B operand X^T(J, R) is row 16R+m of
         // X, i.e. xt[J]; result lane (n, kg) holds W[16R+n][16ct+4kg+i] -- the K16
