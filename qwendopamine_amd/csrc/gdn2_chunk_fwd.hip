@@ -338,7 +338,10 @@ chunk_prep_kernel(ChunkParams p, int items)
     using Q = Q4<PK>;
     constexpr int NKT = KP / 16;
     constexpr int NKS = KP / 32;
-    constexpr int LDK = KP + 8;  // row-major [64][KP] keys (storage precision)
+    // Row-major [64][KP] keys (storage precision).  The 4-element pad: with 8
+    // the pair products' 8-byte row reads counted 1.33 bank-conflict cycles
+    // per LDS instruction over the kernel, with 4 (or 12) 0.80.
+    constexpr int LDK = KP + 4;
     constexpr int LDF = 64 + 4;  // fp32 [64][64]
     constexpr int SZK = 64 * LDK * static_cast<int>(sizeof(st));
     constexpr int SZ1 = SZK > 64 * LDF * 4 ? SZK : 64 * LDF * 4;
