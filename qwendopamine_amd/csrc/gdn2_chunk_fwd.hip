@@ -481,8 +481,10 @@ chunk_prep_kernel(ChunkParams p, int items)
         sk += __shfl_xor(sk, 16, 64);
         sk += __shfl_xor(sk, 32, 64);
         const bool l2 = (p.flags & GDN2_FLAG_L2NORM_QK) != 0;
-        const float invq = l2 ? 1.0f / fmaxf(sqrtf(sq), 1e-6f) : 1.0f;
-        const float invk = l2 ? 1.0f / fmaxf(sqrtf(sk), 1e-6f) : 1.0f;
+        // 1 / max(||x||, 1e-6) = rsqrt(max(||x||^2, 1e-12)), on the hardware
+        // reciprocal square root (1 ulp) instead of an IEEE sqrt and divide.
+        const float invq = l2 ? __builtin_amdgcn_rsqf(fmaxf(sq, 1e-12f)) : 1.0f;
+        const float invk = l2 ? __builtin_amdgcn_rsqf(fmaxf(sk, 1e-12f)) : 1.0f;
         const float qmul = invq * p.scale;
         // Normalised q (scaled), k and the erase vector e = b * k of tile kt.
         auto qke = [&](int kt, float (&xq)[4], float (&xk)[4], float (&xe)[4]) __attribute__((always_inline)) {
