@@ -177,6 +177,34 @@ int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int
                            void *out, int io_dtype, int64_t rows, int N, float eps, void *stream);
 
 /*
+ * Residual add and the next pre-norm of a decoder block in one pass:
+ *   sum_out = x + residual                  (rounded to io_dtype, torch's add)
+ *   out     = gdn2_gated_rmsnorm_fwd(sum_out, z = NULL, weight)
+ * Replaces `x = x + h` followed by `norm_2(x)` inside Block.forward, and the
+ * last block's `x + h` followed by the model's final norm (reference
+ * src/qwendopamine/models/gdn2_gpt/model.py:240-248 and the ln_f call of
+ * GDN2GPT.forward), with RMSNorm.forward's rounding (reference
+ * models/normalization.py:40-51): both outputs equal the two separate ops bit
+ * for bit.  Rows of N values with N / (16 bytes of io_dtype) a power of two in
+ * [4, 256] and 16-byte aligned x, residual, sum_out, out; other shapes return
+ * GDN2_ERR_UNSUPPORTED (the caller keeps the two ops).
+ */
+int gdn2_add_rms_norm_fwd(const void *x, const void *residual, void *sum_out, const void *weight,
+                          int weight_dtype, void *out, int io_dtype, int64_t rows, int N, float eps,
+                          void *stream);
+
+/*
+ * SwiGLU's gated product (reference src/qwendopamine/models/gdn2_gpt/model.py:74-77,
+ * `F.silu(x1) * x2`) on the output of one fused w1 / w2 projection:
+ *   out[r, c] = round(round(silu(ab[r, c])) * ab[r, H + c])
+ * with row r of ab at ab + r * ab_row_stride (>= 2H) and out [rows, H]
+ * contiguous, rounded to io_dtype after each op as torch is.  H and the row
+ * stride multiples of 16 bytes of io_dtype, 16-byte aligned pointers.
+ */
+int gdn2_silu_mul_fwd(const void *ab, int64_t ab_row_stride, void *out, int io_dtype, int64_t rows,
+                      int H, void *stream);
+
+/*
  * Backward of the short convolution on a prefill call (no cache), for training
  * without torch's conv: the gradient of ShortConvolution.forward (reference
  * gdn2.py:395-430, whose backward torch's autograd runs through F.conv1d and

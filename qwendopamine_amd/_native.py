@@ -67,6 +67,8 @@ SIGNATURES: dict[str, tuple] = {
         _i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     ),
     "gdn2_gated_rmsnorm_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i64, _i, _f, _vp]),
+    "gdn2_add_rms_norm_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i64, _i, _f, _vp]),
+    "gdn2_silu_mul_fwd": (_i, [_vp, _i64, _vp, _i, _i64, _i, _vp]),
     "gdn2_decode_fused": (
         _i,
         [_vp, _vp, _vp, _i64, _i, _vp, _i64, _vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _i64, _vp, _i64,

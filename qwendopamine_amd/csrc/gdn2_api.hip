@@ -237,6 +237,49 @@ int gdn2_gated_rmsnorm_fwd(const void *x, const void *z, const void *weight, int
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+int gdn2_add_rms_norm_fwd(const void *x, const void *residual, void *sum_out, const void *weight,
+                          int weight_dtype, void *out, int io_dtype, int64_t rows, int N, float eps,
+                          void *stream)
+{
+    if (!valid_dtype(io_dtype) || !valid_dtype(weight_dtype)) return GDN2_ERR_INVALID;
+    if (weight_dtype != io_dtype && weight_dtype != GDN2_DTYPE_F32) return GDN2_ERR_INVALID;
+    if (rows < 0 || N <= 0) return GDN2_ERR_INVALID;
+    if (rows == 0) return GDN2_OK;
+    if (!x || !residual || !sum_out || !weight || !out) return GDN2_ERR_INVALID;
+    // One vectorised pass: rows of 4..256 16-byte pieces (a power of two), 16-byte aligned.
+    const int epv = io_dtype == GDN2_DTYPE_F32 ? 4 : 8;
+    const int pieces = N / epv;
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) |
+                           reinterpret_cast<uintptr_t>(sum_out) | reinterpret_cast<uintptr_t>(out);
+    if (N % epv != 0 || pieces < 4 || pieces > 256 || (pieces & (pieces - 1)) != 0 || (addr & 15) != 0)
+        return GDN2_ERR_UNSUPPORTED;
+    if (rows > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
+    NormParams p;
+    p.x = x; p.z = nullptr; p.weight = weight; p.out = out;
+    p.rows = rows; p.N = N; p.eps = eps;
+    p.w_f32 = weight_dtype == GDN2_DTYPE_F32 && io_dtype != GDN2_DTYPE_F32;
+    p.res = residual; p.sum_out = sum_out;
+    const hipError_t err = launch_gated_rmsnorm(p, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_silu_mul_fwd(const void *ab, int64_t ab_row_stride, void *out, int io_dtype, int64_t rows,
+                      int H, void *stream)
+{
+    if (!valid_dtype(io_dtype) || rows < 0 || H <= 0) return GDN2_ERR_INVALID;
+    if (rows == 0) return GDN2_OK;
+    if (!ab || !out || ab_row_stride < 2LL * H) return GDN2_ERR_INVALID;
+    const int epv = io_dtype == GDN2_DTYPE_F32 ? 4 : 8;
+    if (H % epv != 0 || ab_row_stride % epv != 0 ||
+        ((reinterpret_cast<uintptr_t>(ab) | reinterpret_cast<uintptr_t>(out)) & 15) != 0)
+        return GDN2_ERR_UNSUPPORTED;
+    if ((rows * (H / epv) + 255) / 256 > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
+    SiluMulParams p;
+    p.ab = ab; p.out = out; p.rows = rows; p.ld = ab_row_stride; p.H = H;
+    const hipError_t err = launch_silu_mul(p, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
 size_t gdn2_short_conv_bwd_workspace_size(int B, int T, int D, int conv_width)
 {
     if (B < 0 || T < 0 || D < 0 || conv_width < 1 || conv_width > 8) return 0;

@@ -156,9 +156,23 @@ struct NormParams {
     int N;
     int w_f32;  // weight (and output) in float32 while x, z are 16-bit
     float eps;
+    // Residual add before a plain norm (z null): x <- round(x + res), written
+    // to sum_out, then normalised.  Null: none.
+    const void *res = nullptr;
+    void *sum_out = nullptr;
 };
 
 hipError_t launch_gated_rmsnorm(const NormParams &p, int io_dtype, hipStream_t stream);
+
+// The SwiGLU product of the decoder hosts: out[r, c] = round(round(silu(a)) * b)
+// with a = ab[r, c], b = ab[r, H + c] (row stride ld), out [rows, H].
+struct SiluMulParams {
+    const void *ab;
+    void *out;
+    int64_t rows, ld;
+    int H;
+};
+hipError_t launch_silu_mul(const SiluMulParams &p, int io_dtype, hipStream_t stream);
 
 // Backward of the short convolution on a prefill call (no cache).
 struct ConvBwdParams {

@@ -266,9 +266,10 @@ __global__ __launch_bounds__(64) void short_conv_vec_kernel(ConvParams p)
 // xor-shuffles inside its lane group.  Each thread takes RPT rows (RPB rows
 // apart) and requests all of them before computing.  GATE false: no z, the
 // plain RMSNorm.
-template <typename T, int LPR, int RPT, int VPL, bool GATE>
+template <typename T, int LPR, int RPT, int VPL, bool GATE, bool ADD = false>
 __global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(NormParams p)
 {
+    static_assert(!(ADD && GATE), "the residual add precedes the plain norm");
     using VT = Vec16<T>;
     constexpr int EPV = VT::N, RPB = 256 / LPR, EPL = VPL * EPV, PS = LPR * EPV;
     const int N = VPL * PS;
@@ -288,6 +289,12 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(NormParams p)
             VT::load(static_cast<const T *>(p.x) + off[r] + v * PS, t);
 #pragma unroll
             for (int e = 0; e < EPV; ++e) xv[r][v * EPV + e] = t[e];
+            if constexpr (ADD) {
+                // The residual sum in the io dtype, as torch's x + h.
+                VT::load(static_cast<const T *>(p.res) + off[r] + v * PS, t);
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) xv[r][v * EPV + e] = round_to<T>(xv[r][v * EPV + e] + t[e]);
+            }
             if constexpr (GATE) {
                 VT::load(static_cast<const T *>(p.z) + off[r] + v * PS, t);
 #pragma unroll
@@ -323,6 +330,15 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(NormParams p)
             }
         }
         if (!live[r]) continue;
+        if constexpr (ADD) {
+#pragma unroll
+            for (int v = 0; v < VPL; ++v) {
+                float t[EPV];
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) t[e] = xv[r][v * EPV + e];
+                VT::store(static_cast<T *>(p.sum_out) + off[r] + v * PS, t);
+            }
+        }
 #pragma unroll
         for (int v = 0; v < VPL; ++v) {
             if (p.w_f32) {
@@ -388,8 +404,14 @@ template <typename T, int LPR, int VPL, bool GATE>
 hipError_t norm_vec(const NormParams &p, hipStream_t s)
 {
     constexpr int RPT = 1, RPB = 256 / LPR;
-    hipLaunchKernelGGL((gated_rmsnorm_vec_kernel<T, LPR, RPT, VPL, GATE>),
-                       dim3(static_cast<unsigned>((p.rows + RPB * RPT - 1) / (RPB * RPT))), dim3(256), 0, s, p);
+    const dim3 grid(static_cast<unsigned>((p.rows + RPB * RPT - 1) / (RPB * RPT)));
+    if constexpr (!GATE) {
+        if (p.res) {
+            hipLaunchKernelGGL((gated_rmsnorm_vec_kernel<T, LPR, RPT, VPL, false, true>), grid, dim3(256), 0, s, p);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gated_rmsnorm_vec_kernel<T, LPR, RPT, VPL, GATE>), grid, dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
@@ -400,7 +422,8 @@ hipError_t norm_g(const NormParams &p, hipStream_t s)
     // VPL in {1, 2, 4}, 16-byte aligned.
     constexpr int EPV = Vec16<T>::N;
     const bool aligned = ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.z) |
-                           reinterpret_cast<uintptr_t>(p.out)) & 15) == 0;
+                           reinterpret_cast<uintptr_t>(p.out) | reinterpret_cast<uintptr_t>(p.res) |
+                           reinterpret_cast<uintptr_t>(p.sum_out)) & 15) == 0;
     if (aligned && p.N % EPV == 0) {
         switch (p.N / EPV) {
         case 4: return norm_vec<T, 4, 1, GATE>(p, s);
@@ -413,6 +436,7 @@ hipError_t norm_g(const NormParams &p, hipStream_t s)
         default: break;
         }
     }
+    if (p.res) return hipErrorInvalidValue;  // the residual add has the vectorised path only (checked by the caller)
     const dim3 grid(static_cast<unsigned>((p.rows + 3) / 4));
     if (p.N <= 64) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 1, GATE>), grid, dim3(256), 0, s, p);
     else if (p.N <= 128) hipLaunchKernelGGL((gated_rmsnorm_kernel<T, 2, GATE>), grid, dim3(256), 0, s, p);
@@ -429,7 +453,49 @@ hipError_t norm_t(const NormParams &p, hipStream_t s)
     return p.z ? norm_g<T, true>(p, s) : norm_g<T, false>(p, s);
 }
 
+// SwiGLU product: one thread per 16-byte piece of the output; a and b are the
+// two column halves of the fused w1 / w2 projection's rows.
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(SiluMulParams p)
+{
+    using VT = Vec16<T>;
+    constexpr int EPV = VT::N;
+    const int PPR = p.H / EPV;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= p.rows * PPR) return;
+    const int64_t row = idx / PPR;
+    const int c = static_cast<int>(idx - row * PPR) * EPV;
+    const T *ab = static_cast<const T *>(p.ab) + row * p.ld + c;
+    float a[EPV], b[EPV], o[EPV];
+    VT::load(ab, a);
+    VT::load(ab + p.H, b);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+        // torch's silu in float: x / (1 + exp(-x)) with an accurate exp and an IEEE divide.
+        const float s = a[e] / (1.0f + expf(-a[e]));
+        o[e] = round_to<T>(round_to<T>(s) * b[e]);
+    }
+    VT::store(static_cast<T *>(p.out) + row * p.H + c, o);
+}
+
+template <typename T>
+hipError_t silu_mul_t(const SiluMulParams &p, hipStream_t s)
+{
+    const int64_t n = p.rows * (p.H / Vec16<T>::N);
+    hipLaunchKernelGGL((silu_mul_kernel<T>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_silu_mul(const SiluMulParams &p, int io_dtype, hipStream_t stream)
+{
+    switch (io_dtype) {
+    case GDN2_DTYPE_F32: return silu_mul_t<float>(p, stream);
+    case GDN2_DTYPE_BF16: return silu_mul_t<bf16_t>(p, stream);
+    default: return silu_mul_t<f16_t>(p, stream);
+    }
+}
 
 hipError_t launch_short_conv(const ConvParams &p, int io_dtype, int maxD, int ntensors,
                              hipStream_t stream)

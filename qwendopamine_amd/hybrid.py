@@ -20,6 +20,10 @@ What differs from the reference host, deliberately:
   (embedding, 24 layers, LM head, argmax, position update) once and replays it;
   the gdn2 caches are refreshed in place at the end of every step, so replays
   advance the recurrence.
+* **Fused elementwise passes** (inference on the GPU). Each residual add runs with the
+  RMSNorm that reads its result (``ops.add_rms_norm``), and SwiGLU's ``silu(a) * b``
+  is one pass (``ops.silu_mul``); both round as the torch ops they replace, and the
+  logits are bit-identical to the unfused host's.
 """
 
 from __future__ import annotations
@@ -146,7 +150,11 @@ class SwiGLU(nn.Module):
         if torch.is_grad_enabled() and any(t.requires_grad for t in (x, self.w1.weight, self.w2.weight)):
             return self.w3(F.silu(self.w1(x)) * self.w2(x))
         # Inference: w1 and w2 as one GEMM (the same dot products, one launch).
-        a, b = F.linear(x, *self._fused12()).chunk(2, dim=-1)
+        ab = F.linear(x, *self._fused12())
+        if ab.is_cuda:
+            # silu(a) * b in one HIP pass with torch's roundings (three launches otherwise).
+            return self.w3(ops.silu_mul(ab))
+        a, b = ab.chunk(2, dim=-1)
         return self.w3(F.silu(a) * b)
 
     def _fused12(self) -> tuple[torch.Tensor, torch.Tensor | None]:
@@ -258,15 +266,32 @@ class Block(nn.Module):
 
     def forward(self, x: torch.Tensor, cos, sin, input_pos=None, mask=None) -> torch.Tensor:
         n1 = self.norm_1(x)
+        h = self._mix(n1, cos, sin, input_pos, mask)
+        x = x + h
+        return x + self.mlp(self.norm_2(x))
+
+    def forward_pending(self, x: torch.Tensor, pending: torch.Tensor | None, cos, sin, input_pos=None,
+                        mask=None) -> tuple[torch.Tensor, torch.Tensor]:
+        """``forward`` with its last residual add left to the caller: returns ``(x', m)``
+        such that ``forward`` would return ``x' + m``, and takes the previous block's
+        pending ``m`` (or None).  Each residual add then runs in one HIP pass with the
+        norm that reads its result (``ops.add_rms_norm``, bit-identical to the add and
+        the norm apart).  Inference on GPU tensors only."""
+        if pending is None:
+            n1 = self.norm_1(x)
+        else:
+            x, n1 = ops.add_rms_norm(x, pending, self.norm_1.weight, self.norm_1.eps)
+        h = self._mix(n1, cos, sin, input_pos, mask)
+        x, n2 = ops.add_rms_norm(x, h, self.norm_2.weight, self.norm_2.eps)
+        return x, self.mlp(n2)
+
+    def _mix(self, n1: torch.Tensor, cos, sin, input_pos, mask) -> torch.Tensor:
         if self.use_gdn2:
             if input_pos is None:
                 h, _, _ = self.attn(n1)
-            else:
-                h = self._gdn2_cached(n1)
-        else:
-            h = self.attn(n1, cos, sin, input_pos, mask)
-        x = x + h
-        return x + self.mlp(self.norm_2(x))
+                return h
+            return self._gdn2_cached(n1)
+        return self.attn(n1, cos, sin, input_pos, mask)
 
     def _gdn2_cached(self, x: torch.Tensor) -> torch.Tensor:
         """Run the mixer on this layer's cache. Once the cache exists, its tensors are
@@ -353,6 +378,15 @@ class HybridDecoder(nn.Module):
             cos, sin = cos.index_select(0, input_pos), sin.index_select(0, input_pos)
             mask = self.mask_cache.index_select(2, input_pos)
         x = self.wte(idx)
+        if _inference(x, self.ln_f.weight) and ops.add_rms_norm_supported(x):
+            # The residual adds fused with the norms that follow them.
+            pending = None
+            for blk in self.h:
+                x, pending = blk.forward_pending(x, pending, cos, sin, input_pos, mask)
+            if pending is None:
+                return self.lm_head(self.ln_f(x))
+            _, xn = ops.add_rms_norm(x, pending, self.ln_f.weight, self.ln_f.eps)
+            return self.lm_head(xn)
         for blk in self.h:
             x = blk(x, cos, sin, input_pos, mask)
         return self.lm_head(self.ln_f(x))

@@ -1159,6 +1159,76 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.
     return out
 
 
+@torch.compiler.disable
+def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                 eps: float = 1e-5) -> tuple[torch.Tensor, torch.Tensor]:
+    """``s = x + residual`` and ``rms_norm(s, weight, eps)`` in one pass; returns ``(s, norm)``.
+
+    The decoder hosts' ``x = x + h`` followed by the next ``RMSNorm`` (reference
+    ``gdn2_gpt/model.py:240-248``, ``models/normalization.py:40-51``), equal to the two
+    separate ops bit for bit.  Rows of ``N`` values with ``N`` times the element size a
+    power of two between 64 and 4096 bytes; other shapes raise ``NotImplementedError``
+    (``add_rms_norm_supported`` tells them apart).  Inference only.
+    """
+    name = "add_rms_norm"
+    _require_gpu(name, x, residual, weight)
+    if residual.shape != x.shape or residual.dtype != x.dtype:
+        raise ValueError(f"{name}: residual must match x in shape and dtype")
+    if weight.numel() != x.shape[-1]:
+        raise ValueError(f"{name}: weight must have {x.shape[-1]} elements")
+    dt = x.dtype
+    N = x.shape[-1]
+    xc, rc = x.contiguous(), residual.contiguous()
+    wd = weight.detach()
+    wdt = torch.float32 if (wd.dtype == torch.float32 and dt != torch.float32) else dt
+    wc = wd.to(wdt).contiguous()
+    s = torch.empty_like(xc)
+    out = torch.empty(x.shape, dtype=wdt, device=x.device)
+    lib = nat.load()
+    st = lib.gdn2_add_rms_norm_fwd(
+        nat.ptr(xc), nat.ptr(rc), nat.ptr(s), nat.ptr(wc), nat.dtype_code(wdt), nat.ptr(out),
+        nat.dtype_code(dt), xc.numel() // N, N, float(eps), nat.stream_handle(x.device),
+    )
+    if st == nat.ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{name}: rows of {N} {dt} values are not supported")
+    nat.check(st, name)
+    return s, out
+
+
+def add_rms_norm_supported(x: torch.Tensor) -> bool:
+    """Whether ``add_rms_norm`` takes rows of ``x``'s width and dtype."""
+    nbytes = x.shape[-1] * x.element_size()
+    return nbytes % 16 == 0 and 4 <= nbytes // 16 <= 256 and (nbytes // 16) & (nbytes // 16 - 1) == 0
+
+
+@torch.compiler.disable
+def silu_mul(ab: torch.Tensor) -> torch.Tensor:
+    """``F.silu(a) * b`` for ``a, b = ab.chunk(2, dim=-1)``: SwiGLU's gated product
+    (reference ``gdn2_gpt/model.py:74-77``) on the output of one fused w1 / w2
+    projection, with torch's rounding to the io dtype after each op.  The last axis of
+    ``ab`` has unit stride; the other axes may be strided as rows.  Inference only."""
+    name = "silu_mul"
+    _require_gpu(name, ab)
+    dt = ab.dtype
+    if ab.shape[-1] % 2:
+        raise ValueError(f"{name}: the last axis must have an even length")
+    H = ab.shape[-1] // 2
+    a2 = ab.reshape(-1, 2 * H) if ab.dim() != 2 else ab
+    if a2.stride(-1) != 1:
+        a2 = a2.contiguous()
+    ld = a2.stride(0) if a2.shape[0] > 1 else 2 * H  # a single row's stride is arbitrary
+    out = torch.empty(ab.shape[:-1] + (H,), dtype=dt, device=ab.device)
+    lib = nat.load()
+    st = lib.gdn2_silu_mul_fwd(
+        nat.ptr(a2), ld, nat.ptr(out), nat.dtype_code(dt), a2.shape[0], H,
+        nat.stream_handle(ab.device),
+    )
+    if st == nat.ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{name}: {H} {dt} columns are not supported")
+    nat.check(st, name)
+    return out
+
+
 def _rows2d(name: str, x: torch.Tensor, dt: torch.dtype, width: int) -> int:
     """Row stride of a [N, >= width] tensor read in place (unit channel stride)."""
     if x.dim() != 2 or x.dtype != dt or x.stride(1) != 1 or x.shape[1] < width:
