@@ -205,6 +205,26 @@ int gdn2_silu_mul_fwd(const void *ab, int64_t ab_row_stride, void *out, int io_d
                       int H, void *stream);
 
 /*
+ * The decoder hosts' linear layers on a decode step's few rows:
+ *   y[m, n] = sum_k x[m, k] * weight[n, k] (+ bias[n]),   m < M <= 8
+ * with fp32 accumulation and one rounding to io_dtype (bf16 or fp16), as
+ * torch's F.linear; the summation order differs from torch's GEMM, so the
+ * results agree to rounding.  Replaces the nn.Linear / F.linear calls of one
+ * decode step: SwiGLU's w1 / w2 / w3 (reference
+ * src/qwendopamine/models/gdn2_gpt/model.py:74-78), the attention and gdn2
+ * projections and the LM head (model.py GDN2GPT.forward; gdn2.py's q / k / v /
+ * gate projections and o_proj).  Rows of x, weight and y are
+ * x_row_stride / weight_row_stride / y_row_stride elements apart (unit column
+ * stride).  K / 512 in {1, 2, 4, 6, 8} (M <= 4 beyond K = 2048), x and weight
+ * 16-byte aligned with row
+ * strides multiples of 8 elements; other shapes return GDN2_ERR_UNSUPPORTED
+ * (the caller keeps torch's GEMM).
+ */
+int gdn2_skinny_linear(const void *x, int64_t x_row_stride, const void *weight, int64_t weight_row_stride,
+                       const void *bias, void *y, int64_t y_row_stride, int io_dtype, int M, int N, int K,
+                       void *stream);
+
+/*
  * Backward of the short convolution on a prefill call (no cache), for training
  * without torch's conv: the gradient of ShortConvolution.forward (reference
  * gdn2.py:395-430, whose backward torch's autograd runs through F.conv1d and

@@ -280,6 +280,26 @@ int gdn2_silu_mul_fwd(const void *ab, int64_t ab_row_stride, void *out, int io_d
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+int gdn2_skinny_linear(const void *x, int64_t x_row_stride, const void *weight, int64_t weight_row_stride,
+                       const void *bias, void *y, int64_t y_row_stride, int io_dtype, int M, int N, int K,
+                       void *stream)
+{
+    if (!valid_dtype(io_dtype) || M < 0 || N < 0 || K < 0) return GDN2_ERR_INVALID;
+    if (M == 0 || N == 0) return GDN2_OK;
+    if (!x || !weight || !y || x_row_stride < K || weight_row_stride < K || y_row_stride < N) return GDN2_ERR_INVALID;
+    if (!skinny_linear_supported(io_dtype, M, K)) return GDN2_ERR_UNSUPPORTED;
+    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) & 15) != 0 ||
+        x_row_stride % 8 != 0 || weight_row_stride % 8 != 0)
+        return GDN2_ERR_UNSUPPORTED;
+    if (N > 2147483647 - 8) return GDN2_ERR_UNSUPPORTED;
+    SkinnyParams p;
+    p.x = x; p.w = weight; p.bias = bias; p.y = y;
+    p.ldx = x_row_stride; p.ldw = weight_row_stride; p.ldy = y_row_stride;
+    p.M = M; p.N = N; p.K = K;
+    const hipError_t err = launch_skinny_linear(p, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
 size_t gdn2_short_conv_bwd_workspace_size(int B, int T, int D, int conv_width)
 {
     if (B < 0 || T < 0 || D < 0 || conv_width < 1 || conv_width > 8) return 0;

@@ -174,6 +174,17 @@ struct SiluMulParams {
 };
 hipError_t launch_silu_mul(const SiluMulParams &p, int io_dtype, hipStream_t stream);
 
+// Few-row linear layer: y[m, n] = x[m, :] . W[n, :] (+ bias[n]) for M <= 8
+// rows, K a multiple of 512 (K / 512 in {1, 2, 4, 6, 8}), 16-bit io.
+struct SkinnyParams {
+    const void *x, *w, *bias;
+    void *y;
+    int64_t ldx, ldw, ldy;  // row strides in elements
+    int M, N, K;
+};
+bool skinny_linear_supported(int io_dtype, int M, int K);
+hipError_t launch_skinny_linear(const SkinnyParams &p, int io_dtype, hipStream_t stream);
+
 // Backward of the short convolution on a prefill call (no cache).
 struct ConvBwdParams {
     const void *x;      // [B, T, D] input rows: row (b, t) at x + (b * T + t) * ldx

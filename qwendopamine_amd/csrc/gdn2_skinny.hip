@@ -1,0 +1,195 @@
+// Few-row linear layer of the decoder hosts' decode step, gfx950.
+//
+// y[m, n] = sum_k x[m, k] W[n, k] (+ bias[n]) for M <= 8 rows of x: the
+// nn.Linear / F.linear calls of one decode step (batch rows of one token
+// each).  At that size the product is a read of W and nothing else, so the
+// kernel is laid out for HBM: each wave owns one or two rows of W and requests
+// all of their 16-byte pieces before any arithmetic (lane l takes pieces l, l + 64,
+// ... of a row, so every request is a contiguous 1 KB row segment), the few x
+// rows sit in LDS (staged once per workgroup, read by all four waves, reused
+// over the row groups of wide outputs), and the 64 lane partial sums of each
+// output are added by xor-shuffles.  Accumulation
+// is fp32 and the output is rounded once, as torch's GEMM does; the summation
+// order differs from hipBLASLt's, so results agree to rounding, not bit for
+// bit.
+#include "gdn2_common.h"
+#include "gdn2_internal.h"
+
+namespace gdn2 {
+namespace {
+
+constexpr int kWaves = 4;
+// Workgroups of a launch at most: enough to fill the chip several times over;
+// wider outputs loop over row groups so that the staged x rows are reused.
+constexpr int kMaxGroups = 2048;
+
+__device__ __forceinline__ void widen8(uint4 u, float (&f)[8], bool bf)
+{
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint16_t lo = static_cast<uint16_t>(w[i] & 0xffffu), hi = static_cast<uint16_t>(w[i] >> 16);
+        if (bf) {
+            f[2 * i] = bf16_bits_to_f32(lo);
+            f[2 * i + 1] = bf16_bits_to_f32(hi);
+        } else {
+            f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
+            f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
+        }
+    }
+}
+
+// MM: rows of x the instantiation holds (p.M <= MM, rows past p.M are zero
+// and not stored); NP: 16-byte pieces of a row per lane (K = 512 NP); RPW:
+// rows of W per wave.  Workgroup b takes the groups of kWaves * RPW rows
+// b, b + gridDim.x, ...
+template <typename T, int MM, int NP, int RPW>
+__global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
+{
+    constexpr int kRowsPerWave = RPW;
+    constexpr bool BF = std::is_same<T, bf16_t>::value;
+    constexpr int PPR = 64 * NP;  // 16-byte pieces per row of x or W
+    __shared__ __align__(16) uint4 sx[MM * PPR];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int groups = (p.N + kWaves * kRowsPerWave - 1) / (kWaves * kRowsPerWave);
+    const T *w = static_cast<const T *>(p.w);
+    const T *x = static_cast<const T *>(p.x);
+
+    // This wave's rows of W in a group (rows past N read row N-1); the first
+    // group's are requested before the x rows are staged.
+    uint4 wr[kRowsPerWave][NP];
+    auto request = [&](int grp) __attribute__((always_inline)) {
+        const int n0 = (grp * kWaves + wave) * kRowsPerWave;
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) {
+            const int row = n0 + r < p.N ? n0 + r : p.N - 1;
+#pragma unroll
+            for (int c = 0; c < NP; ++c)
+                wr[r][c] = *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(row) * p.ldw + (c * 64 + lane) * 8);
+        }
+    };
+    request(blockIdx.x);
+    // x rows into LDS (rows past M as zeros).
+#pragma unroll 4
+    for (int i0 = 0; i0 < MM * PPR; i0 += 256) {
+        const int i = i0 + tid;
+        if (i < MM * PPR) {
+            const int m = i / PPR, c = i - m * PPR;
+            sx[i] = m < p.M ? *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(m) * p.ldx + c * 8)
+                            : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    __syncthreads();
+
+    for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+    const int n0 = (grp * kWaves + wave) * kRowsPerWave;
+    float acc[kRowsPerWave][MM];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+        float wf[kRowsPerWave][8];
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) widen8(wr[r][c], wf[r], BF);
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            float xf[8];
+            widen8(sx[m * PPR + c * 64 + lane], xf, BF);
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[r][m] = fmaf(wf[r][e], xf[e], acc[r][m]);
+        }
+    }
+    // The next group's rows are requested before this group's sums and stores.
+    if (grp + static_cast<int>(gridDim.x) < groups) request(grp + gridDim.x);
+    // Sum over the 64 lanes; every lane ends with every total.
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r)
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) acc[r][m] += __shfl_xor(acc[r][m], o, 64);
+    // Lane r * MM + m stores output (m, n0 + r).
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            const int row = n0 + r;
+            if (lane == r * MM + m && m < p.M && row < p.N) {
+                float v = acc[r][m];
+                if (p.bias) v += io<T>::ld(static_cast<const T *>(p.bias), row);
+                io<T>::st(static_cast<T *>(p.y), static_cast<int64_t>(m) * p.ldy + row, v);
+            }
+        }
+    }
+    }
+}
+
+template <typename T, int MM, int NP, int RPW>
+hipError_t skinny_launch(const SkinnyParams &p, hipStream_t s)
+{
+    const int groups = (p.N + kWaves * RPW - 1) / (kWaves * RPW);
+    const dim3 grid(static_cast<unsigned>(groups < kMaxGroups ? groups : kMaxGroups));
+    hipLaunchKernelGGL((skinny_linear_kernel<T, MM, NP, RPW>), grid, dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+// Rows of W per wave by output width (measured at K = 1024 and 3072, M = 4):
+// one for narrow outputs (more waves, so more of the matrix requested at
+// once), two beyond 2048 rows (four measured slower on a 151,936-row
+// output); capped so that a wave's requests (RPW * NP pieces) and sums
+// (RPW * MM) stay in registers.
+template <typename T, int MM, int NP>
+hipError_t skinny_np(const SkinnyParams &p, hipStream_t s)
+{
+    if constexpr (MM * NP > 32) {
+        return hipErrorInvalidValue;  // rejected by skinny_linear_supported (x pieces would not fit in registers)
+    } else {
+        constexpr int LIM = 8 / NP < 16 / MM ? 8 / NP : 16 / MM;
+        if constexpr (LIM >= 2)
+            if (p.N > 2048) return skinny_launch<T, MM, NP, 2>(p, s);
+        return skinny_launch<T, MM, NP, 1>(p, s);
+    }
+}
+
+template <typename T, int MM>
+hipError_t skinny_m(const SkinnyParams &p, hipStream_t s)
+{
+    switch (p.K / 512) {
+    case 1: return skinny_np<T, MM, 1>(p, s);
+    case 2: return skinny_np<T, MM, 2>(p, s);
+    case 4: return skinny_np<T, MM, 4>(p, s);
+    case 6: return skinny_np<T, MM, 6>(p, s);
+    default: return skinny_np<T, MM, 8>(p, s);
+    }
+}
+
+template <typename T>
+hipError_t skinny_t(const SkinnyParams &p, hipStream_t s)
+{
+    if (p.M <= 1) return skinny_m<T, 1>(p, s);
+    if (p.M <= 2) return skinny_m<T, 2>(p, s);
+    if (p.M <= 4) return skinny_m<T, 4>(p, s);
+    return skinny_m<T, 8>(p, s);
+}
+
+}  // namespace
+
+bool skinny_linear_supported(int io_dtype, int M, int K)
+{
+    if (io_dtype != GDN2_DTYPE_BF16 && io_dtype != GDN2_DTYPE_F16) return false;
+    if (M < 1 || M > 8 || K % 512 != 0) return false;
+    const int np = K / 512;
+    if (M > 4 && np > 4) return false;  // eight rows of x with K > 2048: torch's GEMM
+    return np == 1 || np == 2 || np == 4 || np == 6 || np == 8;
+}
+
+hipError_t launch_skinny_linear(const SkinnyParams &p, int io_dtype, hipStream_t stream)
+{
+    return io_dtype == GDN2_DTYPE_BF16 ? skinny_t<bf16_t>(p, stream) : skinny_t<f16_t>(p, stream);
+}
+
+}  // namespace gdn2

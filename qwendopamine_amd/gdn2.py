@@ -452,7 +452,7 @@ class GatedDeltaNet2(nn.Module):
         result and cache updates as the separate passes of ``forward``."""
         batch = x.shape[0]
         W_in, sizes = self._fused_input_weight()
-        y = F.linear(x.reshape(batch, x.shape[-1]), W_in)  # [B, sum(sizes)]
+        y = ops.linear(x.reshape(batch, x.shape[-1]), W_in)  # [B, sum(sizes)]
         qr, kr, vr, b, w, f0, g0 = y.split(sizes, dim=-1)
         g = self.f_proj[1](f0)
         z = self.g_proj[1](g0)
@@ -474,7 +474,7 @@ class GatedDeltaNet2(nn.Module):
             update_cache_in_place=in_place, output_final_state=want_state)
         if use_cache or past_key_values is not None:
             self._update_cache(past_key_values, state, tuple(new_caches))
-        out = self.o_proj(o.reshape(batch, 1, -1))
+        out = ops.linear(o.reshape(batch, 1, -1), self.o_proj.weight, self.o_proj.bias)
         return out, None, past_key_values
 
     def _algorithm(self, mode: str, backend: str, needs_grad: bool) -> str:

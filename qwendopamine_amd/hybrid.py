@@ -150,10 +150,10 @@ class SwiGLU(nn.Module):
         if torch.is_grad_enabled() and any(t.requires_grad for t in (x, self.w1.weight, self.w2.weight)):
             return self.w3(F.silu(self.w1(x)) * self.w2(x))
         # Inference: w1 and w2 as one GEMM (the same dot products, one launch).
-        ab = F.linear(x, *self._fused12())
+        ab = ops.linear(x, *self._fused12())
         if ab.is_cuda:
             # silu(a) * b in one HIP pass with torch's roundings (three launches otherwise).
-            return self.w3(ops.silu_mul(ab))
+            return ops.linear(ops.silu_mul(ab), self.w3.weight, self.w3.bias)
         a, b = ab.chunk(2, dim=-1)
         return self.w3(F.silu(a) * b)
 
@@ -203,7 +203,7 @@ class CausalSelfAttention(nn.Module):
                 input_pos: torch.Tensor | None = None, mask: torch.Tensor | None = None) -> torch.Tensor:
         b, t, _ = x.shape
         G, qpk, D = self.n_query_groups, self.n_head // self.n_query_groups, self.head_size
-        qkv = self.attn(x).view(b, t, G, qpk + 2, D)
+        qkv = ops.linear(x, self.attn.weight, self.attn.bias).view(b, t, G, qpk + 2, D)
         q, k, v = qkv.split((qpk, 1, 1), dim=-2)
         q = apply_rotary_emb(q.reshape(b, t, self.n_head, D), cos, sin)
         k = apply_rotary_emb(k.reshape(b, t, G, D), cos, sin)
@@ -215,7 +215,8 @@ class CausalSelfAttention(nn.Module):
             ck.index_copy_(2, input_pos, k.transpose(1, 2))
             cv.index_copy_(2, input_pos, v.transpose(1, 2))
             if t == 1:
-                return self.proj(self._decode(q, ck, cv, mask).reshape(b, 1, self.n_head * D))
+                return ops.linear(self._decode(q, ck, cv, mask).reshape(b, 1, self.n_head * D), self.proj.weight,
+                                  self.proj.bias)
         q, k, v = (z.transpose(1, 2) for z in (q, k, v))
         if qpk > 1:
             k, v = k.repeat_interleave(qpk, dim=1), v.repeat_interleave(qpk, dim=1)
@@ -384,9 +385,9 @@ class HybridDecoder(nn.Module):
             for blk in self.h:
                 x, pending = blk.forward_pending(x, pending, cos, sin, input_pos, mask)
             if pending is None:
-                return self.lm_head(self.ln_f(x))
+                return ops.linear(self.ln_f(x), self.lm_head.weight)
             _, xn = ops.add_rms_norm(x, pending, self.ln_f.weight, self.ln_f.eps)
-            return self.lm_head(xn)
+            return ops.linear(xn, self.lm_head.weight)
         for blk in self.h:
             x = blk(x, cos, sin, input_pos, mask)
         return self.lm_head(self.ln_f(x))

@@ -26,6 +26,7 @@ from typing import Any
 import ctypes
 
 import torch
+import torch.nn.functional as F
 
 from . import _native as nat
 
@@ -40,6 +41,9 @@ __all__ = [
     "short_convolution",
     "gated_rmsnorm",
     "rms_norm",
+    "add_rms_norm",
+    "silu_mul",
+    "linear",
     "decode_step_fused",
 ]
 
@@ -1227,6 +1231,48 @@ def silu_mul(ab: torch.Tensor) -> torch.Tensor:
         raise NotImplementedError(f"{name}: {H} {dt} columns are not supported")
     nat.check(st, name)
     return out
+
+
+_SKINNY_NP = (1, 2, 4, 6, 8)
+# Wider outputs (an LM head) stay on torch's GEMM, which reads a weight of that size
+# faster (measured at the config-3 decode step; the few-row kernel wins below).
+_SKINNY_MAX_N = 16384
+
+
+@torch.compiler.disable
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.linear(x, weight, bias)``, on the HIP few-row kernel when ``x`` has at most 8
+    rows (a decode step's batch; at most 4 beyond K = 2048), at most 16384 output
+    columns, 16-bit inputs and ``K / 512`` in {1, 2, 4, 6, 8};
+    other calls, and calls through which a gradient flows, are torch's GEMM.
+
+    The kernel reads each row of ``weight`` once with every request in flight before any
+    arithmetic (the product is a read of the weight at this size) and accumulates in
+    fp32, rounding once as torch does; its summation order differs from torch's GEMM,
+    so results agree to rounding, not bit for bit.
+    """
+    K = x.shape[-1]
+    M = x.numel() // K if K else 0
+    if (not x.is_cuda or weight.shape[0] > _SKINNY_MAX_N or x.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != x.dtype
+            or (bias is not None and bias.dtype != x.dtype) or not 1 <= M <= 8 or K % 512
+            or K // 512 not in _SKINNY_NP or (M > 4 and K > 2048) or weight.dim() != 2 or weight.stride(1) != 1
+            or (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, weight, bias)))):
+        return F.linear(x, weight, bias)
+    x2 = x.reshape(M, K)
+    if x2.stride(1) != 1 or (M > 1 and x2.stride(0) % 8):
+        x2 = x2.contiguous()
+    N = weight.shape[0]
+    b = None if bias is None else bias.contiguous()
+    y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=x.device)
+    lib = nat.load()
+    st = lib.gdn2_skinny_linear(
+        nat.ptr(x2), x2.stride(0) if M > 1 else K, nat.ptr(weight), weight.stride(0), nat.ptr(b),
+        nat.ptr(y), N, nat.dtype_code(x.dtype), M, N, K, nat.stream_handle(x.device),
+    )
+    if st == nat.ERR_UNSUPPORTED:  # alignment: torch's GEMM
+        return F.linear(x, weight, bias)
+    nat.check(st, "linear")
+    return y
 
 
 def _rows2d(name: str, x: torch.Tensor, dt: torch.dtype, width: int) -> int:

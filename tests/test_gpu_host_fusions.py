@@ -4,7 +4,9 @@ Kernels:
 * ``ops.add_rms_norm``: a block's residual add with the RMSNorm that reads its result
   (``gdn2_add_rms_norm_fwd``);
 * ``ops.silu_mul``: SwiGLU's ``silu(a) * b`` on the fused w1 / w2 projection
-  (``gdn2_silu_mul_fwd``).
+  (``gdn2_silu_mul_fwd``);
+* ``ops.linear``: the linear layers of a decode step, at most 8 rows
+  (``gdn2_skinny_linear``).
 
 Checks:
 * **Two ops = one pass.** ``add_rms_norm`` against torch's add followed by the unfused
@@ -15,6 +17,10 @@ Checks:
 * **Oracle.** ``add_rms_norm`` against the float64 oracle of the RMSNorm on the rounded sum.
 * **Model.** The config-3 host's forward with the fused passes against the same model
   with them switched off, bit for bit, uncached and on a cached decode step.
+* **Few-row linear.** Against the fp32 product rounded once and against torch's GEMM in
+  the io dtype: equal up to one unit in the last place (a different fp32 summation
+  order); strided rows, leading batch axes, fallbacks to torch's GEMM (more than 8 rows,
+  unsupported K, fp32, autograd) and graph replays.
 """
 
 from __future__ import annotations
@@ -173,3 +179,121 @@ def test_hybrid_forward_fused_equals_unfused(gpu_device, dtype, monkeypatch):
     plain = run()
     for f, p in zip(fused, plain):
         _bits_equal(f, p)
+
+
+def _ulp_close(y: torch.Tensor, ref: torch.Tensor, dtype) -> None:
+    """Two roundings of the same fp32 sums (different summation orders): equal except
+    where the orders straddle a rounding boundary, i.e. at most one unit in the last
+    place of the io dtype, plus an absolute floor near zero."""
+    ulp = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}[dtype]
+    a, b = y.float(), ref.float()
+    scale = b.abs().amax().item()
+    worst = ((a - b).abs() / (b.abs() + 1e-3 * scale)).max().item()
+    same = (a == b).float().mean().item()
+    print(f"  bit-identical {same:.4f}, worst relative diff {worst:.2e}", flush=True)
+    assert worst <= ulp
+    assert same >= 0.9
+
+
+@pytest.mark.parametrize("dtype,M,K,N,bias", [(torch.bfloat16, 4, 1024, 6144, False),
+                                              (torch.bfloat16, 4, 3072, 1024, False),
+                                              (torch.bfloat16, 1, 512, 7, True),
+                                              (torch.bfloat16, 4, 4096, 1000, True),
+                                              (torch.bfloat16, 8, 2048, 500, True),
+                                              (torch.bfloat16, 3, 2048, 129, False),
+                                              (torch.float16, 5, 1024, 300, True)])
+def test_linear_few_rows_matches_fp32(gpu_device, dtype, M, K, N, bias):
+    """``ops.linear`` on the few-row kernel against the fp32 product rounded once, and
+    against torch's own GEMM (``F.linear``) in the io dtype."""
+    from qwendopamine_amd.ops import linear
+
+    print(f"[case] linear dtype={dtype} M={M} K={K} N={N} bias={bias}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(M * 7 + K + N)
+    x = torch.randn(M, K, generator=g).to(gpu_device, dtype)
+    w = (torch.randn(N, K, generator=g) * K ** -0.5).to(gpu_device, dtype)
+    b = torch.randn(N, generator=g).to(gpu_device, dtype) if bias else None
+    with torch.no_grad():
+        y = linear(x, w, b)
+        ref = x.float() @ w.float().t() + (b.float() if bias else 0.0)
+        yt = F.linear(x, w, b)
+    torch.cuda.synchronize()
+    assert y.dtype == dtype and y.shape == (M, N)
+    _ulp_close(y, ref.to(dtype), dtype)
+    _ulp_close(y, yt, dtype)
+
+
+def test_linear_strided_rows_and_fallbacks(gpu_device):
+    """Rows of x taken from a wider tensor give the contiguous result bit for bit; a
+    leading batch shape is kept; more than 8 rows, an unsupported K, fp32, or a gradient
+    are torch's GEMM exactly."""
+    from qwendopamine_amd.ops import linear
+
+    print("[case] linear strides and fallbacks", flush=True)
+    torch.manual_seed(9)
+    wide = torch.randn(4, 1024 + 64, device=gpu_device, dtype=torch.bfloat16)
+    w = torch.randn(333, 1024, device=gpu_device, dtype=torch.bfloat16) * 0.03
+    with torch.no_grad():
+        _bits_equal(linear(wide[:, :1024], w), linear(wide[:, :1024].contiguous(), w))
+        x3 = torch.randn(2, 1, 1024, device=gpu_device, dtype=torch.bfloat16)
+        y3 = linear(x3, w)
+        assert y3.shape == (2, 1, 333)
+        _bits_equal(y3.reshape(2, 333), linear(x3.reshape(2, 1024), w))
+        for x in (torch.randn(9, 1024, device=gpu_device, dtype=torch.bfloat16),
+                  torch.randn(4, 1000, device=gpu_device, dtype=torch.bfloat16)):
+            ww = torch.randn(50, x.shape[1], device=gpu_device, dtype=torch.bfloat16)
+            _bits_equal(linear(x, ww), F.linear(x, ww))
+        x32, w32 = torch.randn(4, 1024, device=gpu_device), torch.randn(50, 1024, device=gpu_device)
+        _bits_equal(linear(x32, w32), F.linear(x32, w32))
+    xg = torch.randn(4, 1024, device=gpu_device, dtype=torch.bfloat16, requires_grad=True)
+    yg = linear(xg, w)
+    assert yg.grad_fn is not None
+    torch.cuda.synchronize()
+
+
+def test_linear_graph_replays(gpu_device):
+    """Captured in a HIP graph, the few-row product replays to the eager result, with
+    new inputs copied in between replays."""
+    from qwendopamine_amd.ops import linear
+
+    print("[case] linear graph replays", flush=True)
+    torch.manual_seed(11)
+    x = torch.randn(4, 1024, device=gpu_device, dtype=torch.bfloat16)
+    w = torch.randn(2048, 1024, device=gpu_device, dtype=torch.bfloat16) * 0.03
+    with torch.no_grad():
+        linear(x, w)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y = linear(x, w)
+        for rep in range(3):
+            x.copy_(torch.randn(4, 1024, device=gpu_device, dtype=torch.bfloat16))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            _bits_equal(y, linear(x, w))
+
+
+def test_skinny_linear_wide_output_through_the_c_abi(gpu_device):
+    """A wide output (more row groups than workgroups: each workgroup loops over groups
+    with the next group's rows requested ahead) through the C entry point directly, as
+    ``ops.linear`` leaves such widths to torch's GEMM."""
+    from qwendopamine_amd import _native as nat
+
+    print("[case] skinny linear wide output (C ABI)", flush=True)
+    torch.manual_seed(13)
+    M, K, N = 3, 1024, 40000
+    x = torch.randn(M, K, device=gpu_device, dtype=torch.bfloat16)
+    w = torch.randn(N, K, device=gpu_device, dtype=torch.bfloat16) * 0.03
+    b = torch.randn(N, device=gpu_device, dtype=torch.bfloat16)
+    y = torch.empty(M, N, device=gpu_device, dtype=torch.bfloat16)
+    lib = nat.load()
+    st = lib.gdn2_skinny_linear(nat.ptr(x), K, nat.ptr(w), K, nat.ptr(b), nat.ptr(y), N, nat.DTYPE_BF16, M, N, K,
+                                nat.stream_handle(x.device))
+    nat.check(st, "gdn2_skinny_linear")
+    ref = (x.float() @ w.float().t() + b.float()).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    _ulp_close(y, ref, torch.bfloat16)
+    assert lib.gdn2_skinny_linear(nat.ptr(x), K, nat.ptr(w), K, None, nat.ptr(y), N, nat.DTYPE_F32, M, N, K,
+                                  nat.stream_handle(x.device)) == nat.ERR_UNSUPPORTED
+    assert lib.gdn2_skinny_linear(nat.ptr(x), K, nat.ptr(w), K, None, nat.ptr(y), N, nat.DTYPE_BF16, 9, N, K,
+                                  nat.stream_handle(x.device)) == nat.ERR_UNSUPPORTED
