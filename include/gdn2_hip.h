@@ -225,6 +225,32 @@ int gdn2_skinny_linear(const void *x, int64_t x_row_stride, const void *weight, 
                        void *stream);
 
 /*
+ * One decode step of the hybrid host's attention layers (one token per
+ * sequence), in one launch: RoPE of the token's q heads and k (interleaved
+ * pairs, fp32, rounded to io_dtype), the store of k and v into the caches at
+ * position *pos, and softmax attention of each q head over cache positions
+ * 0 .. *pos of its KV group.  Replaces the single-token path of
+ * CausalSelfAttention.forward (reference
+ * src/qwendopamine/models/gdn2_gpt/model.py:89-173: apply_rope :40-61, the KV
+ * cache update and the masked scaled_dot_product_attention).
+ *   qkv      [B, G, qpk + 2, D] io_dtype: per KV group, qpk q heads, k, v
+ *            (the fused attn projection's layout)
+ *   cos, sin fp32 rotation of the token (rope_pairs values; channels from
+ *            2 * rope_pairs on are not rotated)
+ *   pos      device int64: the token's position (one for all sequences)
+ *   k_cache, v_cache  [B, G, max_len, D] io_dtype, updated at pos
+ *   out      [B, G * qpk, D] io_dtype
+ * Scores and probabilities are fp32 (the output is rounded once); the host's
+ * torch path rounds the scores and probabilities to io_dtype, so the two agree
+ * to that rounding.  A position outside [0, max_len) leaves the caches alone
+ * and writes zeros.  bf16 / fp16, D in {64, 128}, qpk in {1, 2, 4}; else
+ * GDN2_ERR_UNSUPPORTED.
+ */
+int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int rope_pairs, const int64_t *pos,
+                     void *k_cache, void *v_cache, void *out, int io_dtype, int B, int G, int qpk, int D,
+                     int64_t max_len, float scale, void *stream);
+
+/*
  * Backward of the short convolution on a prefill call (no cache), for training
  * without torch's conv: the gradient of ShortConvolution.forward (reference
  * gdn2.py:395-430, whose backward torch's autograd runs through F.conv1d and

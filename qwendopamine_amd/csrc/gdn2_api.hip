@@ -300,6 +300,27 @@ int gdn2_skinny_linear(const void *x, int64_t x_row_stride, const void *weight, 
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int rope_pairs, const int64_t *pos,
+                     void *k_cache, void *v_cache, void *out, int io_dtype, int B, int G, int qpk, int D,
+                     int64_t max_len, float scale, void *stream)
+{
+    if (!valid_dtype(io_dtype) || B < 0 || G < 0 || qpk < 1 || D < 1 || max_len < 1) return GDN2_ERR_INVALID;
+    if (B == 0 || G == 0) return GDN2_OK;
+    if (!qkv || !pos || !k_cache || !v_cache || !out) return GDN2_ERR_INVALID;
+    if (rope_pairs < 0 || 2 * rope_pairs > D) return GDN2_ERR_INVALID;
+    if (rope_pairs > 0 && (!cos || !sin)) return GDN2_ERR_INVALID;
+    if (!attn_decode_supported(io_dtype, qpk, D)) return GDN2_ERR_UNSUPPORTED;
+    if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return GDN2_ERR_UNSUPPORTED;
+    if (static_cast<int64_t>(B) * G > 2147483647LL || max_len > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
+    AttnDecodeParams p;
+    p.qkv = qkv; p.cos = cos; p.sin = sin;
+    p.rope_pairs = rope_pairs;
+    p.pos = pos; p.k_cache = k_cache; p.v_cache = v_cache; p.out = out;
+    p.max_len = max_len; p.B = B; p.G = G; p.qpk = qpk; p.D = D; p.scale = scale;
+    const hipError_t err = launch_attn_decode(p, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
 size_t gdn2_short_conv_bwd_workspace_size(int B, int T, int D, int conv_width)
 {
     if (B < 0 || T < 0 || D < 0 || conv_width < 1 || conv_width > 8) return 0;

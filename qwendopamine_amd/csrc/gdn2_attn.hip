@@ -1,0 +1,232 @@
+// Single-token softmax attention of the hybrid decoder host's attention
+// layers, gfx950: RoPE of the token's q and k, the KV-cache store at its
+// position, and attention over the cache up to that position, in one launch
+// per layer (the host's torch path issues about seventeen).
+//
+// One workgroup of eight waves per (sequence, KV group).  The token's rotated
+// q heads, k and v go to LDS (and k, v to the caches).  Each wave then walks
+// the cached positions j = (step * 8 + wave) * PS + slot: the DG lanes of a
+// slot each hold 8 channels (one 16-byte piece) of k_j and v_j, requested
+// together, and the slot's dot products are completed by xor-shuffles over
+// those lanes.  Softmax is online (running maximum, rescaled sums), so the
+// cache is read once; the per-slot states are merged across slots by
+// shuffles and across waves through LDS.  All sums are fp32; the output is
+// rounded once to the io dtype.
+#include "gdn2_common.h"
+#include "gdn2_internal.h"
+
+namespace gdn2 {
+namespace {
+
+constexpr int kAttnWaves = 8;
+constexpr float kNegBig = -1.0e30f;  // "no position yet": exp(kNegBig - m) is 0 for any real m
+
+constexpr int kUnroll = 4;            // positions per slot requested at once
+
+template <typename T>
+__device__ __forceinline__ void widen8(uint4 u, float (&f)[8])
+{
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint16_t lo = static_cast<uint16_t>(w[i] & 0xffffu), hi = static_cast<uint16_t>(w[i] >> 16);
+        if constexpr (std::is_same<T, bf16_t>::value) {
+            f[2 * i] = bf16_bits_to_f32(lo);
+            f[2 * i + 1] = bf16_bits_to_f32(hi);
+        } else {
+            f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
+            f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
+        }
+    }
+}
+
+template <typename T, int D, int QPK>
+__global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
+{
+    constexpr int DG = D / 8;    // 16-byte channel pieces of a row
+    constexpr int PS = 64 / DG;  // position slots per wave
+    static_assert(DG * PS == 64, "a wave is PS slots of DG lanes");
+    __shared__ __align__(16) float sq[QPK][D];
+    __shared__ __align__(16) float skv[2][D];
+    __shared__ float sm[kAttnWaves][QPK], sl[kAttnWaves][QPK];
+    __shared__ __align__(16) float so[kAttnWaves][QPK][D];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = p.G;
+    const int b = blockIdx.x / G, g = blockIdx.x - (blockIdx.x / G) * G;
+    const int64_t pos = *p.pos;
+    const int H = G * QPK;
+    T *out = static_cast<T *>(p.out) + (static_cast<int64_t>(b) * H + g * QPK) * D;
+    if (pos < 0 || pos >= p.max_len) {
+        // Outside the caches: zero output, caches untouched.
+        for (int e = tid; e < QPK * D; e += 512) io<T>::st(out, e, 0.0f);
+        return;
+    }
+    const int n = static_cast<int>(pos) + 1;
+    const T *x = static_cast<const T *>(p.qkv) + static_cast<int64_t>(b * G + g) * (QPK + 2) * D;
+    const int64_t cbase = (static_cast<int64_t>(b) * G + g) * p.max_len * D;
+    T *kc = static_cast<T *>(p.k_cache) + cbase;
+    T *vc = static_cast<T *>(p.v_cache) + cbase;
+
+    // ---- RoPE of the QPK q heads and k (interleaved pairs, fp32, rounded to
+    // the io dtype as the host's torch path), v as is ----
+    for (int e = tid; e < (QPK + 1) * (D / 2); e += 512) {
+        const int h = e / (D / 2), i = e - h * (D / 2);
+        const float x0 = io<T>::ld(x, h * D + 2 * i), x1 = io<T>::ld(x, h * D + 2 * i + 1);
+        float y0 = x0, y1 = x1;
+        if (i < p.rope_pairs) {
+            const float c = p.cos[i], s = p.sin[i];
+            y0 = round_to<T>(x0 * c - x1 * s);
+            y1 = round_to<T>(x0 * s + x1 * c);
+        }
+        if (h < QPK) {
+            sq[h][2 * i] = y0;
+            sq[h][2 * i + 1] = y1;
+        } else {
+            skv[0][2 * i] = y0;
+            skv[0][2 * i + 1] = y1;
+            io<T>::st(kc, pos * D + 2 * i, y0);
+            io<T>::st(kc, pos * D + 2 * i + 1, y1);
+        }
+    }
+    for (int d = tid; d < D; d += 512) {
+        const float v = io<T>::ld(x, (QPK + 1) * D + d);
+        skv[1][d] = v;
+        io<T>::st(vc, pos * D + d, v);
+    }
+    __syncthreads();
+
+    // ---- one pass over positions 0 .. pos with online softmax ----
+    const int slot = lane / DG, dg = lane - (lane / DG) * DG;
+    float qv[QPK][8];
+#pragma unroll
+    for (int h = 0; h < QPK; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[h][e] = sq[h][dg * 8 + e] * p.scale;
+    float m[QPK], l[QPK], acc[QPK][8];
+#pragma unroll
+    for (int h = 0; h < QPK; ++h) {
+        m[h] = kNegBig;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+    }
+    const int per_step = kAttnWaves * PS;
+    for (int j0 = 0; j0 < n; j0 += per_step * kUnroll) {
+        // kUnroll positions per slot requested before any is used; positions
+        // from pos on read row 0 (always valid) and are skipped or replaced.
+        uint4 kr[kUnroll], vr[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int j = j0 + u * per_step + wave * PS + slot;
+            const int64_t jl = j < pos ? j : 0;
+            kr[u] = *reinterpret_cast<const uint4 *>(kc + jl * D + dg * 8);
+            vr[u] = *reinterpret_cast<const uint4 *>(vc + jl * D + dg * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+        const int j = j0 + u * per_step + wave * PS + slot;
+        if (j >= n) continue;  // no shuffles below cross slots, so lanes may drop out per slot
+        float kf[8], vf[8];
+        if (j == pos) {
+            // The token itself: its k, v from LDS (its cache store may still be in flight).
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                kf[e] = skv[0][dg * 8 + e];
+                vf[e] = skv[1][dg * 8 + e];
+            }
+        } else {
+            widen8<T>(kr[u], kf);
+            widen8<T>(vr[u], vf);
+        }
+#pragma unroll
+        for (int h = 0; h < QPK; ++h) {
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s = fmaf(qv[h][e], kf[e], s);
+#pragma unroll
+            for (int o = 1; o < DG; o <<= 1) s += __shfl_xor(s, o, 64);  // within the slot's DG lanes
+            const float mn = fmaxf(m[h], s);
+            const float r = __expf(m[h] - mn), pj = __expf(s - mn);
+            l[h] = l[h] * r + pj;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pj, vf[e], acc[h][e] * r);
+            m[h] = mn;
+        }
+        }
+    }
+    // Merge the PS slot states of the wave (lanes with equal dg).
+#pragma unroll
+    for (int h = 0; h < QPK; ++h) {
+#pragma unroll
+        for (int o = DG; o < 64; o <<= 1) {
+            const float m2 = __shfl_xor(m[h], o, 64), l2 = __shfl_xor(l[h], o, 64);
+            const float mn = fmaxf(m[h], m2);
+            const float r1 = __expf(m[h] - mn), r2 = __expf(m2 - mn);
+            l[h] = l[h] * r1 + l2 * r2;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float a2 = __shfl_xor(acc[h][e], o, 64);
+                acc[h][e] = acc[h][e] * r1 + a2 * r2;
+            }
+            m[h] = mn;
+        }
+        if (slot == 0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) so[wave][h][dg * 8 + e] = acc[h][e];
+            if (dg == 0) {
+                sm[wave][h] = m[h];
+                sl[wave][h] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+    // Merge the waves and normalise.
+    for (int e = tid; e < QPK * D; e += 512) {
+        const int h = e / D, d = e - h * D;
+        float mx = kNegBig;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) mx = fmaxf(mx, sm[w][h]);
+        float num = 0.0f, den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float r = __expf(sm[w][h] - mx);
+            num = fmaf(so[w][h][d], r, num);
+            den = fmaf(sl[w][h], r, den);
+        }
+        io<T>::st(out, e, num / den);
+    }
+}
+
+template <typename T, int D>
+hipError_t attn_d(const AttnDecodeParams &p, hipStream_t s)
+{
+    const dim3 grid(static_cast<unsigned>(p.B * p.G));
+    switch (p.qpk) {
+    case 1: hipLaunchKernelGGL((attn_decode_kernel<T, D, 1>), grid, dim3(512), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((attn_decode_kernel<T, D, 2>), grid, dim3(512), 0, s, p); break;
+    default: hipLaunchKernelGGL((attn_decode_kernel<T, D, 4>), grid, dim3(512), 0, s, p); break;
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t attn_t(const AttnDecodeParams &p, hipStream_t s)
+{
+    return p.D == 64 ? attn_d<T, 64>(p, s) : attn_d<T, 128>(p, s);
+}
+
+}  // namespace
+
+bool attn_decode_supported(int io_dtype, int qpk, int D)
+{
+    return (io_dtype == GDN2_DTYPE_BF16 || io_dtype == GDN2_DTYPE_F16) && (qpk == 1 || qpk == 2 || qpk == 4) &&
+           (D == 64 || D == 128);
+}
+
+hipError_t launch_attn_decode(const AttnDecodeParams &p, int io_dtype, hipStream_t stream)
+{
+    return io_dtype == GDN2_DTYPE_BF16 ? attn_t<bf16_t>(p, stream) : attn_t<f16_t>(p, stream);
+}
+
+}  // namespace gdn2

@@ -185,6 +185,24 @@ struct SkinnyParams {
 bool skinny_linear_supported(int io_dtype, int M, int K);
 hipError_t launch_skinny_linear(const SkinnyParams &p, int io_dtype, hipStream_t stream);
 
+// Single-token attention of the decoder host's attention layers: RoPE of q and
+// k, the KV-cache store at position *pos, softmax attention over positions
+// 0 .. *pos.  qkv [B, G, qpk + 2, D] (qpk q heads, k, v per KV group), caches
+// [B, G, max_len, D], out [B, G * qpk, D]; cos / sin the token's fp32
+// rotation row of rope_pairs values.
+struct AttnDecodeParams {
+    const void *qkv;
+    const float *cos, *sin;
+    int rope_pairs;
+    const int64_t *pos;
+    void *k_cache, *v_cache, *out;
+    int64_t max_len;
+    int B, G, qpk, D;
+    float scale;
+};
+bool attn_decode_supported(int io_dtype, int qpk, int D);
+hipError_t launch_attn_decode(const AttnDecodeParams &p, int io_dtype, hipStream_t stream);
+
 // Backward of the short convolution on a prefill call (no cache).
 struct ConvBwdParams {
     const void *x;      // [B, T, D] input rows: row (b, t) at x + (b * T + t) * ldx

@@ -203,7 +203,13 @@ class CausalSelfAttention(nn.Module):
                 input_pos: torch.Tensor | None = None, mask: torch.Tensor | None = None) -> torch.Tensor:
         b, t, _ = x.shape
         G, qpk, D = self.n_query_groups, self.n_head // self.n_query_groups, self.head_size
-        qkv = ops.linear(x, self.attn.weight, self.attn.bias).view(b, t, G, qpk + 2, D)
+        qkv = ops.linear(x, self.attn.weight, self.attn.bias)
+        if (t == 1 and input_pos is not None and self.kv_cache is not None and _inference(qkv)
+                and ops.attention_decode_supported(qkv, qpk, D)):
+            # RoPE, the cache store and the attention of the token in one HIP launch.
+            o = ops.attention_decode(qkv, cos, sin, input_pos, *self.kv_cache, self.n_head)
+            return ops.linear(o.reshape(b, 1, self.n_head * D), self.proj.weight, self.proj.bias)
+        qkv = qkv.view(b, t, G, qpk + 2, D)
         q, k, v = qkv.split((qpk, 1, 1), dim=-2)
         q = apply_rotary_emb(q.reshape(b, t, self.n_head, D), cos, sin)
         k = apply_rotary_emb(k.reshape(b, t, G, D), cos, sin)

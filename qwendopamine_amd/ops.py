@@ -44,6 +44,7 @@ __all__ = [
     "add_rms_norm",
     "silu_mul",
     "linear",
+    "attention_decode",
     "decode_step_fused",
 ]
 
@@ -1273,6 +1274,50 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
         return F.linear(x, weight, bias)
     nat.check(st, "linear")
     return y
+
+
+def attention_decode_supported(qkv: torch.Tensor, qpk: int, head_dim: int) -> bool:
+    """Whether ``attention_decode`` takes this dtype, head size and query heads per group."""
+    return qkv.is_cuda and qkv.dtype in (torch.bfloat16, torch.float16) and qpk in (1, 2, 4) and head_dim in (64, 128)
+
+
+@torch.compiler.disable
+def attention_decode(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, input_pos: torch.Tensor,
+                     k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int) -> torch.Tensor:
+    """One decode step of the hybrid host's grouped-query attention in one HIP launch:
+    RoPE of the token's q heads and k, the KV-cache store at ``input_pos`` and softmax
+    attention over the cache up to it (the single-token path of reference
+    ``CausalSelfAttention.forward``, ``gdn2_gpt/model.py:89-173``).
+
+    ``qkv`` ``[B, 1, G * (qpk + 2) * D]`` (the fused ``attn`` projection of one token),
+    ``cos`` / ``sin`` the token's rotation ``[1, rot / 2]`` (fp32), ``input_pos`` ``[1]``
+    (device int64), caches ``[B, G, L, D]``.  Returns ``[B, n_head, D]``.  Scores and
+    probabilities stay fp32 (torch's path rounds them to the io dtype), so results agree
+    to that rounding.  Inference only.
+    """
+    name = "attention_decode"
+    _require_gpu(name, qkv, cos, sin, input_pos, k_cache, v_cache)
+    B, G, L, D = k_cache.shape
+    qpk = n_head // G
+    if qkv.numel() != B * G * (qpk + 2) * D or v_cache.shape != k_cache.shape:
+        raise ValueError(f"{name}: qkv, caches and n_head do not agree")
+    if input_pos.numel() != 1 or input_pos.dtype != torch.int64:
+        raise ValueError(f"{name}: input_pos must be one int64 position")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.dtype == qkv.dtype == v_cache.dtype):
+        raise ValueError(f"{name}: caches must be contiguous and of qkv's dtype")
+    pairs = cos.shape[-1]
+    if 2 * pairs > D or sin.shape[-1] != pairs:
+        raise ValueError(f"{name}: the rotation has more than D / 2 pairs")
+    qc = qkv.contiguous()
+    cf, sf = cos.reshape(-1)[:pairs].float().contiguous(), sin.reshape(-1)[:pairs].float().contiguous()
+    out = torch.empty(B, n_head, D, dtype=qkv.dtype, device=qkv.device)
+    lib = nat.load()
+    st = lib.gdn2_attn_decode(
+        nat.ptr(qc), nat.ptr(cf), nat.ptr(sf), pairs, nat.ptr(input_pos), nat.ptr(k_cache), nat.ptr(v_cache),
+        nat.ptr(out), nat.dtype_code(qkv.dtype), B, G, qpk, D, L, float(D) ** -0.5, nat.stream_handle(qkv.device),
+    )
+    nat.check(st, name)
+    return out
 
 
 def _rows2d(name: str, x: torch.Tensor, dt: torch.dtype, width: int) -> int:

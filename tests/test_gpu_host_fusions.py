@@ -21,9 +21,15 @@ Checks:
   the io dtype: equal up to one unit in the last place (a different fp32 summation
   order); strided rows, leading batch axes, fallbacks to torch's GEMM (more than 8 rows,
   unsupported K, fp32, autograd) and graph replays.
+* **Attention decode** (``ops.attention_decode``, ``gdn2_attn_decode``): against float64
+  attention over the same rounded inputs (GQA, D = 64 and 128, first and last cache
+  position), the cache rows it stores, an out-of-range position, and the host's
+  attention layer against its torch path.
 """
 
 from __future__ import annotations
+
+import math
 
 import numpy as np
 import pytest
@@ -297,3 +303,127 @@ def test_skinny_linear_wide_output_through_the_c_abi(gpu_device):
                                   nat.stream_handle(x.device)) == nat.ERR_UNSUPPORTED
     assert lib.gdn2_skinny_linear(nat.ptr(x), K, nat.ptr(w), K, None, nat.ptr(y), N, nat.DTYPE_BF16, 9, N, K,
                                   nat.stream_handle(x.device)) == nat.ERR_UNSUPPORTED
+
+
+def _attn_reference(qkv, cos, sin, pos, kc, vc, n_head, dtype):
+    """float64 attention of one token over cache positions 0..pos, with q and k rotated
+    in fp32 and rounded to the io dtype (as the host's torch path and the kernel do);
+    returns (out [B, n_head, D], rotated k [B, G, D], v [B, G, D])."""
+    B, G, L, D = kc.shape
+    qpk = n_head // G
+    x = qkv.reshape(B, G, qpk + 2, D).float()
+    pairs = cos.shape[-1]
+    c, s = cos.reshape(-1).float(), sin.reshape(-1).float()
+
+    def rot(t):
+        t = t.clone()
+        a, b = t[..., 0:2 * pairs:2].clone(), t[..., 1:2 * pairs:2].clone()
+        t[..., 0:2 * pairs:2] = a * c - b * s
+        t[..., 1:2 * pairs:2] = a * s + b * c
+        return t.to(dtype).double()
+
+    q = rot(x[:, :, :qpk])                       # [B, G, qpk, D]
+    k = rot(x[:, :, qpk])                        # [B, G, D]
+    v = x[:, :, qpk + 1].to(dtype).double()
+    K = kc[:, :, :pos + 1].double().clone()
+    V = vc[:, :, :pos + 1].double().clone()
+    K[:, :, pos], V[:, :, pos] = k, v
+    sc = torch.einsum("bgqd,bgld->bgql", q, K) / math.sqrt(D)
+    o = torch.einsum("bgql,bgld->bgqd", torch.softmax(sc, dim=-1), V)
+    return o.reshape(B, n_head, D), k, v
+
+
+@pytest.mark.parametrize("dtype,G,qpk,D,L,pos", [(torch.bfloat16, 16, 1, 64, 2304, 2047),
+                                                 (torch.bfloat16, 4, 4, 128, 300, 0),
+                                                 (torch.float16, 2, 2, 128, 513, 512),
+                                                 (torch.bfloat16, 3, 1, 64, 100, 37)])
+def test_attention_decode_matches_float64(gpu_device, dtype, G, qpk, D, L, pos):
+    """``ops.attention_decode`` against float64 attention over the same rounded inputs:
+    the output to within its io-dtype rounding, the cache rows at ``pos`` equal to the
+    rotated k and v, every other cache row untouched."""
+    from qwendopamine_amd.ops import attention_decode
+
+    print(f"[case] attention_decode dtype={dtype} G={G} qpk={qpk} D={D} L={L} pos={pos}", flush=True)
+    gen = torch.Generator(device="cpu").manual_seed(G * 100 + D + pos)
+    B, n_head = 3, G * qpk
+    qkv = torch.randn(B, 1, G * (qpk + 2) * D, generator=gen).to(gpu_device, dtype)
+    kc = torch.randn(B, G, L, D, generator=gen).to(gpu_device, dtype)
+    vc = torch.randn(B, G, L, D, generator=gen).to(gpu_device, dtype)
+    ang = torch.rand(1, D // 2, generator=gen) * 6.0
+    cos, sin = torch.cos(ang).to(gpu_device), torch.sin(ang).to(gpu_device)
+    kc0, vc0 = kc.clone(), vc.clone()
+    ref, k_ref, v_ref = _attn_reference(qkv.cpu(), cos.cpu(), sin.cpu(), pos, kc0.cpu(), vc0.cpu(), n_head, dtype)
+    with torch.no_grad():
+        out = attention_decode(qkv, cos, sin, torch.tensor([pos], device=gpu_device), kc, vc, n_head)
+    torch.cuda.synchronize()
+    assert out.shape == (B, n_head, D) and out.dtype == dtype
+    err = rel_l2(out, ref.numpy())
+    print(f"  rel_l2 {err:.2e}", flush=True)
+    assert err <= 4e-3
+    # The rotation in fp32 may contract into fused multiply-adds: a rounding flip to
+    # the io dtype is possible, at most one unit in the last place.
+    kk = kc[:, :, pos].cpu().double()
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    assert (kk == k_ref).double().mean().item() >= 0.99
+    assert ((kk - k_ref).abs() <= ulp * k_ref.abs() + 1e-6).all()
+    assert torch.equal(vc[:, :, pos].cpu().double(), v_ref)
+    keep = torch.ones(L, dtype=torch.bool)
+    keep[pos] = False
+    assert torch.equal(kc[:, :, keep], kc0[:, :, keep]) and torch.equal(vc[:, :, keep], vc0[:, :, keep])
+
+
+def test_attention_decode_out_of_range_position(gpu_device):
+    """A position outside the caches writes zeros and leaves the caches alone."""
+    from qwendopamine_amd.ops import attention_decode
+
+    print("[case] attention_decode out-of-range position", flush=True)
+    torch.manual_seed(17)
+    B, G, L, D = 2, 4, 64, 64
+    qkv = torch.randn(B, 1, G * 3 * D, device=gpu_device, dtype=torch.bfloat16)
+    kc = torch.randn(B, G, L, D, device=gpu_device, dtype=torch.bfloat16)
+    vc = torch.randn_like(kc)
+    kc0, vc0 = kc.clone(), vc.clone()
+    cos, sin = torch.ones(1, D // 2, device=gpu_device), torch.zeros(1, D // 2, device=gpu_device)
+    with torch.no_grad():
+        out = attention_decode(qkv, cos, sin, torch.tensor([L], device=gpu_device), kc, vc, G)
+    torch.cuda.synchronize()
+    assert not bool(out.any())
+    assert torch.equal(kc, kc0) and torch.equal(vc, vc0)
+
+
+def test_hybrid_attention_layer_fused_vs_torch_path(gpu_device, monkeypatch):
+    """The host's attention layer on one cached token: the fused launch against the
+    layer's torch path (RoPE, cache update, masked softmax) on the same state: caches
+    equal, outputs equal to the torch path's rounding of scores and probabilities."""
+    from qwendopamine_amd import ops
+    from qwendopamine_amd.hybrid import CausalSelfAttention, HybridConfig
+
+    print("[case] hybrid attention layer fused vs torch path", flush=True)
+    torch.manual_seed(19)
+    cfg = HybridConfig(n_layer=1, n_embd=1024, n_head=16, head_size=64, n_query_groups=8, gdn2_layers=[])
+    att = CausalSelfAttention(cfg, 0).to(gpu_device, torch.bfloat16).eval()
+    B, L, pos = 4, 400, 311
+    x = torch.randn(B, 1, 1024, device=gpu_device, dtype=torch.bfloat16)
+    from qwendopamine_amd.hybrid import build_rope_cache
+    cos_t, sin_t = build_rope_cache(L, 64, gpu_device)
+    ip = torch.tensor([pos], device=gpu_device)
+    cos, sin = cos_t.index_select(0, ip), sin_t.index_select(0, ip)
+    mask = torch.tril(torch.ones(L, L, dtype=torch.bool, device=gpu_device))[None, None].index_select(2, ip)
+    base = (torch.randn(B, 8, L, 64, device=gpu_device, dtype=torch.bfloat16),
+            torch.randn(B, 8, L, 64, device=gpu_device, dtype=torch.bfloat16))
+    outs, caches = [], []
+    for fused in (True, False):
+        if not fused:
+            monkeypatch.setattr(ops, "attention_decode_supported", lambda *a: False)
+        att.kv_cache = (base[0].clone(), base[1].clone())
+        with torch.no_grad():
+            outs.append(att(x, cos, sin, ip, mask))
+        caches.append(att.kv_cache)
+    torch.cuda.synchronize()
+    a, b = outs[0].float(), outs[1].float()
+    err = ((a - b).norm() / b.norm()).item()
+    print(f"  fused vs torch path rel_l2 {err:.2e}", flush=True)
+    assert err <= 1e-2
+    for (k0, v0), (k1, v1) in zip([caches[0]], [caches[1]]):
+        same = (k0 == k1).float().mean().item()
+        assert same >= 0.999 and torch.equal(v0, v1)
