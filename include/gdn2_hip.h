@@ -225,6 +225,22 @@ int gdn2_skinny_linear(const void *x, int64_t x_row_stride, const void *weight, 
                        void *stream);
 
 /*
+ * Two few-row linear layers with a small inner dimension in one launch:
+ *   y_i[m, n] = sum_k x_i[m, k] * weight_i[n, k] (+ bias_i[n]),  i = 0, 1
+ * for the module's second-stage gate projections of a decode step (reference
+ * gdn2.py:591-594 and :615-618: f_proj[1] Linear(head_v_dim, key_dim) and
+ * g_proj[1] Linear(head_v_dim, value_dim, bias)), which share M and K.
+ * Weights [N_i, K] contiguous; x_i rows x_i_row_stride elements apart (a
+ * multiple of 8, x_i 16-byte aligned); fp32 sums rounded once.  N_i = 0 skips
+ * a problem.  bf16 / fp16, K in {32, 64, 128, 256}, M <= min(8, K / 8); else
+ * GDN2_ERR_UNSUPPORTED.
+ */
+int gdn2_small_linear_pair(const void *x0, int64_t x0_row_stride, const void *weight0, const void *bias0, void *y0,
+                           int64_t y0_row_stride, int N0, const void *x1, int64_t x1_row_stride,
+                           const void *weight1, const void *bias1, void *y1, int64_t y1_row_stride, int N1,
+                           int io_dtype, int M, int K, void *stream);
+
+/*
  * One decode step of the hybrid host's attention layers (one token per
  * sequence), in one launch: RoPE of the token's q heads and k (interleaved
  * pairs, fp32, rounded to io_dtype), the store of k and v into the caches at

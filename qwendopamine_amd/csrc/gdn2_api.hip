@@ -300,6 +300,48 @@ int gdn2_skinny_linear(const void *x, int64_t x_row_stride, const void *weight, 
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+int gdn2_small_linear_pair(const void *x0, int64_t x0_row_stride, const void *weight0, const void *bias0, void *y0,
+                           int64_t y0_row_stride, int N0, const void *x1, int64_t x1_row_stride,
+                           const void *weight1, const void *bias1, void *y1, int64_t y1_row_stride, int N1,
+                           int io_dtype, int M, int K, void *stream)
+{
+    if (!valid_dtype(io_dtype) || M < 0 || K < 1 || N0 < 0 || N1 < 0) return GDN2_ERR_INVALID;
+    if (M == 0 || (N0 == 0 && N1 == 0)) return GDN2_OK;
+    if (!small_linear_supported(io_dtype, M, K)) return GDN2_ERR_UNSUPPORTED;
+    SmallLinearParams p;
+    p.M = M; p.K = K;
+    int n = 0;
+    const void *xs[2] = {x0, x1}, *ws[2] = {weight0, weight1}, *bs[2] = {bias0, bias1};
+    void *ys[2] = {y0, y1};
+    const int64_t lx[2] = {x0_row_stride, x1_row_stride}, ly[2] = {y0_row_stride, y1_row_stride};
+    const int Ns[2] = {N0, N1};
+    for (int i = 0; i < 2; ++i) {
+        if (Ns[i] == 0) continue;
+        if (!xs[i] || !ws[i] || !ys[i] || lx[i] < K || ly[i] < Ns[i]) return GDN2_ERR_INVALID;
+        if (((reinterpret_cast<uintptr_t>(xs[i]) | reinterpret_cast<uintptr_t>(ws[i])) & 15) != 0 || lx[i] % 8 != 0)
+            return GDN2_ERR_UNSUPPORTED;
+        SmallLinearProblem &q = p.prob[n++];
+        q.x = xs[i]; q.w = ws[i]; q.bias = bs[i]; q.y = ys[i]; q.ldx = lx[i]; q.ldy = ly[i]; q.N = Ns[i];
+    }
+    const hipError_t err = launch_small_linear(p, n, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_argmax_rows(const void *x, int64_t x_row_stride, int io_dtype, int64_t rows, int64_t n, int64_t *out,
+                     int64_t out_stride, void *stream)
+{
+    if (!valid_dtype(io_dtype) || rows < 0 || n < 1) return GDN2_ERR_INVALID;
+    if (rows == 0) return GDN2_OK;
+    if (!x || !out || x_row_stride < n || out_stride < 1) return GDN2_ERR_INVALID;
+    const int es = io_dtype == GDN2_DTYPE_F32 ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_row_stride * es) % 16 != 0) return GDN2_ERR_UNSUPPORTED;
+    if (rows > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
+    ArgmaxParams p;
+    p.x = x; p.ld = x_row_stride; p.rows = rows; p.n = n; p.out = out; p.out_stride = out_stride;
+    const hipError_t err = launch_argmax_rows(p, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
 int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int rope_pairs, const int64_t *pos,
                      void *k_cache, void *v_cache, void *out, int io_dtype, int B, int G, int qpk, int D,
                      int64_t max_len, float scale, void *stream)

@@ -21,7 +21,6 @@ namespace {
 constexpr int kAttnWaves = 8;
 constexpr float kNegBig = -1.0e30f;  // "no position yet": exp(kNegBig - m) is 0 for any real m
 
-constexpr int kUnroll = 4;            // positions per slot requested at once
 
 template <typename T>
 __device__ __forceinline__ void widen8(uint4 u, float (&f)[8])
@@ -43,6 +42,10 @@ __device__ __forceinline__ void widen8(uint4 u, float (&f)[8])
 template <typename T, int D, int QPK>
 __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
 {
+    // Positions per slot requested at once: as many as the registers allow
+    // beside the QPK heads' sums (the cache read is latency-bound at one
+    // workgroup per KV group).
+    constexpr int kUnroll = QPK <= 2 ? 8 : 4;
     constexpr int DG = D / 8;    // 16-byte channel pieces of a row
     constexpr int PS = 64 / DG;  // position slots per wave
     static_assert(DG * PS == 64, "a wave is PS slots of DG lanes");
@@ -216,7 +219,89 @@ hipError_t attn_t(const AttnDecodeParams &p, hipStream_t s)
     return p.D == 64 ? attn_d<T, 64>(p, s) : attn_d<T, 128>(p, s);
 }
 
+// Row-wise argmax (greedy decoding over the LM head's logits): one workgroup of
+// 1024 threads per row, each thread scanning 16-byte pieces tid, tid + 1024,
+// ... with every piece of a batch requested before any is compared.  The first
+// index of the maximum wins, and NaN counts as the maximum (torch's argmax).
+template <typename T>
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(ArgmaxParams p)
+{
+    constexpr int EPP = 16 / static_cast<int>(sizeof(T));  // elements per piece
+    constexpr int U = 4;                                     // pieces in flight per thread
+    __shared__ float sv[16];
+    __shared__ int64_t si[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const T *x = static_cast<const T *>(p.x) + static_cast<int64_t>(blockIdx.x) * p.ld;
+    const int64_t pieces = p.n / EPP;
+    float best = -INFINITY;
+    int64_t bi = p.n;  // "none yet": larger than every index
+    auto take = [&](float v, int64_t i) __attribute__((always_inline)) {
+        // v beats best if larger, or NaN where best is not, or equal / both NaN at a smaller index.
+        const bool vn = v != v, bn = best != best;
+        const bool better = (vn && !bn) || (!vn && !bn && v > best) || ((v == best || (vn && bn)) && i < bi);
+        if (better) {
+            best = v;
+            bi = i;
+        }
+    };
+    for (int64_t c0 = tid; c0 < pieces; c0 += 1024 * U) {
+        uint4 raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + 1024 * u;
+            raw[u] = *reinterpret_cast<const uint4 *>(x + (c < pieces ? c : c0) * EPP);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + 1024 * u;
+            if (c >= pieces) continue;
+            const unsigned w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+            for (int e = 0; e < EPP; ++e) {
+                float v;
+                if constexpr (sizeof(T) == 4) {
+                    v = __uint_as_float(w[e]);
+                } else {
+                    const uint16_t h = static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+                    if constexpr (std::is_same<T, bf16_t>::value)
+                        v = bf16_bits_to_f32(h);
+                    else
+                        v = static_cast<float>(__builtin_bit_cast(_Float16, h));
+                }
+                take(v, c * EPP + e);
+            }
+        }
+    }
+    for (int64_t i = pieces * EPP + tid; i < p.n; i += 1024) take(io<T>::ld(x, i), i);  // ragged tail
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float v2 = __shfl_xor(best, o, 64);
+        const int64_t i2 = __shfl_xor(bi, o, 64);
+        take(v2, i2);
+    }
+    if (lane == 0) {
+        sv[wave] = best;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w2 = 1; w2 < 16; ++w2) take(sv[w2], si[w2]);
+        p.out[static_cast<int64_t>(blockIdx.x) * p.out_stride] = bi < p.n ? bi : 0;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_argmax_rows(const ArgmaxParams &p, int io_dtype, hipStream_t stream)
+{
+    const dim3 grid(static_cast<unsigned>(p.rows));
+    switch (io_dtype) {
+    case GDN2_DTYPE_F32: hipLaunchKernelGGL((argmax_rows_kernel<float>), grid, dim3(1024), 0, stream, p); break;
+    case GDN2_DTYPE_BF16: hipLaunchKernelGGL((argmax_rows_kernel<bf16_t>), grid, dim3(1024), 0, stream, p); break;
+    default: hipLaunchKernelGGL((argmax_rows_kernel<f16_t>), grid, dim3(1024), 0, stream, p); break;
+    }
+    return hipGetLastError();
+}
 
 bool attn_decode_supported(int io_dtype, int qpk, int D)
 {

@@ -185,6 +185,21 @@ struct SkinnyParams {
 bool skinny_linear_supported(int io_dtype, int M, int K);
 hipError_t launch_skinny_linear(const SkinnyParams &p, int io_dtype, hipStream_t stream);
 
+// Few-row linear layers with a small inner dimension (K in {32, 64, 128, 256}),
+// up to two independent problems of the same M and K per launch.
+struct SmallLinearProblem {
+    const void *x, *w, *bias;  // x rows ldx apart; W [N, K] contiguous; bias [N] or null
+    void *y;                   // rows ldy apart
+    int64_t ldx, ldy;
+    int N;
+};
+struct SmallLinearParams {
+    SmallLinearProblem prob[2];
+    int M, K;
+};
+bool small_linear_supported(int io_dtype, int M, int K);
+hipError_t launch_small_linear(const SmallLinearParams &p, int nprob, int io_dtype, hipStream_t stream);
+
 // Single-token attention of the decoder host's attention layers: RoPE of q and
 // k, the KV-cache store at position *pos, softmax attention over positions
 // 0 .. *pos.  qkv [B, G, qpk + 2, D] (qpk q heads, k, v per KV group), caches
@@ -201,6 +216,15 @@ struct AttnDecodeParams {
     float scale;
 };
 bool attn_decode_supported(int io_dtype, int qpk, int D);
+
+// Row-wise argmax: out[r * out_stride] = first index of the maximum of row r
+// (rows ld elements apart, n values; NaN is the maximum).
+struct ArgmaxParams {
+    const void *x;
+    int64_t ld, rows, n, out_stride;
+    int64_t *out;
+};
+hipError_t launch_argmax_rows(const ArgmaxParams &p, int io_dtype, hipStream_t stream);
 hipError_t launch_attn_decode(const AttnDecodeParams &p, int io_dtype, hipStream_t stream);
 
 // Backward of the short convolution on a prefill call (no cache).

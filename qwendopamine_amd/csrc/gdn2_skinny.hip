@@ -176,7 +176,93 @@ hipError_t skinny_t(const SkinnyParams &p, hipStream_t s)
     return skinny_m<T, 8>(p, s);
 }
 
+// Small inner dimension (K <= 256), up to two independent problems per launch
+// (blockIdx.y): KP8 = K / 8 lanes share a row of W (one 16-byte piece each),
+// so a wave instruction reads 64 / KP8 consecutive rows, one contiguous 1 KB
+// segment; the row's dot products are completed by xor-shuffles over those
+// lanes.
+template <typename T, int MM, int KP8>
+__global__ __launch_bounds__(256) void small_linear_kernel(SmallLinearParams p)
+{
+    constexpr bool BF = std::is_same<T, bf16_t>::value;
+    constexpr int RPI = 64 / KP8;  // rows per wave
+    __shared__ __align__(16) uint4 sx[MM * KP8];
+    const SmallLinearProblem &q = p.prob[blockIdx.y];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rsub = lane / KP8, c = lane - (lane / KP8) * KP8;
+    const int row = (static_cast<int>(blockIdx.x) * kWaves + wave) * RPI + rsub;
+    const T *w = static_cast<const T *>(q.w);
+    const int rowc = row < q.N ? row : q.N - 1;
+    const uint4 wv = *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(rowc) * p.K + c * 8);
+    if (tid < MM * KP8) {
+        const int m = tid / KP8, cc = tid - m * KP8;
+        sx[tid] = m < p.M ? *reinterpret_cast<const uint4 *>(static_cast<const T *>(q.x) + m * q.ldx + cc * 8)
+                          : make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
+    float wf[8];
+    widen8(wv, wf, BF);
+    float acc[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+        float xf[8];
+        widen8(sx[m * KP8 + c], xf, BF);
+        float a = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a = fmaf(wf[e], xf[e], a);
+#pragma unroll
+        for (int o = 1; o < KP8; o <<= 1) a += __shfl_xor(a, o, 64);
+        acc[m] = a;
+    }
+    if (row < q.N && c < MM && c < p.M) {
+        // Lane c of the row's group stores output (c, row).
+        float v = acc[0];
+#pragma unroll
+        for (int m = 1; m < MM; ++m)
+            if (m == c) v = acc[m];
+        if (q.bias) v += io<T>::ld(static_cast<const T *>(q.bias), row);
+        io<T>::st(static_cast<T *>(q.y), static_cast<int64_t>(c) * q.ldy + row, v);
+    }
+}
+
+template <typename T, int KP8>
+hipError_t small_k(const SmallLinearParams &p, int nprob, hipStream_t s)
+{
+    constexpr int RPW = kWaves * (64 / KP8);
+    int nmax = 0;
+    for (int i = 0; i < nprob; ++i) nmax = p.prob[i].N > nmax ? p.prob[i].N : nmax;
+    const dim3 grid(static_cast<unsigned>((nmax + RPW - 1) / RPW), static_cast<unsigned>(nprob));
+    if (p.M <= 1) hipLaunchKernelGGL((small_linear_kernel<T, 1, KP8>), grid, dim3(256), 0, s, p);
+    else if (p.M <= 2) hipLaunchKernelGGL((small_linear_kernel<T, 2, KP8>), grid, dim3(256), 0, s, p);
+    else if (p.M <= 4) hipLaunchKernelGGL((small_linear_kernel<T, 4, KP8>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((small_linear_kernel<T, 8, KP8>), grid, dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t small_t(const SmallLinearParams &p, int nprob, hipStream_t s)
+{
+    switch (p.K / 8) {
+    case 8: return small_k<T, 8>(p, nprob, s);
+    case 16: return small_k<T, 16>(p, nprob, s);
+    case 32: return small_k<T, 32>(p, nprob, s);
+    default: return small_k<T, 4>(p, nprob, s);
+    }
+}
+
 }  // namespace
+
+bool small_linear_supported(int io_dtype, int M, int K)
+{
+    // Lane c of a row's K / 8 lanes stores output row c, so M <= K / 8.
+    return (io_dtype == GDN2_DTYPE_BF16 || io_dtype == GDN2_DTYPE_F16) && M >= 1 && M <= 8 && M <= K / 8 &&
+           (K == 32 || K == 64 || K == 128 || K == 256);
+}
+
+hipError_t launch_small_linear(const SmallLinearParams &p, int nprob, int io_dtype, hipStream_t stream)
+{
+    return io_dtype == GDN2_DTYPE_BF16 ? small_t<bf16_t>(p, nprob, stream) : small_t<f16_t>(p, nprob, stream);
+}
 
 bool skinny_linear_supported(int io_dtype, int M, int K)
 {

@@ -454,8 +454,8 @@ class GatedDeltaNet2(nn.Module):
         W_in, sizes = self._fused_input_weight()
         y = ops.linear(x.reshape(batch, x.shape[-1]), W_in)  # [B, sum(sizes)]
         qr, kr, vr, b, w, f0, g0 = y.split(sizes, dim=-1)
-        g = self.f_proj[1](f0)
-        z = self.g_proj[1](g0)
+        g, z = ops.linear_pair(f0, self.f_proj[1].weight, self.f_proj[1].bias, g0, self.g_proj[1].weight,
+                               self.g_proj[1].bias)
         dt = x.dtype
         caches = list(conv_states) if all(c is not None for c in conv_states) else None
         if caches is not None and not all(c.dtype == dt and c.is_contiguous() for c in caches):

@@ -44,6 +44,8 @@ __all__ = [
     "add_rms_norm",
     "silu_mul",
     "linear",
+    "linear_pair",
+    "argmax_rows",
     "attention_decode",
     "decode_step_fused",
 ]
@@ -1274,6 +1276,69 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
         return F.linear(x, weight, bias)
     nat.check(st, "linear")
     return y
+
+
+@torch.compiler.disable
+def linear_pair(x0: torch.Tensor, w0: torch.Tensor, b0: torch.Tensor | None, x1: torch.Tensor,
+                w1: torch.Tensor, b1: torch.Tensor | None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(F.linear(x0, w0, b0), F.linear(x1, w1, b1))`` in one HIP launch when both have
+    the same few rows (at most min(8, K / 8)) and a small inner dimension K in {32, 64,
+    128, 256}: the module's second-stage gate projections (``f_proj[1]``, ``g_proj[1]``)
+    of a decode step.  Other calls, and calls with gradients, are torch's GEMMs.  fp32
+    sums rounded once (torch's GEMM agrees to rounding)."""
+    K = x0.shape[-1]
+    M = x0.numel() // K if K else 0
+    ok = (x0.is_cuda and x0.dtype in (torch.bfloat16, torch.float16) and K in (32, 64, 128, 256)
+          and 1 <= M <= min(8, K // 8) and x1.shape[-1] == K and x1.numel() == M * K
+          and all(t.dtype == x0.dtype for t in (x1, w0, w1)) and all(b is None or b.dtype == x0.dtype for b in (b0, b1))
+          and w0.shape[1] == K and w1.shape[1] == K
+          and not (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x0, x1, w0, w1, b0, b1))))
+    if not ok:
+        return F.linear(x0, w0, b0), F.linear(x1, w1, b1)
+    xs = []
+    for x in (x0, x1):
+        x2 = x.reshape(M, K)
+        if x2.stride(1) != 1 or (M > 1 and x2.stride(0) % 8):
+            x2 = x2.contiguous()
+        xs.append(x2)
+    wc = [w.contiguous() for w in (w0, w1)]
+    bc = [None if b is None else b.contiguous() for b in (b0, b1)]
+    ys = [torch.empty(x.shape[:-1] + (w.shape[0],), dtype=x.dtype, device=x.device) for x, w in ((x0, w0), (x1, w1))]
+    lib = nat.load()
+    st = lib.gdn2_small_linear_pair(
+        nat.ptr(xs[0]), xs[0].stride(0) if M > 1 else K, nat.ptr(wc[0]), nat.ptr(bc[0]), nat.ptr(ys[0]), w0.shape[0],
+        w0.shape[0], nat.ptr(xs[1]), xs[1].stride(0) if M > 1 else K, nat.ptr(wc[1]), nat.ptr(bc[1]), nat.ptr(ys[1]),
+        w1.shape[0], w1.shape[0], nat.dtype_code(x0.dtype), M, K, nat.stream_handle(x0.device),
+    )
+    if st == nat.ERR_UNSUPPORTED:  # alignment: torch's GEMMs
+        return F.linear(x0, w0, b0), F.linear(x1, w1, b1)
+    nat.check(st, "linear_pair")
+    return ys[0], ys[1]
+
+
+@torch.compiler.disable
+def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``x.argmax(-1, keepdim=True)`` of a 2-D tensor of logits in one HIP launch (one
+    workgroup per row; the first index of the maximum, NaN counting as the maximum, as
+    torch's argmax), written to ``out`` (int64 ``[rows, 1]``, any row stride) when
+    given.  Rows whose layout the kernel does not take use torch's argmax."""
+    if x.dim() != 2:
+        raise ValueError("argmax_rows: x must be 2-D [rows, n]")
+    rows, n = x.shape
+    if out is None:
+        out = torch.empty(rows, 1, dtype=torch.int64, device=x.device)
+    elif out.dtype != torch.int64 or out.numel() != rows:
+        raise ValueError("argmax_rows: out must hold one int64 per row")
+    st = nat.ERR_UNSUPPORTED
+    if x.is_cuda and x.dtype in (torch.bfloat16, torch.float16, torch.float32) and n > 0 and x.stride(1) == 1:
+        lib = nat.load()
+        st = lib.gdn2_argmax_rows(nat.ptr(x), x.stride(0) if rows > 1 else n, nat.dtype_code(x.dtype), rows, n,
+                                  nat.ptr(out), out.stride(0) if rows > 1 else 1, nat.stream_handle(x.device))
+    if st == nat.ERR_UNSUPPORTED:
+        out.copy_(x.argmax(-1, keepdim=True).view(out.shape))
+        return out
+    nat.check(st, "argmax_rows")
+    return out
 
 
 def attention_decode_supported(qkv: torch.Tensor, qpk: int, head_dim: int) -> bool:

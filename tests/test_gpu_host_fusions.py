@@ -427,3 +427,69 @@ def test_hybrid_attention_layer_fused_vs_torch_path(gpu_device, monkeypatch):
     for (k0, v0), (k1, v1) in zip([caches[0]], [caches[1]]):
         same = (k0 == k1).float().mean().item()
         assert same >= 0.999 and torch.equal(v0, v1)
+
+
+@pytest.mark.parametrize("dtype,M,K,N0,N1", [(torch.bfloat16, 4, 64, 1024, 1024), (torch.bfloat16, 8, 128, 300, 77),
+                                             (torch.float16, 4, 32, 64, 1000), (torch.bfloat16, 1, 256, 5, 4096)])
+def test_linear_pair_matches_fp32(gpu_device, dtype, M, K, N0, N1):
+    """``ops.linear_pair`` (the module's two second-stage gate projections in one launch)
+    against the fp32 products rounded once, with x taken as column ranges of a wider
+    row (as the fused input projection hands them over) and a bias on the second."""
+    from qwendopamine_amd.ops import linear_pair
+
+    print(f"[case] linear_pair dtype={dtype} M={M} K={K} N=({N0}, {N1})", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(M + K + N0 + N1)
+    wide = torch.randn(M, 3 * K + 16, generator=g).to(gpu_device, dtype)
+    x0, x1 = wide[:, 16:16 + K], wide[:, 16 + K:16 + 2 * K]
+    w0 = (torch.randn(N0, K, generator=g) * K ** -0.5).to(gpu_device, dtype)
+    w1 = (torch.randn(N1, K, generator=g) * K ** -0.5).to(gpu_device, dtype)
+    b1 = torch.randn(N1, generator=g).to(gpu_device, dtype)
+    with torch.no_grad():
+        y0, y1 = linear_pair(x0, w0, None, x1, w1, b1)
+    r0 = (x0.float() @ w0.float().t()).to(dtype)
+    r1 = (x1.float() @ w1.float().t() + b1.float()).to(dtype)
+    torch.cuda.synchronize()
+    assert y0.shape == (M, N0) and y1.shape == (M, N1)
+    _ulp_close(y0, r0, dtype)
+    _ulp_close(y1, r1, dtype)
+
+
+def test_linear_pair_fallback(gpu_device):
+    """An inner dimension the kernel does not take is torch's GEMMs exactly."""
+    from qwendopamine_amd.ops import linear_pair
+
+    print("[case] linear_pair fallback", flush=True)
+    torch.manual_seed(23)
+    x = torch.randn(4, 48, device=gpu_device, dtype=torch.bfloat16)
+    w = torch.randn(100, 48, device=gpu_device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        y0, y1 = linear_pair(x, w, None, x, w, None)
+    _bits_equal(y0, F.linear(x, w))
+    _bits_equal(y1, F.linear(x, w))
+
+
+@pytest.mark.parametrize("dtype,rows,n", [(torch.bfloat16, 4, 151936), (torch.float32, 3, 1000), (torch.float16, 5, 77),
+                                          (torch.bfloat16, 2, 8)])
+def test_argmax_rows_matches_torch(gpu_device, dtype, rows, n):
+    """Against torch's argmax: ties resolved to the first index, NaN as the maximum, a
+    strided row view, and the output written in place into a strided int64 column."""
+    from qwendopamine_amd.ops import argmax_rows
+
+    print(f"[case] argmax_rows dtype={dtype} rows={rows} n={n}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(rows * n)
+    x = torch.randn(rows, n, generator=g).to(gpu_device, dtype)
+    x[0, n // 3] = x[0, n // 2] = 100.0               # a tie: the first wins
+    if rows > 1:
+        x[1, n - 1] = float("nan")                    # NaN is the maximum
+        x[1, 1] = float("nan")
+    if rows > 2:
+        x[2] = x[2].min()                             # all equal: index 0
+    ref = x.argmax(-1, keepdim=True)
+    got = argmax_rows(x)
+    wide = torch.zeros(rows, 3, dtype=torch.int64, device=gpu_device)
+    argmax_rows(x, out=wide[:, 1:2])
+    big = torch.randn(rows, 2, n, generator=g).to(gpu_device, dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref), (got.flatten().tolist(), ref.flatten().tolist())
+    assert torch.equal(wide[:, 1:2], ref) and not bool(wide[:, 0].any()) and not bool(wide[:, 2].any())
+    assert torch.equal(argmax_rows(big[:, 1]), big[:, 1].argmax(-1, keepdim=True))
