@@ -342,9 +342,15 @@ int gdn2_argmax_rows(const void *x, int64_t x_row_stride, int io_dtype, int64_t 
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+size_t gdn2_attn_decode_workspace_size(int B, int G, int qpk, int D, int64_t max_len)
+{
+    if (B < 0 || G < 0 || qpk < 1 || D < 1 || max_len < 1) return 0;
+    return attn_decode_workspace_floats(B, G, qpk, D, max_len) * sizeof(float);
+}
+
 int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int rope_pairs, const int64_t *pos,
                      void *k_cache, void *v_cache, void *out, int io_dtype, int B, int G, int qpk, int D,
-                     int64_t max_len, float scale, void *stream)
+                     int64_t max_len, float scale, void *workspace, size_t workspace_bytes, void *stream)
 {
     if (!valid_dtype(io_dtype) || B < 0 || G < 0 || qpk < 1 || D < 1 || max_len < 1) return GDN2_ERR_INVALID;
     if (B == 0 || G == 0) return GDN2_OK;
@@ -359,6 +365,10 @@ int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int ro
     p.rope_pairs = rope_pairs;
     p.pos = pos; p.k_cache = k_cache; p.v_cache = v_cache; p.out = out;
     p.max_len = max_len; p.B = B; p.G = G; p.qpk = qpk; p.D = D; p.scale = scale;
+    p.splits = attn_decode_splits(max_len);
+    p.part = static_cast<float *>(workspace);
+    if (p.splits > 1 && (!workspace || workspace_bytes < gdn2_attn_decode_workspace_size(B, G, qpk, D, max_len)))
+        return GDN2_ERR_WORKSPACE;
     const hipError_t err = launch_attn_decode(p, io_dtype, static_cast<hipStream_t>(stream));
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }

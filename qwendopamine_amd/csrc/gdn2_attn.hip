@@ -3,7 +3,9 @@
 // position, and attention over the cache up to that position, in one launch
 // per layer (the host's torch path issues about seventeen).
 //
-// One workgroup of eight waves per (sequence, KV group).  The token's rotated
+// Eight-wave workgroups per (sequence, KV group): one, or for caches longer
+// than 512 positions up to eight, each over its share of the positions, whose
+// partial softmax states a second kernel merges.  The token's rotated
 // q heads, k and v go to LDS (and k, v to the caches).  Each wave then walks
 // the cached positions j = (step * 8 + wave) * PS + slot: the DG lanes of a
 // slot each hold 8 channels (one 16-byte piece) of k_j and v_j, requested
@@ -66,6 +68,13 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
         return;
     }
     const int n = static_cast<int>(pos) + 1;
+    // This workgroup's share of the positions: split blockIdx.y of p.splits,
+    // in whole steps of the wave layout below.
+    const int per_step_all = kAttnWaves * PS;
+    const int steps = (n + per_step_all - 1) / per_step_all;
+    const int sps = (steps + p.splits - 1) / p.splits;
+    const int lo = static_cast<int>(blockIdx.y) * sps * per_step_all;
+    const int hi = lo + sps * per_step_all < n ? lo + sps * per_step_all : n;
     const T *x = static_cast<const T *>(p.qkv) + static_cast<int64_t>(b * G + g) * (QPK + 2) * D;
     const int64_t cbase = (static_cast<int64_t>(b) * G + g) * p.max_len * D;
     T *kc = static_cast<T *>(p.k_cache) + cbase;
@@ -73,6 +82,7 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
 
     // ---- RoPE of the QPK q heads and k (interleaved pairs, fp32, rounded to
     // the io dtype as the host's torch path), v as is ----
+    const bool store = blockIdx.y == 0;  // one split stores the token's k, v
     for (int e = tid; e < (QPK + 1) * (D / 2); e += 512) {
         const int h = e / (D / 2), i = e - h * (D / 2);
         const float x0 = io<T>::ld(x, h * D + 2 * i), x1 = io<T>::ld(x, h * D + 2 * i + 1);
@@ -88,14 +98,16 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
         } else {
             skv[0][2 * i] = y0;
             skv[0][2 * i + 1] = y1;
-            io<T>::st(kc, pos * D + 2 * i, y0);
-            io<T>::st(kc, pos * D + 2 * i + 1, y1);
+            if (store) {
+                io<T>::st(kc, pos * D + 2 * i, y0);
+                io<T>::st(kc, pos * D + 2 * i + 1, y1);
+            }
         }
     }
     for (int d = tid; d < D; d += 512) {
         const float v = io<T>::ld(x, (QPK + 1) * D + d);
         skv[1][d] = v;
-        io<T>::st(vc, pos * D + d, v);
+        if (store) io<T>::st(vc, pos * D + d, v);
     }
     __syncthreads();
 
@@ -115,21 +127,21 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
     }
     const int per_step = kAttnWaves * PS;
-    for (int j0 = 0; j0 < n; j0 += per_step * kUnroll) {
+    for (int j0 = lo; j0 < hi; j0 += per_step * kUnroll) {
         // kUnroll positions per slot requested before any is used; positions
         // from pos on read row 0 (always valid) and are skipped or replaced.
         uint4 kr[kUnroll], vr[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int j = j0 + u * per_step + wave * PS + slot;
-            const int64_t jl = j < pos ? j : 0;
+            const int64_t jl = j < pos && j < hi ? j : 0;
             kr[u] = *reinterpret_cast<const uint4 *>(kc + jl * D + dg * 8);
             vr[u] = *reinterpret_cast<const uint4 *>(vc + jl * D + dg * 8);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
         const int j = j0 + u * per_step + wave * PS + slot;
-        if (j >= n) continue;  // no shuffles below cross slots, so lanes may drop out per slot
+        if (j >= hi) continue;  // no shuffles below cross slots, so lanes may drop out per slot
         float kf[8], vf[8];
         if (j == pos) {
             // The token itself: its k, v from LDS (its cache store may still be in flight).
@@ -184,7 +196,10 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
         }
     }
     __syncthreads();
-    // Merge the waves and normalise.
+    // Merge the waves; one split normalises and stores, several leave their
+    // (max, sum, weighted values) for attn_merge_kernel.
+    float *part = p.splits > 1 ? p.part + ((static_cast<int64_t>(blockIdx.x) * p.splits + blockIdx.y) * QPK) * (D + 2)
+                               : nullptr;
     for (int e = tid; e < QPK * D; e += 512) {
         const int h = e / D, d = e - h * D;
         float mx = kNegBig;
@@ -197,20 +212,67 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
             num = fmaf(so[w][h][d], r, num);
             den = fmaf(sl[w][h], r, den);
         }
-        io<T>::st(out, e, num / den);
+        if (p.splits == 1) {
+            io<T>::st(out, e, num / den);
+        } else {
+            part[h * (D + 2) + d] = num;
+            if (d == 0) {
+                part[h * (D + 2) + D] = mx;
+                part[h * (D + 2) + D + 1] = den;
+            }
+        }
     }
+}
+
+// Combines the splits' partial states: thread (row, h, d) of the output.
+template <typename T, int D, int QPK>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeParams p)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t total = static_cast<int64_t>(p.B) * p.G * QPK * D;
+    if (e >= total) return;
+    const int d = static_cast<int>(e % D);
+    const int64_t bgh = e / D;                 // (b * G + g) * QPK + h
+    const int h = static_cast<int>(bgh % QPK);
+    const int64_t bg = bgh / QPK;
+    if (*p.pos < 0 || *p.pos >= p.max_len) {
+        io<T>::st(static_cast<T *>(p.out), e, 0.0f);
+        return;
+    }
+    const float *part = p.part + (bg * p.splits * QPK + h) * (D + 2);
+    const int64_t sstride = static_cast<int64_t>(QPK) * (D + 2);
+    float mx = kNegBig;
+    for (int s = 0; s < p.splits; ++s) mx = fmaxf(mx, part[s * sstride + D]);
+    float num = 0.0f, den = 0.0f;
+    for (int s = 0; s < p.splits; ++s) {
+        const float r = __expf(part[s * sstride + D] - mx);
+        num = fmaf(part[s * sstride + d], r, num);
+        den = fmaf(part[s * sstride + D + 1], r, den);
+    }
+    io<T>::st(static_cast<T *>(p.out), e, num / den);
+}
+
+template <typename T, int D, int QPK>
+hipError_t attn_q(const AttnDecodeParams &p, hipStream_t s)
+{
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, QPK>), dim3(static_cast<unsigned>(p.B * p.G), p.splits), dim3(512),
+                       0, s, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.splits == 1) return e;
+    const int64_t total = static_cast<int64_t>(p.B) * p.G * QPK * D;
+    hipLaunchKernelGGL((attn_merge_kernel<T, D, QPK>), dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                       s, p);
+    return hipGetLastError();
 }
 
 template <typename T, int D>
 hipError_t attn_d(const AttnDecodeParams &p, hipStream_t s)
 {
-    const dim3 grid(static_cast<unsigned>(p.B * p.G));
     switch (p.qpk) {
-    case 1: hipLaunchKernelGGL((attn_decode_kernel<T, D, 1>), grid, dim3(512), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((attn_decode_kernel<T, D, 2>), grid, dim3(512), 0, s, p); break;
-    default: hipLaunchKernelGGL((attn_decode_kernel<T, D, 4>), grid, dim3(512), 0, s, p); break;
+    case 1: return attn_q<T, D, 1>(p, s);
+    case 2: return attn_q<T, D, 2>(p, s);
+    default: return attn_q<T, D, 4>(p, s);
     }
-    return hipGetLastError();
 }
 
 template <typename T>
@@ -301,6 +363,19 @@ hipError_t launch_argmax_rows(const ArgmaxParams &p, int io_dtype, hipStream_t s
     default: hipLaunchKernelGGL((argmax_rows_kernel<f16_t>), grid, dim3(1024), 0, stream, p); break;
     }
     return hipGetLastError();
+}
+
+int attn_decode_splits(int64_t max_len)
+{
+    // About 512 positions per workgroup at a full cache, at most 8 splits.
+    const int64_t s = (max_len + 511) / 512;
+    return static_cast<int>(s < 1 ? 1 : (s > 8 ? 8 : s));
+}
+
+size_t attn_decode_workspace_floats(int B, int G, int qpk, int D, int64_t max_len)
+{
+    const int s = attn_decode_splits(max_len);
+    return s == 1 ? 0 : static_cast<size_t>(B) * G * s * qpk * (D + 2);
 }
 
 bool attn_decode_supported(int io_dtype, int qpk, int D)

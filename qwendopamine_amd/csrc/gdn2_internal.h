@@ -214,8 +214,15 @@ struct AttnDecodeParams {
     int64_t max_len;
     int B, G, qpk, D;
     float scale;
+    // Positions split over `splits` workgroups per KV group; with more than
+    // one, their partial states go to part (attn_decode_workspace_floats) and
+    // a second kernel merges them.
+    int splits;
+    float *part;
 };
 bool attn_decode_supported(int io_dtype, int qpk, int D);
+int attn_decode_splits(int64_t max_len);
+size_t attn_decode_workspace_floats(int B, int G, int qpk, int D, int64_t max_len);
 
 // Row-wise argmax: out[r * out_stride] = first index of the maximum of row r
 // (rows ld elements apart, n values; NaN is the maximum).

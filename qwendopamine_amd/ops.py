@@ -1377,9 +1377,12 @@ def attention_decode(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, in
     cf, sf = cos.reshape(-1)[:pairs].float().contiguous(), sin.reshape(-1)[:pairs].float().contiguous()
     out = torch.empty(B, n_head, D, dtype=qkv.dtype, device=qkv.device)
     lib = nat.load()
+    ws_bytes = lib.gdn2_attn_decode_workspace_size(B, G, qpk, D, L)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qkv.device) if ws_bytes else None
     st = lib.gdn2_attn_decode(
         nat.ptr(qc), nat.ptr(cf), nat.ptr(sf), pairs, nat.ptr(input_pos), nat.ptr(k_cache), nat.ptr(v_cache),
-        nat.ptr(out), nat.dtype_code(qkv.dtype), B, G, qpk, D, L, float(D) ** -0.5, nat.stream_handle(qkv.device),
+        nat.ptr(out), nat.dtype_code(qkv.dtype), B, G, qpk, D, L, float(D) ** -0.5, nat.ptr(ws), ws_bytes,
+        nat.stream_handle(qkv.device),
     )
     nat.check(st, name)
     return out
