@@ -225,6 +225,26 @@ int gdn2_skinny_linear(const void *x, int64_t x_row_stride, const void *weight, 
                        void *stream);
 
 /*
+ * A decoder block's residual add and pre-norm feeding a few-row linear layer,
+ * in one launch:
+ *   sum_out = x + residual                      (written once)
+ *   y       = gdn2_skinny_linear(RMSNorm(sum_out; norm_weight, eps), weight, bias)
+ * with the normalised rows formed while the product stages its input, with
+ * gdn2_add_rms_norm_fwd's roundings and summation order: equal bit for bit to
+ * gdn2_add_rms_norm_fwd followed by gdn2_skinny_linear.  Replaces
+ * `x = x + h; mlp(norm_2(x))`'s first GEMM in Block.forward (reference
+ * src/qwendopamine/models/gdn2_gpt/model.py:240-248, models/normalization.py:40-51).
+ * M <= 4, K in {512, 1024, 2048}, norm_weight in io_dtype; 16-byte aligned
+ * x, residual, sum_out, weight with row strides multiples of 8 elements;
+ * else GDN2_ERR_UNSUPPORTED.
+ */
+int gdn2_skinny_linear_addnorm(const void *x, int64_t x_row_stride, const void *residual,
+                               int64_t residual_row_stride, void *sum_out, int64_t sum_row_stride,
+                               const void *norm_weight, float eps, const void *weight, int64_t weight_row_stride,
+                               const void *bias, void *y, int64_t y_row_stride, int io_dtype, int M, int N, int K,
+                               void *stream);
+
+/*
  * Two few-row linear layers with a small inner dimension in one launch:
  *   y_i[m, n] = sum_k x_i[m, k] * weight_i[n, k] (+ bias_i[n]),  i = 0, 1
  * for the module's second-stage gate projections of a decode step (reference

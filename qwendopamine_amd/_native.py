@@ -70,6 +70,8 @@ SIGNATURES: dict[str, tuple] = {
     "gdn2_add_rms_norm_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i64, _i, _f, _vp]),
     "gdn2_silu_mul_fwd": (_i, [_vp, _i64, _vp, _i, _i64, _i, _vp]),
     "gdn2_skinny_linear": (_i, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i, _i, _i, _i, _vp]),
+    "gdn2_skinny_linear_addnorm": (_i, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _f, _vp, _i64, _vp, _vp, _i64, _i, _i,
+                                        _i, _i, _vp]),
     "gdn2_small_linear_pair": (_i, [_vp, _i64, _vp, _vp, _vp, _i64, _i, _vp, _i64, _vp, _vp, _vp, _i64, _i, _i, _i,
                                     _i, _vp]),
     "gdn2_argmax_rows": (_i, [_vp, _i64, _i, _i64, _i64, _vp, _i64, _vp]),

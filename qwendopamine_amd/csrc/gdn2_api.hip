@@ -300,6 +300,33 @@ int gdn2_skinny_linear(const void *x, int64_t x_row_stride, const void *weight, 
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+int gdn2_skinny_linear_addnorm(const void *x, int64_t x_row_stride, const void *residual,
+                               int64_t residual_row_stride, void *sum_out, int64_t sum_row_stride,
+                               const void *norm_weight, float eps, const void *weight, int64_t weight_row_stride,
+                               const void *bias, void *y, int64_t y_row_stride, int io_dtype, int M, int N, int K,
+                               void *stream)
+{
+    if (!valid_dtype(io_dtype) || M < 0 || N < 0 || K < 0) return GDN2_ERR_INVALID;
+    if (M == 0 || N == 0) return GDN2_OK;
+    if (!x || !residual || !sum_out || !norm_weight || !weight || !y || x_row_stride < K ||
+        residual_row_stride < K || sum_row_stride < K || weight_row_stride < K || y_row_stride < N)
+        return GDN2_ERR_INVALID;
+    if (!skinny_linear_supported(io_dtype, M, K) || M > 4 || K > 2048) return GDN2_ERR_UNSUPPORTED;
+    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) |
+          reinterpret_cast<uintptr_t>(sum_out) | reinterpret_cast<uintptr_t>(weight)) & 15) != 0 ||
+        x_row_stride % 8 != 0 || residual_row_stride % 8 != 0 || sum_row_stride % 8 != 0 || weight_row_stride % 8 != 0)
+        return GDN2_ERR_UNSUPPORTED;
+    if (N > 2147483647 - 8) return GDN2_ERR_UNSUPPORTED;
+    SkinnyParams p;
+    p.x = x; p.w = weight; p.bias = bias; p.y = y;
+    p.ldx = x_row_stride; p.ldw = weight_row_stride; p.ldy = y_row_stride;
+    p.M = M; p.N = N; p.K = K;
+    p.norm = 1; p.res = residual; p.nw = norm_weight; p.sum_out = sum_out;
+    p.ldres = residual_row_stride; p.ldsum = sum_row_stride; p.eps = eps;
+    const hipError_t err = launch_skinny_linear(p, io_dtype, static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
 int gdn2_small_linear_pair(const void *x0, int64_t x0_row_stride, const void *weight0, const void *bias0, void *y0,
                            int64_t y0_row_stride, int N0, const void *x1, int64_t x1_row_stride,
                            const void *weight1, const void *bias1, void *y1, int64_t y1_row_stride, int N1,

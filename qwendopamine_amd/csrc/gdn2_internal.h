@@ -181,6 +181,14 @@ struct SkinnyParams {
     void *y;
     int64_t ldx, ldw, ldy;  // row strides in elements
     int M, N, K;
+    // norm: the product's input is RMSNorm(x + res) with weight nw (io dtype)
+    // and eps, as gdn2_add_rms_norm_fwd computes it; workgroup 0 writes the
+    // sums x + res to sum_out.  M <= 4, K in {512, 1024, 2048}.
+    int norm = 0;
+    const void *res = nullptr, *nw = nullptr;
+    void *sum_out = nullptr;
+    int64_t ldres = 0, ldsum = 0;
+    float eps = 0.f;
 };
 bool skinny_linear_supported(int io_dtype, int M, int K);
 hipError_t launch_skinny_linear(const SkinnyParams &p, int io_dtype, hipStream_t stream);

@@ -39,6 +39,25 @@ __device__ __forceinline__ void widen8(uint4 u, float (&f)[8], bool bf)
     }
 }
 
+template <typename T>
+__device__ __forceinline__ uint4 narrow8(const float (&f)[8])
+{
+    unsigned w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint16_t lo, hi;
+        if constexpr (std::is_same<T, bf16_t>::value) {
+            lo = f32_to_bf16_bits(f[2 * i]);
+            hi = f32_to_bf16_bits(f[2 * i + 1]);
+        } else {
+            lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f[2 * i]));
+            hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f[2 * i + 1]));
+        }
+        w[i] = static_cast<unsigned>(lo) | (static_cast<unsigned>(hi) << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // MM: rows of x the instantiation holds (p.M <= MM, rows past p.M are zero
 // and not stored); NP: 16-byte pieces of a row per lane (K = 512 NP); RPW:
 // rows of W per wave.  Workgroup b takes the groups of kWaves * RPW rows
@@ -69,6 +88,55 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
         }
     };
     request(blockIdx.x);
+    if (p.norm) {
+        // x = RMSNorm(x + res) staged by wave m for row m (M <= 4, NP <= 4),
+        // with gated_rmsnorm_vec_kernel's roundings and summation order (lane l
+        // holds pieces l + 64 v, squares summed piece by piece, then the
+        // xor-tree over the 64 lanes), so the staged rows equal
+        // gdn2_add_rms_norm_fwd's output bit for bit.  Workgroup 0 stores the
+        // residual sums.
+        if (wave < MM) {
+            uint4 st[NP];
+            if (wave < p.M) {
+                float sv[NP][8], sq = 0.0f;
+                const T *xr = x + static_cast<int64_t>(wave) * p.ldx;
+                const T *rr = static_cast<const T *>(p.res) + static_cast<int64_t>(wave) * p.ldres;
+#pragma unroll
+                for (int v = 0; v < NP; ++v) {
+                    float a[8], b[8];
+                    widen8(*reinterpret_cast<const uint4 *>(xr + (v * 64 + lane) * 8), a, BF);
+                    widen8(*reinterpret_cast<const uint4 *>(rr + (v * 64 + lane) * 8), b, BF);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) sv[v][e] = round_to<T>(a[e] + b[e]);
+                }
+#pragma unroll
+                for (int v = 0; v < NP; ++v)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) sq += round_to<T>(sv[v][e] * sv[v][e]);
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) sq += __shfl_xor(sq, o, 64);
+                const float var = round_to<T>(sq / static_cast<float>(p.K));
+                const float inv = round_to<T>(rsqrtf(round_to<T>(var + p.eps)));
+                T *so = static_cast<T *>(p.sum_out) + static_cast<int64_t>(wave) * p.ldsum;
+#pragma unroll
+                for (int v = 0; v < NP; ++v) {
+                    if (blockIdx.x == 0) *reinterpret_cast<uint4 *>(so + (v * 64 + lane) * 8) = narrow8<T>(sv[v]);
+                    float o8[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float wgt = io<T>::ld(static_cast<const T *>(p.nw), (v * 64 + lane) * 8 + e);
+                        o8[e] = round_to<T>(round_to<T>(sv[v][e] * inv) * wgt);
+                    }
+                    st[v] = narrow8<T>(o8);
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < NP; ++v) st[v] = make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int v = 0; v < NP; ++v) sx[wave * PPR + v * 64 + lane] = st[v];
+        }
+    } else {
     // x rows into LDS (rows past M as zeros).
 #pragma unroll 4
     for (int i0 = 0; i0 < MM * PPR; i0 += 256) {
@@ -78,6 +146,7 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
             sx[i] = m < p.M ? *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(m) * p.ldx + c * 8)
                             : make_uint4(0u, 0u, 0u, 0u);
         }
+    }
     }
     __syncthreads();
 

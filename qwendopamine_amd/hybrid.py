@@ -289,6 +289,12 @@ class Block(nn.Module):
         else:
             x, n1 = ops.add_rms_norm(x, pending, self.norm_1.weight, self.norm_1.eps)
         h = self._mix(n1, cos, sin, input_pos, mask)
+        if x.shape[0] * x.shape[1] <= 4:
+            # Decode-sized rows: the add and norm_2 formed while SwiGLU's w1 / w2
+            # product stages its input (one launch less, the same bits).
+            sw = self.mlp.swiglu
+            ab, x = ops.linear_addnorm(x, h, self.norm_2.weight, self.norm_2.eps, *sw._fused12())
+            return x, ops.linear(ops.silu_mul(ab), sw.w3.weight, sw.w3.bias)
         x, n2 = ops.add_rms_norm(x, h, self.norm_2.weight, self.norm_2.eps)
         return x, self.mlp(n2)
 

@@ -44,6 +44,7 @@ __all__ = [
     "add_rms_norm",
     "silu_mul",
     "linear",
+    "linear_addnorm",
     "linear_pair",
     "argmax_rows",
     "attention_decode",
@@ -1276,6 +1277,40 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
         return F.linear(x, weight, bias)
     nat.check(st, "linear")
     return y
+
+
+@torch.compiler.disable
+def linear_addnorm(x: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                   weight: torch.Tensor, bias: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``s, n = add_rms_norm(x, residual, norm_weight, eps); return linear(n, weight, bias), s``
+    in one launch on decode-sized rows (at most 4, K in {512, 1024, 2048}, 16-bit, the
+    norm weight in the io dtype): the normalised rows are formed while the few-row
+    kernel stages its input, bit for bit as the two ops.  Other shapes run the two ops."""
+    K = x.shape[-1]
+    M = x.numel() // K if K else 0
+    N = weight.shape[0]
+    if (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and 1 <= M <= 4 and K in (512, 1024, 2048)
+            and residual.shape == x.shape and residual.dtype == x.dtype and norm_weight.dtype == x.dtype
+            and norm_weight.numel() == K and weight.dtype == x.dtype and weight.dim() == 2 and weight.shape[1] == K
+            and weight.stride(1) == 1 and N <= _SKINNY_MAX_N and (bias is None or bias.dtype == x.dtype)
+            and not (torch.is_grad_enabled()
+                     and any(t is not None and t.requires_grad for t in (x, residual, norm_weight, weight, bias)))):
+        xc, rc = x.reshape(M, K).contiguous(), residual.reshape(M, K).contiguous()
+        nwc = norm_weight.detach().contiguous()
+        s = torch.empty_like(x)
+        y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=x.device)
+        b = None if bias is None else bias.contiguous()
+        lib = nat.load()
+        st = lib.gdn2_skinny_linear_addnorm(
+            nat.ptr(xc), K, nat.ptr(rc), K, nat.ptr(s), K, nat.ptr(nwc), float(eps), nat.ptr(weight),
+            weight.stride(0), nat.ptr(b), nat.ptr(y), N, nat.dtype_code(x.dtype), M, N, K,
+            nat.stream_handle(x.device),
+        )
+        if st != nat.ERR_UNSUPPORTED:
+            nat.check(st, "linear_addnorm")
+            return y, s
+    s, n = add_rms_norm(x, residual, norm_weight, eps)
+    return linear(n, weight, bias), s
 
 
 @torch.compiler.disable

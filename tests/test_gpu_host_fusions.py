@@ -496,3 +496,62 @@ def test_argmax_rows_matches_torch(gpu_device, dtype, rows, n):
     assert torch.equal(got, ref), (got.flatten().tolist(), ref.flatten().tolist())
     assert torch.equal(wide[:, 1:2], ref) and not bool(wide[:, 0].any()) and not bool(wide[:, 2].any())
     assert torch.equal(argmax_rows(big[:, 1]), big[:, 1].argmax(-1, keepdim=True))
+
+
+@pytest.mark.parametrize("dtype,M,K,N", [(torch.bfloat16, 4, 1024, 6144), (torch.bfloat16, 1, 512, 100),
+                                         (torch.float16, 3, 2048, 700), (torch.bfloat16, 5, 1024, 64)])
+def test_linear_addnorm_equals_add_norm_then_linear(gpu_device, dtype, M, K, N):
+    """The residual add and RMSNorm formed while the few-row kernel stages its input:
+    bit for bit ``add_rms_norm`` followed by ``linear`` for both outputs (the product
+    and the residual sums); 5 rows run the two ops."""
+    from qwendopamine_amd.ops import add_rms_norm, linear, linear_addnorm
+
+    print(f"[case] linear_addnorm dtype={dtype} M={M} K={K} N={N}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(M * K + N)
+    x = (torch.randn(M, K, generator=g) * 2).to(gpu_device, dtype)
+    h = torch.randn(M, K, generator=g).to(gpu_device, dtype)
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(gpu_device, dtype)
+    w = (torch.randn(N, K, generator=g) * K ** -0.5).to(gpu_device, dtype)
+    with torch.no_grad():
+        y, s = linear_addnorm(x, h, nw, 1e-5, w)
+        s_ref, n_ref = add_rms_norm(x, h, nw, 1e-5)
+        y_ref = linear(n_ref, w)
+    torch.cuda.synchronize()
+    _bits_equal(s, s_ref)
+    _bits_equal(y, y_ref)
+
+
+def test_hybrid_decode_with_norm_in_projection(gpu_device, monkeypatch):
+    """A bf16 host whose width the add-and-norm staging takes (512): decode-step logits
+    with the fused passes equal the unfused host's bit for bit."""
+    from qwendopamine_amd import ops
+    from qwendopamine_amd.hybrid import HybridConfig, HybridDecoder
+
+    print("[case] hybrid decode with the norm in the w1|w2 projection", flush=True)
+    torch.manual_seed(29)
+    cfg = HybridConfig(n_layer=3, n_embd=512, n_head=8, head_size=64, n_query_groups=4, intermediate_size=1024,
+                       vocab_size=1000, gdn2_layers=[0, 1], block_size=256)
+    m = HybridDecoder(cfg).to(gpu_device, torch.bfloat16).eval()
+    idx = torch.randint(0, 1000, (3, 40), device=gpu_device)
+    calls = {"n": 0}
+    real = ops.linear_addnorm
+
+    def counted(*a, **k):
+        calls["n"] += 1
+        return real(*a, **k)
+
+    def run():
+        with torch.no_grad():
+            m.setup_caches(3, 42)
+            m(idx, input_pos=torch.arange(40, device=gpu_device))
+            out = [m(idx[:, -1:], input_pos=torch.tensor([40 + i], device=gpu_device)) for i in range(2)]
+        torch.cuda.synchronize()
+        return out
+
+    monkeypatch.setattr(ops, "linear_addnorm", counted)
+    fused = run()
+    assert calls["n"] == 2 * 3
+    monkeypatch.setattr(ops, "add_rms_norm_supported", lambda x: False)
+    plain = run()
+    for f, p in zip(fused, plain):
+        _bits_equal(f, p)
