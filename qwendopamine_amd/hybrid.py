@@ -376,10 +376,13 @@ class HybridDecoder(nn.Module):
                 blk.attn.kv_cache = (torch.zeros(shape, dtype=p.dtype, device=p.device),
                                      torch.zeros(shape, dtype=p.dtype, device=p.device))
 
-    def forward(self, idx: torch.Tensor, input_pos: torch.Tensor | None = None) -> torch.Tensor:
+    def forward(self, idx: torch.Tensor, input_pos: torch.Tensor | None = None,
+                last_only: bool = False) -> torch.Tensor:
         """Logits ``[B, T, vocab]``. With ``input_pos`` (positions of ``idx``'s tokens,
         a device tensor), the caches are read and extended: the first cached call after
-        ``setup_caches`` is the prefill, later ones continue it."""
+        ``setup_caches`` is the prefill, later ones continue it.  ``last_only`` applies the
+        final norm and the LM head to the last position only (logits ``[B, 1, vocab]``):
+        what greedy decoding reads of a prefill, without the ``T x vocab`` product."""
         t = idx.shape[1]
         cos, sin = self._rope_tables(t, idx.device)
         mask = None
@@ -396,12 +399,17 @@ class HybridDecoder(nn.Module):
             pending = None
             for blk in self.h:
                 x, pending = blk.forward_pending(x, pending, cos, sin, input_pos, mask)
+            if last_only:
+                x = x[:, -1:]
+                pending = None if pending is None else pending[:, -1:]
             if pending is None:
                 return ops.linear(self.ln_f(x), self.lm_head.weight)
             _, xn = ops.add_rms_norm(x, pending, self.ln_f.weight, self.ln_f.eps)
             return ops.linear(xn, self.lm_head.weight)
         for blk in self.h:
             x = blk(x, cos, sin, input_pos, mask)
+        if last_only:
+            x = x[:, -1:]
         return self.lm_head(self.ln_f(x))
 
 
@@ -426,7 +434,7 @@ class GreedyDecoder:
         dev = prompt.device
         self.model.setup_caches(B, T + max_new_tokens)
         self.graph = None
-        logits = self.model(prompt, input_pos=torch.arange(T, device=dev))[:, -1]
+        logits = self.model(prompt, input_pos=torch.arange(T, device=dev), last_only=True)[:, -1]
         self.tok = logits.argmax(-1, keepdim=True)
         self.pos = torch.full((1,), T, dtype=torch.long, device=dev)
         if self.keep_logits:

@@ -90,3 +90,23 @@ def test_c3_full_size_streaming(gpu_device):
     for t in (0, 127, 128, 131):
         err = rel_l2(inc[:, t], full[:, t].double().cpu().numpy())
         assert err <= 1e-4, (t, err)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_last_only_logits(gpu_device, dtype):
+    """``last_only`` (the prefill of greedy decoding) gives the full forward's last
+    position: the same rows through the final norm, the LM head on one row instead of T
+    (torch's GEMM may tile them differently, hence the tolerance)."""
+    print(f"[case] hybrid last_only logits {dtype}", flush=True)
+    m = _small(dtype, gpu_device)
+    idx = torch.randint(0, 1000, (2, 70), device=gpu_device)
+    with torch.no_grad():
+        full = m(idx)
+        last = m(idx, last_only=True)
+        m.setup_caches(2, 70)
+        cached = m(idx, input_pos=torch.arange(70, device=gpu_device), last_only=True)
+    torch.cuda.synchronize()
+    assert last.shape == (2, 1, 1000) and cached.shape == (2, 1, 1000)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert rel_l2(last[:, 0], full[:, -1].double().cpu().numpy()) <= tol
+    assert rel_l2(cached[:, 0], full[:, -1].double().cpu().numpy()) <= (1e-4 if dtype == torch.float32 else 2e-2)
