@@ -742,10 +742,17 @@ chunk_prep_kernel(ChunkParams p, int items)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 // Four partial sums: the dependent FMA chain of row i is i / 4 long.
+                // Row i of the block is read as 16-byte pieces (one LDS request per
+                // four values; the products and their order are unchanged).
                 float acc[4] = {(i == j) ? 1.f : 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int mm = 0; mm < i; ++mm)
-                    acc[mm & 3] = fmaf(-sL[(16 * R + i) * LDF + 16 * R + mm], x[mm], acc[mm & 3]);
+                for (int q4 = 0; q4 < (i + 3) / 4; ++q4) {
+                    const float4 l4 = *reinterpret_cast<const float4 *>(&sL[(16 * R + i) * LDF + 16 * R + 4 * q4]);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (4 * q4 + e < i) acc[e] = fmaf(-lv[e], x[4 * q4 + e], acc[e]);
+                }
                 x[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
             }
 #pragma unroll
