@@ -201,9 +201,13 @@ class CausalSelfAttention(nn.Module):
 
     def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                 input_pos: torch.Tensor | None = None, mask: torch.Tensor | None = None) -> torch.Tensor:
-        b, t, _ = x.shape
+        return self.forward_qkv(ops.linear(x, self.attn.weight, self.attn.bias), cos, sin, input_pos, mask)
+
+    def forward_qkv(self, qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                    input_pos: torch.Tensor | None = None, mask: torch.Tensor | None = None) -> torch.Tensor:
+        """``forward`` from the fused ``attn`` projection's output ``[B, T, (n_head + 2 G) D]``."""
+        b, t, _ = qkv.shape
         G, qpk, D = self.n_query_groups, self.n_head // self.n_query_groups, self.head_size
-        qkv = ops.linear(x, self.attn.weight, self.attn.bias)
         if (t == 1 and input_pos is not None and self.kv_cache is not None and _inference(qkv)
                 and ops.attention_decode_supported(qkv, qpk, D)):
             # RoPE, the cache store and the attention of the token in one HIP launch.
@@ -284,12 +288,19 @@ class Block(nn.Module):
         pending ``m`` (or None).  Each residual add then runs in one HIP pass with the
         norm that reads its result (``ops.add_rms_norm``, bit-identical to the add and
         the norm apart).  Inference on GPU tensors only."""
+        decode_rows = x.shape[0] * x.shape[1] <= 4
         if pending is None:
-            n1 = self.norm_1(x)
+            h = self._mix(self.norm_1(x), cos, sin, input_pos, mask)
+        elif decode_rows and not self.use_gdn2 and input_pos is not None:
+            # Attention layer on decode-sized rows: the add and norm_1 formed while
+            # the qkv product stages its input (one launch less, the same bits).
+            at = self.attn
+            qkv, x = ops.linear_addnorm(x, pending, self.norm_1.weight, self.norm_1.eps, at.attn.weight, at.attn.bias)
+            h = at.forward_qkv(qkv, cos, sin, input_pos, mask)
         else:
             x, n1 = ops.add_rms_norm(x, pending, self.norm_1.weight, self.norm_1.eps)
-        h = self._mix(n1, cos, sin, input_pos, mask)
-        if x.shape[0] * x.shape[1] <= 4:
+            h = self._mix(n1, cos, sin, input_pos, mask)
+        if decode_rows:
             # Decode-sized rows: the add and norm_2 formed while SwiGLU's w1 / w2
             # product stages its input (one launch less, the same bits).
             sw = self.mlp.swiglu
