@@ -444,6 +444,22 @@ class GatedDeltaNet2(nn.Module):
         drop(self, "_in_cache", "_gate_cache")
         return super()._apply(fn, *args, **kwargs)
 
+    def _fused_decode_ok(self, x: torch.Tensor) -> bool:
+        """Whether a single-token inference call on ``x`` can take the fused decode kernel
+        (the caller has checked the token count, padding and ``cu_seqlens``)."""
+        convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d) if self.use_short_conv else ()
+        return bool(
+            self.fused_decode and self.use_short_conv and self.fp32_decay and not self.allow_neg_eigval
+            and self.num_v_heads == self.num_heads and self.head_k_dim == self.head_v_dim
+            and self.head_k_dim in (64, 128) and self.conv_size == 4
+            and all(c.activation == "silu" for c in convs)
+            and self._algorithm("fused_recurrent" if not self.training else self.mode,
+                                resolve_gdn2_backend(self.backend, training=self.training, seq_len=1),
+                                False) == "recurrent"
+            and _inference(x, self.A_log, self.dt_bias, self.b_proj.weight, self.w_proj.weight,
+                           *(c.conv1d.weight for c in convs), self.o_norm.weight,
+                           self.f_proj[1].weight, self.g_proj[1].weight))
+
     def _decode_fused(self, x, past_key_values, recurrent_state, conv_states, want_state, in_place,
                       use_cache):
         """Single-token inference step on the fused decode kernel (``ops.decode_step_fused``):
@@ -453,10 +469,39 @@ class GatedDeltaNet2(nn.Module):
         batch = x.shape[0]
         W_in, sizes = self._fused_input_weight()
         y = ops.linear(x.reshape(batch, x.shape[-1]), W_in)  # [B, sum(sizes)]
+        return self._decode_fused_rows(y, x.dtype, past_key_values, recurrent_state, conv_states, want_state,
+                                       in_place, use_cache)
+
+    def decode_step_from_residual(self, residual: torch.Tensor, delta: torch.Tensor, norm_weight: torch.Tensor,
+                                  eps: float, cache: dict) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """A host block's single-token step from its pre-norm inputs: ``s = residual +
+        delta``, ``x = RMSNorm(s)`` (the block's norm_1) and this mixer on ``x``, with the
+        add and the norm formed while the input projections stage their input
+        (``ops.linear_addnorm``, bit for bit the separate ops).  ``cache`` is the layer's
+        cache dict; its tensors are updated where they lie (as ``update_cache_in_place``)
+        and the dict's entries set to the new states.  Returns
+        ``(s, mixer output)``, or None when the fused decode path does not apply (the
+        caller then runs the ops apart).  No counterpart in the reference."""
+        batch, seq_len, _ = residual.shape
+        state = cache.get("recurrent_state") if cache else None
+        conv = cache.get("conv_state") if cache else None
+        if (seq_len != 1 or state is None or conv is None or any(c is None for c in conv)
+                or state.dtype != torch.float32 or not state.is_contiguous()
+                or not _inference(residual, delta, norm_weight) or not self._fused_decode_ok(residual)):
+            return None
+        W_in, sizes = self._fused_input_weight()
+        y, s = ops.linear_addnorm(residual.reshape(batch, -1), delta.reshape(batch, -1), norm_weight, eps, W_in)
+        out, _, _ = self._decode_fused_rows(y, residual.dtype, cache, state, tuple(conv), True, True, True)
+        return s.view_as(residual), out
+
+    def _decode_fused_rows(self, y, dt, past_key_values, recurrent_state, conv_states, want_state, in_place,
+                           use_cache):
+        """The fused decode step from the input projections' output ``y`` [B, sum(sizes)]."""
+        batch = y.shape[0]
+        _, sizes = self._fused_input_weight()
         qr, kr, vr, b, w, f0, g0 = y.split(sizes, dim=-1)
         g, z = ops.linear_pair(f0, self.f_proj[1].weight, self.f_proj[1].bias, g0, self.g_proj[1].weight,
                                self.g_proj[1].bias)
-        dt = x.dtype
         caches = list(conv_states) if all(c is not None for c in conv_states) else None
         if caches is not None and not all(c.dtype == dt and c.is_contiguous() for c in caches):
             caches, in_place = [c.to(dt).contiguous() for c in caches], False
@@ -540,14 +585,7 @@ class GatedDeltaNet2(nn.Module):
                            self.w_proj.weight)
                 and self.fp32_decay and not self.allow_neg_eigval)
         convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d) if self.use_short_conv else ()
-        if (fuse and self.fused_decode and seq_len == 1 and not padded and cu_seqlens is None and self.use_short_conv
-                and self.num_v_heads == self.num_heads and self.head_k_dim == self.head_v_dim
-                and self.head_k_dim in (64, 128) and self.conv_size == 4
-                and all(c.activation == "silu" for c in convs)
-                and self._algorithm(mode, resolve_gdn2_backend(self.backend, training=self.training,
-                                                               seq_len=seq_len), False) == "recurrent"
-                and _inference(x, *(c.conv1d.weight for c in convs), self.o_norm.weight,
-                               self.f_proj[1].weight, self.g_proj[1].weight)):
+        if fuse and seq_len == 1 and not padded and cu_seqlens is None and self._fused_decode_ok(x):
             return self._decode_fused(x, past_key_values, recurrent_state, (cq, ck, cv), want_state,
                                       in_place, use_cache)
         g0 = None

@@ -289,7 +289,18 @@ class Block(nn.Module):
         norm that reads its result (``ops.add_rms_norm``, bit-identical to the add and
         the norm apart).  Inference on GPU tensors only."""
         decode_rows = x.shape[0] * x.shape[1] <= 4
-        if pending is None:
+        fused = None
+        if (pending is not None and decode_rows and self.use_gdn2 and input_pos is not None
+                and self.gdn2_cache is not None and x.shape[1] == 1):
+            # gdn2 layer's decode step: the add and norm_1 formed while the mixer's
+            # input projections stage their input (one launch less, the same bits).
+            step = dict(self.gdn2_cache)
+            fused = self.attn.decode_step_from_residual(x, pending, self.norm_1.weight, self.norm_1.eps, step)
+            if fused is not None:
+                self._keep_cache(step)
+        if fused is not None:
+            x, h = fused
+        elif pending is None:
             h = self._mix(self.norm_1(x), cos, sin, input_pos, mask)
         elif decode_rows and not self.use_gdn2 and input_pos is not None:
             # Attention layer on decode-sized rows: the add and norm_1 formed while
@@ -328,13 +339,17 @@ class Block(nn.Module):
             return h
         step = dict(self.gdn2_cache)
         h, _, step = self.attn(x, past_key_values=step, use_cache=True, update_cache_in_place=True)
-        # Decode steps update the cache where it lies; other calls return fresh tensors.
+        self._keep_cache(step)
+        return h
+
+    def _keep_cache(self, step: dict) -> None:
+        """Decode steps update the cache where it lies; other calls return fresh tensors,
+        which are copied into the cache's own (so its addresses stay fixed)."""
         if step["recurrent_state"] is not self.gdn2_cache["recurrent_state"]:
             self.gdn2_cache["recurrent_state"].copy_(step["recurrent_state"])
         for dst, src in zip(self.gdn2_cache["conv_state"], step["conv_state"]):
             if src is not dst:
                 dst.copy_(src)
-        return h
 
 
 class HybridDecoder(nn.Module):

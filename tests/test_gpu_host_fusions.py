@@ -550,9 +550,9 @@ def test_hybrid_decode_with_norm_in_projection(gpu_device, monkeypatch):
 
     monkeypatch.setattr(ops, "linear_addnorm", counted)
     fused = run()
-    # Per decode step: norm_2 of each of the 3 blocks, and norm_1 of the attention
-    # block (block 2; block 0's norm_1 has no pending add).
-    assert calls["n"] == 2 * (3 + 1)
+    # Per decode step: norm_2 of each of the 3 blocks, and norm_1 of blocks 1 (gdn2)
+    # and 2 (attention); block 0's norm_1 has no pending add.
+    assert calls["n"] == 2 * (3 + 2)
     monkeypatch.setattr(ops, "add_rms_norm_supported", lambda x: False)
     plain = run()
     for f, p in zip(fused, plain):
