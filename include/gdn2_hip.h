@@ -245,6 +245,23 @@ int gdn2_skinny_linear_addnorm(const void *x, int64_t x_row_stride, const void *
                                void *stream);
 
 /*
+ * gdn2_skinny_linear_addnorm whose output is SwiGLU's gated product: with
+ * weight the stacked [w1; w2] (N rows, N even), y[m, c] =
+ * round(round(silu(a)) * b) for a = p[m, c], b = p[m, c + N / 2] of the
+ * product p (each rounded to io_dtype first), y [M, N / 2]: bit for bit
+ * gdn2_skinny_linear_addnorm followed by gdn2_silu_mul_fwd, in one launch (a
+ * wave holds rows c and c + N / 2).  Replaces `F.silu(w1(n)) * w2(n)` with
+ * n = norm_2(x + h) (reference src/qwendopamine/models/gdn2_gpt/model.py:74-78,
+ * :240-248) on a decode step's rows.  Same limits as
+ * gdn2_skinny_linear_addnorm.
+ */
+int gdn2_skinny_linear_addnorm_swiglu(const void *x, int64_t x_row_stride, const void *residual,
+                                      int64_t residual_row_stride, void *sum_out, int64_t sum_row_stride,
+                                      const void *norm_weight, float eps, const void *weight,
+                                      int64_t weight_row_stride, const void *bias, void *y, int64_t y_row_stride,
+                                      int io_dtype, int M, int N, int K, void *stream);
+
+/*
  * Two few-row linear layers with a small inner dimension in one launch:
  *   y_i[m, n] = sum_k x_i[m, k] * weight_i[n, k] (+ bias_i[n]),  i = 0, 1
  * for the module's second-stage gate projections of a decode step (reference

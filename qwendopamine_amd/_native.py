@@ -72,6 +72,8 @@ SIGNATURES: dict[str, tuple] = {
     "gdn2_skinny_linear": (_i, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i, _i, _i, _i, _vp]),
     "gdn2_skinny_linear_addnorm": (_i, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _f, _vp, _i64, _vp, _vp, _i64, _i, _i,
                                         _i, _i, _vp]),
+    "gdn2_skinny_linear_addnorm_swiglu": (_i, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _f, _vp, _i64, _vp, _vp, _i64,
+                                               _i, _i, _i, _i, _vp]),
     "gdn2_small_linear_pair": (_i, [_vp, _i64, _vp, _vp, _vp, _i64, _i, _vp, _i64, _vp, _vp, _vp, _i64, _i, _i, _i,
                                     _i, _vp]),
     "gdn2_argmax_rows": (_i, [_vp, _i64, _i, _i64, _i64, _vp, _i64, _vp]),

@@ -300,16 +300,17 @@ int gdn2_skinny_linear(const void *x, int64_t x_row_stride, const void *weight, 
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
-int gdn2_skinny_linear_addnorm(const void *x, int64_t x_row_stride, const void *residual,
+static int skinny_addnorm_impl(const void *x, int64_t x_row_stride, const void *residual,
                                int64_t residual_row_stride, void *sum_out, int64_t sum_row_stride,
                                const void *norm_weight, float eps, const void *weight, int64_t weight_row_stride,
                                const void *bias, void *y, int64_t y_row_stride, int io_dtype, int M, int N, int K,
-                               void *stream)
+                               int glu, void *stream)
 {
     if (!valid_dtype(io_dtype) || M < 0 || N < 0 || K < 0) return GDN2_ERR_INVALID;
     if (M == 0 || N == 0) return GDN2_OK;
+    if (glu && N % 2 != 0) return GDN2_ERR_INVALID;
     if (!x || !residual || !sum_out || !norm_weight || !weight || !y || x_row_stride < K ||
-        residual_row_stride < K || sum_row_stride < K || weight_row_stride < K || y_row_stride < N)
+        residual_row_stride < K || sum_row_stride < K || weight_row_stride < K || y_row_stride < (glu ? N / 2 : N))
         return GDN2_ERR_INVALID;
     if (!skinny_linear_supported(io_dtype, M, K) || M > 4 || K > 2048) return GDN2_ERR_UNSUPPORTED;
     if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) |
@@ -323,8 +324,29 @@ int gdn2_skinny_linear_addnorm(const void *x, int64_t x_row_stride, const void *
     p.M = M; p.N = N; p.K = K;
     p.norm = 1; p.res = residual; p.nw = norm_weight; p.sum_out = sum_out;
     p.ldres = residual_row_stride; p.ldsum = sum_row_stride; p.eps = eps;
+    p.glu_out = glu;
     const hipError_t err = launch_skinny_linear(p, io_dtype, static_cast<hipStream_t>(stream));
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+}
+
+int gdn2_skinny_linear_addnorm(const void *x, int64_t x_row_stride, const void *residual,
+                               int64_t residual_row_stride, void *sum_out, int64_t sum_row_stride,
+                               const void *norm_weight, float eps, const void *weight, int64_t weight_row_stride,
+                               const void *bias, void *y, int64_t y_row_stride, int io_dtype, int M, int N, int K,
+                               void *stream)
+{
+    return skinny_addnorm_impl(x, x_row_stride, residual, residual_row_stride, sum_out, sum_row_stride, norm_weight,
+                               eps, weight, weight_row_stride, bias, y, y_row_stride, io_dtype, M, N, K, 0, stream);
+}
+
+int gdn2_skinny_linear_addnorm_swiglu(const void *x, int64_t x_row_stride, const void *residual,
+                                      int64_t residual_row_stride, void *sum_out, int64_t sum_row_stride,
+                                      const void *norm_weight, float eps, const void *weight,
+                                      int64_t weight_row_stride, const void *bias, void *y, int64_t y_row_stride,
+                                      int io_dtype, int M, int N, int K, void *stream)
+{
+    return skinny_addnorm_impl(x, x_row_stride, residual, residual_row_stride, sum_out, sum_row_stride, norm_weight,
+                               eps, weight, weight_row_stride, bias, y, y_row_stride, io_dtype, M, N, K, 1, stream);
 }
 
 int gdn2_small_linear_pair(const void *x0, int64_t x0_row_stride, const void *weight0, const void *bias0, void *y0,

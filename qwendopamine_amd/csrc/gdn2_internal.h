@@ -189,6 +189,10 @@ struct SkinnyParams {
     void *sum_out = nullptr;
     int64_t ldres = 0, ldsum = 0;
     float eps = 0.f;
+    // glu_out: y[m, c] = round(round(silu(a)) * b) for a = row c and b = row
+    // c + N / 2 of the product (N even; y has N / 2 columns): SwiGLU's product
+    // as the epilogue of the fused w1 / w2 projection.  K <= 2048.
+    int glu_out = 0;
 };
 bool skinny_linear_supported(int io_dtype, int M, int K);
 hipError_t launch_skinny_linear(const SkinnyParams &p, int io_dtype, hipStream_t stream);

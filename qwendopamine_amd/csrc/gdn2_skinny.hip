@@ -77,11 +77,19 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
     // This wave's rows of W in a group (rows past N read row N-1); the first
     // group's are requested before the x rows are staged.
     uint4 wr[kRowsPerWave][NP];
+    // Row r of the wave in group grp: rows n0 + r, or with the SwiGLU epilogue
+    // (RPW = 2) rows c and c + N / 2 of output column c.
+    auto row_of = [&](int grp, int r) __attribute__((always_inline)) {
+        if constexpr (RPW == 2) {
+            if (p.glu_out) return (grp * kWaves + wave) + r * (p.N / 2);
+        }
+        return (grp * kWaves + wave) * kRowsPerWave + r;
+    };
     auto request = [&](int grp) __attribute__((always_inline)) {
-        const int n0 = (grp * kWaves + wave) * kRowsPerWave;
 #pragma unroll
         for (int r = 0; r < kRowsPerWave; ++r) {
-            const int row = n0 + r < p.N ? n0 + r : p.N - 1;
+            const int rr = row_of(grp, r);
+            const int row = rr < p.N ? rr : p.N - 1;
 #pragma unroll
             for (int c = 0; c < NP; ++c)
                 wr[r][c] = *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(row) * p.ldw + (c * 64 + lane) * 8);
@@ -181,6 +189,30 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
         for (int m = 0; m < MM; ++m)
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) acc[r][m] += __shfl_xor(acc[r][m], o, 64);
+    if constexpr (RPW == 2) {
+        if (p.glu_out) {
+            // SwiGLU epilogue: lane m stores out[m, c] = round(round(silu(a)) * b)
+            // from a = round(row c), b = round(row c + N / 2), as a product
+            // followed by gdn2_silu_mul_fwd computes it.
+            const int c = grp * kWaves + wave;
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                if (lane == m && m < p.M && c < p.N / 2) {
+                    float a = acc[0][m], b = acc[1][m];
+                    if (p.bias) {
+                        a += io<T>::ld(static_cast<const T *>(p.bias), c);
+                        b += io<T>::ld(static_cast<const T *>(p.bias), c + p.N / 2);
+                    }
+                    a = round_to<T>(a);
+                    b = round_to<T>(b);
+                    const float sl = a / (1.0f + expf(-a));
+                    io<T>::st(static_cast<T *>(p.y), static_cast<int64_t>(m) * p.ldy + c,
+                              round_to<T>(round_to<T>(sl) * b));
+                }
+            }
+            continue;
+        }
+    }
     // Lane r * MM + m stores output (m, n0 + r).
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r) {
@@ -219,7 +251,8 @@ hipError_t skinny_np(const SkinnyParams &p, hipStream_t s)
     } else {
         constexpr int LIM = 8 / NP < 16 / MM ? 8 / NP : 16 / MM;
         if constexpr (LIM >= 2)
-            if (p.N > 2048) return skinny_launch<T, MM, NP, 2>(p, s);
+            if (p.N > 2048 || p.glu_out) return skinny_launch<T, MM, NP, 2>(p, s);
+        if (p.glu_out) return hipErrorInvalidValue;  // rejected before (the epilogue needs two rows per wave)
         return skinny_launch<T, MM, NP, 1>(p, s);
     }
 }

@@ -315,8 +315,8 @@ class Block(nn.Module):
             # Decode-sized rows: the add and norm_2 formed while SwiGLU's w1 / w2
             # product stages its input (one launch less, the same bits).
             sw = self.mlp.swiglu
-            ab, x = ops.linear_addnorm(x, h, self.norm_2.weight, self.norm_2.eps, *sw._fused12())
-            return x, ops.linear(ops.silu_mul(ab), sw.w3.weight, sw.w3.bias)
+            gated, x = ops.linear_addnorm(x, h, self.norm_2.weight, self.norm_2.eps, *sw._fused12(), swiglu=True)
+            return x, ops.linear(gated, sw.w3.weight, sw.w3.bias)
         x, n2 = ops.add_rms_norm(x, h, self.norm_2.weight, self.norm_2.eps)
         return x, self.mlp(n2)
 

@@ -1281,15 +1281,18 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
 
 @torch.compiler.disable
 def linear_addnorm(x: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
-                   weight: torch.Tensor, bias: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                   weight: torch.Tensor, bias: torch.Tensor | None = None,
+                   swiglu: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """``s, n = add_rms_norm(x, residual, norm_weight, eps); return linear(n, weight, bias), s``
     in one launch on decode-sized rows (at most 4, K in {512, 1024, 2048}, 16-bit, the
     norm weight in the io dtype): the normalised rows are formed while the few-row
-    kernel stages its input, bit for bit as the two ops.  Other shapes run the two ops."""
+    kernel stages its input, bit for bit as the two ops.  With ``swiglu`` (``weight`` the
+    stacked [w1; w2]) the first output is ``silu_mul`` of the product, formed in the
+    kernel's epilogue.  Other shapes run the separate ops."""
     K = x.shape[-1]
     M = x.numel() // K if K else 0
     N = weight.shape[0]
-    if (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and 1 <= M <= 4 and K in (512, 1024, 2048)
+    if (x.is_cuda and (not swiglu or N % 2 == 0) and x.dtype in (torch.bfloat16, torch.float16) and 1 <= M <= 4 and K in (512, 1024, 2048)
             and residual.shape == x.shape and residual.dtype == x.dtype and norm_weight.dtype == x.dtype
             and norm_weight.numel() == K and weight.dtype == x.dtype and weight.dim() == 2 and weight.shape[1] == K
             and weight.stride(1) == 1 and N <= _SKINNY_MAX_N and (bias is None or bias.dtype == x.dtype)
@@ -1298,19 +1301,28 @@ def linear_addnorm(x: torch.Tensor, residual: torch.Tensor, norm_weight: torch.T
         xc, rc = x.reshape(M, K).contiguous(), residual.reshape(M, K).contiguous()
         nwc = norm_weight.detach().contiguous()
         s = torch.empty_like(x)
-        y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=x.device)
+        NO = N // 2 if swiglu else N
+        y = torch.empty(x.shape[:-1] + (NO,), dtype=x.dtype, device=x.device)
         b = None if bias is None else bias.contiguous()
         lib = nat.load()
-        st = lib.gdn2_skinny_linear_addnorm(
+        fn = lib.gdn2_skinny_linear_addnorm_swiglu if swiglu else lib.gdn2_skinny_linear_addnorm
+        st = fn(
             nat.ptr(xc), K, nat.ptr(rc), K, nat.ptr(s), K, nat.ptr(nwc), float(eps), nat.ptr(weight),
-            weight.stride(0), nat.ptr(b), nat.ptr(y), N, nat.dtype_code(x.dtype), M, N, K,
+            weight.stride(0), nat.ptr(b), nat.ptr(y), NO, nat.dtype_code(x.dtype), M, N, K,
             nat.stream_handle(x.device),
         )
         if st != nat.ERR_UNSUPPORTED:
             nat.check(st, "linear_addnorm")
             return y, s
     s, n = add_rms_norm(x, residual, norm_weight, eps)
-    return linear(n, weight, bias), s
+    y = linear(n, weight, bias)
+    if not swiglu:
+        return y, s
+    try:
+        return silu_mul(y), s
+    except NotImplementedError:  # widths silu_mul's 16-byte pieces do not cover
+        a, b = y.chunk(2, dim=-1)
+        return F.silu(a) * b, s
 
 
 @torch.compiler.disable

@@ -499,12 +499,13 @@ def test_argmax_rows_matches_torch(gpu_device, dtype, rows, n):
 
 
 @pytest.mark.parametrize("dtype,M,K,N", [(torch.bfloat16, 4, 1024, 6144), (torch.bfloat16, 1, 512, 100),
-                                         (torch.float16, 3, 2048, 700), (torch.bfloat16, 5, 1024, 64)])
+                                         (torch.float16, 3, 2048, 704), (torch.bfloat16, 5, 1024, 64),
+                                         (torch.bfloat16, 2, 1024, 4112)])
 def test_linear_addnorm_equals_add_norm_then_linear(gpu_device, dtype, M, K, N):
     """The residual add and RMSNorm formed while the few-row kernel stages its input:
     bit for bit ``add_rms_norm`` followed by ``linear`` for both outputs (the product
     and the residual sums); 5 rows run the two ops."""
-    from qwendopamine_amd.ops import add_rms_norm, linear, linear_addnorm
+    from qwendopamine_amd.ops import add_rms_norm, linear, linear_addnorm, silu_mul
 
     print(f"[case] linear_addnorm dtype={dtype} M={M} K={K} N={N}", flush=True)
     g = torch.Generator(device="cpu").manual_seed(M * K + N)
@@ -516,9 +517,17 @@ def test_linear_addnorm_equals_add_norm_then_linear(gpu_device, dtype, M, K, N):
         y, s = linear_addnorm(x, h, nw, 1e-5, w)
         s_ref, n_ref = add_rms_norm(x, h, nw, 1e-5)
         y_ref = linear(n_ref, w)
+        # SwiGLU epilogue (w as a stacked [w1; w2]): silu_mul of the same product
+        # (where silu_mul's 16-byte pieces cover the width).
+        yg, sg = linear_addnorm(x, h, nw, 1e-5, w, swiglu=True)
+        yg_ref = silu_mul(y_ref) if (N // 2) % 8 == 0 else None
     torch.cuda.synchronize()
     _bits_equal(s, s_ref)
     _bits_equal(y, y_ref)
+    _bits_equal(sg, s_ref)
+    assert yg.shape == (M, N // 2)
+    if yg_ref is not None:
+        _bits_equal(yg, yg_ref)
 
 
 def test_hybrid_decode_with_norm_in_projection(gpu_device, monkeypatch):
