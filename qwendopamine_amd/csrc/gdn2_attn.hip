@@ -283,13 +283,14 @@ hipError_t attn_t(const AttnDecodeParams &p, hipStream_t s)
 
 // Row-wise argmax (greedy decoding over the LM head's logits): one workgroup of
 // 1024 threads per row, each thread scanning 16-byte pieces tid, tid + 1024,
-// ... with every piece of a batch requested before any is compared.  The first
-// index of the maximum wins, and NaN counts as the maximum (torch's argmax).
-template <typename T>
+// ..., tid + 1024 (U - 1) with all U of them requested before any is compared
+// (U is picked so that one such batch covers a row of the usual vocabulary
+// sizes: a row then costs one memory round trip).  The first index of the
+// maximum wins, and NaN counts as the maximum (torch's argmax).
+template <typename T, int U>
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(ArgmaxParams p)
 {
     constexpr int EPP = 16 / static_cast<int>(sizeof(T));  // elements per piece
-    constexpr int U = 4;                                     // pieces in flight per thread
     __shared__ float sv[16];
     __shared__ int64_t si[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -297,14 +298,26 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(ArgmaxParams p)
     const int64_t pieces = p.n / EPP;
     float best = -INFINITY;
     int64_t bi = p.n;  // "none yet": larger than every index
+    // Merge of two candidates: v beats best if larger, or NaN where best is not,
+    // or equal / both NaN at a smaller index.
     auto take = [&](float v, int64_t i) __attribute__((always_inline)) {
-        // v beats best if larger, or NaN where best is not, or equal / both NaN at a smaller index.
         const bool vn = v != v, bn = best != best;
         const bool better = (vn && !bn) || (!vn && !bn && v > best) || ((v == best || (vn && bn)) && i < bi);
         if (better) {
             best = v;
             bi = i;
         }
+    };
+    // A thread's own elements arrive in increasing index order, so there a
+    // candidate only has to be strictly larger (or the first NaN, or the first
+    // element at all) to win.
+    bool have = false;
+    auto scan = [&](float v, int64_t i) __attribute__((always_inline)) {
+        if (!have || v > best || (v != v && best == best)) {
+            best = v;
+            bi = i;
+        }
+        have = true;
     };
     for (int64_t c0 = tid; c0 < pieces; c0 += 1024 * U) {
         uint4 raw[U];
@@ -330,11 +343,12 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(ArgmaxParams p)
                     else
                         v = static_cast<float>(__builtin_bit_cast(_Float16, h));
                 }
-                take(v, c * EPP + e);
+                scan(v, c * EPP + e);
             }
         }
     }
-    for (int64_t i = pieces * EPP + tid; i < p.n; i += 1024) take(io<T>::ld(x, i), i);  // ragged tail
+    // Ragged tail: these indexes exceed every piece's, so the in-order rule holds.
+    for (int64_t i = pieces * EPP + tid; i < p.n; i += 1024) scan(io<T>::ld(x, i), i);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float v2 = __shfl_xor(best, o, 64);
@@ -352,15 +366,29 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(ArgmaxParams p)
     }
 }
 
+template <typename T>
+void argmax_launch(const ArgmaxParams &p, hipStream_t stream)
+{
+    // Pieces in flight per thread: one batch covers a row of up to 1024 * U
+    // pieces (U = 20: 163,840 bf16 logits), longer rows loop.
+    const dim3 grid(static_cast<unsigned>(p.rows));
+    const int64_t per = (p.n / (16 / static_cast<int64_t>(sizeof(T))) + 1023) / 1024;
+    if (per <= 4)
+        hipLaunchKernelGGL((argmax_rows_kernel<T, 4>), grid, dim3(1024), 0, stream, p);
+    else if (per <= 8)
+        hipLaunchKernelGGL((argmax_rows_kernel<T, 8>), grid, dim3(1024), 0, stream, p);
+    else
+        hipLaunchKernelGGL((argmax_rows_kernel<T, 20>), grid, dim3(1024), 0, stream, p);
+}
+
 }  // namespace
 
 hipError_t launch_argmax_rows(const ArgmaxParams &p, int io_dtype, hipStream_t stream)
 {
-    const dim3 grid(static_cast<unsigned>(p.rows));
     switch (io_dtype) {
-    case GDN2_DTYPE_F32: hipLaunchKernelGGL((argmax_rows_kernel<float>), grid, dim3(1024), 0, stream, p); break;
-    case GDN2_DTYPE_BF16: hipLaunchKernelGGL((argmax_rows_kernel<bf16_t>), grid, dim3(1024), 0, stream, p); break;
-    default: hipLaunchKernelGGL((argmax_rows_kernel<f16_t>), grid, dim3(1024), 0, stream, p); break;
+    case GDN2_DTYPE_F32: argmax_launch<float>(p, stream); break;
+    case GDN2_DTYPE_BF16: argmax_launch<bf16_t>(p, stream); break;
+    default: argmax_launch<f16_t>(p, stream); break;
     }
     return hipGetLastError();
 }

@@ -472,10 +472,13 @@ def test_linear_pair_fallback(gpu_device):
 
 
 @pytest.mark.parametrize("dtype,rows,n", [(torch.bfloat16, 4, 151936), (torch.float32, 3, 1000), (torch.float16, 5, 77),
-                                          (torch.bfloat16, 2, 8)])
+                                          (torch.bfloat16, 2, 8), (torch.float16, 4, 50001), (torch.float32, 2, 151936),
+                                          (torch.bfloat16, 4, 400003)])
 def test_argmax_rows_matches_torch(gpu_device, dtype, rows, n):
-    """Against torch's argmax: ties resolved to the first index, NaN as the maximum, a
-    strided row view, and the output written in place into a strided int64 column."""
+    """Against torch's argmax: ties resolved to the first index (also -0.0 against +0.0),
+    NaN as the maximum, -inf rows, rows that take one batch of requests per thread and
+    rows that loop over several, ragged tails, a strided row view, and the output
+    written in place into a strided int64 column."""
     from qwendopamine_amd.ops import argmax_rows
 
     print(f"[case] argmax_rows dtype={dtype} rows={rows} n={n}", flush=True)
@@ -487,6 +490,10 @@ def test_argmax_rows_matches_torch(gpu_device, dtype, rows, n):
         x[1, 1] = float("nan")
     if rows > 2:
         x[2] = x[2].min()                             # all equal: index 0
+    if rows > 3:
+        x[3] = float("-inf")                          # all -inf: index 0
+        x[3, n - 2] = -0.0                            # -0.0 then +0.0: equal, the first wins
+        x[3, n - 1] = 0.0
     ref = x.argmax(-1, keepdim=True)
     got = argmax_rows(x)
     wide = torch.zeros(rows, 3, dtype=torch.int64, device=gpu_device)
