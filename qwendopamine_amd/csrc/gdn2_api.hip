@@ -314,7 +314,8 @@ static int skinny_addnorm_impl(const void *x, int64_t x_row_stride, const void *
         return GDN2_ERR_INVALID;
     if (!skinny_linear_supported(io_dtype, M, K) || M > 4 || K > 2048) return GDN2_ERR_UNSUPPORTED;
     if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) |
-          reinterpret_cast<uintptr_t>(sum_out) | reinterpret_cast<uintptr_t>(weight)) & 15) != 0 ||
+          reinterpret_cast<uintptr_t>(sum_out) | reinterpret_cast<uintptr_t>(weight) |
+          reinterpret_cast<uintptr_t>(norm_weight)) & 15) != 0 ||
         x_row_stride % 8 != 0 || residual_row_stride % 8 != 0 || sum_row_stride % 8 != 0 || weight_row_stride % 8 != 0)
         return GDN2_ERR_UNSUPPORTED;
     if (N > 2147483647 - 8) return GDN2_ERR_UNSUPPORTED;

@@ -81,38 +81,66 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
     T *vc = static_cast<T *>(p.v_cache) + cbase;
 
     // ---- RoPE of the QPK q heads and k (interleaved pairs, fp32, rounded to
-    // the io dtype as the host's torch path), v as is ----
+    // the io dtype as the host's torch path), v as is.  The token's rows are
+    // requested first, then this workgroup's first batch of cached k, v rows
+    // (below), and only then is anything computed: loads complete in order,
+    // so the cache rows' latency overlaps the RoPE, the stores and the barrier. ----
+    static_assert((QPK + 1) * (D / 2) <= 512 && D <= 512, "one RoPE pair / v channel per thread");
     const bool store = blockIdx.y == 0;  // one split stores the token's k, v
-    for (int e = tid; e < (QPK + 1) * (D / 2); e += 512) {
-        const int h = e / (D / 2), i = e - h * (D / 2);
-        const float x0 = io<T>::ld(x, h * D + 2 * i), x1 = io<T>::ld(x, h * D + 2 * i + 1);
-        float y0 = x0, y1 = x1;
-        if (i < p.rope_pairs) {
-            const float c = p.cos[i], s = p.sin[i];
-            y0 = round_to<T>(x0 * c - x1 * s);
-            y1 = round_to<T>(x0 * s + x1 * c);
+    const int he = tid / (D / 2), ie = tid - (tid / (D / 2)) * (D / 2);
+    const bool has_pair = tid < (QPK + 1) * (D / 2), has_v = tid < D;
+    float x0 = 0.0f, x1 = 0.0f, cs = 1.0f, sn = 0.0f, xv = 0.0f;
+    if (has_pair) {
+        x0 = io<T>::ld(x, he * D + 2 * ie);
+        x1 = io<T>::ld(x, he * D + 2 * ie + 1);
+        if (ie < p.rope_pairs) {
+            cs = p.cos[ie];
+            sn = p.sin[ie];
         }
-        if (h < QPK) {
-            sq[h][2 * i] = y0;
-            sq[h][2 * i + 1] = y1;
+    }
+    if (has_v) xv = io<T>::ld(x, (QPK + 1) * D + tid);
+
+    const int slot = lane / DG, dg = lane - (lane / DG) * DG;
+    const int per_step = kAttnWaves * PS;
+    // kUnroll positions per slot requested at once; positions from pos on read
+    // row 0 (always valid) and are skipped or replaced.
+    uint4 kr[kUnroll], vr[kUnroll];
+    auto request = [&](int j0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int j = j0 + u * per_step + wave * PS + slot;
+            const int64_t jl = j < pos && j < hi ? j : 0;
+            kr[u] = *reinterpret_cast<const uint4 *>(kc + jl * D + dg * 8);
+            vr[u] = *reinterpret_cast<const uint4 *>(vc + jl * D + dg * 8);
+        }
+    };
+    request(lo);
+
+    if (has_pair) {
+        float y0 = x0, y1 = x1;
+        if (ie < p.rope_pairs) {
+            y0 = round_to<T>(x0 * cs - x1 * sn);
+            y1 = round_to<T>(x0 * sn + x1 * cs);
+        }
+        if (he < QPK) {
+            sq[he][2 * ie] = y0;
+            sq[he][2 * ie + 1] = y1;
         } else {
-            skv[0][2 * i] = y0;
-            skv[0][2 * i + 1] = y1;
+            skv[0][2 * ie] = y0;
+            skv[0][2 * ie + 1] = y1;
             if (store) {
-                io<T>::st(kc, pos * D + 2 * i, y0);
-                io<T>::st(kc, pos * D + 2 * i + 1, y1);
+                io<T>::st(kc, pos * D + 2 * ie, y0);
+                io<T>::st(kc, pos * D + 2 * ie + 1, y1);
             }
         }
     }
-    for (int d = tid; d < D; d += 512) {
-        const float v = io<T>::ld(x, (QPK + 1) * D + d);
-        skv[1][d] = v;
-        if (store) io<T>::st(vc, pos * D + d, v);
+    if (has_v) {
+        skv[1][tid] = xv;
+        if (store) io<T>::st(vc, pos * D + tid, xv);
     }
     __syncthreads();
 
     // ---- one pass over positions 0 .. pos with online softmax ----
-    const int slot = lane / DG, dg = lane - (lane / DG) * DG;
     float qv[QPK][8];
 #pragma unroll
     for (int h = 0; h < QPK; ++h)
@@ -126,18 +154,7 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
     }
-    const int per_step = kAttnWaves * PS;
     for (int j0 = lo; j0 < hi; j0 += per_step * kUnroll) {
-        // kUnroll positions per slot requested before any is used; positions
-        // from pos on read row 0 (always valid) and are skipped or replaced.
-        uint4 kr[kUnroll], vr[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int j = j0 + u * per_step + wave * PS + slot;
-            const int64_t jl = j < pos && j < hi ? j : 0;
-            kr[u] = *reinterpret_cast<const uint4 *>(kc + jl * D + dg * 8);
-            vr[u] = *reinterpret_cast<const uint4 *>(vc + jl * D + dg * 8);
-        }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
         const int j = j0 + u * per_step + wave * PS + slot;
@@ -169,6 +186,8 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
             m[h] = mn;
         }
         }
+        // The next batch (a workgroup's share is one batch at up to 512 positions).
+        if (j0 + per_step * kUnroll < hi) request(j0 + per_step * kUnroll);
     }
     // Merge the PS slot states of the wave (lanes with equal dg).
 #pragma unroll

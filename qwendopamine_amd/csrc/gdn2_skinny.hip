@@ -6,9 +6,10 @@
 // kernel is laid out for HBM: each wave owns one or two rows of W and requests
 // all of their 16-byte pieces before any arithmetic (lane l takes pieces l, l + 64,
 // ... of a row, so every request is a contiguous 1 KB row segment), the few x
-// rows sit in LDS (staged once per workgroup, read by all four waves, reused
-// over the row groups of wide outputs), and the 64 lane partial sums of each
-// output are added by xor-shuffles.  Accumulation
+// rows sit in LDS (staged once per workgroup, read by all its waves, reused
+// over the row groups of wide outputs; their own requests leave before W's,
+// since loads complete in order and x requested after W would wait for W),
+// and the 64 lane partial sums of each output are added by xor-shuffles.  Accumulation
 // is fp32 and the output is rounded once, as torch's GEMM does; the summation
 // order differs from hipBLASLt's, so results agree to rounding, not bit for
 // bit.
@@ -60,30 +61,30 @@ __device__ __forceinline__ uint4 narrow8(const float (&f)[8])
 
 // MM: rows of x the instantiation holds (p.M <= MM, rows past p.M are zero
 // and not stored); NP: 16-byte pieces of a row per lane (K = 512 NP); RPW:
-// rows of W per wave.  Workgroup b takes the groups of kWaves * RPW rows
-// b, b + gridDim.x, ...
-template <typename T, int MM, int NP, int RPW>
-__global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
+// rows of W per wave; NW: waves per workgroup.  Workgroup b takes the groups
+// of NW * RPW rows b, b + gridDim.x, ...
+template <typename T, int MM, int NP, int RPW, int NW>
+__global__ __launch_bounds__(64 * NW) void skinny_linear_kernel(SkinnyParams p)
 {
     constexpr int kRowsPerWave = RPW;
     constexpr bool BF = std::is_same<T, bf16_t>::value;
     constexpr int PPR = 64 * NP;  // 16-byte pieces per row of x or W
     __shared__ __align__(16) uint4 sx[MM * PPR];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int groups = (p.N + kWaves * kRowsPerWave - 1) / (kWaves * kRowsPerWave);
+    const int groups = (p.N + NW * kRowsPerWave - 1) / (NW * kRowsPerWave);
     const T *w = static_cast<const T *>(p.w);
     const T *x = static_cast<const T *>(p.x);
 
     // This wave's rows of W in a group (rows past N read row N-1); the first
-    // group's are requested before the x rows are staged.
+    // group's are requested right after the x rows' own requests.
     uint4 wr[kRowsPerWave][NP];
     // Row r of the wave in group grp: rows n0 + r, or with the SwiGLU epilogue
     // (RPW = 2) rows c and c + N / 2 of output column c.
     auto row_of = [&](int grp, int r) __attribute__((always_inline)) {
         if constexpr (RPW == 2) {
-            if (p.glu_out) return (grp * kWaves + wave) + r * (p.N / 2);
+            if (p.glu_out) return (grp * NW + wave) + r * (p.N / 2);
         }
-        return (grp * kWaves + wave) * kRowsPerWave + r;
+        return (grp * NW + wave) * kRowsPerWave + r;
     };
     auto request = [&](int grp) __attribute__((always_inline)) {
 #pragma unroll
@@ -95,6 +96,35 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
                 wr[r][c] = *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(row) * p.ldw + (c * 64 + lane) * 8);
         }
     };
+    // The staging rows (x, the residual and the norm weight) are requested
+    // before W: loads complete in order, so rows requested after W would wait
+    // for all of W to land before the norm could start.
+    uint4 xq[NP], rq[NP], nq[NP];
+    if (p.norm && wave < MM) {
+        const int mr = wave < p.M ? wave : 0;
+        const T *xr = x + static_cast<int64_t>(mr) * p.ldx;
+        const T *rr = static_cast<const T *>(p.res) + static_cast<int64_t>(mr) * p.ldres;
+#pragma unroll
+        for (int v = 0; v < NP; ++v) {
+            xq[v] = *reinterpret_cast<const uint4 *>(xr + (v * 64 + lane) * 8);
+            rq[v] = *reinterpret_cast<const uint4 *>(rr + (v * 64 + lane) * 8);
+            nq[v] = *reinterpret_cast<const uint4 *>(static_cast<const T *>(p.nw) + (v * 64 + lane) * 8);
+        }
+    }
+    // Plain staging: this thread's x pieces requested before W as well (rows
+    // past M and pieces past the end read piece 0 of row 0 and become zeros).
+    constexpr int XPT = (MM * PPR + 64 * NW - 1) / (64 * NW);
+    uint4 xp[XPT];
+    if (!p.norm) {
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) {
+            const int idx = i * 64 * NW + tid;
+            const int m = idx / PPR, c = idx - m * PPR;
+            const bool ok = idx < MM * PPR && m < p.M;
+            xp[i] = *reinterpret_cast<const uint4 *>(x + (ok ? static_cast<int64_t>(m) * p.ldx + c * 8 : 0));
+            if (!ok) xp[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
     request(blockIdx.x);
     if (p.norm) {
         // x = RMSNorm(x + res) staged by wave m for row m (M <= 4, NP <= 4),
@@ -107,13 +137,11 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
             uint4 st[NP];
             if (wave < p.M) {
                 float sv[NP][8], sq = 0.0f;
-                const T *xr = x + static_cast<int64_t>(wave) * p.ldx;
-                const T *rr = static_cast<const T *>(p.res) + static_cast<int64_t>(wave) * p.ldres;
 #pragma unroll
                 for (int v = 0; v < NP; ++v) {
                     float a[8], b[8];
-                    widen8(*reinterpret_cast<const uint4 *>(xr + (v * 64 + lane) * 8), a, BF);
-                    widen8(*reinterpret_cast<const uint4 *>(rr + (v * 64 + lane) * 8), b, BF);
+                    widen8(xq[v], a, BF);
+                    widen8(rq[v], b, BF);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) sv[v][e] = round_to<T>(a[e] + b[e]);
                 }
@@ -129,12 +157,10 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
 #pragma unroll
                 for (int v = 0; v < NP; ++v) {
                     if (blockIdx.x == 0) *reinterpret_cast<uint4 *>(so + (v * 64 + lane) * 8) = narrow8<T>(sv[v]);
-                    float o8[8];
+                    float o8[8], wn[8];
+                    widen8(nq[v], wn, BF);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float wgt = io<T>::ld(static_cast<const T *>(p.nw), (v * 64 + lane) * 8 + e);
-                        o8[e] = round_to<T>(round_to<T>(sv[v][e] * inv) * wgt);
-                    }
+                    for (int e = 0; e < 8; ++e) o8[e] = round_to<T>(round_to<T>(sv[v][e] * inv) * wn[e]);
                     st[v] = narrow8<T>(o8);
                 }
             } else {
@@ -145,21 +171,16 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
             for (int v = 0; v < NP; ++v) sx[wave * PPR + v * 64 + lane] = st[v];
         }
     } else {
-    // x rows into LDS (rows past M as zeros).
-#pragma unroll 4
-    for (int i0 = 0; i0 < MM * PPR; i0 += 256) {
-        const int i = i0 + tid;
-        if (i < MM * PPR) {
-            const int m = i / PPR, c = i - m * PPR;
-            sx[i] = m < p.M ? *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(m) * p.ldx + c * 8)
-                            : make_uint4(0u, 0u, 0u, 0u);
-        }
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        const int idx = i * 64 * NW + tid;
+        if (idx < MM * PPR) sx[idx] = xp[i];
     }
     }
     __syncthreads();
 
     for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
-    const int n0 = (grp * kWaves + wave) * kRowsPerWave;
+    const int n0 = (grp * NW + wave) * kRowsPerWave;
     float acc[kRowsPerWave][MM];
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r)
@@ -194,7 +215,7 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
             // SwiGLU epilogue: lane m stores out[m, c] = round(round(silu(a)) * b)
             // from a = round(row c), b = round(row c + N / 2), as a product
             // followed by gdn2_silu_mul_fwd computes it.
-            const int c = grp * kWaves + wave;
+            const int c = grp * NW + wave;
 #pragma unroll
             for (int m = 0; m < MM; ++m) {
                 if (lane == m && m < p.M && c < p.N / 2) {
@@ -229,12 +250,12 @@ __global__ __launch_bounds__(256) void skinny_linear_kernel(SkinnyParams p)
     }
 }
 
-template <typename T, int MM, int NP, int RPW>
+template <typename T, int MM, int NP, int RPW, int NW>
 hipError_t skinny_launch(const SkinnyParams &p, hipStream_t s)
 {
-    const int groups = (p.N + kWaves * RPW - 1) / (kWaves * RPW);
+    const int groups = (p.N + NW * RPW - 1) / (NW * RPW);
     const dim3 grid(static_cast<unsigned>(groups < kMaxGroups ? groups : kMaxGroups));
-    hipLaunchKernelGGL((skinny_linear_kernel<T, MM, NP, RPW>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((skinny_linear_kernel<T, MM, NP, RPW, NW>), grid, dim3(64 * NW), 0, s, p);
     return hipGetLastError();
 }
 
@@ -242,7 +263,11 @@ hipError_t skinny_launch(const SkinnyParams &p, hipStream_t s)
 // one for narrow outputs (more waves, so more of the matrix requested at
 // once), two beyond 2048 rows (four measured slower on a 151,936-row
 // output); capped so that a wave's requests (RPW * NP pieces) and sums
-// (RPW * MM) stay in registers.
+// (RPW * MM) stay in registers.  Wide outputs run sixteen-wave workgroups
+// where the 128 registers of a 1024-thread workgroup hold the wave's state
+// (MM <= 4, NP <= 2): a quarter of the workgroups to dispatch and a quarter
+// of the x stagings (config-3 decode step 0.95 vs 0.98 ms at four waves);
+// narrow outputs keep four, which gives 256 workgroups at 1024 rows.
 template <typename T, int MM, int NP>
 hipError_t skinny_np(const SkinnyParams &p, hipStream_t s)
 {
@@ -251,9 +276,9 @@ hipError_t skinny_np(const SkinnyParams &p, hipStream_t s)
     } else {
         constexpr int LIM = 8 / NP < 16 / MM ? 8 / NP : 16 / MM;
         if constexpr (LIM >= 2)
-            if (p.N > 2048 || p.glu_out) return skinny_launch<T, MM, NP, 2>(p, s);
+            if (p.N > 2048 || p.glu_out) return skinny_launch<T, MM, NP, 2, (MM <= 4 && NP <= 2) ? 16 : 4>(p, s);
         if (p.glu_out) return hipErrorInvalidValue;  // rejected before (the epilogue needs two rows per wave)
-        return skinny_launch<T, MM, NP, 1>(p, s);
+        return skinny_launch<T, MM, NP, 1, 4>(p, s);
     }
 }
 
@@ -295,12 +320,14 @@ __global__ __launch_bounds__(256) void small_linear_kernel(SmallLinearParams p)
     const int row = (static_cast<int>(blockIdx.x) * kWaves + wave) * RPI + rsub;
     const T *w = static_cast<const T *>(q.w);
     const int rowc = row < q.N ? row : q.N - 1;
+    // The x piece is requested before the row of W (loads complete in order, so
+    // the LDS staging and the barrier then overlap W's latency).
+    uint4 xv = make_uint4(0u, 0u, 0u, 0u);
+    const int xm = tid / KP8, xc = tid - (tid / KP8) * KP8;
+    if (tid < MM * KP8 && xm < p.M)
+        xv = *reinterpret_cast<const uint4 *>(static_cast<const T *>(q.x) + xm * q.ldx + xc * 8);
     const uint4 wv = *reinterpret_cast<const uint4 *>(w + static_cast<int64_t>(rowc) * p.K + c * 8);
-    if (tid < MM * KP8) {
-        const int m = tid / KP8, cc = tid - m * KP8;
-        sx[tid] = m < p.M ? *reinterpret_cast<const uint4 *>(static_cast<const T *>(q.x) + m * q.ldx + cc * 8)
-                          : make_uint4(0u, 0u, 0u, 0u);
-    }
+    if (tid < MM * KP8) sx[tid] = xv;
     __syncthreads();
     float wf[8];
     widen8(wv, wf, BF);
