@@ -289,7 +289,10 @@ int gdn2_small_linear_pair(const void *x0, int64_t x0_row_stride, const void *we
  *   qkv      [B, G, qpk + 2, D] io_dtype: per KV group, qpk q heads, k, v
  *            (the fused attn projection's layout)
  *   cos, sin fp32 rotation of the token (rope_pairs values; channels from
- *            2 * rope_pairs on are not rotated)
+ *            2 * rope_pairs on are not rotated); with rope_row_stride > 0
+ *            they are instead whole tables of at least max_len rows,
+ *            rope_row_stride floats apart, and the kernel reads row *pos
+ *            (so the host needs no per-step selection of the row)
  *   pos      device int64: the token's position (one for all sequences)
  *   k_cache, v_cache  [B, G, max_len, D] io_dtype, updated at pos
  *   out      [B, G * qpk, D] io_dtype
@@ -303,9 +306,10 @@ int gdn2_small_linear_pair(const void *x0, int64_t x0_row_stride, const void *we
  * (0 for caches of up to 512 positions, where workspace may be NULL).
  */
 size_t gdn2_attn_decode_workspace_size(int B, int G, int qpk, int D, int64_t max_len);
-int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int rope_pairs, const int64_t *pos,
-                     void *k_cache, void *v_cache, void *out, int io_dtype, int B, int G, int qpk, int D,
-                     int64_t max_len, float scale, void *workspace, size_t workspace_bytes, void *stream);
+int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int rope_pairs, int64_t rope_row_stride,
+                     const int64_t *pos, void *k_cache, void *v_cache, void *out, int io_dtype, int B, int G,
+                     int qpk, int D, int64_t max_len, float scale, void *workspace, size_t workspace_bytes,
+                     void *stream);
 
 /*
  * Backward of the short convolution on a prefill call (no cache), for training

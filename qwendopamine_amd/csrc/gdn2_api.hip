@@ -398,21 +398,24 @@ size_t gdn2_attn_decode_workspace_size(int B, int G, int qpk, int D, int64_t max
     return attn_decode_workspace_floats(B, G, qpk, D, max_len) * sizeof(float);
 }
 
-int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int rope_pairs, const int64_t *pos,
-                     void *k_cache, void *v_cache, void *out, int io_dtype, int B, int G, int qpk, int D,
-                     int64_t max_len, float scale, void *workspace, size_t workspace_bytes, void *stream)
+int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int rope_pairs, int64_t rope_row_stride,
+                     const int64_t *pos, void *k_cache, void *v_cache, void *out, int io_dtype, int B, int G,
+                     int qpk, int D, int64_t max_len, float scale, void *workspace, size_t workspace_bytes,
+                     void *stream)
 {
     if (!valid_dtype(io_dtype) || B < 0 || G < 0 || qpk < 1 || D < 1 || max_len < 1) return GDN2_ERR_INVALID;
     if (B == 0 || G == 0) return GDN2_OK;
     if (!qkv || !pos || !k_cache || !v_cache || !out) return GDN2_ERR_INVALID;
     if (rope_pairs < 0 || 2 * rope_pairs > D) return GDN2_ERR_INVALID;
     if (rope_pairs > 0 && (!cos || !sin)) return GDN2_ERR_INVALID;
+    if (rope_row_stride < 0 || (rope_row_stride > 0 && rope_row_stride < rope_pairs)) return GDN2_ERR_INVALID;
     if (!attn_decode_supported(io_dtype, qpk, D)) return GDN2_ERR_UNSUPPORTED;
     if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) return GDN2_ERR_UNSUPPORTED;
     if (static_cast<int64_t>(B) * G > 2147483647LL || max_len > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
     AttnDecodeParams p;
     p.qkv = qkv; p.cos = cos; p.sin = sin;
     p.rope_pairs = rope_pairs;
+    p.rope_stride = rope_row_stride;
     p.pos = pos; p.k_cache = k_cache; p.v_cache = v_cache; p.out = out;
     p.max_len = max_len; p.B = B; p.G = G; p.qpk = qpk; p.D = D; p.scale = scale;
     p.splits = attn_decode_splits(max_len);

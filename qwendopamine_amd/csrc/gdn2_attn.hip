@@ -94,8 +94,8 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(AttnDecodeParams p)
         x0 = io<T>::ld(x, he * D + 2 * ie);
         x1 = io<T>::ld(x, he * D + 2 * ie + 1);
         if (ie < p.rope_pairs) {
-            cs = p.cos[ie];
-            sn = p.sin[ie];
+            cs = p.cos[pos * p.rope_stride + ie];
+            sn = p.sin[pos * p.rope_stride + ie];
         }
     }
     if (has_v) xv = io<T>::ld(x, (QPK + 1) * D + tid);

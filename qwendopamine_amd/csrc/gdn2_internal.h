@@ -221,6 +221,7 @@ struct AttnDecodeParams {
     const void *qkv;
     const float *cos, *sin;
     int rope_pairs;
+    int64_t rope_stride;  // 0: cos / sin are the token's row; else rows of tables indexed by *pos
     const int64_t *pos;
     void *k_cache, *v_cache, *out;
     int64_t max_len;

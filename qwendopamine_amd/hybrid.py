@@ -385,6 +385,19 @@ class HybridDecoder(nn.Module):
                                          c.rope_base, c.condense_ratio)
         return self.rope
 
+    def _attention_decode_fused(self) -> bool:
+        """Whether every attention layer's single-token step takes ``ops.attention_decode``
+        (the condition ``CausalSelfAttention.forward_qkv`` tests, on the weights)."""
+        for blk in self.h:
+            if blk.use_gdn2:
+                continue
+            at = blk.attn
+            w = at.attn.weight
+            G, qpk, D = at.n_query_groups, at.n_head // at.n_query_groups, at.head_size
+            if at.kv_cache is None or not _inference(w) or not ops.attention_decode_supported(w, qpk, D):
+                return False
+        return True
+
     def setup_caches(self, batch: int, max_seq_length: int) -> None:
         """Allocate the attention KV caches ``[batch, groups, max_seq_length, head_size]``
         and the causal mask, and drop every gdn2 cache (the next cached forward is a
@@ -417,8 +430,11 @@ class HybridDecoder(nn.Module):
         else:
             if self.mask_cache is None:
                 raise RuntimeError("call setup_caches before a cached forward")
-            cos, sin = cos.index_select(0, input_pos), sin.index_select(0, input_pos)
-            mask = self.mask_cache.index_select(2, input_pos)
+            if not (t == 1 and self._attention_decode_fused()):
+                cos, sin = cos.index_select(0, input_pos), sin.index_select(0, input_pos)
+                mask = self.mask_cache.index_select(2, input_pos)
+            # else: every attention layer takes the fused decode kernel, which reads
+            # the rotation tables' row input_pos itself and needs no mask.
         x = self.wte(idx)
         if _inference(x, self.ln_f.weight) and ops.add_rms_norm_supported(x):
             # The residual adds fused with the norms that follow them.

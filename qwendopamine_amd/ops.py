@@ -1402,8 +1402,9 @@ def attention_decode(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, in
     ``CausalSelfAttention.forward``, ``gdn2_gpt/model.py:89-173``).
 
     ``qkv`` ``[B, 1, G * (qpk + 2) * D]`` (the fused ``attn`` projection of one token),
-    ``cos`` / ``sin`` the token's rotation ``[1, rot / 2]`` (fp32), ``input_pos`` ``[1]``
-    (device int64), caches ``[B, G, L, D]``.  Returns ``[B, n_head, D]``.  Scores and
+    ``cos`` / ``sin`` the token's rotation ``[1, rot / 2]`` (fp32), or the whole tables
+    ``[R >= L, rot / 2]`` (fp32, contiguous), whose row ``input_pos`` the kernel reads,
+    ``input_pos`` ``[1]`` (device int64), caches ``[B, G, L, D]``.  Returns ``[B, n_head, D]``.  Scores and
     probabilities stay fp32 (torch's path rounds them to the io dtype), so results agree
     to that rounding.  Inference only.
     """
@@ -1418,16 +1419,26 @@ def attention_decode(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, in
     if not (k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.dtype == qkv.dtype == v_cache.dtype):
         raise ValueError(f"{name}: caches must be contiguous and of qkv's dtype")
     pairs = cos.shape[-1]
-    if 2 * pairs > D or sin.shape[-1] != pairs:
-        raise ValueError(f"{name}: the rotation has more than D / 2 pairs")
+    if 2 * pairs > D or sin.shape != cos.shape:
+        raise ValueError(f"{name}: the rotation has more than D / 2 pairs, or cos and sin differ in shape")
     qc = qkv.contiguous()
-    cf, sf = cos.reshape(-1)[:pairs].float().contiguous(), sin.reshape(-1)[:pairs].float().contiguous()
+    rope_stride = 0
+    if cos.dim() == 2 and cos.shape[0] > 1:
+        # Whole tables: the kernel reads row input_pos (in range: positions from L on
+        # leave the caches alone and read no row).
+        if cos.shape[0] < L or cos.dtype != torch.float32 or sin.dtype != torch.float32 or not (
+                cos.is_contiguous() and sin.is_contiguous()):
+            raise ValueError(f"{name}: rotation tables must be contiguous fp32 with at least {L} rows")
+        cf, sf, rope_stride = cos, sin, pairs
+    else:
+        cf, sf = cos.reshape(-1)[:pairs].float().contiguous(), sin.reshape(-1)[:pairs].float().contiguous()
     out = torch.empty(B, n_head, D, dtype=qkv.dtype, device=qkv.device)
     lib = nat.load()
     ws_bytes = lib.gdn2_attn_decode_workspace_size(B, G, qpk, D, L)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qkv.device) if ws_bytes else None
     st = lib.gdn2_attn_decode(
-        nat.ptr(qc), nat.ptr(cf), nat.ptr(sf), pairs, nat.ptr(input_pos), nat.ptr(k_cache), nat.ptr(v_cache),
+        nat.ptr(qc), nat.ptr(cf), nat.ptr(sf), pairs, rope_stride, nat.ptr(input_pos), nat.ptr(k_cache),
+        nat.ptr(v_cache),
         nat.ptr(out), nat.dtype_code(qkv.dtype), B, G, qpk, D, L, float(D) ** -0.5, nat.ptr(ws), ws_bytes,
         nat.stream_handle(qkv.device),
     )

@@ -356,9 +356,16 @@ def test_attention_decode_matches_float64(gpu_device, dtype, G, qpk, D, L, pos):
     cos, sin = torch.cos(ang).to(gpu_device), torch.sin(ang).to(gpu_device)
     kc0, vc0 = kc.clone(), vc.clone()
     ref, k_ref, v_ref = _attn_reference(qkv.cpu(), cos.cpu(), sin.cpu(), pos, kc0.cpu(), vc0.cpu(), n_head, dtype)
+    # The same rotation as row pos of whole tables, which the kernel indexes itself.
+    tab_c = torch.randn(L, D // 2, generator=gen).to(gpu_device)
+    tab_s = torch.randn(L, D // 2, generator=gen).to(gpu_device)
+    tab_c[pos], tab_s[pos] = cos[0], sin[0]
+    kc_t, vc_t = kc.clone(), vc.clone()
     with torch.no_grad():
         out = attention_decode(qkv, cos, sin, torch.tensor([pos], device=gpu_device), kc, vc, n_head)
+        out_t = attention_decode(qkv, tab_c, tab_s, torch.tensor([pos], device=gpu_device), kc_t, vc_t, n_head)
     torch.cuda.synchronize()
+    assert torch.equal(out_t, out) and torch.equal(kc_t, kc) and torch.equal(vc_t, vc)
     assert out.shape == (B, n_head, D) and out.dtype == dtype
     err = rel_l2(out, ref.numpy())
     print(f"  rel_l2 {err:.2e}", flush=True)
