@@ -300,10 +300,10 @@ int gdn2_small_linear_pair(const void *x0, int64_t x0_row_stride, const void *we
  * torch path rounds the scores and probabilities to io_dtype, so the two agree
  * to that rounding.  A position outside [0, max_len) leaves the caches alone
  * and writes zeros.  bf16 / fp16, D in {64, 128}, qpk in {1, 2, 4}; else
- * GDN2_ERR_UNSUPPORTED.  Caches longer than 512 positions are split over
+ * GDN2_ERR_UNSUPPORTED.  Caches longer than 1024 positions are split over
  * several workgroups per KV group, whose partial softmax states are merged by
  * a second kernel: workspace of gdn2_attn_decode_workspace_size() bytes
- * (0 for caches of up to 512 positions, where workspace may be NULL).
+ * (0 for caches of up to 1024 positions, where workspace may be NULL).
  */
 size_t gdn2_attn_decode_workspace_size(int B, int G, int qpk, int D, int64_t max_len);
 int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int rope_pairs, int64_t rope_row_stride,

@@ -336,12 +336,13 @@ def _attn_reference(qkv, cos, sin, pos, kc, vc, n_head, dtype):
 @pytest.mark.parametrize("dtype,G,qpk,D,L,pos", [(torch.bfloat16, 16, 1, 64, 2304, 2047),
                                                  (torch.bfloat16, 4, 4, 128, 300, 0),
                                                  (torch.float16, 2, 2, 128, 513, 512),
+                                                 (torch.float16, 2, 2, 128, 1025, 1024),
                                                  (torch.bfloat16, 3, 1, 64, 100, 37),
                                                  (torch.bfloat16, 4, 2, 64, 2304, 10)])
 def test_attention_decode_matches_float64(gpu_device, dtype, G, qpk, D, L, pos):
     """``ops.attention_decode`` against float64 attention over the same rounded inputs:
     the output to within its io-dtype rounding, the cache rows at ``pos`` equal to the
-    rotated k and v, every other cache row untouched.  Caches over 512 positions split
+    rotated k and v, every other cache row untouched.  Caches over 1024 positions split
     the positions over several workgroups (a token early in a long cache leaves most
     splits empty)."""
     from qwendopamine_amd.ops import attention_decode
