@@ -312,6 +312,22 @@ int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int ro
                      void *stream);
 
 /*
+ * Greedy decoding's argmax over the LM head's logits (the logits of reference
+ * src/qwendopamine/models/gdn2_gpt/model.py:304-380, GPT.forward; the
+ * reference has no decoding loop, the hybrid host's greedy decoder calls this
+ * in place of torch.argmax and keeps its semantics): out[r * out_stride] = the first index of the
+ * maximum of row r, NaN counting as the maximum.  x rows x_row_stride
+ * elements apart (16-byte aligned), n values each, io_dtype f32 / bf16 / fp16.
+ * With a workspace of gdn2_argmax_rows_workspace_size() bytes (8-byte
+ * aligned; 0 for rows of up to 1024 16-byte pieces) each row is split over
+ * several workgroups and a second launch merges their candidates; with
+ * workspace NULL one workgroup scans each row (one launch).
+ */
+size_t gdn2_argmax_rows_workspace_size(int64_t rows, int64_t n, int io_dtype);
+int gdn2_argmax_rows(const void *x, int64_t x_row_stride, int io_dtype, int64_t rows, int64_t n, int64_t *out,
+                     int64_t out_stride, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Backward of the short convolution on a prefill call (no cache), for training
  * without torch's conv: the gradient of ShortConvolution.forward (reference
  * gdn2.py:395-430, whose backward torch's autograd runs through F.conv1d and

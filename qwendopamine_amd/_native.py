@@ -76,7 +76,8 @@ SIGNATURES: dict[str, tuple] = {
                                                _i, _i, _i, _i, _vp]),
     "gdn2_small_linear_pair": (_i, [_vp, _i64, _vp, _vp, _vp, _i64, _i, _vp, _i64, _vp, _vp, _vp, _i64, _i, _i, _i,
                                     _i, _vp]),
-    "gdn2_argmax_rows": (_i, [_vp, _i64, _i, _i64, _i64, _vp, _i64, _vp]),
+    "gdn2_argmax_rows_workspace_size": (_sz, [_i64, _i64, _i]),
+    "gdn2_argmax_rows": (_i, [_vp, _i64, _i, _i64, _i64, _vp, _i64, _vp, _sz, _vp]),
     "gdn2_attn_decode_workspace_size": (_sz, [_i, _i, _i, _i, _i64]),
     "gdn2_attn_decode": (_i, [_vp, _vp, _vp, _i, _i64, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64, _f, _vp, _sz, _vp]),
     "gdn2_decode_fused": (

@@ -377,8 +377,15 @@ int gdn2_small_linear_pair(const void *x0, int64_t x0_row_stride, const void *we
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+size_t gdn2_argmax_rows_workspace_size(int64_t rows, int64_t n, int io_dtype)
+{
+    if (!valid_dtype(io_dtype) || rows < 1 || n < 1 || rows > 65535) return 0;
+    const int s = argmax_splits(n, io_dtype);
+    return s > 1 ? static_cast<size_t>(rows) * s * (sizeof(int64_t) + sizeof(float)) : 0;
+}
+
 int gdn2_argmax_rows(const void *x, int64_t x_row_stride, int io_dtype, int64_t rows, int64_t n, int64_t *out,
-                     int64_t out_stride, void *stream)
+                     int64_t out_stride, void *workspace, size_t workspace_bytes, void *stream)
 {
     if (!valid_dtype(io_dtype) || rows < 0 || n < 1) return GDN2_ERR_INVALID;
     if (rows == 0) return GDN2_OK;
@@ -388,6 +395,16 @@ int gdn2_argmax_rows(const void *x, int64_t x_row_stride, int io_dtype, int64_t 
     if (rows > 2147483647LL) return GDN2_ERR_UNSUPPORTED;
     ArgmaxParams p;
     p.x = x; p.ld = x_row_stride; p.rows = rows; p.n = n; p.out = out; p.out_stride = out_stride;
+    p.splits = 1; p.pps = 0; p.part_v = nullptr; p.part_i = nullptr;
+    const size_t need = gdn2_argmax_rows_workspace_size(rows, n, io_dtype);
+    if (workspace && need > 0) {
+        if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 7) != 0) return GDN2_ERR_WORKSPACE;
+        p.splits = argmax_splits(n, io_dtype);
+        const int64_t pieces = n / (io_dtype == GDN2_DTYPE_F32 ? 4 : 8);
+        p.pps = (pieces + p.splits - 1) / p.splits;
+        p.part_i = static_cast<int64_t *>(workspace);
+        p.part_v = reinterpret_cast<float *>(p.part_i + rows * p.splits);
+    }
     const hipError_t err = launch_argmax_rows(p, io_dtype, static_cast<hipStream_t>(stream));
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }

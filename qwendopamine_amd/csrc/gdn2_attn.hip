@@ -385,9 +385,121 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(ArgmaxParams p)
     }
 }
 
+// Merge rule of two argmax candidates (value, index): larger value, or NaN
+// where the other is not, or equal / both NaN at a smaller index.
+__device__ __forceinline__ void argmax_take(float &best, int64_t &bi, float v, int64_t i)
+{
+    const bool vn = v != v, bn = best != best;
+    const bool better = (vn && !bn) || (!vn && !bn && v > best) || ((v == best || (vn && bn)) && i < bi);
+    if (better) {
+        best = v;
+        bi = i;
+    }
+}
+
+// Split form, first pass: workgroup (s, row) scans pieces [s pps, (s + 1) pps)
+// of the row (pps = 256 threads x 4 pieces: one batch of requests per
+// thread), the last split also the ragged tail, and leaves its candidate.
+// A row of 151,936 bf16 logits takes 19 workgroups on 19 CUs instead of one
+// CU streaming the whole 304 KB.
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_part_kernel(ArgmaxParams p)
+{
+    constexpr int EPP = 16 / static_cast<int>(sizeof(T));
+    constexpr int U = 4;
+    __shared__ float sv[4];
+    __shared__ int64_t si[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t row = blockIdx.y;
+    const T *x = static_cast<const T *>(p.x) + row * p.ld;
+    const int64_t pieces = p.n / EPP;
+    const int64_t c_lo = static_cast<int64_t>(blockIdx.x) * p.pps;
+    const int64_t c_hi = c_lo + p.pps < pieces ? c_lo + p.pps : pieces;
+    float best = -INFINITY;
+    int64_t bi = p.n;
+    bool have = false;
+    auto scan = [&](float v, int64_t i) __attribute__((always_inline)) {
+        if (!have || v > best || (v != v && best == best)) {
+            best = v;
+            bi = i;
+        }
+        have = true;
+    };
+    for (int64_t c0 = c_lo + tid; c0 < c_hi; c0 += 256 * U) {
+        uint4 raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + 256 * u;
+            raw[u] = *reinterpret_cast<const uint4 *>(x + (c < c_hi ? c : c0) * EPP);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + 256 * u;
+            if (c >= c_hi) continue;
+            const unsigned w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+            for (int e = 0; e < EPP; ++e) {
+                float v;
+                if constexpr (sizeof(T) == 4) {
+                    v = __uint_as_float(w[e]);
+                } else {
+                    const uint16_t h = static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+                    if constexpr (std::is_same<T, bf16_t>::value)
+                        v = bf16_bits_to_f32(h);
+                    else
+                        v = static_cast<float>(__builtin_bit_cast(_Float16, h));
+                }
+                scan(v, c * EPP + e);
+            }
+        }
+    }
+    if (blockIdx.x == gridDim.x - 1)
+        for (int64_t i = pieces * EPP + tid; i < p.n; i += 256) scan(io<T>::ld(x, i), i);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float v2 = __shfl_xor(best, o, 64);
+        const int64_t i2 = __shfl_xor(bi, o, 64);
+        argmax_take(best, bi, v2, i2);
+    }
+    if (lane == 0) {
+        sv[wave] = best;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w2 = 1; w2 < 4; ++w2) argmax_take(best, bi, sv[w2], si[w2]);
+        p.part_v[row * p.splits + blockIdx.x] = best;
+        p.part_i[row * p.splits + blockIdx.x] = bi;
+    }
+}
+
+// Split form, second pass: one wave per row merges the splits' candidates.
+__global__ __launch_bounds__(64) void argmax_finish_kernel(ArgmaxParams p)
+{
+    const int lane = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    float best = -INFINITY;
+    int64_t bi = p.n;
+    for (int s = lane; s < p.splits; s += 64)
+        argmax_take(best, bi, p.part_v[row * p.splits + s], p.part_i[row * p.splits + s]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float v2 = __shfl_xor(best, o, 64);
+        const int64_t i2 = __shfl_xor(bi, o, 64);
+        argmax_take(best, bi, v2, i2);
+    }
+    if (lane == 0) p.out[row * p.out_stride] = bi < p.n ? bi : 0;
+}
+
 template <typename T>
 void argmax_launch(const ArgmaxParams &p, hipStream_t stream)
 {
+    if (p.splits > 1) {
+        hipLaunchKernelGGL((argmax_part_kernel<T>), dim3(static_cast<unsigned>(p.splits), static_cast<unsigned>(p.rows)),
+                           dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(argmax_finish_kernel, dim3(static_cast<unsigned>(p.rows)), dim3(64), 0, stream, p);
+        return;
+    }
     // Pieces in flight per thread: one batch covers a row of up to 1024 * U
     // pieces (U = 20: 163,840 bf16 logits), longer rows loop.
     const dim3 grid(static_cast<unsigned>(p.rows));
@@ -401,6 +513,13 @@ void argmax_launch(const ArgmaxParams &p, hipStream_t stream)
 }
 
 }  // namespace
+
+int argmax_splits(int64_t n, int io_dtype)
+{
+    const int64_t epp = io_dtype == GDN2_DTYPE_F32 ? 4 : 8;
+    const int64_t s = (n / epp + 1023) / 1024;
+    return static_cast<int>(s < 1 ? 1 : (s > 4096 ? 4096 : s));
+}
 
 hipError_t launch_argmax_rows(const ArgmaxParams &p, int io_dtype, hipStream_t stream)
 {

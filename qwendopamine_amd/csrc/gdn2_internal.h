@@ -243,7 +243,16 @@ struct ArgmaxParams {
     const void *x;
     int64_t ld, rows, n, out_stride;
     int64_t *out;
+    // Split form: each row's pieces over `splits` workgroups of pps pieces,
+    // whose (value, index) candidates part_v / part_i [rows][splits] a second
+    // kernel merges.
+    int splits;
+    int64_t pps;
+    float *part_v;
+    int64_t *part_i;
 };
+// Workgroups per row of the split form (1: the single-workgroup kernel).
+int argmax_splits(int64_t n, int io_dtype);
 hipError_t launch_argmax_rows(const ArgmaxParams &p, int io_dtype, hipStream_t stream);
 hipError_t launch_attn_decode(const AttnDecodeParams &p, int io_dtype, hipStream_t stream);
 

@@ -1364,11 +1364,13 @@ def linear_pair(x0: torch.Tensor, w0: torch.Tensor, b0: torch.Tensor | None, x1:
 
 
 @torch.compiler.disable
-def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """``x.argmax(-1, keepdim=True)`` of a 2-D tensor of logits in one HIP launch (one
-    workgroup per row; the first index of the maximum, NaN counting as the maximum, as
-    torch's argmax), written to ``out`` (int64 ``[rows, 1]``, any row stride) when
-    given.  Rows whose layout the kernel does not take use torch's argmax."""
+def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None, split: bool = True) -> torch.Tensor:
+    """``x.argmax(-1, keepdim=True)`` of a 2-D tensor of logits on the HIP kernels (the
+    first index of the maximum, NaN counting as the maximum, as torch's argmax), written
+    to ``out`` (int64 ``[rows, 1]``, any row stride) when given.  Rows longer than 1024
+    16-byte pieces are split over several workgroups and merged by a second launch
+    (workspace allocated here); ``split=False`` keeps one workgroup per row, one launch.
+    Rows whose layout the kernel does not take use torch's argmax."""
     if x.dim() != 2:
         raise ValueError("argmax_rows: x must be 2-D [rows, n]")
     rows, n = x.shape
@@ -1379,8 +1381,11 @@ def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
     st = nat.ERR_UNSUPPORTED
     if x.is_cuda and x.dtype in (torch.bfloat16, torch.float16, torch.float32) and n > 0 and x.stride(1) == 1:
         lib = nat.load()
-        st = lib.gdn2_argmax_rows(nat.ptr(x), x.stride(0) if rows > 1 else n, nat.dtype_code(x.dtype), rows, n,
-                                  nat.ptr(out), out.stride(0) if rows > 1 else 1, nat.stream_handle(x.device))
+        dt = nat.dtype_code(x.dtype)
+        ws_bytes = lib.gdn2_argmax_rows_workspace_size(rows, n, dt) if split else 0
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+        st = lib.gdn2_argmax_rows(nat.ptr(x), x.stride(0) if rows > 1 else n, dt, rows, n, nat.ptr(out),
+                                  out.stride(0) if rows > 1 else 1, nat.ptr(ws), ws_bytes, nat.stream_handle(x.device))
     if st == nat.ERR_UNSUPPORTED:
         out.copy_(x.argmax(-1, keepdim=True).view(out.shape))
         return out

@@ -44,6 +44,16 @@ def test_library_exports_every_declared_symbol(lib):
         assert name in nat.SIGNATURES, f"{name} has no ctypes signature in _native.py"
 
 
+def test_every_bound_entry_point_is_declared():
+    """The reverse direction: every entry point the ctypes binding names (the
+    library's public surface) is declared in gdn2_hip.h."""
+    from qwendopamine_amd import _native as nat
+
+    declared = set(_declared_functions())
+    missing = sorted(n for n in nat.SIGNATURES if n not in declared)
+    assert not missing, f"bound in _native.py but not declared in gdn2_hip.h: {missing}"
+
+
 def test_abi_version_and_status_strings(lib):
     from qwendopamine_amd import _native as nat
 

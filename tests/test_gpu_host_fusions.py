@@ -504,11 +504,13 @@ def test_argmax_rows_matches_torch(gpu_device, dtype, rows, n):
         x[3, n - 1] = 0.0
     ref = x.argmax(-1, keepdim=True)
     got = argmax_rows(x)
+    got_one = argmax_rows(x, split=False)             # one workgroup per row
     wide = torch.zeros(rows, 3, dtype=torch.int64, device=gpu_device)
     argmax_rows(x, out=wide[:, 1:2])
     big = torch.randn(rows, 2, n, generator=g).to(gpu_device, dtype)
     torch.cuda.synchronize()
     assert torch.equal(got, ref), (got.flatten().tolist(), ref.flatten().tolist())
+    assert torch.equal(got_one, ref), (got_one.flatten().tolist(), ref.flatten().tolist())
     assert torch.equal(wide[:, 1:2], ref) and not bool(wide[:, 0].any()) and not bool(wide[:, 2].any())
     assert torch.equal(argmax_rows(big[:, 1]), big[:, 1].argmax(-1, keepdim=True))
 
