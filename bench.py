@@ -35,6 +35,7 @@ BF16_PEAK_TFLOPS = 2500.0
 
 PREFILL = dict(B=8, T=4096, H=16, K=128, V=128, C=64)
 DECODE = dict(N=64, H=16, K=128, V=128, steps=1024)
+DECODE_BEYOND_MALL = dict(N=256, steps=256)  # 268 MB of state, more than the 256 MB MALL
 TRAIN = dict(B=4, T=8192, H=16, K=128, V=128, C=64)
 # Mixer prologue / epilogue at config 3's module shape (hidden 1024, 16 heads x 64).
 PROLOGUE = dict(B=4, T=2048, H=16, Dh=64, W=4)
@@ -207,11 +208,15 @@ def bench_train(torch, nat, dev, steps, warmup):
                        "grads": "dq, dk, dv, dg, db, dw"}}
 
 
-def bench_decode(torch, nat, dev, reps=3, eager_steps=0, variant="plain"):
+def bench_decode(torch, nat, dev, reps=3, eager_steps=0, variant="plain", N=None, steps=None):
     """Config-2 decode steps in one HIP graph.  ``variant``: "plain" (state [N,H,K,V] in place),
     "pooled" (the states live in a pool of 2N slots addressed through int32
-    ssm_state_indices, updated in place) or "transposed" ([N,H,V,K] states)."""
-    N, H, K, V, S = (DECODE[x] for x in ("N", "H", "K", "V", "steps"))
+    ssm_state_indices, updated in place) or "transposed" ([N,H,V,K] states).  ``N`` and
+    ``steps`` override config 2's 64 sequences and 1024 steps (the line whose state does
+    not fit the 256 MB MALL uses N = 256)."""
+    H, K, V = (DECODE[x] for x in ("H", "K", "V"))
+    N = DECODE["N"] if N is None else N
+    S = DECODE["steps"] if steps is None else steps
     F = torch.nn.functional
     gen = torch.Generator(device=dev).manual_seed(2)
     bf = torch.bfloat16
@@ -299,16 +304,17 @@ def bench_decode(torch, nat, dev, reps=3, eager_steps=0, variant="plain"):
     return dict(us_per_step=round(us_step, 3), steps=S, reps=reps,
                 bytes_per_step=nbytes, achieved_GBps=round(gbs, 1),
                 frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4),
-                config={"workload": "C2 decode N64 H16 K128 V128, fp32 state in place, 1024 steps "
+                config={"workload": f"C2 decode N{N} H{H} K{K} V{V}, fp32 state in place, {S} steps "
                                     "in one HIP graph", "dtype": "bf16 in / fp32 state",
-                        "state": variant})
+                        "state": variant, "state_bytes": N * H * K * V * 4})
 
 
-def copy_ceiling(torch, dev, reps=3, copies=256):
+def copy_ceiling(torch, dev, reps=3, copies=256, N=None):
     """Device-to-device copy of a tensor the size of the C2 state (67.1 MB read + 67.1 MB
-    written), `copies` back to back in one HIP graph: the practical read+write bandwidth
-    the decode step is compared with."""
-    N, H, K, V = (DECODE[x] for x in ("N", "H", "K", "V"))
+    written; N sequences' states with ``N``), `copies` back to back in one HIP graph: the
+    practical read+write bandwidth the decode step is compared with."""
+    H, K, V = (DECODE[x] for x in ("H", "K", "V"))
+    N = DECODE["N"] if N is None else N
     src = torch.randn(N, H, K, V, device=dev)
     dst = torch.empty_like(src)
     side = torch.cuda.Stream(dev)
@@ -580,6 +586,28 @@ def bench_e2e(torch, dev, n_prompt=2048, n_new=256, batch=4):
     t_pre, t_first, t_dec = (e[i].elapsed_time(e[i + 1]) for i in range(3))
     n_rep = n_new - 2
     total_ms = t_pre + t_first + t_dec
+    last_tok = dec.tok.clone()
+    check = e2e_check(torch, dec, prompt, n_new, cfg.vocab_size)
+    check["timed_run_last_tokens_in_range"] = bool(((last_tok >= 0) & (last_tok < cfg.vocab_size)).all())
+    if not (check["timed_run_last_tokens_in_range"] and check["logits_finite"] and check["tokens_in_range"]
+            and check["graph_equals_eager"]):
+        raise RuntimeError(f"config-3 decode check failed: {check}")
+    # HBM bytes one decode step must read (and write): every weight but the embedding
+    # table (of which the batch's rows are read), the attention layers' KV caches up to
+    # the current position (mean over the timed steps), and the gdn2 layers' recurrent
+    # states and conv caches (read and written in place).
+    io = next(model.parameters()).element_size()
+    n_gdn2 = sum(cfg.is_gdn2(i) for i in range(cfg.n_layer))
+    n_attn = cfg.n_layer - n_gdn2
+    hv = int(cfg.head_size * cfg.expand_v)
+    weights = sum(p.numel() * p.element_size() for n, p in model.named_parameters()
+                  if not n.startswith("wte.")) + batch * cfg.n_embd * io
+    pos_mean = n_prompt + 1 + (n_new - 2) / 2.0
+    kv = int(n_attn * 2 * batch * cfg.n_query_groups * pos_mean * cfg.head_size * io)
+    states = n_gdn2 * batch * cfg.n_head * cfg.head_size * hv * 4 * 2
+    convs = n_gdn2 * batch * cfg.n_head * (2 * cfg.head_size + hv) * (cfg.conv_size - 1) * io * 2
+    step_bytes = weights + kv + states + convs
+    step_s = t_dec / n_rep * 1e-3
     return {
         "config": {"workload": "C3 hybrid decoder, prefill B4 x 2048 then greedy decode 256",
                    "layers": "24 (18 gdn2 + 6 attention)", "hidden": cfg.n_embd,
@@ -593,7 +621,35 @@ def bench_e2e(torch, dev, n_prompt=2048, n_new=256, batch=4):
         "decode_tokens_per_s": round(batch * n_rep / (t_dec * 1e-3), 1),
         "e2e_tokens_per_s": round(batch * (n_prompt + n_new) / (total_ms * 1e-3), 1),
         "wall_s": round(wall, 3),
+        "decode_step_bytes": {"weights": weights, "kv_cache": kv, "gdn2_states": states,
+                              "gdn2_conv_caches": convs, "total": step_bytes},
+        "decode_achieved_GBps": round(step_bytes / step_s / 1e9, 1),
+        "decode_frac_hbm_peak": round(step_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
+        "check": check,
     }
+
+
+def e2e_check(torch, dec, prompt, n_new, vocab, n_eager=32):
+    """Untimed checks of the config-3 decode: a graph run over all ``n_new`` steps with
+    the logits kept (every step's logits finite, every token in range), and an eager run
+    of the first ``n_eager`` steps that must give the graph run's tokens."""
+    from qwendopamine_amd.hybrid import GreedyDecoder
+
+    runs = {}
+    for use_graph, n in ((True, n_new), (False, n_eager)):
+        d = GreedyDecoder(dec.model, use_graph=use_graph, keep_logits=True)
+        toks = [d.prefill(prompt, n_new).clone()]
+        finite = [torch.isfinite(d.logits).all()]
+        for _ in range(n - 1):
+            toks.append(d.step().clone())
+            finite.append(torch.isfinite(d.logits).all())
+        torch.cuda.synchronize()
+        runs[use_graph] = (torch.cat(toks, 1), bool(torch.stack(finite).all()))
+    tg, fg = runs[True]
+    te, fe = runs[False]
+    return {"steps_checked": n_new, "logits_finite": fg and fe,
+            "tokens_in_range": bool(((tg >= 0) & (tg < vocab)).all()),
+            "eager_steps_compared": n_eager, "graph_equals_eager": bool(torch.equal(tg[:, :n_eager], te))}
 
 
 def traffic_probe(torch, nat, dev):
@@ -820,6 +876,13 @@ def main() -> int:
         cc = copy_ceiling(torch, dev)
         out["decode"]["copy_ceiling"] = cc
         out["decode"]["frac_copy_ceiling"] = round(out["decode"]["achieved_GBps"] / cc["GBps"], 4)
+        # The config-2 state (67 MB) stays in the 256 MB MALL across graph steps; this
+        # line's state (268 MB) does not, so its rate is a DRAM rate.
+        big = bench_decode(torch, nat, dev, N=DECODE_BEYOND_MALL["N"], steps=DECODE_BEYOND_MALL["steps"])
+        cc_big = copy_ceiling(torch, dev, copies=64, N=DECODE_BEYOND_MALL["N"])
+        big["copy_ceiling"] = cc_big
+        big["frac_copy_ceiling"] = round(big["achieved_GBps"] / cc_big["GBps"], 4)
+        out["decode"]["beyond_mall"] = big
     if not args.no_train:
         out["train"] = bench_train(torch, nat, dev, max(2, args.steps // 2), 1)
     if not args.no_prologue:

@@ -1182,20 +1182,10 @@ hipError_t launch_bwd(const BwdParams &p, int total_chunks, hipStream_t stream)
     // looked up once per device), each walking items (chunk, head) =
     // item / H, item % H with a stride of the grid.
     const auto kern = chunk_bwd_kside_kernel<PK, KP, TI, TG>;
-    static int resident[64] = {};  // per instantiation
-    int dev = 0;
-    e = hipGetDevice(&dev);
+    static std::atomic<int> resident[64];  // per instantiation
+    int slots = 0;
+    e = resident_slots(kern, 512, resident, &slots);
     if (e != hipSuccess) return e;
-    int slots = dev < 64 ? resident[dev] : 0;
-    if (slots == 0) {
-        int cus = 0, per_cu = 0;
-        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 512, 0);
-        if (e != hipSuccess) return e;
-        slots = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
-        if (dev < 64) resident[dev] = slots;
-    }
     const int64_t items = static_cast<int64_t>(total_chunks) * p.H;
     if (items > (int64_t{1} << 30)) return hipErrorInvalidValue;  // item indices stay in int
     const int grid = static_cast<int>(items < slots ? items : slots);

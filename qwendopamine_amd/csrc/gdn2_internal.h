@@ -6,7 +6,34 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace gdn2 {
+
+// Workgroups of `kern` (at `threads` per workgroup) that the current device
+// holds at once: occupancy per CU x CUs, looked up once per device and kept in
+// `cache` (one per kernel instantiation, zero = not yet known).  The entries
+// are atomics, so host threads that launch together for the first time may
+// both compute the value and store the same result.
+template <typename Kern>
+hipError_t resident_slots(Kern kern, int threads, std::atomic<int> (&cache)[64], int *slots)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    int n = dev < 64 ? cache[dev].load(std::memory_order_relaxed) : 0;
+    if (n == 0) {
+        int cus = 0, per_cu = 0;
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0);
+        if (e != hipSuccess) return e;
+        n = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+        if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+    }
+    *slots = n;
+    return hipSuccess;
+}
 
 struct RecurrentParams {
     const void *q, *k, *v, *g, *b, *w;

@@ -80,7 +80,7 @@ def resolve_gdn2_backend(requested: str, *, training: bool, seq_len: int) -> str
     execution backend of this package on every supported device.
     """
     if requested not in GDN2_BACKENDS:
-        raise ValueError(f"Invalid GDN-2 backend '{requested}'. Valid backends: {list(GDN2_BACKENDS)}")
+        raise ValueError(f"gdn2 backend {requested!r} is not one of {', '.join(GDN2_BACKENDS)}")
     del training, seq_len
     return "hip" if requested == "auto" else requested
 

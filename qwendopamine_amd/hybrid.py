@@ -213,6 +213,15 @@ class CausalSelfAttention(nn.Module):
             # RoPE, the cache store and the attention of the token in one HIP launch.
             o = ops.attention_decode(qkv, cos, sin, input_pos, *self.kv_cache, self.n_head)
             return ops.linear(o.reshape(b, 1, self.n_head * D), self.proj.weight, self.proj.bias)
+        if input_pos is not None and cos.shape[0] != t:
+            # Whole rotation tables without a mask: the caller expected the fused decode
+            # launch above, which this call cannot take (its predicate reads the weights,
+            # this one the projection output).  Select the rows of input_pos and build the
+            # causal mask over the cache here.
+            cos, sin = cos.index_select(0, input_pos), sin.index_select(0, input_pos)
+            if mask is None and self.kv_cache is not None:
+                L = self.kv_cache[0].shape[2]
+                mask = (torch.arange(L, device=qkv.device)[None, :] <= input_pos[:, None]).reshape(1, 1, t, L)
         qkv = qkv.view(b, t, G, qpk + 2, D)
         q, k, v = qkv.split((qpk, 1, 1), dim=-2)
         q = apply_rotary_emb(q.reshape(b, t, self.n_head, D), cos, sin)

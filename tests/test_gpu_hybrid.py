@@ -110,3 +110,29 @@ def test_last_only_logits(gpu_device, dtype):
     tol = 1e-5 if dtype == torch.float32 else 1e-2
     assert rel_l2(last[:, 0], full[:, -1].double().cpu().numpy()) <= tol
     assert rel_l2(cached[:, 0], full[:, -1].double().cpu().numpy()) <= (1e-4 if dtype == torch.float32 else 2e-2)
+
+
+def test_decode_with_frozen_attention_and_grad_enabled(gpu_device):
+    """A cached single-token step with autograd on, the attention weights frozen and the
+    rest trainable: the decoder's fused-attention decision (made on the weights) says
+    fused, but each attention layer sees a projection output that carries a gradient and
+    takes its torch path, which must then select the rotation rows and build the mask
+    itself.  The logits equal the no-grad run's to the bf16 bar (the two runs take
+    different kernels: chunk vs token-serial gdn2, torch vs fused attention)."""
+    print("[case] hybrid decode, frozen attention, grad enabled", flush=True)
+    m = _small(torch.bfloat16, gpu_device)
+    for blk in m.h:
+        if not blk.use_gdn2:
+            blk.attn.requires_grad_(False)
+    idx = torch.randint(0, 1000, (2, 72), device=gpu_device)
+    outs = {}
+    for grad in (False, True):
+        m.setup_caches(2, 72)
+        assert m._attention_decode_fused()
+        with torch.set_grad_enabled(grad):
+            pre = m(idx[:, :70], input_pos=torch.arange(70, device=gpu_device))
+            steps = [m(idx[:, t:t + 1], input_pos=torch.tensor([t], device=gpu_device)) for t in (70, 71)]
+        torch.cuda.synchronize()
+        outs[grad] = torch.cat([pre[:, -1:], *steps], 1).detach()
+    assert outs[True].shape == (2, 3, 1000)
+    assert rel_l2(outs[True], outs[False].double().cpu().numpy()) <= 2e-2

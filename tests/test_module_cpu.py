@@ -257,6 +257,38 @@ def test_stacked_input_weight_is_the_only_copy():
     assert W3.dtype == torch.float64 and m.q_proj.weight.data_ptr() == W3.data_ptr()
 
 
+def test_state_dict_round_trip_after_stacking():
+    """After the stacking that the first inference call does, a ``torch.save`` /
+    ``torch.load`` round trip of the state dict keeps every value and shape and loads into
+    a fresh module; a single stacked parameter saved on its own carries the whole stack's
+    storage (torch saves a view's storage), so it is cloned first when it is saved alone."""
+    import io
+
+    torch.manual_seed(0)
+    m = GatedDeltaNet2(hidden_size=64, num_heads=2, head_dim=32)
+    ref = {k: v.clone() for k, v in m.state_dict().items()}
+    with torch.inference_mode():
+        W, _ = m._fused_input_weight()
+    sd = m.state_dict()
+    assert sd["q_proj.weight"].untyped_storage().data_ptr() == W.untyped_storage().data_ptr()
+    buf = io.BytesIO()
+    torch.save(sd, buf)
+    buf.seek(0)
+    back = torch.load(buf, weights_only=True)
+    assert back.keys() == ref.keys()
+    for k, v in ref.items():
+        assert back[k].shape == v.shape and torch.equal(back[k], v), k
+    fresh = GatedDeltaNet2(hidden_size=64, num_heads=2, head_dim=32)
+    fresh.load_state_dict(back)
+    assert all(torch.equal(fresh.state_dict()[k], v) for k, v in ref.items())
+    one, alone = io.BytesIO(), io.BytesIO()
+    torch.save(m.q_proj.weight, one)
+    torch.save(m.q_proj.weight.detach().clone(), alone)
+    assert len(one.getvalue()) > len(alone.getvalue()) + W.numel() * W.element_size() // 2
+    one.seek(0)
+    assert torch.equal(torch.load(one, weights_only=True), ref["q_proj.weight"])
+
+
 def test_ops_are_not_traced_by_torch_compile():
     """As the reference's ops (chunk_gdn2.py:1267, fused_recurrent_gdn2.py:344), the public
     ops carry torch.compiler.disable: a compiled caller runs them eagerly, so the op's own
