@@ -414,6 +414,9 @@ size_t gdn2_chunk_fwd_workspace_size(int B, int T, int H, int K, int V, int io_d
  * device workspace of at least gdn2_chunk_fwd_workspace_size() bytes.
  * cu_seqlens_host mirrors cu_seqlens on the host (the reference's
  * cu_seqlens_cpu); both NULL or both given.
+ * d_k <= 256 in every io dtype.  float32 inputs with 128 < d_k <= 256 (and
+ * d_v <= 256) run the recurrence token by token with the chunk start states
+ * kept for the backward; they need no workspace outside training.
  */
 int gdn2_chunk_fwd(const void *q, const void *k, const void *v, const void *g, const void *b,
                    const void *w, int io_dtype, int g_dtype, void *o,

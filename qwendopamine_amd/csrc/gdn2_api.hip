@@ -730,10 +730,18 @@ int gdn2_chunk_states(const void *saved, size_t saved_bytes, int io_dtype, void 
 {
     if (!valid_dtype(io_dtype) || B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0) return GDN2_ERR_INVALID;
     if (cu_seqlens_host && (B != 1 || num_seqs < 0)) return GDN2_ERR_INVALID;
-    if (!chunk_k_supported(K, io_dtype)) return GDN2_ERR_UNSUPPORTED;
+    const bool wide = chunk_wide(K, io_dtype);
+    if (!wide && !chunk_k_supported(K, io_dtype)) return GDN2_ERR_UNSUPPORTED;
     const int64_t nc = count_chunks(B, T, cu_seqlens_host, num_seqs);
     if (nc == 0) return GDN2_OK;
     if (!saved || !out) return GDN2_ERR_INVALID;
+    if (wide) {
+        if (saved_bytes < wide_train_workspace_bytes(B, T, H, K, V, cu_seqlens_host, num_seqs))
+            return GDN2_ERR_WORKSPACE;
+        const hipError_t err = launch_chunk_states_wide(saved, out, transpose != 0, nc, H, K, V,
+                                                        static_cast<hipStream_t>(stream));
+        return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
+    }
     const TrainLayout tl = train_layout(nc, H, K, V, io_dtype);
     if (saved_bytes < static_cast<size_t>(tl.total)) return GDN2_ERR_WORKSPACE;
     const hipError_t err = launch_chunk_states(static_cast<const unsigned char *>(saved) + tl.hs, io_dtype, out,

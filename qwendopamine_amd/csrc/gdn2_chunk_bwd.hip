@@ -1211,6 +1211,7 @@ hipError_t launch_bwd_kp(const BwdParams &p, int total_chunks, hipStream_t strea
 size_t chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype,
                                  const int64_t *cu_host, int num_seqs)
 {
+    if (chunk_wide(K, io_dtype)) return wide_bwd_workspace_bytes(B, T, H, K, V, cu_host, num_seqs);
     if (!chunk_k_supported(K, io_dtype)) return 0;
     const int64_t nc = count_chunks(B, T, cu_host, num_seqs);
     return static_cast<size_t>(bwd_layout(nc, H, K, V, io_dtype).total);
@@ -1219,6 +1220,7 @@ size_t chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
 size_t chunk_train_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype,
                                    const int64_t *cu_host, int num_seqs)
 {
+    if (chunk_wide(K, io_dtype)) return wide_train_workspace_bytes(B, T, H, K, V, cu_host, num_seqs);
     if (!chunk_k_supported(K, io_dtype)) return 0;
     const int64_t nc = count_chunks(B, T, cu_host, num_seqs);
     return static_cast<size_t>(train_layout(nc, H, K, V, io_dtype).total);
@@ -1226,6 +1228,7 @@ size_t chunk_train_workspace_bytes(int B, int T, int H, int K, int V, int io_dty
 
 int launch_chunk_bwd(const ChunkBwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream)
 {
+    if (chunk_wide(a.K, io_dtype)) return launch_chunk_bwd_wide(a, g_dtype, stream);
     if (!chunk_k_supported(a.K, io_dtype)) return GDN2_ERR_UNSUPPORTED;
     if (g_dtype != GDN2_DTYPE_F32 && g_dtype != io_dtype) return GDN2_ERR_UNSUPPORTED;
     const int64_t nc = count_chunks(a.B, a.T, a.cu_host, a.num_seqs);

@@ -1613,6 +1613,7 @@ size_t chunk_fwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
                                  const int64_t *cu_host, int num_seqs)
 {
     (void)V;
+    if (chunk_wide(K, io_dtype)) return 0;  // the token-serial path needs no blobs
     if (!chunk_k_supported(K, io_dtype)) return 0;
     const int64_t nc = count_chunks(B, T, cu_host, num_seqs);
     return static_cast<size_t>(nc) * H * static_cast<size_t>(blob_bytes(io_dtype, kp_for(K)));
@@ -1620,6 +1621,7 @@ size_t chunk_fwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
 
 int launch_chunk_fwd(const ChunkFwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream)
 {
+    if (chunk_wide(a.K, io_dtype)) return launch_chunk_fwd_wide(a, g_dtype, stream);
     if (!chunk_k_supported(a.K, io_dtype)) return GDN2_ERR_UNSUPPORTED;
     if (a.z && (io_dtype != GDN2_DTYPE_BF16 || a.V != bv_for(a.V) || (a.V % 16) != 0 ||
                 (a.flags & GDN2_FLAG_SAVE_FOR_BWD)))

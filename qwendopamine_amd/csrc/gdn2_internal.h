@@ -149,6 +149,17 @@ size_t chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
                                  const int64_t *cu_host, int num_seqs);
 int launch_chunk_bwd(const ChunkBwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream);
 
+// Float32 chunk op with 128 < d_k <= 256 (gdn2_chunk_wide.hip): token-serial
+// kernels with chunk start states kept for the backward, for the key widths
+// whose fp32 chunk workspace does not fit the MFMA kernels' LDS.
+bool chunk_wide(int K, int io_dtype);
+size_t wide_train_workspace_bytes(int B, int T, int H, int K, int V, const int64_t *cu_host, int num_seqs);
+size_t wide_bwd_workspace_bytes(int B, int T, int H, int K, int V, const int64_t *cu_host, int num_seqs);
+int launch_chunk_fwd_wide(const ChunkFwdArgs &a, int g_dtype, hipStream_t stream);
+int launch_chunk_bwd_wide(const ChunkBwdArgs &a, int g_dtype, hipStream_t stream);
+hipError_t launch_chunk_states_wide(const void *hs, void *out, bool transpose, int64_t nc, int H, int K, int V,
+                                    hipStream_t stream);
+
 // Chunk start states saved by a training forward -> [nc, H, K, V] (or
 // [nc, H, V, K]) in io_dtype.
 hipError_t launch_chunk_states(const void *hs, int io_dtype, void *out, bool transpose, int64_t nc,

@@ -150,7 +150,14 @@ def test_chunk_workspace_size(lib):
     n2 = lib.gdn2_chunk_fwd_workspace_size(1, 75, 2, 64, 64, 0, ctypes.cast(cu, ctypes.c_void_p), 3)
     assert n2 == (1 + 0 + 2) * 2 * ((192 * 64 + 8192) * 4 + 64 * 4)
     # d_k in (128, 256]: KP = 256 blobs (X, Aqk 64x64; -W, Qbar 64x256; Ktilde^T 256x64; 256
-    # decay floats) for 16-bit inputs; float32 inputs are not supported there, nor d_k > 256.
+    # decay floats) for 16-bit inputs.  float32 inputs there take the token-serial wide path:
+    # no inference workspace; in training the chunk start states [nc, H, K, V] fp32, and a
+    # backward scratch of 64 decayed states per (sequence, head, 128-column slice) plus, with
+    # two slices, four [B*T*H, K] planes of the second slice's row sums.  d_k > 256: nothing.
     assert lib.gdn2_chunk_fwd_workspace_size(1, 64, 1, 200, 64, 1, None, 1) == (2 * 4096 + 3 * 16384) * 2 + 256 * 4
     assert lib.gdn2_chunk_fwd_workspace_size(1, 64, 1, 200, 64, 0, None, 1) == 0
     assert lib.gdn2_chunk_fwd_workspace_size(1, 64, 1, 257, 64, 1, None, 1) == 0
+    assert lib.gdn2_chunk_train_workspace_size(2, 130, 3, 200, 64, 0, None, 2) == 2 * 3 * 3 * 200 * 64 * 4
+    assert lib.gdn2_chunk_bwd_workspace_size(2, 130, 3, 200, 64, 0, None, 2) == 2 * 3 * 64 * 4 * 16 * 64 * 16
+    assert lib.gdn2_chunk_bwd_workspace_size(2, 130, 3, 200, 200, 0, None, 2) == (
+        2 * 3 * 2 * 64 * 8 * 16 * 64 * 16 + 4 * 2 * 130 * 3 * 200 * 4)

@@ -2,9 +2,8 @@
 accepts d_k <= 256): the KP = 256 instantiations of prep, scan and the backward, for
 bf16 / fp16 inputs, against the float64 oracle at the 16-bit bar (rel. L2 <= 2e-2).
 
-float32 inputs beyond d_k = 128 do not fit the scans' LDS (a 231 KB blob); the chunk op
-raises ``NotImplementedError`` for them, and the token-serial op (d_k <= 256) covers
-their inference.
+float32 inputs beyond d_k = 128 take the token-serial wide path instead (a 231 KB fp32
+blob does not fit the scans' LDS); its tests are in ``test_gpu_wide_keys_fp32.py``.
 """
 
 from __future__ import annotations
@@ -78,22 +77,6 @@ def test_chunk_backward_wide_keys(gpu_device, K, V, T, decay):
     print("  rel_l2 " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
     for k, e in errs.items():
         assert e <= 2e-2, (k, e)
-
-
-def test_chunk_fp32_wide_keys_rejected_recurrent_ok(gpu_device):
-    from qwendopamine_amd.ops import chunk_gdn2, fused_recurrent_gdn2
-
-    print("[case] fp32 d_k=256: chunk op rejects, token-serial op computes", flush=True)
-    inp = rand_inputs(1, 70, 2, 256, 32, seed=9)
-    t, r = to_device(inp, gpu_device, torch.float32)
-    with pytest.raises(NotImplementedError, match="d_k <= 128"):
-        chunk_gdn2(*(t[n] for n in NAMES), use_qk_l2norm_in_kernel=True)
-    with torch.no_grad():
-        o, ht = fused_recurrent_gdn2(*(t[n] for n in NAMES), initial_state=t["h0"], output_final_state=True,
-                                     use_qk_l2norm_in_kernel=True)
-    torch.cuda.synchronize()
-    o_ref, s_ref = orc.recurrent_fwd(*(r[n] for n in NAMES), r["h0"])
-    assert rel_l2(o, o_ref) <= 1e-4 and rel_l2(ht, s_ref) <= 1e-4
 
 
 def test_module_head_dim_256_prefill_and_training(gpu_device):
