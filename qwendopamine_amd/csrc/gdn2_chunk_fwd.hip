@@ -328,7 +328,8 @@ __device__ __forceinline__ PrepItem prep_item(const ChunkParams &p, int item)
 // ---------------------------------------------------------------------------
 template <PrecKind PK, int KP, typename TI, typename TG, bool CONV = false>
 __global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu((PK == PrecKind::F32 && KP == 128) || KP > 128 ? 1 : 3))) void
+__attribute__((amdgpu_waves_per_eu((PK == PrecKind::F32 && KP == 128) || KP > 128 ? 1
+                                   : (PK != PrecKind::F32 && KP <= 64 ? 4 : 3)))) void
 chunk_prep_kernel(ChunkParams p, int items)
 {
     static_assert(!CONV || (sizeof(TI) == 2 && KP <= 128), "the fused convolution takes 16-bit rows, d_k <= 128");
@@ -348,7 +349,12 @@ chunk_prep_kernel(ChunkParams p, int items)
     __shared__ __align__(16) unsigned char smem1[SZ1];  // Kend, then L (fp32)
     __shared__ __align__(16) st sEt[NKT * 4 * 256];     // Ebar^T, K16 blocks (channel, token)
     // sX holds, in turn: waves 0-1's row staging, the block vectors, then X.
-    constexpr int SZX0 = 64 * LDF > 24 * KP ? 64 * LDF : 24 * KP;
+    // X keeps only its ten lower 16x16 blocks, (I, J) for J <= I at block
+    // I (I + 1) / 2 + J, rows LDB apart: with 16-bit storage at d_k <= 64 this
+    // brings the kernel to 40 KB of LDS, four workgroups per CU.
+    constexpr int LDB = 16 + 4;
+    constexpr int XBS = 16 * LDB;
+    constexpr int SZX0 = 10 * XBS > 24 * KP ? 10 * XBS : 24 * KP;
     constexpr int SZX = SZX0 > 8 * (KP * 4 + 16) ? SZX0 : 8 * (KP * 4 + 16);
     __shared__ __align__(16) float sX[SZX];
     __shared__ __align__(16) float sT[4][KP];           // in-block decay totals (log2)
@@ -735,7 +741,8 @@ chunk_prep_kernel(ChunkParams p, int items)
         __syncthreads();
 
         // X = (I + L)^{-1} in fp32: diagonal 16x16 blocks by forward substitution
-        // (lane j = column j), strictly-upper blocks zero.
+        // (lane j = column j); the strictly-upper blocks are zero and not stored.
+        auto xblk = [&](int I, int J) __attribute__((always_inline)) { return sX + (I * (I + 1) / 2 + J) * XBS; };
         if (l < 16) {
             const int j = l;
             float x[16];
@@ -756,10 +763,8 @@ chunk_prep_kernel(ChunkParams p, int items)
                 x[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
             }
 #pragma unroll
-            for (int i = 0; i < 16; ++i) sX[(16 * R + i) * LDF + 16 * R + j] = x[i];
+            for (int i = 0; i < 16; ++i) xblk(R, R)[i * LDB + j] = x[i];
         }
-        for (int I = R + 1; I < 4; ++I)
-            for (int e = l; e < 256; e += 64) sX[(16 * R + (e >> 4)) * LDF + 16 * I + (e & 15)] = 0.f;
         __syncthreads();
         // Off-diagonal blocks, one sub-diagonal at a time:
         //   X_RI = -X_RR * sum_{J=I}^{R-1} L_RJ X_JI.
@@ -768,16 +773,16 @@ chunk_prep_kernel(ChunkParams p, int items)
                 const int Rr = R + d, I = R;
                 f32x4 t = zero4();
                 for (int J = I; J < Rr; ++J)
-                    t = mm16_f32(t, sL + (16 * Rr) * LDF + 16 * J, LDF, sX + (16 * J) * LDF + 16 * I, LDF, l);
+                    t = mm16_f32(t, sL + (16 * Rr) * LDF + 16 * J, LDF, xblk(J, I), LDB, l);
                 // Transposing scratch of wave R (<= 2): L's upper block (0, R + 1).
                 float *scr = sL + 16 * (R + 1);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) scr[(4 * kg + i) * LDF + m] = t[i];
                 __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
                 __builtin_amdgcn_wave_barrier();
-                const f32x4 xr = mm16_f32(zero4(), sX + (16 * Rr) * LDF + 16 * Rr, LDF, scr, LDF, l);
+                const f32x4 xr = mm16_f32(zero4(), xblk(Rr, Rr), LDB, scr, LDF, l);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sX[(16 * Rr + 4 * kg + i) * LDF + 16 * I + m] = -xr[i];
+                for (int i = 0; i < 4; ++i) xblk(Rr, I)[(4 * kg + i) * LDB + m] = -xr[i];
             }
             __syncthreads();
         }
@@ -786,7 +791,10 @@ chunk_prep_kernel(ChunkParams p, int items)
         Q xt[4];
 #pragma unroll
         for (int J = 0; J < 4; ++J) {
-            const float4 xv = *reinterpret_cast<const float4 *>(&sX[(16 * R + m) * LDF + 16 * J + 4 * kg]);
+            // Blocks above the diagonal (J > R) are zero: read the diagonal block's
+            // address and select zero, so that no branch separates the reads.
+            float4 xv = *reinterpret_cast<const float4 *>(xblk(R, J <= R ? J : R) + m * LDB + 4 * kg);
+            if (J > R) xv = make_float4(0.f, 0.f, 0.f, 0.f);
             xt[J] = pack4<PK>(xv.x, xv.y, xv.z, xv.w);
             if (p.hs || !(R < 2 && J >= 2))  // as for Aqk above
                 st_q4<PK>(ws + BL::X + k16_block(R, J, 64) + 4 * l, xt[J]);
