@@ -508,8 +508,21 @@ def bench_prologue(torch, dev, reps=20):
     # fused decode: state read + write, raw q/k/v/g/b/w/z rows, conv caches read + write,
     # conv weights, normalised output
     dec_bytes = 2 * B * H * Dh * Dh * 4 + 7 * B * D * 2 + 2 * 3 * B * D * (W - 1) * 2 + 3 * D * W * 2 + B * D * 2
+    # Floors of a one-launch decode step in the same graph replay: a launch that does
+    # (almost) nothing, and one elementwise pass that reads and writes the decode's
+    # state once (1 MB at this shape), torch's kernels.
+    tiny = torch.zeros(64, device=dev)
+    state_copy = state.clone()
+
+    def floor_launch():
+        tiny.add_(1.0)
+
+    def floor_state():
+        state_copy.mul_(1.0)
+
     t = {k: timed(f) for k, f in (("conv", conv_hip), ("conv_torch", conv_torch),
                                   ("norm", norm_hip), ("norm_torch", norm_torch),
+                                  ("floor_launch", floor_launch), ("floor_state", floor_state),
                                   ("dec_fused", dec_fused), ("dec_separate", dec_separate),
                                   ("pre_fused", pre_fused), ("pre_separate", pre_separate),
                                   ("pconv_fused", pconv_fused), ("pconv_separate", pconv_separate))}
@@ -527,7 +540,9 @@ def bench_prologue(torch, dev, reps=20):
         "decode_step": {"workload": f"B{B} one token, {H} heads x {Dh}, conv caches and state in place",
                         "fused_us": round(t["dec_fused"], 2), "separate_hip_us": round(t["dec_separate"], 2),
                         "algorithmic_bytes": dec_bytes,
-                        "achieved_GBps": round(dec_bytes / (t["dec_fused"] * 1e-6) / 1e9, 1)},
+                        "achieved_GBps": round(dec_bytes / (t["dec_fused"] * 1e-6) / 1e9, 1),
+                        "floor_launch_us": round(t["floor_launch"], 2),
+                        "floor_state_rw_us": round(t["floor_state"], 2)},
         "training_fwd_bwd": {"workload": "forward + backward, eager (autograd), same shapes",
                              "short_conv_qkv_us": round(train_t["conv_hip"], 1),
                              "short_conv_qkv_torch_us": round(train_t["conv_torch"], 1),
@@ -657,7 +672,8 @@ def traffic_probe(torch, nat, dev):
     kernels whose bytes are known, which calibrate the counters -- a 256 MiB
     device-to-device copy (256 MiB read + written), a 1 GiB fill (written only) and a
     sum over the same 1 GiB (read only) -- then two prefill ops, eight eager decode
-    steps and two training forward + backward steps."""
+    steps, eight eager decode steps with the state beyond the MALL (N = 256) and two
+    training forward + backward steps."""
     a = torch.empty(64 << 20, dtype=torch.float32, device=dev).uniform_()
     c = torch.empty_like(a)
     c.copy_(a)
@@ -670,6 +686,7 @@ def traffic_probe(torch, nat, dev):
     del big, total
     bench_prefill(torch, nat, dev, steps=2, warmup=0)
     bench_decode(torch, nat, dev, eager_steps=8)
+    bench_decode(torch, nat, dev, eager_steps=8, N=DECODE_BEYOND_MALL["N"], steps=8)
     bench_train(torch, nat, dev, steps=2, warmup=0)
     print("traffic probe done", flush=True)
 

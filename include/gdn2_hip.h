@@ -328,6 +328,29 @@ int gdn2_argmax_rows(const void *x, int64_t x_row_stride, int io_dtype, int64_t 
                      int64_t out_stride, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * The in-kernel decay gate as a separate differentiable step, for training
+ * calls of the chunk op with use_gate_in_kernel (reference kda_gate_fwd and
+ * kda_gate_bwd, src/qwendopamine/models/gdn2/gdn2_ops/chunk_kda.py:3223-3292,
+ * kernels :3089-3220).  g_raw [tokens, H, K] in g_dtype (f32 / bf16 / fp16),
+ * A_log [H] and dt_bias [H*K] (or NULL) float32, K <= 256:
+ *   y = -exp(A_log[h]) * softplus(g_raw + dt_bias[h, c]), or with
+ *   GDN2_FLAG_LOWER_BOUND y = lower_bound * sigmoid(exp(A_log[h]) * (g_raw + dt_bias)),
+ * the formula of GDN2_FLAG_GATE_IN_KERNEL.  gdn2_gate_fwd writes y (float32);
+ * gdn2_gate_bwd takes dy (float32) and writes dg_raw (g_dtype), dA_log [H] and
+ * ddt_bias [H*K] (float32; NULL with dt_bias NULL), the two sums over tokens
+ * taken per 64-token block and then added in block order (deterministic).
+ * workspace: at least gdn2_gate_bwd_workspace_size() bytes.
+ */
+size_t gdn2_gate_bwd_workspace_size(int64_t tokens, int H, int K, int has_dt_bias);
+int gdn2_gate_fwd(const void *g_raw, int g_dtype, const float *A_log, const float *dt_bias,
+                  float lower_bound, unsigned flags, float *y, int64_t tokens, int H, int K,
+                  void *stream);
+int gdn2_gate_bwd(const void *g_raw, int g_dtype, const float *A_log, const float *dt_bias,
+                  float lower_bound, unsigned flags, const float *dy, void *dg_raw, float *dA_log,
+                  float *ddt_bias, int64_t tokens, int H, int K, void *workspace,
+                  size_t workspace_bytes, void *stream);
+
+/*
  * Backward of the short convolution on a prefill call (no cache), for training
  * without torch's conv: the gradient of ShortConvolution.forward (reference
  * gdn2.py:395-430, whose backward torch's autograd runs through F.conv1d and

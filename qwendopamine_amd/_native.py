@@ -92,6 +92,12 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp,
          _i, _i, _i, _i, _i, _i, _f, _u, _vp, _sz, _vp],
     ),
+    "gdn2_gate_bwd_workspace_size": (_sz, [_i64, _i, _i, _i]),
+    "gdn2_gate_fwd": (_i, [_vp, _i, _vp, _vp, _f, _u, _vp, _i64, _i, _i, _vp]),
+    "gdn2_gate_bwd": (
+        _i,
+        [_vp, _i, _vp, _vp, _f, _u, _vp, _vp, _vp, _vp, _i64, _i, _i, _vp, _sz, _vp],
+    ),
     "gdn2_short_conv_bwd_workspace_size": (_sz, [_i, _i, _i, _i]),
     "gdn2_short_conv_bwd": (
         _i,

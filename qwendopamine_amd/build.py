@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 INCLUDE = PKG.parent / "include"
 LIB_NAME = "libgdn2_hip.so"
-SOURCES = ["gdn2_api.hip", "gdn2_recurrent.hip", "gdn2_chunk_fwd.hip", "gdn2_chunk_bwd.hip", "gdn2_chunk_wide.hip",
+SOURCES = ["gdn2_api.hip", "gdn2_recurrent.hip", "gdn2_chunk_fwd.hip", "gdn2_chunk_bwd.hip", "gdn2_chunk_wide.hip", "gdn2_gate.hip",
            "gdn2_prologue.hip", "gdn2_prologue_bwd.hip", "gdn2_noalloc.hip", "gdn2_skinny.hip",
            "gdn2_attn.hip"]
 ARCH = os.environ.get("GDN2_OFFLOAD_ARCH", "gfx950")

@@ -443,6 +443,46 @@ int gdn2_attn_decode(const void *qkv, const float *cos, const float *sin, int ro
     return err == hipSuccess ? GDN2_OK : GDN2_ERR_LAUNCH;
 }
 
+size_t gdn2_gate_bwd_workspace_size(int64_t tokens, int H, int K, int has_dt_bias)
+{
+    if (tokens < 0 || H <= 0 || K <= 0 || K > 256) return 0;
+    return gate_bwd_workspace_bytes(tokens, H, K, has_dt_bias != 0);
+}
+
+static int check_gate_args(const void *g_raw, int g_dtype, const float *A_log, unsigned flags, int64_t tokens,
+                           int H, int K)
+{
+    if (!valid_dtype(g_dtype) || tokens < 0 || H <= 0 || K <= 0) return GDN2_ERR_INVALID;
+    if (flags & ~GDN2_FLAG_LOWER_BOUND) return GDN2_ERR_INVALID;
+    if (K > 256) return GDN2_ERR_UNSUPPORTED;
+    if (!A_log || (tokens > 0 && !g_raw)) return GDN2_ERR_INVALID;
+    return GDN2_OK;
+}
+
+int gdn2_gate_fwd(const void *g_raw, int g_dtype, const float *A_log, const float *dt_bias, float lower_bound,
+                  unsigned flags, float *y, int64_t tokens, int H, int K, void *stream)
+{
+    const int st = check_gate_args(g_raw, g_dtype, A_log, flags, tokens, H, K);
+    if (st != GDN2_OK) return st;
+    if (tokens > 0 && !y) return GDN2_ERR_INVALID;
+    return launch_gate_fwd(g_raw, g_dtype, A_log, dt_bias, lower_bound, flags, y, tokens, H, K,
+                           static_cast<hipStream_t>(stream));
+}
+
+int gdn2_gate_bwd(const void *g_raw, int g_dtype, const float *A_log, const float *dt_bias, float lower_bound,
+                  unsigned flags, const float *dy, void *dg_raw, float *dA_log, float *ddt_bias, int64_t tokens,
+                  int H, int K, void *workspace, size_t workspace_bytes, void *stream)
+{
+    const int st = check_gate_args(g_raw, g_dtype, A_log, flags, tokens, H, K);
+    if (st != GDN2_OK) return st;
+    if ((tokens > 0 && (!dy || !dg_raw)) || !dA_log || (dt_bias != nullptr) != (ddt_bias != nullptr))
+        return GDN2_ERR_INVALID;
+    if (!workspace || workspace_bytes < gate_bwd_workspace_bytes(tokens, H, K, dt_bias != nullptr))
+        return GDN2_ERR_WORKSPACE;
+    return launch_gate_bwd(g_raw, g_dtype, A_log, dt_bias, lower_bound, flags, dy, dg_raw, dA_log, ddt_bias,
+                           tokens, H, K, workspace, static_cast<hipStream_t>(stream));
+}
+
 size_t gdn2_short_conv_bwd_workspace_size(int B, int T, int D, int conv_width)
 {
     if (B < 0 || T < 0 || D < 0 || conv_width < 1 || conv_width > 8) return 0;

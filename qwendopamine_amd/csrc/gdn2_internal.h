@@ -149,6 +149,14 @@ size_t chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int io_dtype
                                  const int64_t *cu_host, int num_seqs);
 int launch_chunk_bwd(const ChunkBwdArgs &a, int io_dtype, int g_dtype, hipStream_t stream);
 
+// Decay gate activation and its VJP (gdn2_gate.hip).
+size_t gate_bwd_workspace_bytes(int64_t tokens, int H, int K, bool has_bias);
+int launch_gate_fwd(const void *g, int g_dtype, const float *A_log, const float *dt_bias, float lower_bound,
+                    unsigned flags, float *y, int64_t tokens, int H, int K, hipStream_t stream);
+int launch_gate_bwd(const void *g, int g_dtype, const float *A_log, const float *dt_bias, float lower_bound,
+                    unsigned flags, const float *dy, void *dg, float *dA_log, float *ddt_bias, int64_t tokens,
+                    int H, int K, void *workspace, hipStream_t stream);
+
 // Float32 chunk op with 128 < d_k <= 256 (gdn2_chunk_wide.hip): token-serial
 // kernels with chunk start states kept for the backward, for the key widths
 // whose fp32 chunk workspace does not fit the MFMA kernels' LDS.

@@ -333,23 +333,69 @@ def fused_recurrent_gdn2(
     )
 
 
+class GateFunction(torch.autograd.Function):
+    """The decay gate on its HIP kernels with their VJP: ``gdn2_gate_fwd`` /
+    ``gdn2_gate_bwd`` (reference ``kda_gate_fwd`` / ``kda_gate_bwd`` and
+    ``KDAGateFunction``, ``chunk_kda.py:3223-3340``)."""
+
+    @staticmethod
+    def forward(ctx, g, A_log, dt_bias, lower_bound):
+        name = "gate_activation"
+        _require_gpu(name, g, A_log, dt_bias)
+        H, K = g.shape[-2], g.shape[-1]
+        dt = g.dtype if g.dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
+        gr = _io(g, dt)
+        a = _io(A_log.reshape(-1), torch.float32)
+        db = None if dt_bias is None else _io(dt_bias.reshape(-1), torch.float32)
+        if a.numel() != H or (db is not None and db.numel() != H * K):
+            raise ValueError(f"{name}: A_log must hold {H} values and dt_bias {H * K}, got "
+                             f"{a.numel()} and {None if db is None else db.numel()}")
+        flags = nat.FLAG_LOWER_BOUND if lower_bound is not None else 0
+        y = torch.empty(gr.shape, dtype=torch.float32, device=g.device)
+        st = nat.load().gdn2_gate_fwd(
+            nat.ptr(gr), nat.dtype_code(dt), nat.ptr(a), nat.ptr(db),
+            float(lower_bound) if lower_bound is not None else 0.0, flags, nat.ptr(y),
+            gr.numel() // (H * K), H, K, nat.stream_handle(g.device))
+        nat.check(st, name)
+        ctx.save_for_backward(gr, a, db)
+        ctx.meta = (lower_bound, flags, g.dtype, A_log.dtype, A_log.shape,
+                    None if dt_bias is None else (dt_bias.dtype, dt_bias.shape))
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        gr, a, db = ctx.saved_tensors
+        lower_bound, flags, g_dtype, a_dtype, a_shape, db_meta = ctx.meta
+        H, K = gr.shape[-2], gr.shape[-1]
+        tokens = gr.numel() // (H * K)
+        dyc = _io(dy, torch.float32)
+        dgr = torch.empty_like(gr)
+        dA = torch.empty(H, dtype=torch.float32, device=gr.device)
+        ddt = None if db is None else torch.empty(H * K, dtype=torch.float32, device=gr.device)
+        lib = nat.load()
+        ws_bytes = lib.gdn2_gate_bwd_workspace_size(tokens, H, K, int(db is not None))
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=gr.device)
+        st = lib.gdn2_gate_bwd(
+            nat.ptr(gr), nat.dtype_code(gr.dtype), nat.ptr(a), nat.ptr(db),
+            float(lower_bound) if lower_bound is not None else 0.0, flags, nat.ptr(dyc), nat.ptr(dgr),
+            nat.ptr(dA), nat.ptr(ddt), tokens, H, K, ws.data_ptr(), ws.numel(), nat.stream_handle(gr.device))
+        nat.check(st, "gate_activation backward")
+        d_db = None if ddt is None else ddt.to(db_meta[0]).reshape(db_meta[1])
+        return dgr.to(g_dtype), dA.to(a_dtype).reshape(a_shape), d_db, None
+
+
 def gate_activation(g: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor | None,
                     lower_bound: float | None) -> torch.Tensor:
-    """The in-kernel decay activation as torch ops (differentiable), float32.
+    """The in-kernel decay activation as a differentiable step on the HIP kernels, float32.
 
     ``g = -exp(A_log[h]) * softplus(g + dt_bias[h, d])``, or with a lower bound
     ``g = lower_bound * sigmoid(exp(A_log[h]) * (g + dt_bias[h, d]))``
     (reference ``kda_gate`` forward, ``chunk_kda.py:3025-3053``; the same
-    formula the HIP kernels apply under ``GDN2_FLAG_GATE_IN_KERNEL``).
+    formula the HIP kernels apply under ``GDN2_FLAG_GATE_IN_KERNEL``).  Its
+    backward gives the gradients of ``g``, ``A_log`` and ``dt_bias``
+    (``kda_gate_bwd``, ``chunk_kda.py:3254-3292``).
     """
-    H, K = g.shape[-2], g.shape[-1]
-    x = g.float()
-    if dt_bias is not None:
-        x = x + dt_bias.float().reshape(H, K)
-    a = A_log.float().exp().reshape(H, 1)
-    if lower_bound is not None:
-        return lower_bound * torch.sigmoid(a * x)
-    return -a * torch.nn.functional.softplus(x)
+    return GateFunction.apply(g, A_log, dt_bias, lower_bound)
 
 
 def chunk_gdn2_fwd(

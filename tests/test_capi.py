@@ -161,3 +161,23 @@ def test_chunk_workspace_size(lib):
     assert lib.gdn2_chunk_bwd_workspace_size(2, 130, 3, 200, 64, 0, None, 2) == 2 * 3 * 64 * 4 * 16 * 64 * 16
     assert lib.gdn2_chunk_bwd_workspace_size(2, 130, 3, 200, 200, 0, None, 2) == (
         2 * 3 * 2 * 64 * 8 * 16 * 64 * 16 + 4 * 2 * 130 * 3 * 200 * 4)
+
+
+def test_gate_argument_checks(lib):
+    """The gate entry points reject bad arguments before any launch (no GPU needed)."""
+    from qwendopamine_amd import _native as nat
+
+    assert lib.gdn2_gate_bwd_workspace_size(1000, 3, 257, 1) == 0
+    # 16 blocks of 64 tokens: dA_log partials [16, 3] and ddt_bias partials [16, 3, 100], 256-byte aligned
+    assert lib.gdn2_gate_bwd_workspace_size(1000, 3, 100, 1) == 256 + 16 * 3 * 100 * 4
+    assert lib.gdn2_gate_bwd_workspace_size(1000, 3, 100, 0) == 256
+    fake = ctypes.c_void_p(256)  # never dereferenced: each call returns before launching
+    assert lib.gdn2_gate_fwd(fake, 0, fake, None, 0.0, 0, fake, 10, 3, 257, None) == nat.ERR_UNSUPPORTED
+    assert lib.gdn2_gate_fwd(None, 0, fake, None, 0.0, 0, fake, 10, 3, 100, None) == nat.ERR_INVALID
+    assert lib.gdn2_gate_fwd(fake, 0, None, None, 0.0, 0, fake, 10, 3, 100, None) == nat.ERR_INVALID
+    assert lib.gdn2_gate_fwd(fake, 0, fake, None, 0.0, nat.FLAG_L2NORM_QK, fake, 10, 3, 100, None) == nat.ERR_INVALID
+    assert lib.gdn2_gate_bwd(fake, 0, fake, fake, 0.0, 0, fake, fake, fake, None, 10, 3, 100, fake, 1 << 20,
+                             None) == nat.ERR_INVALID
+    assert lib.gdn2_gate_bwd(fake, 0, fake, None, 0.0, 0, fake, fake, fake, None, 10, 3, 100, fake, 8,
+                             None) == nat.ERR_WORKSPACE
+
