@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -464,6 +465,30 @@ def bench_prologue(torch, dev, reps=20):
         op_, _ = ops.chunk_gdn2_conv(rq, rk, rv, ws, pf, pb, pw, num_heads=H, output_final_state=True, **pkw)
         ops.gated_rmsnorm(op_, z, nw, 1e-5)
 
+    # The same call with the decay gate's inputs as a GatedDeltaNet2 of this shape makes them
+    # (its f_proj of random hidden states, its A_log / dt_bias init).  The random logits above
+    # with decay rates up to 16 put most 16-token decay spans beyond 2^115, where the diagonal
+    # blocks take the slower quarter-referred and exact pair paths; the module's init puts none
+    # there.  Both are reported.
+    from qwendopamine_amd import GatedDeltaNet2
+
+    torch.manual_seed(3)
+    gmod = GatedDeltaNet2(hidden_size=D, num_heads=H, head_dim=Dh).to(dev, bf).eval()
+    with torch.no_grad():
+        mf = gmod.f_proj(torch.randn(B, T, D, generator=gen, device=dev).to(bf)).view(B, T, H, Dh)
+    mkw = dict(pkw, A_log=gmod.A_log.detach().float(), dt_bias=gmod.dt_bias.detach().float())
+    del gmod
+
+    def pconv_fused_module():
+        op_, _ = ops.chunk_gdn2_conv(rq, rk, rv, ws, mf, pb, pw, num_heads=H, output_final_state=True, **mkw)
+        ops.gated_rmsnorm(op_, z, nw, 1e-5)
+
+    def wide_fraction(f, kw):
+        with torch.no_grad():
+            gl = ops.gate_activation(f.float(), kw["A_log"], kw["dt_bias"], None)
+            span = -(gl.view(B, T // 16, 16, H, Dh).sum(2)) / math.log(2.0)
+        return round(float((span > 115).float().mean()), 4)
+
     # Training: forward + backward of the q / k / v convolutions and of the gated norm, on the
     # HIP kernels (autograd functions) against torch's autograd through the reference's ops.
     xg = [x.detach().clone().requires_grad_(True) for x in xs]
@@ -525,7 +550,8 @@ def bench_prologue(torch, dev, reps=20):
                                   ("floor_launch", floor_launch), ("floor_state", floor_state),
                                   ("dec_fused", dec_fused), ("dec_separate", dec_separate),
                                   ("pre_fused", pre_fused), ("pre_separate", pre_separate),
-                                  ("pconv_fused", pconv_fused), ("pconv_separate", pconv_separate))}
+                                  ("pconv_fused", pconv_fused), ("pconv_separate", pconv_separate),
+                                  ("pconv_fused_module", pconv_fused_module))}
     return {
         "config": {"workload": "C3 module shape: B4 T2048, q/k/v 1024 channels, conv width 4; "
                                "norm over 16 heads x 64", "dtype": "bf16"},
@@ -553,7 +579,11 @@ def bench_prologue(torch, dev, reps=20):
         "prefill_conv": {"workload": f"B{B} T{T}, {H} heads x {Dh}: q/k/v convolutions + chunk op + gated norm, "
                                      "from the raw projections",
                          "fused_us": round(t["pconv_fused"], 2), "separate_hip_us": round(t["pconv_separate"], 2),
-                         "hbm_bytes_removed": conv_bytes},
+                         "hbm_bytes_removed": conv_bytes,
+                         "gate_inputs": "random logits, decay rates exp(A_log) in [1, 16]",
+                         "wide_span_fraction": wide_fraction(pf, pkw),
+                         "fused_module_gates_us": round(t["pconv_fused_module"], 2),
+                         "module_gates_wide_span_fraction": wide_fraction(mf, mkw)},
     }
 
 

@@ -16,8 +16,11 @@
 // sub-block's decay span in log2 units): rows q*2^(G_r - G_start(R)), columns
 // k*2^(G_end(I) - G_i) times the decay between the blocks (<= 1), and 2^D on
 // the diagonal block.  A diagonal block whose span exceeds kDiagSpanLimit2
-// (factors would leave the normal fp32/bf16 range) is recomputed exactly,
-// pair by pair, on the VALU.  Decays are handled in log2 units so every
+// (factors would leave the normal fp32/bf16 range) is formed from four
+// products referred to the starts of its 4-token quarters, and the pairs inside
+// a quarter whose own span exceeds the limit are summed exactly, pair by pair,
+// on the VALU (all 16 columns, in the instantiations whose registers do not
+// hold the quarter products).  Decays are handled in log2 units so every
 // exponential is one v_exp_f32.
 //
 // Operands follow the K16 convention of gdn2_mfma.h: accumulators of one
@@ -559,13 +562,39 @@ chunk_prep_kernel(ChunkParams p, int items)
         // A diagonal block whose decay span is too wide for the factored form is
         // summed exactly, pair by pair (row m, column j of block R).
         const bool wave_slow = __ballot(wide) != 0;
-        f32x4 dq = zero4(), dl = zero4();
-        if (wave_slow) {
-            // Channel tiles outer, so that one tile's normalised values are
-            // live at a time; each column j still sums over (kt, i) in order.
-            float accq[16], accl[16];
+        // A wide block is still formed on MFMA (bf16 storage at d_k <= 64 and
+        // fp32 storage, where it fits the register budget): four products, each
+        // with the factors referred to the decay at the start of one 4-token
+        // quarter s, q_r 2^(G_r - G_s) and k_j 2^(G_s - G_j); the lane of row r
+        // keeps the product of its quarter.  For a key j before the quarter both
+        // factors are <= 1 (one that underflows belongs to a pair whose exact
+        // value is below 2^-115 |q||k|).  Pairs inside the quarter are exact as
+        // long as its span is <= kDiagSpanLimit2; factors of pairs that the
+        // causal mask drops, or of rows of other quarters, are clamped (finite,
+        // discarded).  A wave with a wider quarter recomputes the pairs inside
+        // the quarters exactly, pair by pair (4 of the 16 columns of a row).
+        constexpr bool QPATH = PK == PrecKind::F32 || (KP <= 64 && std::is_same<TI, bf16_t>::value);
+        bool qwide = !QPATH;
+        if (QPATH && wave_slow) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) accq[j] = accl[j] = 0.f;
+            for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float prev = __shfl(gv[kt][i], m >= 4 ? l - 4 : l, 64);
+                    const float span = m >= 4 ? prev - gv[kt][i] : -gv[kt][i];
+                    qwide = qwide || ((m & 3) == 3 && span > kDiagSpanLimit2);
+                }
+        }
+        const bool wave_exact = wave_slow && __ballot(qwide) != 0;
+        f32x4 dq = zero4(), dl = zero4();
+        // Exact pair sums of row m (this lane's channels, then over the lane
+        // groups) for the columns j0 + jj, jj < NJ, with j0 + jj > m dropped;
+        // each column sums over (kt, i) in order.
+        auto exact_pairs = [&](auto NJc, int j0, float (&cq)[decltype(NJc)::value],
+                               float (&cl)[decltype(NJc)::value]) __attribute__((always_inline)) {
+            constexpr int NJ = decltype(NJc)::value;
+#pragma unroll
+            for (int jj = 0; jj < NJ; ++jj) cq[jj] = cl[jj] = 0.f;
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) {
                 float xq[4], xk[4], xe[4];
@@ -573,26 +602,84 @@ chunk_prep_kernel(ChunkParams p, int items)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) {
+                    for (int jj = 0; jj < NJ; ++jj) {
+                        const int j = j0 + jj;
                         const float kj = __shfl(xk[i], 16 * kg + j, 64);
                         const float Gj = __shfl(gv[kt][i], 16 * kg + j, 64);
                         const float ex = (j <= m) ? fexp2(gv[kt][i] - Gj) : 0.f;
-                        accq[j] = fmaf(xq[i] * kj, ex, accq[j]);
-                        accl[j] = fmaf(xe[i] * kj, ex, accl[j]);
+                        cq[jj] = fmaf(xq[i] * kj, ex, cq[jj]);
+                        cl[jj] = fmaf(xe[i] * kj, ex, cl[jj]);
                     }
             }
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                float aq_ = accq[j], al_ = accl[j];
-                aq_ += __shfl_xor(aq_, 16, 64);
-                aq_ += __shfl_xor(aq_, 32, 64);
-                al_ += __shfl_xor(al_, 16, 64);
-                al_ += __shfl_xor(al_, 32, 64);
-                if (kg == (j >> 2)) {
-                    dq[j & 3] = aq_;
-                    dl[j & 3] = al_;
+            for (int jj = 0; jj < NJ; ++jj) {
+                cq[jj] += __shfl_xor(cq[jj], 16, 64);
+                cq[jj] += __shfl_xor(cq[jj], 32, 64);
+                cl[jj] += __shfl_xor(cl[jj], 16, 64);
+                cl[jj] += __shfl_xor(cl[jj], 32, 64);
+            }
+        };
+        if constexpr (QPATH) {
+            if (wave_slow) {
+                constexpr float kClamp2 = 120.0f;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    // Two key tiles at a time (one 32-wide contraction step), so
+                    // that only their factors are live.
+                    f32x4 pq = zero4(), pl = zero4();
+#pragma unroll
+                    for (int s2 = 0; s2 < NKS; ++s2) {
+                        Q fa[2], fb[2], fe[2];
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            const int kt = 2 * s2 + hh;
+                            float xq[4], xk[4], xe[4], a[4], bq[4], be[4];
+                            qke(kt, xq, xk, xe);
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const float G = gv[kt][i];
+                                const float Gs = s == 0 ? 0.0f : __shfl(G, 16 * kg + 4 * s - 1, 64);
+                                const float up = fexp2(fminf(G - Gs, kClamp2));
+                                a[i] = xk[i] * fexp2(fminf(Gs - G, kClamp2));
+                                bq[i] = xq[i] * up;
+                                be[i] = xe[i] * up;
+                            }
+                            fa[hh] = pack4<PK>(a[0], a[1], a[2], a[3]);
+                            fb[hh] = pack4<PK>(bq[0], bq[1], bq[2], bq[3]);
+                            fe[hh] = pack4<PK>(be[0], be[1], be[2], be[3]);
+                        }
+                        pq = mma2<PK>(pq, fa[0], fa[1], fb[0], fb[1]);
+                        pl = mma2<PK>(pl, fa[0], fa[1], fe[0], fe[1]);
+                    }
+                    if ((m >> 2) == s) {
+                        dq = pq;
+                        dl = pl;
+                    }
                 }
             }
+            if (wave_exact) {
+                // Lane (m, kg) of the products holds columns 4 kg .. 4 kg + 3
+                // of row m, so the lane with kg = m / 4 holds row m's quarter.
+                float cq[4], cl[4];
+                exact_pairs(std::integral_constant<int, 4>{}, 4 * (m >> 2), cq, cl);
+                if (kg == (m >> 2)) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        dq[i] = cq[i];
+                        dl[i] = cl[i];
+                    }
+                }
+            }
+        } else if (wave_exact) {
+            // All 16 columns of row m; lane (m, kg) keeps columns 4 kg .. 4 kg + 3.
+            float cq[16], cl[16];
+            exact_pairs(std::integral_constant<int, 16>{}, 0, cq, cl);
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (kg == (j >> 2)) {
+                    dq[j & 3] = cq[j];
+                    dl[j & 3] = cl[j];
+                }
         }
         __syncthreads();
 

@@ -24,6 +24,7 @@ def rand_inputs(B, T, H, K, V, HV=None, seed=0, decay="paper", h0_std=0.1, gate_
     decay="paper":   g = -softplus(N(0,1) + 2)        (BASELINE distribution)
     decay="unit":    g = -|U(0,1)|                      (reference test_gdn2.py:122)
     decay="extreme": g = -softplus(2 N(0,1) + 7)        (spans > 80 per 16 tokens)
+    decay="sheer":   g = -softplus(2 N(0,1) + 28)       (spans > 115 per 4 tokens)
     """
     HV = HV or H
     rng = np.random.default_rng(seed)
@@ -36,6 +37,8 @@ def rand_inputs(B, T, H, K, V, HV=None, seed=0, decay="paper", h0_std=0.1, gate_
         g = -np.abs(rng.random((B, T, HV, K)))
     elif decay == "extreme":
         g = -np.logaddexp(0.0, 2.0 * rng.standard_normal((B, T, HV, K)) + 7.0)
+    elif decay == "sheer":
+        g = -np.logaddexp(0.0, 2.0 * rng.standard_normal((B, T, HV, K)) + 28.0)
     else:
         raise ValueError(decay)
     g = g * gate_scale

@@ -169,6 +169,43 @@ def test_fused_conv_matches_oracle(gpu_device, V, norm):
     assert eo <= 2e-2 and es <= 2e-2
 
 
+def test_fused_conv_gate_logits_matches_oracle(gpu_device):
+    """The in-kernel gate on random logits with decay rates up to 16 (as the config-3 bench
+    line): most 16-token diagonal blocks span more than 2^115 and a share of their 4-token
+    quarters too, so the quarter-referred products and the exact within-quarter pair sums
+    both run.  Against the float64 oracle on g = -exp(A_log) softplus(logit + dt_bias),
+    b = sigmoid(logit), w = sigmoid(logit)."""
+    from qwendopamine_amd import ops
+
+    B, T, H, K, V = 2, 200, 4, 64, 64
+    print(f"[case] fused conv, gate logits with wide decays, vs oracle B={B} T={T} H={H}", flush=True)
+    dev = gpu_device
+    raw, taps, g, b, w = _inputs(dev, B, T, H, K, V, seed=21, gate_logits=True)
+    gen = torch.Generator(device="cpu").manual_seed(23)
+    A_log = torch.log(torch.linspace(4.0, 16.0, H))
+    dt_bias = torch.randn(H * K, generator=gen) * 0.5
+    kw = dict(use_gate_in_kernel=True, A_log=A_log.to(dev), dt_bias=dt_bias.to(dev), bw_logits=True)
+    with torch.no_grad():
+        o, ht = ops.chunk_gdn2_conv(*raw, taps, g, b, w, num_heads=H, initial_state=None,
+                                    output_final_state=True, use_qk_l2norm_in_kernel=True, **kw)
+    torch.cuda.synchronize()
+    np64 = lambda t: t.detach().double().cpu().numpy()  # noqa: E731
+    x = np64(g) + dt_bias.double().numpy().reshape(H, K)
+    g_ref = -np.exp(A_log.double().numpy()).reshape(H, 1) * np.logaddexp(0.0, x)
+    sig = lambda t: 1.0 / (1.0 + np.exp(-np64(t)))  # noqa: E731
+    G2 = g_ref[:, : T // 16 * 16].reshape(B, T // 16, 16, H, K) / np.log(2.0)
+    wide16 = float((-G2.sum(2) > 115).mean())
+    wide4 = float((-G2.reshape(B, T // 16, 4, 4, H, K).sum(3) > 115).any(2).mean())
+    cq, ck, cv = (orc.short_conv(np64(xx), np64(wt).reshape(-1, 4))[0] for xx, wt in zip(raw, taps))
+    o_ref, s_ref = orc.recurrent_fwd(cq.reshape(B, T, H, K), ck.reshape(B, T, H, K), cv.reshape(B, T, H, V),
+                                     g_ref, sig(b), sig(w), None)
+    eo, es = rel_l2(o, o_ref), rel_l2(ht, s_ref)
+    print(f"  wide 16-token blocks {wide16:.3f}, with a wide quarter {wide4:.4f}; "
+          f"rel_l2 o={eo:.2e} state={es:.2e}", flush=True)
+    assert wide16 > 0.3 and wide4 > 0.0
+    assert eo <= 2e-2 and es <= 2e-2
+
+
 def test_fused_conv_rejects_unsupported(gpu_device):
     from qwendopamine_amd import ops
 
