@@ -170,15 +170,17 @@ def test_chunk_matches_oracle(gpu_device, dtype, K, V, T):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("decay,K", [("extreme", 64), ("extreme", 128), ("sheer", 64), ("sheer", 128)])
-def test_chunk_wide_decay_diagonal_blocks(gpu_device, dtype, decay, K):
+@pytest.mark.parametrize("decay,K,T", [("extreme", 64, 128), ("extreme", 128, 128), ("sheer", 64, 128),
+                                         ("sheer", 128, 128), ("extreme", 64, 77), ("sheer", 40, 77)])
+def test_chunk_wide_decay_diagonal_blocks(gpu_device, dtype, decay, K, T):
     """Diagonal blocks whose decay span leaves the factored range.  "extreme" spans (> 115
     per 16 tokens, within it per 4-token quarter) take the four quarter-referred MFMA
     products; "sheer" ones (> 115 per quarter) add the exact pair sums inside each quarter.
     float32 storage and bf16 at d_k = 64 take these paths; bf16 at d_k = 128 sums every
-    pair of a wide block exactly."""
-    print(f"[case] chunk {decay} decay {dtype} K={K}", flush=True)
-    o, ht, o_ref, s_ref = _chunk(gpu_device, dtype, 1, 128, 2, K, 64, decay=decay)
+    pair of a wide block exactly.  T = 77 ends in a partial chunk whose last 16-token block
+    and last quarter are partial; K = 40 leaves channels of the padded width unused."""
+    print(f"[case] chunk {decay} decay {dtype} K={K} T={T}", flush=True)
+    o, ht, o_ref, s_ref = _chunk(gpu_device, dtype, 1, T, 2, K, 64, decay=decay)
     assert np.isfinite(o.float().cpu().numpy()).all()
     eo, es = rel_l2(o, o_ref), rel_l2(ht, s_ref)
     print(f"  rel_l2 o={eo:.2e} state={es:.2e}", flush=True)
