@@ -549,6 +549,70 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p, int i
     const int tid0 = threadIdx.x, wv0 = __builtin_amdgcn_readfirstlane(tid0 >> 6);
     const int H = p.H, K = p.K, V = p.V, VP = p.VP;
 
+    // Rows of an item by direct LDS loads into the factor tiles (16-bit inputs
+    // with two factor planes, K == KP): an item's q, k, b, g rows are requested
+    // once the previous item's pair products are done, so that it starts on
+    // rows already in LDS.  Tensor regions: q -> sKT plane 0, k -> sKT plane 1,
+    // b -> sQT plane 0, g -> sET; wave w's part of a region starts at w times its
+    // size.  Lane (m, kg) uses row 16R + m, channels 16 (hh NKH + j) + 4 kg + i.
+    //  * 16-bit rows: 16-byte piece p = 32 j + 16 h + m holds channels
+    //    16 (hh NKH + j) + 8 h .. + 7 of row m at byte 16 p, so lane (m, kg)
+    //    reads tile j at 16 (32 j + 16 (kg / 2) + m) + 8 (kg % 2): one 512-byte
+    //    run per tile, no bank conflicts.
+    //  * fp32 rows: piece 64 j + l (lane l = 16 kg + m) is exactly lane l's tile j.
+    // Each request covers 64 consecutive pieces, fetched by 64 lanes from 16
+    // rows (64 contiguous bytes of each row).
+    constexpr bool PFR = NPL == 2 && sizeof(TI) == 2;
+    auto rows_lds = [&](int tensor) __attribute__((always_inline)) {
+        return tensor == 0 ? reinterpret_cast<unsigned char *>(&sKT[0][0][0][0])
+             : tensor == 1 ? reinterpret_cast<unsigned char *>(&sKT[1][0][0][0])
+             : tensor == 2 ? reinterpret_cast<unsigned char *>(&sQT[0][0][0][0])
+                           : reinterpret_cast<unsigned char *>(&sET[0][0][0][0]);
+    };
+    static_assert(!PFR || (8 * NKH * 512 <= static_cast<int>(sizeof(sKT[0])) &&
+                           8 * NKH * 256 * static_cast<int>(sizeof(TG)) <= static_cast<int>(sizeof(sET))),
+                  "prefetched rows must fit the factor tiles");
+    auto dma_rows = [&](int itm, int wvx, int lx) __attribute__((always_inline)) {
+        const int gcn = itm / H, hn = itm - gcn * H;
+        int nn, jcn;
+        int64_t bosn, lenn;
+        locate_chunk(p, gcn, nn, jcn, bosn, lenn);
+        const int64_t t0n = bosn + static_cast<int64_t>(jcn) * kChunk;
+        const int64_t remn = lenn - static_cast<int64_t>(jcn) * kChunk;
+        const int lcn = remn < kChunk ? static_cast<int>(remn) : kChunk;
+        const int rowi = 16 * (wvx >> 1) + (lx & 15);
+        // Rows past the chunk end read its first row (in bounds); they are
+        // zeroed where they are used.
+        const int64_t row0 = ((t0n + (rowi < lcn ? rowi : 0)) * H + hn) * static_cast<int64_t>(K) +
+                             16 * (wvx & 1) * NKH;
+        auto go16 = [&](const TI *base, int tensor) __attribute__((always_inline)) {
+            unsigned char *dst = rows_lds(tensor) + wvx * (NKH * 512);
+#pragma unroll
+            for (int t = 0; t < (32 * NKH + 63) / 64; ++t) {
+                const int pc = 64 * t + lx;  // piece
+                if (pc < 32 * NKH) {
+                    const int j = pc >> 5, h = (pc >> 4) & 1;
+                    __builtin_amdgcn_global_load_lds(reinterpret_cast<const char *>(base + row0 + 16 * j + 8 * h),
+                                                     dst + 1024 * t, 16, 0, 0);
+                }
+            }
+        };
+        go16(static_cast<const TI *>(p.q), 0);
+        go16(static_cast<const TI *>(p.k), 1);
+        go16(static_cast<const TI *>(p.b), 2);
+        if constexpr (sizeof(TG) == 4) {
+            const TG *gb = static_cast<const TG *>(p.g);
+            unsigned char *dst = rows_lds(3) + wvx * (NKH * 1024);
+#pragma unroll
+            for (int j = 0; j < NKH; ++j)
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const char *>(gb + row0 + 16 * j + 4 * (lx >> 4)),
+                                                 dst + 1024 * j, 16, 0, 0);
+        } else {
+            go16(reinterpret_cast<const TI *>(p.g), 3);
+        }
+    };
+    if (PFR && K == KP && static_cast<int>(blockIdx.x) < items) dma_rows(blockIdx.x, wv0, tid0 & 63);
+
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
     // The thread and wave indices are made opaque per item so that the
     // compiler does not hoist the many per-lane LDS and global addresses out of
@@ -559,6 +623,10 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p, int i
     const int R = wv >> 1, hh = wv & 1;
     const int l = tid & 63, m = l & 15, kg = l >> 4;
     const int gc = item / H, h = item - (item / H) * H;
+    // The rows' direct LDS loads (and, with them, the previous item's
+    // gradient stores) are complete before anything of this item, on every
+    // path, so that no later barrier has to wait for them.
+    if constexpr (PFR) __builtin_amdgcn_s_waitcnt(0);
 
     int n, jc;
     int64_t bos, len;
@@ -698,15 +766,34 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p, int i
         if (K == KP) {
             // Every channel tile is inside K: all loads are requested before any
             // is used (rows past the chunk end read its first row and are zeroed).
-            const int64_t off = row_ok ? roff : (t0 * H + h) * static_cast<int64_t>(K);
             Raw4<TG> rg[NKH];
+            if constexpr (PFR) {
+                // Requested during the previous item (or before the first),
+                // complete since the wait at the top of the item.
+                auto rd16 = [&](int tensor, int j) __attribute__((always_inline)) {
+                    return *reinterpret_cast<const uint2 *>(rows_lds(tensor) + wv * (NKH * 512) +
+                                                            16 * (32 * j + 16 * (kg >> 1) + m) + 8 * (kg & 1));
+                };
 #pragma unroll
-            for (int j = 0; j < NKH; ++j) {
-                const int c0 = 16 * (hh * NKH + j) + 4 * kg;
-                qv[j].load(q + off + c0);
-                kv[j].load(k + off + c0);
-                bv[j].load(b + off + c0);
-                rg[j].load(g + off + c0);
+                for (int j = 0; j < NKH; ++j) {
+                    qv[j].u = rd16(0, j);
+                    kv[j].u = rd16(1, j);
+                    bv[j].u = rd16(2, j);
+                    if constexpr (sizeof(TG) == 4)
+                        rg[j].f = *reinterpret_cast<const float4 *>(rows_lds(3) + wv * (NKH * 1024) + 1024 * j + 16 * l);
+                    else
+                        rg[j].u = rd16(3, j);
+                }
+            } else {
+                const int64_t off = row_ok ? roff : (t0 * H + h) * static_cast<int64_t>(K);
+#pragma unroll
+                for (int j = 0; j < NKH; ++j) {
+                    const int c0 = 16 * (hh * NKH + j) + 4 * kg;
+                    qv[j].load(q + off + c0);
+                    kv[j].load(k + off + c0);
+                    bv[j].load(b + off + c0);
+                    rg[j].load(g + off + c0);
+                }
             }
             between();  // more requests, issued before these rows are used
 #pragma unroll
@@ -1127,6 +1214,9 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p, int i
         sRow[1][hh][r] = pk;
     }
     __syncthreads();
+    // Every wave's pair products are done: the factor tiles take the next
+    // item's rows.
+    if (PFR && K == KP && item + static_cast<int>(gridDim.x) < items) dma_rows(item + gridDim.x, wv, l);
     pq = sRow[0][0][r] + sRow[0][1][r];
     pk = sRow[1][0][r] + sRow[1][1][r];
     if (row_ok) {
@@ -1156,7 +1246,14 @@ __global__ __launch_bounds__(512) void chunk_bwd_kside_kernel(BwdParams p, int i
         store4<TI>(static_cast<TI *>(p.dk), roff, c0, K, dk4);
     }
     }
-    __syncthreads();  // sRow, sT and the block tables are rewritten by the next item
+    // sRow, sT and the block tables are rewritten by the next item.  With the
+    // rows' direct LDS loads in flight, the barrier waits only for this
+    // wave's LDS accesses (a workgroup fence would also wait for the loads,
+    // which the next item's first wait covers).
+    if constexpr (PFR)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+        __syncthreads();
     }
 }
 
