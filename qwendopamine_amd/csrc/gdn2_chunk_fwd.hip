@@ -559,8 +559,8 @@ chunk_prep_kernel(ChunkParams p, int items)
                 for (int i = 0; i < 4; ++i) wide = wide || (-gv[kt][i] > kDiagSpanLimit2);
             }
         }
-        // A diagonal block whose decay span is too wide for the factored form is
-        // summed exactly, pair by pair (row m, column j of block R).
+        // A diagonal block whose decay span (in any channel) is too wide for the
+        // factored form is formed below instead of by the block products.
         const bool wave_slow = __ballot(wide) != 0;
         // A wide block is still formed on MFMA (bf16 storage at d_k <= 64 and
         // fp32 storage, where it fits the register budget): four products, each
