@@ -855,6 +855,10 @@ chunk_prep_kernel(ChunkParams p, int items)
         __syncthreads();
         // Off-diagonal blocks, one sub-diagonal at a time:
         //   X_RI = -X_RR * sum_{J=I}^{R-1} L_RJ X_JI.
+        // Wave R forms column I = R: besides L and the diagonal blocks it reads
+        // only the blocks of its own column from earlier steps, so the steps
+        // need a workgroup barrier only at the end (other waves read every
+        // column afterwards).
         for (int d = 1; d <= 3; ++d) {
             if (R < 4 - d) {
                 const int Rr = R + d, I = R;
@@ -871,7 +875,12 @@ chunk_prep_kernel(ChunkParams p, int items)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) xblk(Rr, I)[(4 * kg + i) * LDB + m] = -xr[i];
             }
-            __syncthreads();
+            if (d < 3) {
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+            } else {
+                __syncthreads();
+            }
         }
 
         // X to the blob (row block R).
