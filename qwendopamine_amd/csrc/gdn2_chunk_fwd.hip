@@ -960,11 +960,15 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     const int H = p.H, K = p.K, V = p.V;
     const int n = pair / H, h = pair % H;
 
-    // Waves 0..3 compute (wave c owns value columns 16c..16c+15 of the
-    // slice); waves 4..7 only move the per-chunk blobs from HBM to LDS.
+    // The first 8 - NCW waves compute (wave c owns value columns 16c..16c+15
+    // of the slice); the last NCW waves only move the per-chunk blobs and z
+    // from HBM to LDS.  A 16-column slice has one compute wave and seven copy
+    // waves, since there the copies set the pace; wider slices four of each.
+    constexpr int NCW = (NCT == 1 && !NORM) ? 7 : 4;
+    constexpr int CT = 64 * NCW;  // copy threads
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, m = l & 15, kg = l >> 4;
-    const bool copier = wv >= 4;
-    const int ctid = tid - 256;
+    const bool copier = wv >= 8 - NCW;
+    const int ctid = tid - 64 * (8 - NCW);
     const bool active = wv < NCT;
     const int col = vs * BV + 16 * wv + m;
     const bool col_ok = active && col < V;
@@ -1002,16 +1006,16 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         constexpr int CB = 8;
         const u32x4 *src = blob(gci);
         u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf]);
-        for (int u0 = 0; u0 < U16; u0 += 256 * CB) {
+        for (int u0 = 0; u0 < U16; u0 += CT * CB) {
             u32x4 t[CB];
 #pragma unroll
             for (int c = 0; c < CB; ++c) {
-                const int u = u0 + ctid + 256 * c;
+                const int u = u0 + ctid + CT * c;
                 t[c] = src[u < U16 ? u : U16 - 1];
             }
 #pragma unroll
             for (int c = 0; c < CB; ++c) {
-                const int u = u0 + ctid + 256 * c;
+                const int u = u0 + ctid + CT * c;
                 if (u < U16) dst[u] = t[c];
             }
         }
@@ -1023,17 +1027,17 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     const int v0 = vs * BV;
     constexpr int EPV = 16 / static_cast<int>(sizeof(TI));  // values per 16-byte load
     constexpr int ZT = kChunk * BV / EPV;                    // loads per tensor per chunk
-    constexpr int NZT = (ZT + 255) / 256;
+    constexpr int NZT = (ZT + CT - 1) / CT;
     // Whole 16-byte row pieces for every row of this slice (uniform per workgroup).
     const bool zfast = (V % EPV) == 0 && v0 + BV <= V;
     // CONV: lane ctid takes row piece ctid % PPR of NZC consecutive tokens
     // (plus the three rows before them, the convolution window) instead of
-    // tokens 256a / PPR apart, so the window rows are shared by its tokens.
+    // tokens CT a / PPR apart, so the window rows are shared by its tokens.
     // Slices narrower than 64 use 8-byte pieces (CW = 4 channels), so that
-    // all four copy waves share the convolution arithmetic.
+    // more copy lanes share the convolution arithmetic.
     constexpr int CW = BV >= 64 ? EPV : EPV / 2;  // channels per CONV piece
     constexpr int PPR = BV / CW;                  // CONV pieces per token
-    constexpr int NZC = (kChunk * PPR + 255) / 256;
+    constexpr int NZC = (kChunk * PPR + CT - 1) / CT;
     constexpr int NH = 3;                         // window rows before a lane's first token
     using CPiece = std::conditional_t<CW == EPV, u32x4, uint2>;
     using ZRaw = std::conditional_t<CONV, ZRows<CPiece, NZC + NH, NZC>, ZRows<u32x4, NZT, NZT>>;
@@ -1095,7 +1099,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             // make the request wait for its own data.
 #pragma unroll
             for (int a = 0; a < NZT; ++a) {
-                const int task = ctid + 256 * a;
+                const int task = ctid + CT * a;
                 const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
                 const bool live = task < ZT && tok < lc;
                 const int64_t off = live ? ((t0 + tok) * H + h) * V + v0 + c : (t0 * H + h) * V + v0;
@@ -1105,7 +1109,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         } else {
 #pragma unroll
             for (int a = 0; a < NZT; ++a) {
-                const int task = ctid + 256 * a;
+                const int task = ctid + CT * a;
                 const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
                 const bool live = task < ZT && tok < lc;
                 const int64_t off = ((t0 + tok) * H + h) * V + v0 + c;
@@ -1168,7 +1172,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         }
 #pragma unroll
         for (int a = 0; a < NZT; ++a) {
-            const int task = ctid + 256 * a;
+            const int task = ctid + CT * a;
             if (task >= ZT) continue;
             const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
             const TI *rv = reinterpret_cast<const TI *>(&r.v[a]);
@@ -1201,7 +1205,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         }
     }
 
-    // Copy waves (4..7) and compute waves (0..3) run separate loops with the
+    // Copy waves and compute waves run separate loops with the
     // same barrier schedule -- one barrier after the prologue, one per chunk,
     // and in the single-buffer case one more per reload -- so the copy waves'
     // prefetch registers never overlap the compute waves' live ranges.
@@ -1222,15 +1226,15 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // causal diagonal and are never read here (the products use blocks
                 // (R, J) with J < 2 or J <= R, see pair_off), so the per-chunk copies
                 // skip them: compact unit c maps to blob unit cmap(c), which steps over
-                // the four skipped runs of 2 * BU units.  With c = ctid + 256 u and
-                // ctid < 256, each threshold test folds to a constant except in the
+                // the four skipped runs of 2 * BU units.  With c = ctid + CT u and
+                // ctid < CT, each threshold test folds to a constant except in the
                 // one step u it falls in.
                 constexpr int BU = 256 * static_cast<int>(sizeof(st)) / 16;  // units per 16x16 block
                 constexpr int AQU = static_cast<int>(BL::AQ * static_cast<int64_t>(sizeof(st)) / 16);
-                constexpr int NC = U16 - 8 * BU, PFC = (NC + 255) / 256;
+                constexpr int NC = U16 - 8 * BU, PFC = (NC + CT - 1) / CT;
                 auto cmap = [&](int c, int u) __attribute__((always_inline)) {
                     auto ge = [&](int t) __attribute__((always_inline)) {
-                        return t <= 256 * u ? 1 : (t >= 256 * u + 256 ? 0 : (c >= t ? 1 : 0));
+                        return t <= CT * u ? 1 : (t >= CT * u + CT ? 0 : (c >= t ? 1 : 0));
                     };
                     return c + 2 * BU * (ge(2 * BU) + ge(4 * BU) + ge(AQU - 2 * BU) + ge(AQU));
                 };
@@ -1239,7 +1243,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     const u32x4 *src = blob(gci);
 #pragma unroll
                     for (int u = 0; u < PFC; ++u) {
-                        const int c = ctid + 256 * u;
+                        const int c = ctid + CT * u;
                         dst[u] = src[cmap(c < NC ? c : NC - 1, u)];
                     }
                 };
@@ -1247,7 +1251,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf]);
 #pragma unroll
                     for (int u = 0; u < PFC; ++u) {
-                        const int c = ctid + 256 * u;
+                        const int c = ctid + CT * u;
                         if (c < NC) dst[cmap(c, u)] = src[u];
                     }
                 };
