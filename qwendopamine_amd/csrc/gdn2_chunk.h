@@ -258,6 +258,17 @@ inline TrainLayout train_layout(int64_t nc, int H, int K, int V, int io_dtype)
     return t;
 }
 
+// Wait until at most N vector memory requests of this wave are outstanding
+// (gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at their
+// no-wait maxima).  Loads complete in issue order, so this waits for every
+// request older than the N newest.
+template <int N>
+__device__ __forceinline__ void wait_vm_newest()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // Backward scratch: per-chunk end-state gradients (dhs) and dY = X^T dU (dys).
 struct BwdLayout {
     int64_t dhs, dys, total;

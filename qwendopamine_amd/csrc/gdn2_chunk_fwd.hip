@@ -1221,6 +1221,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 issue_z(fastc, zA, 0);
                 land_z(zA, 0, 0);
             }
+            // Lanes without z rows of their own skip land_z; wait for their
+            // requests too, so that no request of chunk 0 is left outstanding
+            // into the prefetch below.
+            wait_vm_newest<0>();
             if constexpr (DB) {
                 // Blocks (0, 2), (0, 3), (1, 2), (1, 3) of X and of Aqk lie above the
                 // causal diagonal and are never read here (the products use blocks
@@ -1280,6 +1284,13 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // the prefetch synchronous.
                 auto cl = [&](int j) __attribute__((always_inline)) { return j < nch ? j : nch - 1; };
                 ZRaw &zC = ONEZ ? zA : zB;  // the set holding chunk jc+2 at the second half
+                // Requests of one chunk (blob units and z rows), all unconditional
+                // for 16-byte rows.  Before a set lands, the only newer requests
+                // are the other set's, so an explicit count waits for exactly the
+                // set being landed: the compiler's own count, merged over the
+                // paths of the masked landings, waited for every request there.
+                constexpr int NREQ = PFC + (CONV ? NZC + NH + NZC : 2 * NZT);
+                constexpr bool EXACT = decltype(fastc)::value && !ONEZ;
                 if (nch > 0) {
                     issue(pA, gc0 + cl(1));
                     issue_z(fastc, zA, cl(1));
@@ -1289,24 +1300,30 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     }
                 }
                 __syncthreads();
-                for (int jc = 0; jc < nch; jc += 2) {
+                // Pairs of chunk steps, then the last step of an odd count, which
+                // has nothing left to land: the loop has no exit between its two
+                // halves, so every path into its header has issued both sets in
+                // the same order and the compiler's load counts stay exact.
+                int jc = 0;
+                for (; jc + 1 < nch; jc += 2) {
                     if (!DEEP) {
                         issue(pB, gc0 + cl(jc + 2));
                         if (!ONEZ) issue_z(fastc, zB, cl(jc + 2));
                     }
-                    if (jc + 1 < nch) land_z(zA, jc + 1, 1);
+                    if constexpr (EXACT) wait_vm_newest<NREQ>();
+                    land_z(zA, jc + 1, 1);
                     if (ONEZ) issue_z(fastc, zA, cl(jc + 2));
-                    if (jc + 1 < nch) land(pA, 1);
+                    land(pA, 1);
                     if (DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
                         issue_z(fastc, zA, cl(jc + 3));
                     }
                     __syncthreads();
-                    if (jc + 1 >= nch) break;
                     if (!DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
                         if (!ONEZ) issue_z(fastc, zA, cl(jc + 3));
                     }
+                    if constexpr (EXACT) wait_vm_newest<NREQ>();
                     if (jc + 2 < nch) land_z(zC, jc + 2, 0);
                     if (ONEZ) issue_z(fastc, zA, cl(jc + 3));
                     if (jc + 2 < nch) land(pB, 0);
@@ -1316,6 +1333,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     }
                     __syncthreads();
                 }
+                if (jc < nch) __syncthreads();
             } else {
                 __syncthreads();
                 for (int jc = 0; jc < nch; ++jc) {
@@ -1543,9 +1561,14 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // access instead of four 2- or 4-byte ones.
                 const int c0 = vs * BV + 16 * wv + 4 * kg;
                 const bool vec = o_vec && c0 + 4 <= V;
+                // All four transposes are issued before the first store, so that
+                // their latencies overlap instead of each one stalling its store.
+                Q trs[4];
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) trs[rt] = pack4<PK>(mma1<PK>(zero4(), pack4<PK>(oa[rt]), ident));
 #pragma unroll
                 for (int rt = 0; rt < 4; ++rt) {
-                    const Q tr = pack4<PK>(mma1<PK>(zero4(), pack4<PK>(oa[rt]), ident));
+                    const Q tr = trs[rt];
                     if constexpr (NORM) {
                         // Rounded squares summed in order over this lane's 4
                         // columns, continuing the left neighbour's 4 (lanes kg
