@@ -923,6 +923,32 @@ struct ZRows {
     Piece v[NV], w[NW];
 };
 
+// Blob units per chunk and lane for the scan's copy waves that also land z rows
+// (z) and for those that only copy the blob (b): zl and bl lanes, nc units, one
+// lane's z rows costing about zc units.  Chosen so that the busier of the two
+// roles has the least work; without blob-only lanes every lane takes an equal
+// share.
+struct CopySplit {
+    int z, b;
+};
+constexpr CopySplit copy_split(int nc, int zl, int bl, int zc)
+{
+    const int even = (nc + zl + bl - 1) / (zl + bl);
+    if (bl == 0) return CopySplit{even, 0};
+    CopySplit best{even, even};
+    int best_cost = 1 << 30;
+    for (int z = 1; z * zl <= nc; ++z) {
+        const int rem = nc - z * zl;
+        const int b = rem > 0 ? (rem + bl - 1) / bl : 1;
+        const int cost = z + zc > b ? z + zc : b;
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = CopySplit{z, b};
+        }
+    }
+    return best;
+}
+
 // ---------------------------------------------------------------------------
 // Scan: one workgroup per (sequence, head, value slice of BV columns).
 // ---------------------------------------------------------------------------
@@ -1060,6 +1086,11 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     // barrier is needed.
     const int cz = CW * (ctid % PPR), tz0 = NZC * (ctid / PPR);
     const bool zlane = copier && tz0 < kChunk;
+    // Copy lanes with z rows to land (the first ZLANES), and the whole waves
+    // holding them (ZL): with seven copy waves some have none, and those take
+    // a larger share of the blob instead.
+    constexpr int ZLANES = CONV ? PPR * ((kChunk + NZC - 1) / NZC) : (ZT < CT ? ZT : CT);
+    constexpr int ZL = (ZLANES + 63) / 64 * 64 < CT ? (ZLANES + 63) / 64 * 64 : CT;
     __shared__ __align__(16) TI sZT[CONV ? BV * 4 : 8];
     if constexpr (CONV) {
         if (copier) {
@@ -1214,7 +1245,16 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         // for the element-wise rows of ragged slices (uniform per workgroup),
         // so that each loop body is straight-line and the compiler's
         // load-completion waits stay exact.
-        auto copy_loop = [&](auto fastc) __attribute__((always_inline)) {
+        auto copy_loop = [&](auto fastc, auto zrole) __attribute__((always_inline)) {
+            // zrole: this wave lands z rows (and its share of the blob); the
+            // other copy waves only move blob units.
+            constexpr bool ZR = decltype(zrole)::value;
+            auto iz = [&](ZRaw &r, int j) __attribute__((always_inline)) {
+                if constexpr (ZR) issue_z(fastc, r, j);
+            };
+            auto lz = [&](const ZRaw &r, int j, int b) __attribute__((always_inline)) {
+                if constexpr (ZR) land_z(r, j, b);
+            };
             ZRaw zA, zB;
             if (nch > 0) {
                 copy_blob(gc0, 0);
@@ -1235,10 +1275,19 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // one step u it falls in.
                 constexpr int BU = 256 * static_cast<int>(sizeof(st)) / 16;  // units per 16x16 block
                 constexpr int AQU = static_cast<int>(BL::AQ * static_cast<int64_t>(sizeof(st)) / 16);
-                constexpr int NC = U16 - 8 * BU, PFC = (NC + CT - 1) / CT;
+                constexpr int NC = U16 - 8 * BU;
+                // Compact units [B0 + WD u, B0 + WD u + WD) at step u of this
+                // role's lanes: the z lanes take the first SPL.z steps of ZL
+                // units, the blob-only lanes the rest, CT - ZL units a step.
+                constexpr CopySplit SPL = copy_split(NC, ZL, CT - ZL, CONV ? 4 : 1);
+                constexpr int PFC = ZR ? SPL.z : SPL.b;
+                constexpr int WD = ZR ? ZL : CT - ZL;
+                constexpr int B0 = ZR ? 0 : ZL * SPL.z;
+                static_assert(ZL * SPL.z + (CT - ZL) * SPL.b >= NC, "every blob unit has a copy lane");
+                const int rl = ZR ? ctid : ctid - ZL;
                 auto cmap = [&](int c, int u) __attribute__((always_inline)) {
                     auto ge = [&](int t) __attribute__((always_inline)) {
-                        return t <= CT * u ? 1 : (t >= CT * u + CT ? 0 : (c >= t ? 1 : 0));
+                        return t <= B0 + WD * u ? 1 : (t >= B0 + WD * u + WD ? 0 : (c >= t ? 1 : 0));
                     };
                     return c + 2 * BU * (ge(2 * BU) + ge(4 * BU) + ge(AQU - 2 * BU) + ge(AQU));
                 };
@@ -1247,7 +1296,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     const u32x4 *src = blob(gci);
 #pragma unroll
                     for (int u = 0; u < PFC; ++u) {
-                        const int c = ctid + CT * u;
+                        const int c = B0 + rl + WD * u;
                         dst[u] = src[cmap(c < NC ? c : NC - 1, u)];
                     }
                 };
@@ -1255,7 +1304,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf]);
 #pragma unroll
                     for (int u = 0; u < PFC; ++u) {
-                        const int c = ctid + CT * u;
+                        const int c = B0 + rl + WD * u;
                         if (c < NC) dst[cmap(c, u)] = src[u];
                     }
                 };
@@ -1289,14 +1338,14 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // are the other set's, so an explicit count waits for exactly the
                 // set being landed: the compiler's own count, merged over the
                 // paths of the masked landings, waited for every request there.
-                constexpr int NREQ = PFC + (CONV ? NZC + NH + NZC : 2 * NZT);
+                constexpr int NREQ = PFC + (!ZR ? 0 : CONV ? NZC + NH + NZC : 2 * NZT);
                 constexpr bool EXACT = decltype(fastc)::value && !ONEZ;
                 if (nch > 0) {
                     issue(pA, gc0 + cl(1));
-                    issue_z(fastc, zA, cl(1));
+                    iz(zA, cl(1));
                     if (DEEP) {
                         issue(pB, gc0 + cl(2));
-                        issue_z(fastc, zB, cl(2));
+                        iz(zB, cl(2));
                     }
                 }
                 __syncthreads();
@@ -1308,28 +1357,28 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 for (; jc + 1 < nch; jc += 2) {
                     if (!DEEP) {
                         issue(pB, gc0 + cl(jc + 2));
-                        if (!ONEZ) issue_z(fastc, zB, cl(jc + 2));
+                        if (!ONEZ) iz(zB, cl(jc + 2));
                     }
                     if constexpr (EXACT) wait_vm_newest<NREQ>();
-                    land_z(zA, jc + 1, 1);
-                    if (ONEZ) issue_z(fastc, zA, cl(jc + 2));
+                    lz(zA, jc + 1, 1);
+                    if (ONEZ) iz(zA, cl(jc + 2));
                     land(pA, 1);
                     if (DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
-                        issue_z(fastc, zA, cl(jc + 3));
+                        iz(zA, cl(jc + 3));
                     }
                     __syncthreads();
                     if (!DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
-                        if (!ONEZ) issue_z(fastc, zA, cl(jc + 3));
+                        if (!ONEZ) iz(zA, cl(jc + 3));
                     }
                     if constexpr (EXACT) wait_vm_newest<NREQ>();
-                    if (jc + 2 < nch) land_z(zC, jc + 2, 0);
-                    if (ONEZ) issue_z(fastc, zA, cl(jc + 3));
+                    if (jc + 2 < nch) lz(zC, jc + 2, 0);
+                    if (ONEZ) iz(zA, cl(jc + 3));
                     if (jc + 2 < nch) land(pB, 0);
                     if (DEEP) {
                         issue(pB, gc0 + cl(jc + 4));
-                        issue_z(fastc, zB, cl(jc + 4));
+                        iz(zB, cl(jc + 4));
                     }
                     __syncthreads();
                 }
@@ -1340,19 +1389,29 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     __syncthreads();
                     if (jc + 1 < nch) {
                         copy_blob(gc0 + jc + 1, 0);
-                        issue_z(fastc, zA, jc + 1);
-                        land_z(zA, jc + 1, 0);
+                        iz(zA, jc + 1);
+                        lz(zA, jc + 1, 0);
                         __syncthreads();
                     }
                 }
             }
         };
+        auto by_role = [&](auto fastc) __attribute__((always_inline)) {
+            if constexpr (ZL < CT) {
+                if (ctid < ZL)
+                    copy_loop(fastc, std::true_type{});
+                else
+                    copy_loop(fastc, std::false_type{});
+            } else {
+                copy_loop(fastc, std::true_type{});
+            }
+        };
         if constexpr (CONV)
-            copy_loop(std::true_type{});  // whole 16-byte row pieces (checked by the host)
+            by_role(std::true_type{});  // whole 16-byte row pieces (checked by the host)
         else if (zfast)
-            copy_loop(std::true_type{});
+            by_role(std::true_type{});
         else
-            copy_loop(std::false_type{});
+            by_role(std::false_type{});
     } else {
         // NORM (gated output norm, BV == V): chunk jc's rounded, transposed
         // outputs and its gate rows stay in registers until the barrier that
