@@ -1091,6 +1091,11 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     // a larger share of the blob instead.
     constexpr int ZLANES = CONV ? PPR * ((kChunk + NZC - 1) / NZC) : (ZT < CT ? ZT : CT);
     constexpr int ZL = (ZLANES + 63) / 64 * 64 < CT ? (ZLANES + 63) / 64 * 64 : CT;
+    // WSTAGE (CONV with blob-only copy waves): those waves also request the w
+    // rows, activate them (SIGW) and stage them in sW by chunk parity a step
+    // before the z lanes form z = v * w, which then read w from LDS.
+    constexpr bool WSTAGE = CONV && DB && ZL < CT;
+    __shared__ __align__(16) TI sW[WSTAGE ? 2 : 1][WSTAGE ? kChunk * BV : 8];
     __shared__ __align__(16) TI sZT[CONV ? BV * 4 : 8];
     if constexpr (CONV) {
         if (copier) {
@@ -1103,7 +1108,9 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             for (int i = 0; i < CW / 2; ++i) reinterpret_cast<u32x4 *>(sZT + 4 * cz)[i] = t4[i];
         }
     }
-    auto issue_z = [&](auto fastc, ZRaw &r, int jc) __attribute__((always_inline)) {
+    // wrows (CONV): this call also requests the lane's w rows (else they are
+    // staged in sW by other copy waves).
+    auto issue_z = [&](auto fastc, ZRaw &r, int jc, auto wrows) __attribute__((always_inline)) {
         int64_t t0;
         int lc;
         chunk_rows(jc, t0, lc);
@@ -1118,11 +1125,13 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 const bool ok = zlane && tok < lc && kChunk * jc + tok >= 0;
                 r.v[j] = *reinterpret_cast<const CPiece *>(vp + (t0 + (ok ? tok : 0)) * p.ldv + colv);
             }
+            if constexpr (decltype(wrows)::value) {
 #pragma unroll
-            for (int a = 0; a < NZC; ++a) {
-                const int tok = tz0 + a;
-                const bool live = zlane && tok < lc;
-                r.w[a] = *reinterpret_cast<const CPiece *>(wp + ((t0 + (live ? tok : 0)) * H + h) * V + v0 + cz);
+                for (int a = 0; a < NZC; ++a) {
+                    const int tok = tz0 + a;
+                    const bool live = zlane && tok < lc;
+                    r.w[a] = *reinterpret_cast<const CPiece *>(wp + ((t0 + (live ? tok : 0)) * H + h) * V + v0 + cz);
+                }
             }
         } else if constexpr (decltype(fastc)::value) {
             // Dead lanes load the chunk's first row piece (always valid) and
@@ -1157,7 +1166,9 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
         }
     };
     // SIGW (GDN2_FLAG_SIGMOID_BW, inference only): w holds the logits.
-    auto land_z = [&](const ZRaw &r, int jc, int buf) __attribute__((always_inline)) {
+    // wlds (CONV): w of chunk jc is read from sW, staged (and activated) by
+    // other copy waves, instead of from this lane's registers.
+    auto land_z = [&](const ZRaw &r, int jc, int buf, auto wlds) __attribute__((always_inline)) {
         int64_t t0;
         int lc;
         chunk_rows(jc, t0, lc);
@@ -1171,6 +1182,12 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
 #pragma unroll
             for (int j = 0; j < NH; ++j) hok[j] = kChunk * jc + tz0 - NH + j >= 0;
             const bool silu = p.conv_silu != 0;
+            CPiece wl[NZC];
+            if constexpr (decltype(wlds)::value) {
+#pragma unroll
+                for (int a = 0; a < NZC; ++a)
+                    wl[a] = *reinterpret_cast<const CPiece *>(&sW[jc & 1][(tz0 + a) * BV + cz]);
+            }
             st zr[NZC][CW];
             // Channel by channel, so that only one column's window is unpacked
             // at a time.
@@ -1191,8 +1208,13 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     for (int jj = 0; jj < 4; ++jj) acc = fmaf(io<TI>::ld(tw, jj), x[a + jj], acc);
                     float vc = round_to<TI>(acc + 0.0f);
                     if (silu) vc = round_to<TI>(silu_f32(vc));
-                    const TI *rw = reinterpret_cast<const TI *>(&r.w[a]);
-                    const float wv_ = SIGW ? round_to<TI>(sigmoid_f(io<TI>::ld(rw, e))) : io<TI>::ld(rw, e);
+                    float wv_;
+                    if constexpr (decltype(wlds)::value) {
+                        wv_ = io<TI>::ld(reinterpret_cast<const TI *>(&wl[a]), e);
+                    } else {
+                        const TI *rw = reinterpret_cast<const TI *>(&r.w[a]);
+                        wv_ = SIGW ? round_to<TI>(sigmoid_f(io<TI>::ld(rw, e))) : io<TI>::ld(rw, e);
+                    }
                     zr[a][e] = P::from_f32(tz0 + a < lc ? vc * wv_ : 0.f);
                 }
             }
@@ -1250,16 +1272,16 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             // other copy waves only move blob units.
             constexpr bool ZR = decltype(zrole)::value;
             auto iz = [&](ZRaw &r, int j) __attribute__((always_inline)) {
-                if constexpr (ZR) issue_z(fastc, r, j);
+                if constexpr (ZR) issue_z(fastc, r, j, std::bool_constant<!WSTAGE>{});
             };
             auto lz = [&](const ZRaw &r, int j, int b) __attribute__((always_inline)) {
-                if constexpr (ZR) land_z(r, j, b);
+                if constexpr (ZR) land_z(r, j, b, std::bool_constant<WSTAGE>{});
             };
             ZRaw zA, zB;
             if (nch > 0) {
                 copy_blob(gc0, 0);
-                issue_z(fastc, zA, 0);
-                land_z(zA, 0, 0);
+                issue_z(fastc, zA, 0, std::true_type{});
+                land_z(zA, 0, 0, std::false_type{});
             }
             // Lanes without z rows of their own skip land_z; wait for their
             // requests too, so that no request of chunk 0 is left outstanding
@@ -1279,7 +1301,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // Compact units [B0 + WD u, B0 + WD u + WD) at step u of this
                 // role's lanes: the z lanes take the first SPL.z steps of ZL
                 // units, the blob-only lanes the rest, CT - ZL units a step.
-                constexpr CopySplit SPL = copy_split(NC, ZL, CT - ZL, CONV ? 4 : 1);
+                // A lane's z rows cost about 24 blob units with the convolution
+                // (s_memtime stamps: ~1.85 K cycles against ~65 per unit), one
+                // without it.
+                constexpr CopySplit SPL = copy_split(NC, ZL, CT - ZL, CONV ? 24 : 1);
                 constexpr int PFC = ZR ? SPL.z : SPL.b;
                 constexpr int WD = ZR ? ZL : CT - ZL;
                 constexpr int B0 = ZR ? 0 : ZL * SPL.z;
@@ -1338,14 +1363,72 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // are the other set's, so an explicit count waits for exactly the
                 // set being landed: the compiler's own count, merged over the
                 // paths of the masked landings, waited for every request there.
-                constexpr int NREQ = PFC + (!ZR ? 0 : CONV ? NZC + NH + NZC : 2 * NZT);
-                constexpr bool EXACT = decltype(fastc)::value && !ONEZ;
+                // WSTAGE, blob-only waves: w rows of chunk j in 16-byte pieces,
+                // staged in sW[j & 1] (activated) two half-steps after their
+                // request: at step c (landing chunk c+1) the lanes stage chunk
+                // c+2, read by the z lanes at step c+1 after a barrier.  The
+                // z lanes read sW[(c+1) & 1] at step c, never the buffer that
+                // is being staged.
+                constexpr bool WB = !ZR && WSTAGE;
+                constexpr int WT = kChunk * BV / EPV;
+                constexpr int NWT = WB ? (WT + (CT - ZL) - 1) / (CT - ZL) : 1;
+                u32x4 wA[NWT], wB[NWT];
+                auto issue_w = [&](u32x4 (&d)[NWT], int j) __attribute__((always_inline)) {
+                    if constexpr (WB) {
+                        int64_t t0;
+                        int lc;
+                        chunk_rows(j, t0, lc);
+#pragma unroll
+                        for (int a = 0; a < NWT; ++a) {
+                            const int task = rl + (CT - ZL) * a;
+                            const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
+                            const bool live = task < WT && tok < lc;
+                            const int64_t off = live ? ((t0 + tok) * H + h) * V + v0 + c : (t0 * H + h) * V + v0;
+                            d[a] = *reinterpret_cast<const u32x4 *>(wp + off);
+                        }
+                    }
+                };
+                auto land_w = [&](const u32x4 (&d)[NWT], int j) __attribute__((always_inline)) {
+                    if constexpr (WB) {
+#pragma unroll
+                        for (int a = 0; a < NWT; ++a) {
+                            const int task = rl + (CT - ZL) * a;
+                            if (task >= WT) continue;
+                            const int tok = task / (BV / EPV), c = EPV * (task % (BV / EPV));
+                            const TI *x = reinterpret_cast<const TI *>(&d[a]);
+                            TI y[EPV];
+#pragma unroll
+                            for (int e = 0; e < EPV; ++e) {
+                                // As the z lanes would: the module's torch sigmoid,
+                                // rounded to the input dtype (gdn2.py:865).
+                                const float w = io<TI>::ld(x, e);
+                                io<TI>::st(y, e, SIGW ? round_to<TI>(sigmoid_f(w)) : w);
+                            }
+                            *reinterpret_cast<u32x4 *>(&sW[j & 1][tok * BV + c]) = __builtin_bit_cast(u32x4, y);
+                        }
+                    }
+                };
+                constexpr int NREQ = PFC + (!ZR ? (WB ? NWT : 0) : CONV ? NZC + NH + (WSTAGE ? 0 : NZC) : 2 * NZT);
+                constexpr bool EXACT = decltype(fastc)::value && (!ONEZ || !ZR);
+                // The sets are requested here in the order the loop requests
+                // them (the compiler merges the two paths into its header).
                 if (nch > 0) {
-                    issue(pA, gc0 + cl(1));
-                    iz(zA, cl(1));
-                    if (DEEP) {
+                    if constexpr (WB) {
+                        issue_w(wA, cl(1));
+                        land_w(wA, 1);
+                    }
+                    if constexpr (DEEP) {
+                        issue(pA, gc0 + cl(1));
+                        iz(zA, cl(1));
+                        issue_w(wA, cl(2));
                         issue(pB, gc0 + cl(2));
                         iz(zB, cl(2));
+                        issue_w(wB, cl(3));
+                    } else {
+                        issue_w(wA, cl(2));
+                        issue(pA, gc0 + cl(1));
+                        iz(zA, cl(1));
+                        issue_w(wB, cl(3));
                     }
                 }
                 __syncthreads();
@@ -1363,10 +1446,12 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     lz(zA, jc + 1, 1);
                     if (ONEZ) iz(zA, cl(jc + 2));
                     land(pA, 1);
+                    land_w(wA, jc + 2);
                     if (DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
                         iz(zA, cl(jc + 3));
                     }
+                    issue_w(wA, cl(jc + 4));
                     __syncthreads();
                     if (!DEEP) {
                         issue(pA, gc0 + cl(jc + 3));
@@ -1376,10 +1461,12 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                     if (jc + 2 < nch) lz(zC, jc + 2, 0);
                     if (ONEZ) iz(zA, cl(jc + 3));
                     if (jc + 2 < nch) land(pB, 0);
+                    land_w(wB, jc + 3);
                     if (DEEP) {
                         issue(pB, gc0 + cl(jc + 4));
                         iz(zB, cl(jc + 4));
                     }
+                    issue_w(wB, cl(jc + 5));
                     __syncthreads();
                 }
                 if (jc < nch) __syncthreads();
