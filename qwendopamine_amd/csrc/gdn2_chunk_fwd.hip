@@ -1026,6 +1026,30 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     auto blob = [&](int gci) {
         return reinterpret_cast<const u32x4 *>(wsb + (static_cast<int64_t>(gci) * H + h) * BL::SIZE);
     };
+    // Blocks (0, 2), (0, 3), (1, 2), (1, 3) of X and of Aqk lie above the causal
+    // diagonal and are never read here (the products use blocks (R, J) with
+    // J < 2 or J <= R, see pair_off), so the double-buffered per-chunk copies
+    // skip them: compact unit c maps to blob unit cmap_unit(c), which steps over
+    // the four skipped runs of 2 * BU units.  With c in [b0 + wd u, b0 + wd u +
+    // wd) at unrolled step u, each threshold test folds to a constant except in
+    // the one step it falls in.
+    constexpr int BU = 256 * static_cast<int>(sizeof(st)) / 16;  // units per 16x16 block
+    constexpr int AQU = static_cast<int>(BL::AQ * static_cast<int64_t>(sizeof(st)) / 16);
+    constexpr int NC = U16 - 8 * BU;
+    auto cmap_unit = [](int c, int b0, int wd, int u) __attribute__((always_inline)) {
+        auto ge = [&](int t) __attribute__((always_inline)) {
+            return t <= b0 + wd * u ? 1 : (t >= b0 + wd * u + wd ? 0 : (c >= t ? 1 : 0));
+        };
+        return c + 2 * BU * (ge(2 * BU) + ge(4 * BU) + ge(AQU - 2 * BU) + ge(AQU));
+    };
+    // ASSIST (64-column inference slices, where the four copy waves set the
+    // pace and the compute waves wait at the step barrier): each compute lane
+    // also copies PFA units of the next chunk, the last NCA compact units,
+    // requested after its products and landed before the step's barrier.
+    constexpr bool ASSIST = DB && NCT == 4 && NCW == 4 && !TRAIN && !NORM && !CONV;
+    constexpr int PFA = ASSIST ? 4 : 0;
+    constexpr int NCA = 256 * PFA;
+    constexpr int NCC = NC - NCA;  // compact units the copy waves move
     // Whole blob into LDS, CB requests in flight per copy wave lane at a time
     // (a plain element loop would wait for each load before its store).
     auto copy_blob = [&](int gci, int buf) __attribute__((always_inline)) {
@@ -1288,41 +1312,25 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             // into the prefetch below.
             wait_vm_newest<0>();
             if constexpr (DB) {
-                // Blocks (0, 2), (0, 3), (1, 2), (1, 3) of X and of Aqk lie above the
-                // causal diagonal and are never read here (the products use blocks
-                // (R, J) with J < 2 or J <= R, see pair_off), so the per-chunk copies
-                // skip them: compact unit c maps to blob unit cmap(c), which steps over
-                // the four skipped runs of 2 * BU units.  With c = ctid + CT u and
-                // ctid < CT, each threshold test folds to a constant except in the
-                // one step u it falls in.
-                constexpr int BU = 256 * static_cast<int>(sizeof(st)) / 16;  // units per 16x16 block
-                constexpr int AQU = static_cast<int>(BL::AQ * static_cast<int64_t>(sizeof(st)) / 16);
-                constexpr int NC = U16 - 8 * BU;
                 // Compact units [B0 + WD u, B0 + WD u + WD) at step u of this
                 // role's lanes: the z lanes take the first SPL.z steps of ZL
                 // units, the blob-only lanes the rest, CT - ZL units a step.
                 // A lane's z rows cost about 24 blob units with the convolution
                 // (s_memtime stamps: ~1.85 K cycles against ~65 per unit), one
                 // without it.
-                constexpr CopySplit SPL = copy_split(NC, ZL, CT - ZL, CONV ? 24 : 1);
+                constexpr CopySplit SPL = copy_split(NCC, ZL, CT - ZL, CONV ? 24 : 1);
                 constexpr int PFC = ZR ? SPL.z : SPL.b;
                 constexpr int WD = ZR ? ZL : CT - ZL;
                 constexpr int B0 = ZR ? 0 : ZL * SPL.z;
-                static_assert(ZL * SPL.z + (CT - ZL) * SPL.b >= NC, "every blob unit has a copy lane");
+                static_assert(ZL * SPL.z + (CT - ZL) * SPL.b >= NCC, "every blob unit has a copy lane");
                 const int rl = ZR ? ctid : ctid - ZL;
-                auto cmap = [&](int c, int u) __attribute__((always_inline)) {
-                    auto ge = [&](int t) __attribute__((always_inline)) {
-                        return t <= B0 + WD * u ? 1 : (t >= B0 + WD * u + WD ? 0 : (c >= t ? 1 : 0));
-                    };
-                    return c + 2 * BU * (ge(2 * BU) + ge(4 * BU) + ge(AQU - 2 * BU) + ge(AQU));
-                };
                 u32x4 pA[PFC], pB[PFC];
                 auto issue = [&](u32x4 (&dst)[PFC], int gci) __attribute__((always_inline)) {
                     const u32x4 *src = blob(gci);
 #pragma unroll
                     for (int u = 0; u < PFC; ++u) {
                         const int c = B0 + rl + WD * u;
-                        dst[u] = src[cmap(c < NC ? c : NC - 1, u)];
+                        dst[u] = src[cmap_unit(c < NCC ? c : NCC - 1, B0, WD, u)];
                     }
                 };
                 auto land = [&](const u32x4 (&src)[PFC], int buf) __attribute__((always_inline)) {
@@ -1330,7 +1338,7 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
 #pragma unroll
                     for (int u = 0; u < PFC; ++u) {
                         const int c = B0 + rl + WD * u;
-                        if (c < NC) dst[cmap(c, u)] = src[u];
+                        if (c < NCC) dst[cmap_unit(c, B0, WD, u)] = src[u];
                     }
                 };
                 // Chunk jc+1 lands in the idle buffer at step jc.  Unrolled by
@@ -1559,6 +1567,18 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
             const int buf = DB ? (jc & 1) : 0;
             if (active) {
             const st *Bk = sB[buf];
+            // ASSIST: this lane's units of chunk jc+1 (the last chunk again past
+            // the end, data unused), requested before the products so that they
+            // hide the latency.
+            u32x4 pa[PFA > 0 ? PFA : 1];
+            if constexpr (ASSIST) {
+                const u32x4 *src = blob(gc0 + (jc + 1 < nch ? jc + 1 : nch - 1));
+#pragma unroll
+                for (int u = 0; u < PFA; ++u) {
+                    const int c = NCC + tid + 256 * u;
+                    pa[u] = src[cmap_unit(c < NC ? c : NC - 1, NCC, 256, u)];
+                }
+            }
             const int64_t t0 = bos + static_cast<int64_t>(jc) * kChunk;
             const int64_t rem = len - static_cast<int64_t>(jc) * kChunk;
             const int lc = rem < kChunk ? static_cast<int>(rem) : kChunk;
@@ -1696,6 +1716,18 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                         __builtin_amdgcn_sched_barrier(0);
                         run_step(st_ + 1, bufB, gB);
                         __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+            }
+            // ASSIST: land this lane's units of chunk jc+1 before the output
+            // stores, so that the wait covers no store.
+            if constexpr (ASSIST) {
+                if (jc + 1 < nch) {
+                    u32x4 *dst = reinterpret_cast<u32x4 *>(sB[buf ^ 1]);
+#pragma unroll
+                    for (int u = 0; u < PFA; ++u) {
+                        const int c = NCC + tid + 256 * u;
+                        if (c < NC) dst[cmap_unit(c, NCC, 256, u)] = pa[u];
                     }
                 }
             }
