@@ -925,21 +925,22 @@ struct ZRows {
 
 // Blob units per chunk and lane for the scan's copy waves that also land z rows
 // (z) and for those that only copy the blob (b): zl and bl lanes, nc units, one
-// lane's z rows costing about zc units.  Chosen so that the busier of the two
-// roles has the least work; without blob-only lanes every lane takes an equal
-// share.
+// lane's z rows costing about zc units, at most maxu units per lane (two
+// register sets of them are live).  Chosen so that the busier of the two roles
+// has the least work; without blob-only lanes every lane takes an equal share.
 struct CopySplit {
     int z, b;
 };
-constexpr CopySplit copy_split(int nc, int zl, int bl, int zc)
+constexpr CopySplit copy_split(int nc, int zl, int bl, int zc, int maxu)
 {
     const int even = (nc + zl + bl - 1) / (zl + bl);
     if (bl == 0) return CopySplit{even, 0};
     CopySplit best{even, even};
     int best_cost = 1 << 30;
-    for (int z = 1; z * zl <= nc; ++z) {
+    for (int z = 1; z * zl <= nc && z <= maxu; ++z) {
         const int rem = nc - z * zl;
         const int b = rem > 0 ? (rem + bl - 1) / bl : 1;
+        if (b > maxu) continue;
         const int cost = z + zc > b ? z + zc : b;
         if (cost < best_cost) {
             best_cost = cost;
@@ -988,9 +989,11 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
 
     // The first 8 - NCW waves compute (wave c owns value columns 16c..16c+15
     // of the slice); the last NCW waves only move the per-chunk blobs and z
-    // from HBM to LDS.  A 16-column slice has one compute wave and seven copy
-    // waves, since there the copies set the pace; wider slices four of each.
-    constexpr int NCW = (NCT == 1 && !NORM) ? 7 : 4;
+    // from HBM to LDS.  Every wave that a slice does not need for compute
+    // copies (the copies set the pace there): one compute wave and seven copy
+    // waves at 16 columns, two and six at 32, four of each at 64 and with the
+    // fused norm (whose per-token sums take four compute waves' slots).
+    constexpr int NCW = NORM ? 4 : 8 - NCT;
     constexpr int CT = 64 * NCW;  // copy threads
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, m = l & 15, kg = l >> 4;
     const bool copier = wv >= 8 - NCW;
@@ -1318,7 +1321,10 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // A lane's z rows cost about 24 blob units with the convolution
                 // (s_memtime stamps: ~1.85 K cycles against ~65 per unit), one
                 // without it.
-                constexpr CopySplit SPL = copy_split(NCC, ZL, CT - ZL, CONV ? 24 : 1);
+                // At most 20 units per lane, 16 with the convolution at d_k > 64
+                // (where the z lanes' window and the staged gate rows also hold
+                // registers).
+                constexpr CopySplit SPL = copy_split(NCC, ZL, CT - ZL, CONV ? 24 : 1, CONV && KP > 64 ? 16 : 20);
                 constexpr int PFC = ZR ? SPL.z : SPL.b;
                 constexpr int WD = ZR ? ZL : CT - ZL;
                 constexpr int B0 = ZR ? 0 : ZL * SPL.z;
