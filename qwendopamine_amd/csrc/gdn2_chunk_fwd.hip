@@ -1319,8 +1319,8 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // role's lanes: the z lanes take the first SPL.z steps of ZL
                 // units, the blob-only lanes the rest, CT - ZL units a step.
                 // A lane's z rows cost about 24 blob units with the convolution
-                // (s_memtime stamps: ~1.85 K cycles against ~65 per unit), one
-                // without it.
+                // (measured with s_memtime stamps in the copy waves: ~1.85 K
+                // cycles against ~65 per unit), one without it.
                 // At most 20 units per lane, 16 with the convolution at d_k > 64
                 // (where the z lanes' window and the staged gate rows also hold
                 // registers).
@@ -1372,11 +1372,6 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                 // the prefetch synchronous.
                 auto cl = [&](int j) __attribute__((always_inline)) { return j < nch ? j : nch - 1; };
                 ZRaw &zC = ONEZ ? zA : zB;  // the set holding chunk jc+2 at the second half
-                // Requests of one chunk (blob units and z rows), all unconditional
-                // for 16-byte rows.  Before a set lands, the only newer requests
-                // are the other set's, so an explicit count waits for exactly the
-                // set being landed: the compiler's own count, merged over the
-                // paths of the masked landings, waited for every request there.
                 // WSTAGE, blob-only waves: w rows of chunk j in 16-byte pieces,
                 // staged in sW[j & 1] (activated) two half-steps after their
                 // request: at step c (landing chunk c+1) the lanes stage chunk
@@ -1422,6 +1417,12 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
                         }
                     }
                 };
+                // Requests of one chunk and role (blob units, z rows or staged w
+                // rows), all unconditional for 16-byte rows.  Before a set lands,
+                // the only newer requests are the other set's, so an explicit
+                // count waits for exactly the set being landed.  It can only add
+                // waiting; the compiler's own counts stay exact as long as every
+                // path into the loop header has issued the sets in one order.
                 constexpr int NREQ = PFC + (!ZR ? (WB ? NWT : 0) : CONV ? NZC + NH + (WSTAGE ? 0 : NZC) : 2 * NZT);
                 constexpr bool EXACT = decltype(fastc)::value && (!ONEZ || !ZR);
                 // The sets are requested here in the order the loop requests
