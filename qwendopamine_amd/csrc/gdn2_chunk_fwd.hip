@@ -1048,7 +1048,8 @@ __global__ __launch_bounds__(512) void chunk_scan_kernel(ChunkParams p, int NVB,
     // ASSIST (64-column inference slices, where the four copy waves set the
     // pace and the compute waves wait at the step barrier): each compute lane
     // also copies PFA units of the next chunk, the last NCA compact units,
-    // requested after its products and landed before the step's barrier.
+    // requested before its products and landed after them, ahead of the
+    // output stores (so that the wait for them covers no store).
     constexpr bool ASSIST = DB && NCT == 4 && NCW == 4 && !TRAIN && !NORM && !CONV;
     constexpr int PFA = ASSIST ? 4 : 0;
     constexpr int NCA = 256 * PFA;
